@@ -1,0 +1,100 @@
+/*
+ * fp8.c -- OCP FP8 E4M3FN ("e4m3fn": bias 7, no infinities, max finite 448,
+ * NaN = S.1111.111) encode/decode and the per-tensor-scaled fp8 GEMM oracle.
+ *
+ * Not in the reference: its only fp8 type is the gfx942 FNUZ encoding
+ * (crates/fe2o3-device/src/fp8.rs:53-110, bias 8, max 240), which gfx950's
+ * MFMA does not consume.  This restatement follows the OCP 8-bit floating
+ * point specification (OFP8, rev 1.0) and is pinned by its closed forms.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker, never the product).
+ */
+#include <math.h>
+#include <string.h>
+
+#include "fe2o3_oracle.h"
+
+/* Exact decode: e == 0 -> m * 2^-9 (subnormal), e in 1..15 -> (1 + m/8) *
+ * 2^(e-7), except e == 15 && m == 7 -> NaN. */
+float fe2o3o_fp8e4m3_to_f32(uint8_t bits) {
+  uint32_t s = bits >> 7, e = (bits >> 3) & 0xf, m = bits & 0x7;
+  float v;
+  if (e == 15 && m == 7) return s ? -NAN : NAN;
+  if (e == 0)
+    v = ldexpf((float)m, -9);
+  else
+    v = ldexpf((float)(8 + m), (int)e - 10);
+  return s ? -v : v;
+}
+
+/* Round-to-nearest-even encode with saturation to +-448 (the OCP "satfinite"
+ * conversion); NaN maps to 0x7f with the input sign. */
+uint8_t fe2o3o_fp8e4m3_from_f32(float value) {
+  uint32_t bits;
+  memcpy(&bits, &value, 4);
+  uint8_t sign = (uint8_t)((bits >> 24) & 0x80);
+  if (isnan(value)) return (uint8_t)(sign | 0x7f);
+  float a = fabsf(value);
+  if (a >= 448.0f) return (uint8_t)(sign | 0x7e);
+  /* quantum of the target binade: 2^-9 below 2^-6, else 2^(floor(log2 a)-3) */
+  int exp2v;
+  frexpf(a, &exp2v); /* a = f * 2^exp2v, f in [0.5, 1) */
+  int unbiased = exp2v - 1;
+  int q = unbiased < -6 ? -9 : unbiased - 3;
+  float scaled = ldexpf(a, -q); /* exact: a is a binary32 value */
+  float r = nearbyintf(scaled); /* default rounding mode: ties-to-even */
+  float rv = ldexpf(r, q);
+  if (rv > 448.0f) rv = 448.0f;
+  /* rv is now exactly representable in e4m3: encode it */
+  if (rv == 0.0f) return sign;
+  int e2;
+  frexpf(rv, &e2);
+  int ub = e2 - 1;
+  if (ub < -6) {
+    int m = (int)ldexpf(rv, 9);
+    return (uint8_t)(sign | (uint8_t)m);
+  }
+  int m = (int)ldexpf(rv, -ub + 3) - 8;
+  return (uint8_t)(sign | (uint8_t)((ub + 7) << 3) | (uint8_t)m);
+}
+
+float fe2o3o_amax_f32(const float *x, uint64_t n, int32_t threads) {
+  float amax = 0.0f;
+#pragma omp parallel for reduction(max : amax) num_threads(threads > 0 ? threads : 1)
+  for (uint64_t i = 0; i < n; ++i) {
+    float a = fabsf(x[i]);
+    if (a > amax) amax = a;
+  }
+  return amax;
+}
+
+/* q = e4m3(x / scale) with one correctly rounded f32 division. */
+void fe2o3o_quantize_e4m3(const float *x, uint64_t n, float scale,
+                          uint8_t *out, int32_t threads) {
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+  for (uint64_t i = 0; i < n; ++i) out[i] = fe2o3o_fp8e4m3_from_f32(x[i] / scale);
+}
+
+/* acc = sum_k dec(a)*dec(b) in increasing k with separate rounding (each
+ * product of two e4m3 values is exact in binary32); c = acc * (sa*sb); the
+ * bf16 output is the RNE narrowing of c. */
+void fe2o3o_gemm_fp8_points(uint32_t k, const uint8_t *a_rows,
+                            const uint8_t *b_cols, uint64_t points,
+                            float scale_ab, float *out_f32, uint16_t *out_bf16,
+                            int32_t threads) {
+  float lut[256];
+  for (int i = 0; i < 256; ++i) lut[i] = fe2o3o_fp8e4m3_to_f32((uint8_t)i);
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+  for (uint64_t p = 0; p < points; ++p) {
+    const uint8_t *ar = a_rows + p * k;
+    const uint8_t *bc = b_cols + p * k;
+    float acc = 0.0f;
+    for (uint32_t d = 0; d < k; ++d) {
+      float prod = lut[ar[d]] * lut[bc[d]];
+      acc = acc + prod;
+    }
+    float c = acc * scale_ab;
+    if (out_f32) out_f32[p] = c;
+    if (out_bf16) out_bf16[p] = fe2o3o_bf16_from_f32(c);
+  }
+}
