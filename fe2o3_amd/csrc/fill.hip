@@ -1,0 +1,105 @@
+// fill.hip -- counter-based synthetic inputs generated directly in HBM.
+//
+// hash(i)    = mix64(seed ^ domain ^ i * 0xd6e8feb86659fd93), with mix64 the
+//              SplitMix64 finaliser the reference's input generator uses
+//              (examples/tiled_gemm_v1/src/inputs.rs:57-78);
+// normal(i)  = (sum of the four 16-bit fields of hash(3i), hash(3i+1),
+//              hash(3i+2)) - 393210, times 2^-16 (Irwin-Hall of twelve
+//              uniforms: mean 0, variance 1, every step exact);
+// uniform(i) = ((hash(i) >> 40) - 2^23) * 2^-23 on [-1, 1).
+// All integer work plus one exact int->f32 conversion and one RNE multiply,
+// so the values are bit-identical to any IEEE binary32 host evaluation.
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace {
+
+__device__ __forceinline__ uint64_t mix64(uint64_t v) {
+  v += 0x9e3779b97f4a7c15ull;
+  v = (v ^ (v >> 30)) * 0xbf58476d1ce4e5b9ull;
+  v = (v ^ (v >> 27)) * 0x94d049bb133111ebull;
+  return v ^ (v >> 31);
+}
+
+__device__ __forceinline__ uint64_t counter_hash(uint64_t seed, uint64_t domain, uint64_t i) {
+  return mix64(seed ^ domain ^ (i * 0xd6e8feb86659fd93ull));
+}
+
+__device__ __forceinline__ float counter_normal(uint64_t seed, uint64_t domain, uint64_t i) {
+  int64_t sum = 0;
+#pragma unroll
+  for (uint64_t j = 0; j < 3; ++j) {
+    uint64_t h = counter_hash(seed, domain, 3 * i + j);
+    sum += (int64_t)(h & 0xffff) + (int64_t)((h >> 16) & 0xffff) + (int64_t)((h >> 32) & 0xffff) +
+           (int64_t)(h >> 48);
+  }
+  int32_t centred = (int32_t)(sum - 393210);
+  return (float)centred * 0x1p-16f;
+}
+
+__global__ void __launch_bounds__(256) fill_normal_bf16_kernel(uint16_t* out, uint64_t n,
+                                                               uint64_t seed, uint64_t domain,
+                                                               float scale, uint64_t first) {
+  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    float x = counter_normal(seed, domain, first + i);
+    out[i] = fe2o3::bf16_bits_from_f32(__fmul_rn(x, scale));
+  }
+}
+
+__global__ void __launch_bounds__(256) fill_normal_f32_kernel(float* out, uint64_t n, uint64_t seed,
+                                                              uint64_t domain, float scale,
+                                                              uint64_t first) {
+  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    out[i] = __fmul_rn(counter_normal(seed, domain, first + i), scale);
+}
+
+__global__ void __launch_bounds__(256) fill_uniform_f32_kernel(float* out, uint64_t n,
+                                                               uint64_t seed, uint64_t domain,
+                                                               uint64_t first) {
+  uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    uint64_t h = counter_hash(seed, domain, first + i);
+    int32_t v = (int32_t)(h >> 40) - (1 << 23);
+    out[i] = (float)v * 0x1p-23f;
+  }
+}
+
+unsigned fill_blocks(uint64_t n) {
+  uint64_t b = (n + 255) / 256;
+  return (unsigned)(b < 16384 ? (b ? b : 1) : 16384);
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fe2o3_fill_normal_bf16(uint16_t* out, uint64_t n, uint64_t seed, uint64_t domain,
+                               float scale, uint64_t first_index, void* stream) {
+  if (n == 0) return FE2O3_OK;
+  if (out == nullptr) return FE2O3_ERR_NULL;
+  fill_normal_bf16_kernel<<<fill_blocks(n), 256, 0, (hipStream_t)stream>>>(out, n, seed, domain,
+                                                                            scale, first_index);
+  return fe2o3_host::after_launch();
+}
+
+int32_t fe2o3_fill_normal_f32(float* out, uint64_t n, uint64_t seed, uint64_t domain, float scale,
+                              uint64_t first_index, void* stream) {
+  if (n == 0) return FE2O3_OK;
+  if (out == nullptr) return FE2O3_ERR_NULL;
+  fill_normal_f32_kernel<<<fill_blocks(n), 256, 0, (hipStream_t)stream>>>(out, n, seed, domain,
+                                                                           scale, first_index);
+  return fe2o3_host::after_launch();
+}
+
+int32_t fe2o3_fill_uniform_f32(float* out, uint64_t n, uint64_t seed, uint64_t domain,
+                               uint64_t first_index, void* stream) {
+  if (n == 0) return FE2O3_OK;
+  if (out == nullptr) return FE2O3_ERR_NULL;
+  fill_uniform_f32_kernel<<<fill_blocks(n), 256, 0, (hipStream_t)stream>>>(out, n, seed, domain,
+                                                                            first_index);
+  return fe2o3_host::after_launch();
+}
+
+}  // extern "C"

@@ -1,0 +1,134 @@
+// gemm_bf16.hip -- bf16 "NT" GEMM for gfx950: C[m,n] (bf16, row-major) =
+// A[m,k] (row-major) * B^T with B stored [n,k] (k contiguous, i.e. the
+// BASELINE's column-major B), fp32 accumulation, RNE bf16 output.
+//
+// Fast path (m, n multiples of 256, k multiple of 64, 16-byte aligned):
+//   * workgroup tile 256x256x64, 256 threads = 4 waves in 2x2, each wave
+//     128x128 = 4x4 tiles of v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators
+//     per lane);
+//   * A and B tiles go global -> LDS directly with 16-byte
+//     global_load_lds_dwordx4 (no VGPR staging); each 128-byte LDS row (64 k
+//     values) holds its eight 16-byte chunks XOR-permuted by
+//     swz(row) = (row ^ (row >> 3)) & 7, so the MFMA operand reads (32
+//     consecutive rows, same chunk) fall in distinct banks;
+//   * two LDS stages (2 x 64 KiB), one barrier per K step;
+//   * the MFMA is issued as D = B_frag x A_frag, which leaves four
+//     consecutive output columns in each lane for 8-byte bf16 stores;
+//   * XCD-aware workgroup order: consecutive workgroup ids land on different
+//     XCDs, so ids are regrouped so that each XCD's workgroups cover a
+//     compact 4 x (n/256/2) block of output tiles sharing A and B panels in
+//     that XCD's L2.
+// Any other shape uses a bounds-checked 64x64-tile MFMA kernel.
+#include "common.hpp"
+#include "gemm_core.hpp"
+#include "internal.hpp"
+
+namespace {
+
+using namespace fe2o3;
+
+// ---- generic path -------------------------------------------------------------------
+constexpr int N_BM = 64, N_BN = 64, N_BK = 32, N_LDK = N_BK + 8;
+
+__global__ void __launch_bounds__(256) gemm_bf16_nt_generic_kernel(
+    const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint16_t* __restrict__ c,
+    uint32_t m, uint32_t n, uint32_t k) {
+  __shared__ __attribute__((aligned(16))) uint16_t a_lds[N_BM * N_LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t b_lds[N_BN * N_LDK];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const uint64_t row0 = (uint64_t)blockIdx.y * N_BM, col0 = (uint64_t)blockIdx.x * N_BN;
+  f32x4_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (uint64_t k0 = 0; k0 < k; k0 += N_BK) {
+    const int r = t >> 2, d0 = (t & 3) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint64_t gd = k0 + d0 + e;
+      const uint64_t ga = row0 + r, gb = col0 + r;
+      a_lds[r * N_LDK + d0 + e] = (ga < m && gd < k) ? a[ga * k + gd] : (uint16_t)0;
+      b_lds[r * N_LDK + d0 + e] = (gb < n && gd < k) ? b[gb * k + gd] : (uint16_t)0;
+    }
+    __syncthreads();
+    const int rc = lane & 15, chunk = lane >> 4;
+    bf16x8_t af[2], bf[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      af[i] = *reinterpret_cast<const bf16x8_t*>(a_lds + (wm * 32 + i * 16 + rc) * N_LDK + chunk * 8);
+      bf[i] = *reinterpret_cast<const bf16x8_t*>(b_lds + (wn * 32 + i * 16 + rc) * N_LDK + chunk * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    __syncthreads();
+  }
+  const int col_in = lane & 15, row_in = (lane >> 4) * 4;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint64_t gr = row0 + wm * 32 + i * 16 + row_in + e;
+        const uint64_t gc = col0 + wn * 32 + j * 16 + col_in;
+        if (gr < m && gc < n) c[gr * n + gc] = bf16_bits_from_f32(acc[i][j][e]);
+      }
+}
+
+// ---- fast path ----------------------------------------------------------------------------
+__global__ void __launch_bounds__(256, 1) gemm_bf16_nt_256_kernel(const uint16_t* __restrict__ a,
+                                                                   const uint16_t* __restrict__ b,
+                                                                   uint16_t* __restrict__ c,
+                                                                   uint32_t m, uint32_t n,
+                                                                   uint32_t k) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const uint32_t tiles_m = m / 256, tiles_n = n / 256;
+  uint32_t tm, tn;
+  gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  gemm_core::Acc256 acc;
+  gemm_core::zero(acc);
+  gemm_core::mainloop_nt_256(a + (uint64_t)tm * 256 * k, b + (uint64_t)tn * 256 * k, k, k, k, smem,
+                             acc);
+  gemm_core::store_bf16_256(acc, c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256, n);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+extern "C" int32_t fe2o3_gemm_bf16_nt(const uint16_t* a, uint64_t a_len, const uint16_t* b,
+                                      uint64_t b_len, uint16_t* c, uint64_t c_len, uint32_t m,
+                                      uint32_t n, uint32_t k, void* stream) {
+  FE2O3_FAULT("fe2o3_gemm_bf16_nt");
+  if (a_len != (uint64_t)m * k || b_len != (uint64_t)n * k || c_len != (uint64_t)m * n)
+    return FE2O3_ERR_LENGTH;
+  if (c_len == 0) return FE2O3_OK;
+  if ((a_len && !a) || (b_len && !b) || !c) return FE2O3_ERR_NULL;
+  if (k == 0) return (int32_t)hipMemsetAsync(c, 0, c_len * 2, (hipStream_t)stream);
+  const bool fast = m % 256 == 0 && n % 256 == 0 && k % 64 == 0 && aligned16(a) &&
+                    aligned16(b) && aligned16(c);
+  if (fast) {
+    static bool attr_set = false;
+    if (!attr_set) {
+      hipError_t e = hipFuncSetAttribute((const void*)gemm_bf16_nt_256_kernel,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         gemm_core::kSmemBytes256);
+      if (e != hipSuccess) return (int32_t)e;
+      attr_set = true;
+    }
+    const uint64_t tiles = (uint64_t)(m / 256) * (n / 256);
+    if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
+    gemm_bf16_nt_256_kernel<<<(unsigned)tiles, 256, gemm_core::kSmemBytes256,
+                              (hipStream_t)stream>>>(a, b, c, m, n, k);
+    return fe2o3_host::after_launch();
+  }
+  dim3 grid((n + N_BN - 1) / N_BN, (m + N_BM - 1) / N_BM);
+  if (grid.y > 65535u) return FE2O3_ERR_SHAPE;
+  gemm_bf16_nt_generic_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(a, b, c, m, n, k);
+  return fe2o3_host::after_launch();
+}

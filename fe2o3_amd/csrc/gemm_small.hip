@@ -1,0 +1,277 @@
+// gemm_small.hip -- the reference's fixed-profile and general GEMM kernels,
+// rebuilt for gfx950:
+//   * tiled_gemm_lds_slice1 / moe_expert_gemm_bf16_m16_n16_k16: one 16x16x16
+//     bf16 tile, one wave64, LDS staging, one v_mfma_f32_16x16x32_bf16 with
+//     the upper K half zero;
+//   * tiled_gemm_general_v1: any m, n, k, strides, alpha/beta; 64x64 output
+//     tiles per 256-thread workgroup, guarded zero-filled loads, MFMA
+//     16x16x32 bf16, unfused alpha/beta epilogue;
+//   * scalar_gemm_v1: f32, the reference's per-output sequential unfused
+//     recurrence, LDS-tiled and register-blocked (4x4 outputs per thread),
+//     bit-identical to the scalar oracle.
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace {
+
+using namespace fe2o3;
+
+// ---- 16x16x16 bf16 tile ------------------------------------------------------------
+// A row-major [16 rows][16 k]; B row-major [16 k][16 n]; C row-major f32.
+// LDS holds A as [row][k] and B transposed as [n][k] so both MFMA operands
+// are one 16-byte read: lane l < 32 reads row/col l%16, k-chunk l/16 (8 k
+// values); lanes 32..63 feed zeros for the unused upper K half.  The output
+// fragment of lane l is column l%16, rows 4*(l/16)+i (i = 0..3), i.e. the
+// reference's Blocked<Index1D,16,4> ownership
+// (crates/fe2o3-device/src/thread.rs:569-600) of the row-major C tile.
+__global__ void __launch_bounds__(64) tile16_bf16_kernel(const uint16_t* __restrict__ a,
+                                                         const uint16_t* __restrict__ b,
+                                                         float* __restrict__ c) {
+  __shared__ __attribute__((aligned(16))) uint16_t a_lds[16 * 16];
+  __shared__ __attribute__((aligned(16))) uint16_t bt_lds[16 * 16];
+  const int l = threadIdx.x;
+  // stage: lane l owns elements 4l..4l+3 of each operand
+  {
+    const uint2 av = *reinterpret_cast<const uint2*>(a + 4 * l);
+    *reinterpret_cast<uint2*>(a_lds + 4 * l) = av;
+    const uint2 bv = *reinterpret_cast<const uint2*>(b + 4 * l);
+    const int kk = l >> 2, n0 = (l & 3) * 4;
+    bt_lds[(n0 + 0) * 16 + kk] = (uint16_t)(bv.x & 0xffffu);
+    bt_lds[(n0 + 1) * 16 + kk] = (uint16_t)(bv.x >> 16);
+    bt_lds[(n0 + 2) * 16 + kk] = (uint16_t)(bv.y & 0xffffu);
+    bt_lds[(n0 + 3) * 16 + kk] = (uint16_t)(bv.y >> 16);
+  }
+  __syncthreads();
+  bf16x8_t af = {}, bf = {};
+  if (l < 32) {
+    const int rc = l & 15, chunk = l >> 4;
+    af = *reinterpret_cast<const bf16x8_t*>(a_lds + rc * 16 + chunk * 8);
+    bf = *reinterpret_cast<const bf16x8_t*>(bt_lds + rc * 16 + chunk * 8);
+  }
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf, acc, 0, 0, 0);
+  const int col = l & 15, row0 = (l >> 4) * 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[(row0 + i) * 16 + col] = acc[i];
+}
+
+// ---- general bf16 GEMM with alpha/beta -----------------------------------------------
+// C[r*ldc+j] = alpha * (A B)[r][j] + beta * C[r*ldc+j] for r < m, j < n.
+// A row-major (lda), B row-major [k][n] (ldb).  Workgroup tile 64x64, K step
+// 32, four waves in a 2x2 arrangement each owning 32x32 (2x2 MFMA tiles).
+constexpr int G_BM = 64, G_BN = 64, G_BK = 32;
+constexpr int G_LDK = G_BK + 8;  // padded LDS row (bf16 elements), 80 bytes
+
+__global__ void __launch_bounds__(256) gemm_general_kernel(
+    const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, float* __restrict__ c,
+    uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha,
+    float beta) {
+  __shared__ __attribute__((aligned(16))) uint16_t a_lds[G_BM * G_LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t bt_lds[G_BN * G_LDK];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const uint64_t row0 = (uint64_t)blockIdx.y * G_BM, col0 = (uint64_t)blockIdx.x * G_BN;
+  f32x4_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const uint32_t phases = (k + G_BK - 1) / G_BK;
+  for (uint32_t ph = 0; ph < phases; ++ph) {
+    const uint64_t k0 = (uint64_t)ph * G_BK;
+    // A: thread t loads row t/4, depths (t%4)*8 .. +7 (zero outside m x k)
+    {
+      const int r = t >> 2, d0 = (t & 3) * 8;
+      const uint64_t gr = row0 + r;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint64_t gd = k0 + d0 + e;
+        a_lds[r * G_LDK + d0 + e] = (gr < m && gd < k) ? a[gr * lda + gd] : (uint16_t)0;
+      }
+    }
+    // B: thread t loads depth t/8, columns (t%8)*8 .. +7, stored transposed
+    {
+      const int d = t >> 3, n0 = (t & 7) * 8;
+      const uint64_t gd = k0 + d;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint64_t gc = col0 + n0 + e;
+        bt_lds[(n0 + e) * G_LDK + d] = (gd < k && gc < n) ? b[gd * ldb + gc] : (uint16_t)0;
+      }
+    }
+    __syncthreads();
+    const int rc = lane & 15, chunk = lane >> 4;
+    bf16x8_t af[2], bf[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      af[i] = *reinterpret_cast<const bf16x8_t*>(a_lds + (wm * 32 + i * 16 + rc) * G_LDK + chunk * 8);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      bf[j] = *reinterpret_cast<const bf16x8_t*>(bt_lds + (wn * 32 + j * 16 + rc) * G_LDK + chunk * 8);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    __syncthreads();
+  }
+  // epilogue: alpha * acc and beta * C rounded separately, then added
+  // (examples/tiled_gemm_v1/src/numerical_contract.rs:310-331 order).
+  {
+#pragma clang fp contract(off)
+    const int col_in = lane & 15, row_in = (lane >> 4) * 4;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint64_t gr = row0 + wm * 32 + i * 16 + row_in + e;
+          const uint64_t gc = col0 + wn * 32 + j * 16 + col_in;
+          if (gr < m && gc < n) {
+            float* p = c + gr * ldc + gc;
+            const float product = alpha * acc[i][j][e];
+            const float initial = beta * *p;
+            *p = product + initial;
+          }
+        }
+  }
+}
+
+// ---- scalar f32 GEMM (sequential, unfused) -----------------------------------------
+// Workgroup tile 64x64, 256 threads, each thread a 4x4 block of outputs whose
+// accumulators each follow acc = acc + a*b over t = 0..k-1 in order.
+constexpr int S_BM = 64, S_BN = 64, S_BK = 16;
+
+__global__ void __launch_bounds__(256) scalar_gemm_kernel(const float* __restrict__ a,
+                                                          const float* __restrict__ b,
+                                                          float* __restrict__ c, uint32_t m,
+                                                          uint32_t n, uint32_t k) {
+#pragma clang fp contract(off)
+  __shared__ float a_lds[S_BK][S_BM + 4];  // [depth][row]
+  __shared__ float b_lds[S_BK][S_BN + 4];  // [depth][col]
+  const int t = threadIdx.x;
+  const int tr = t >> 4, tc = t & 15;  // thread owns rows tr+16*i, cols tc+16*j
+  const uint64_t row0 = (uint64_t)blockIdx.y * S_BM, col0 = (uint64_t)blockIdx.x * S_BN;
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+  for (uint64_t k0 = 0; k0 < k; k0 += S_BK) {
+    // A tile 64 rows x 16 depths: thread t loads row t/4, depths (t%4)*4..+3
+    {
+      const int r = t >> 2, d0 = (t & 3) * 4;
+      const uint64_t gr = row0 + r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint64_t gd = k0 + d0 + e;
+        a_lds[d0 + e][r] = (gr < m && gd < k) ? a[gr * k + gd] : 0.0f;
+      }
+    }
+    // B tile 16 depths x 64 cols: thread t loads depth t/16, cols (t%16)*4..+3
+    {
+      const int d = t >> 4, c0 = (t & 15) * 4;
+      const uint64_t gd = k0 + d;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint64_t gc = col0 + c0 + e;
+        b_lds[d][c0 + e] = (gd < k && gc < n) ? b[gd * n + gc] : 0.0f;
+      }
+    }
+    __syncthreads();
+    const int depth = (k - k0) < (uint64_t)S_BK ? (int)(k - k0) : S_BK;
+    for (int d = 0; d < depth; ++d) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = a_lds[d][tr + 16 * i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = b_lds[d][tc + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float p = av[i] * bv[j];
+          acc[i][j] = acc[i][j] + p;
+        }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint64_t gr = row0 + tr + 16 * i, gc = col0 + tc + 16 * j;
+      if (gr < m && gc < n) c[gr * n + gc] = acc[i][j];
+    }
+}
+
+bool aligned(const void* p, uintptr_t bytes) { return ((uintptr_t)p & (bytes - 1)) == 0; }
+
+int32_t tile16(const uint16_t* a, uint64_t a_len, const uint16_t* b, uint64_t b_len, float* c,
+               uint64_t c_len, void* stream) {
+  if (a_len != 256 || b_len != 256 || c_len != 256) return FE2O3_ERR_LENGTH;
+  if (!a || !b || !c) return FE2O3_ERR_NULL;
+  if (!aligned(a, 8) || !aligned(b, 8) || !aligned(c, 4)) return FE2O3_ERR_ALIGNMENT;
+  tile16_bf16_kernel<<<1, 64, 0, (hipStream_t)stream>>>(a, b, c);
+  return fe2o3_host::after_launch();
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fe2o3_tiled_gemm_lds_slice1_v1(const uint16_t* a, uint64_t a_len, const uint16_t* b,
+                                       uint64_t b_len, float* c, uint64_t c_len, void* stream) {
+  FE2O3_FAULT("fe2o3_tiled_gemm_lds_slice1_v1");
+  return tile16(a, a_len, b, b_len, c, c_len, stream);
+}
+
+int32_t fe2o3_moe_expert_gemm_bf16_m16_n16_k16_v1(const uint16_t* activations,
+                                                  uint64_t activations_len,
+                                                  const uint16_t* weights, uint64_t weights_len,
+                                                  float* output, uint64_t output_len,
+                                                  void* stream) {
+  FE2O3_FAULT("fe2o3_moe_expert_gemm_bf16_m16_n16_k16_v1");
+  return tile16(activations, activations_len, weights, weights_len, output, output_len, stream);
+}
+
+int32_t fe2o3_tiled_gemm_general_v1(const uint16_t* a, uint64_t a_len, const uint16_t* b,
+                                    uint64_t b_len, float* c, uint64_t c_len, uint32_t m,
+                                    uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb,
+                                    uint32_t ldc, float alpha, float beta, void* stream) {
+  FE2O3_FAULT("fe2o3_tiled_gemm_general_v1");
+  // examples/tiled_gemm_general_v1/src/kernel.rs:80-89
+  if ((m != 0 && k != 0 && lda < k) || (k != 0 && n != 0 && ldb < n) ||
+      (m != 0 && n != 0 && ldc < n))
+    return FE2O3_ERR_STRIDE;
+  uint64_t ea, eb, ec;
+  fe2o3_host::extent_ok(m, k, lda, &ea);
+  fe2o3_host::extent_ok(k, n, ldb, &eb);
+  fe2o3_host::extent_ok(m, n, ldc, &ec);
+  if (a_len < ea || b_len < eb || c_len < ec) return FE2O3_ERR_LENGTH;
+  if (m == 0 || n == 0) return FE2O3_OK;  // empty output: no dispatch
+  if ((ea && !a) || (eb && !b) || !c) return FE2O3_ERR_NULL;
+  dim3 grid((n + G_BN - 1) / G_BN, (m + G_BM - 1) / G_BM);
+  if (grid.y > 65535u) return FE2O3_ERR_SHAPE;
+  gemm_general_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(a, b, c, m, n, k, lda, ldb, ldc,
+                                                             alpha, beta);
+  return fe2o3_host::after_launch();
+}
+
+int32_t fe2o3_scalar_gemm_v1(const float* a, uint64_t a_len, const float* b, uint64_t b_len,
+                             float* c, uint64_t c_len, uint32_t m, uint32_t n, uint32_t k,
+                             void* stream) {
+  FE2O3_FAULT("fe2o3_scalar_gemm_v1");
+  const uint64_t ea = (uint64_t)m * k, eb = (uint64_t)k * n, ec = (uint64_t)m * n;
+  if (a_len < ea || b_len < eb || c_len < ec) return FE2O3_ERR_LENGTH;
+  if (ec == 0) return FE2O3_OK;
+  if ((ea && !a) || (eb && !b) || !c) return FE2O3_ERR_NULL;
+  dim3 grid((n + S_BN - 1) / S_BN, (m + S_BM - 1) / S_BM);
+  if (grid.y > 65535u) return FE2O3_ERR_SHAPE;
+  scalar_gemm_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(a, b, c, m, n, k);
+  return fe2o3_host::after_launch();
+}
+
+}  // extern "C"

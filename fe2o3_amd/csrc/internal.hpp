@@ -1,0 +1,26 @@
+// internal.hpp -- host-side helpers shared by the entry points (not exported).
+#pragma once
+
+#include <stdint.h>
+
+#include <hip/hip_runtime.h>
+
+namespace fe2o3_host {
+
+// True when the environment variable FE2O3_FAULT_POINT names `entry`: the
+// entry point then fails with FE2O3_ERR_INJECTED before any launch.  This is
+// the host-forced failure path used by the failure-handling tests.
+bool fault_point(const char* entry);
+
+// Enqueue status: 0, or the hipError_t of the launch just made.
+inline int32_t after_launch() {
+  hipError_t e = hipGetLastError();
+  return (int32_t)e;
+}
+
+}  // namespace fe2o3_host
+
+#define FE2O3_FAULT(entry)                                   \
+  do {                                                      \
+    if (fe2o3_host::fault_point(entry)) return FE2O3_ERR_INJECTED; \
+  } while (0)

@@ -1,0 +1,193 @@
+// runtime.hip -- the runtime seam of the C-ABI: device discovery, the
+// 312-byte property record, streams, events and memory.  Mirrors the
+// capability set of crates/fe2o3-hip-sys/src/lib.rs:92-165 and the C shim
+// crates/fe2o3-hip-sys/native/device_properties.c:63-101.
+#include <stdlib.h>
+#include <string.h>
+
+#include "common.hpp"
+#include "internal.hpp"
+
+static_assert(sizeof(Fe2o3HipDeviceProperties) == 312, "property record is 312 bytes");
+static_assert(offsetof(Fe2o3HipDeviceProperties, warp_size) == 256, "warp_size offset");
+static_assert(offsetof(Fe2o3HipDeviceProperties, max_threads_per_block) == 260, "offset");
+static_assert(offsetof(Fe2o3HipDeviceProperties, max_block_dim) == 264, "offset");
+static_assert(offsetof(Fe2o3HipDeviceProperties, max_grid_dim) == 276, "offset");
+static_assert(offsetof(Fe2o3HipDeviceProperties, shared_mem_per_block) == 288, "offset");
+static_assert(offsetof(Fe2o3HipDeviceProperties, shared_mem_per_block_optin) == 296, "offset");
+static_assert(offsetof(Fe2o3HipDeviceProperties, architecture_features) == 304, "offset");
+
+namespace fe2o3_host {
+
+bool fault_point(const char* entry) {
+  const char* env = getenv("FE2O3_FAULT_POINT");
+  return env != nullptr && strcmp(env, entry) == 0;
+}
+
+}  // namespace fe2o3_host
+
+extern "C" {
+
+const char* fe2o3_status_string(int32_t status) {
+  switch (status) {
+    case FE2O3_OK: return "success";
+    case FE2O3_ERR_LENGTH: return "slice length does not match the shape";
+    case FE2O3_ERR_SHAPE: return "unsupported shape or profile";
+    case FE2O3_ERR_STRIDE: return "stride smaller than the row extent";
+    case FE2O3_ERR_NONFINITE: return "non-finite input rejected by the contract";
+    case FE2O3_ERR_WEIGHTS: return "route weight pair violates the policy";
+    case FE2O3_ERR_OVERFLOW: return "extent arithmetic overflows";
+    case FE2O3_ERR_NULL: return "required pointer is NULL";
+    case FE2O3_ERR_DEVICE: return "current device is not gfx950";
+    case FE2O3_ERR_ALIGNMENT: return "pointer misaligned for this entry point";
+    case FE2O3_ERR_WORKSPACE: return "workspace too small";
+    case FE2O3_ERR_INJECTED: return "failure injected by FE2O3_FAULT_POINT";
+    default: break;
+  }
+  if (status > 0) return hipGetErrorString((hipError_t)status);
+  return "unknown fe2o3 status";
+}
+
+// device_properties.c:63-101: zero the record, then fill the stable subset;
+// on failure the record stays zeroed.
+int32_t fe2o3HipGetDeviceProperties(int32_t device_id, Fe2o3HipDeviceProperties* properties) {
+  if (properties == nullptr) return (int32_t)hipErrorInvalidValue;
+  memset(properties, 0, sizeof(*properties));
+  hipDeviceProp_t p;
+  hipError_t e = hipGetDeviceProperties(&p, device_id);
+  if (e != hipSuccess) return (int32_t)e;
+  strncpy(properties->gcn_arch_name, p.gcnArchName, sizeof(properties->gcn_arch_name) - 1);
+  properties->warp_size = p.warpSize;
+  properties->max_threads_per_block = p.maxThreadsPerBlock;
+  for (int i = 0; i < 3; ++i) {
+    properties->max_block_dim[i] = p.maxThreadsDim[i];
+    properties->max_grid_dim[i] = p.maxGridSize[i];
+  }
+  properties->shared_mem_per_block = (uint64_t)p.sharedMemPerBlock;
+  properties->shared_mem_per_block_optin = (uint64_t)p.sharedMemPerBlockOptin;
+  uint64_t f = 0;
+  if (p.arch.hasGlobalInt32Atomics) f |= FE2O3_HIP_DEVICE_ARCH_HAS_GLOBAL_INT32_ATOMICS;
+  if (p.arch.hasSharedInt32Atomics) f |= FE2O3_HIP_DEVICE_ARCH_HAS_SHARED_INT32_ATOMICS;
+  if (p.arch.hasGlobalInt64Atomics) f |= FE2O3_HIP_DEVICE_ARCH_HAS_GLOBAL_INT64_ATOMICS;
+  if (p.arch.hasSharedInt64Atomics) f |= FE2O3_HIP_DEVICE_ARCH_HAS_SHARED_INT64_ATOMICS;
+  if (p.arch.hasWarpVote) f |= FE2O3_HIP_DEVICE_ARCH_HAS_WARP_VOTE;
+  if (p.arch.hasWarpBallot) f |= FE2O3_HIP_DEVICE_ARCH_HAS_WARP_BALLOT;
+  if (p.arch.hasWarpShuffle) f |= FE2O3_HIP_DEVICE_ARCH_HAS_WARP_SHUFFLE;
+  properties->architecture_features = f;
+  return FE2O3_OK;
+}
+
+int32_t fe2o3_rt_init(uint32_t flags) { return (int32_t)hipInit(flags); }
+
+int32_t fe2o3_rt_get_device_count(int32_t* count) {
+  if (count == nullptr) return FE2O3_ERR_NULL;
+  int c = 0;
+  hipError_t e = hipGetDeviceCount(&c);
+  *count = e == hipSuccess ? c : 0;
+  return (int32_t)e;
+}
+
+int32_t fe2o3_rt_set_device(int32_t device_id) { return (int32_t)hipSetDevice(device_id); }
+
+int32_t fe2o3_rt_get_device(int32_t* device_id) {
+  if (device_id == nullptr) return FE2O3_ERR_NULL;
+  int d = 0;
+  hipError_t e = hipGetDevice(&d);
+  *device_id = d;
+  return (int32_t)e;
+}
+
+int32_t fe2o3_rt_device_rates(int32_t device_id, int32_t* compute_units, int32_t* clock_khz,
+                              int32_t* memory_clock_khz, int32_t* memory_bus_bits) {
+  hipDeviceProp_t p;
+  hipError_t e = hipGetDeviceProperties(&p, device_id);
+  if (e != hipSuccess) return (int32_t)e;
+  if (compute_units) *compute_units = p.multiProcessorCount;
+  if (clock_khz) *clock_khz = p.clockRate;
+  if (memory_clock_khz) *memory_clock_khz = p.memoryClockRate;
+  if (memory_bus_bits) *memory_bus_bits = p.memoryBusWidth;
+  return FE2O3_OK;
+}
+
+int32_t fe2o3_rt_require_gfx950(int32_t device_id) {
+  hipDeviceProp_t p;
+  hipError_t e = hipGetDeviceProperties(&p, device_id);
+  if (e != hipSuccess) return (int32_t)e;
+  return strncmp(p.gcnArchName, "gfx950", 6) == 0 ? FE2O3_OK : FE2O3_ERR_DEVICE;
+}
+
+int32_t fe2o3_rt_device_synchronize(void) { return (int32_t)hipDeviceSynchronize(); }
+
+int32_t fe2o3_rt_stream_create(void** stream) {
+  if (stream == nullptr) return FE2O3_ERR_NULL;
+  hipStream_t s = nullptr;
+  hipError_t e = hipStreamCreate(&s);  // default priority, as every stream here
+  *stream = (void*)s;
+  return (int32_t)e;
+}
+
+int32_t fe2o3_rt_stream_destroy(void* stream) {
+  return (int32_t)hipStreamDestroy((hipStream_t)stream);
+}
+
+int32_t fe2o3_rt_stream_synchronize(void* stream) {
+  return (int32_t)hipStreamSynchronize((hipStream_t)stream);
+}
+
+int32_t fe2o3_rt_event_create(void** event, uint32_t flags) {
+  if (event == nullptr) return FE2O3_ERR_NULL;
+  hipEvent_t ev = nullptr;
+  hipError_t e = hipEventCreateWithFlags(&ev, flags);
+  *event = (void*)ev;
+  return (int32_t)e;
+}
+
+int32_t fe2o3_rt_event_destroy(void* event) { return (int32_t)hipEventDestroy((hipEvent_t)event); }
+
+int32_t fe2o3_rt_event_record(void* event, void* stream) {
+  return (int32_t)hipEventRecord((hipEvent_t)event, (hipStream_t)stream);
+}
+
+int32_t fe2o3_rt_event_synchronize(void* event) {
+  return (int32_t)hipEventSynchronize((hipEvent_t)event);
+}
+
+int32_t fe2o3_rt_event_query(void* event) { return (int32_t)hipEventQuery((hipEvent_t)event); }
+
+int32_t fe2o3_rt_event_elapsed_ms(float* milliseconds, void* start, void* stop) {
+  if (milliseconds == nullptr) return FE2O3_ERR_NULL;
+  return (int32_t)hipEventElapsedTime(milliseconds, (hipEvent_t)start, (hipEvent_t)stop);
+}
+
+int32_t fe2o3_rt_malloc(void** ptr, size_t bytes) {
+  if (ptr == nullptr) return FE2O3_ERR_NULL;
+  *ptr = nullptr;
+  return (int32_t)hipMalloc(ptr, bytes);
+}
+
+int32_t fe2o3_rt_free(void* ptr) { return (int32_t)hipFree(ptr); }
+
+int32_t fe2o3_rt_host_malloc(void** ptr, size_t bytes) {
+  if (ptr == nullptr) return FE2O3_ERR_NULL;
+  *ptr = nullptr;
+  return (int32_t)hipHostMalloc(ptr, bytes, 0);
+}
+
+int32_t fe2o3_rt_host_free(void* ptr) { return (int32_t)hipHostFree(ptr); }
+
+int32_t fe2o3_rt_memcpy_async(void* dst, const void* src, size_t bytes, uint32_t kind,
+                              void* stream) {
+  if (kind > 4) return (int32_t)hipErrorInvalidMemcpyDirection;
+  return (int32_t)hipMemcpyAsync(dst, src, bytes, (hipMemcpyKind)kind, (hipStream_t)stream);
+}
+
+int32_t fe2o3_rt_memcpy(void* dst, const void* src, size_t bytes, uint32_t kind) {
+  if (kind > 4) return (int32_t)hipErrorInvalidMemcpyDirection;
+  return (int32_t)hipMemcpy(dst, src, bytes, (hipMemcpyKind)kind);
+}
+
+int32_t fe2o3_rt_memset_async(void* dst, int32_t value, size_t bytes, void* stream) {
+  return (int32_t)hipMemsetAsync(dst, value, bytes, (hipStream_t)stream);
+}
+
+}  // extern "C"

