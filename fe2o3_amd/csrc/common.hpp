@@ -9,6 +9,7 @@
 #include <stdint.h>
 
 #include "../../include/fe2o3_mi355x.h"
+#include "fp8_codec.hpp"
 
 #define FE2O3_DEVICE __device__ __forceinline__
 
@@ -50,50 +51,7 @@ FE2O3_DEVICE uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 // ---- OCP FP8 E4M3FN ----------------------------------------------------------------
-// Decoding and RNE/satfinite encoding of the OCP 8-bit float (bias 7, max
-// finite 448, NaN = S.1111.111, no infinities).  Encoding is done on the
-// exact binary32 value with integer arithmetic so it is bit-reproducible.
-FE2O3_DEVICE uint8_t e4m3_from_f32(float v) {
-  uint32_t bits = __float_as_uint(v);
-  uint8_t sign = (uint8_t)((bits >> 24) & 0x80u);
-  uint32_t mag = bits & 0x7fffffffu;
-  if (mag > 0x7f800000u) return (uint8_t)(sign | 0x7f);   // NaN
-  if (mag >= 0x43e00000u) return (uint8_t)(sign | 0x7e);  // >= 448 (incl. inf) saturates
-  int exp = (int)(mag >> 23);                             // biased binary32 exponent
-  uint32_t mant = (mag & 0x7fffffu) | (exp ? 0x800000u : 0u);
-  int unbiased = exp ? exp - 127 : -126;
-  // target quantum exponent: 2^-9 for subnormal e4m3 (unbiased < -6), else unbiased-3
-  int q = unbiased < -6 ? -9 : unbiased - 3;
-  // value = mant * 2^(unbiased-23); we want round(value / 2^q) = mant >> (q - unbiased + 23)
-  int shift = q - unbiased + 23;  // >= 20
-  uint32_t r;
-  if (shift >= 32) {
-    r = 0;
-    // ties: only if mant * 2^-shift == 0.5 exactly, impossible for shift >= 32 with mant < 2^24... except
-    // mant == 2^(shift-1) which needs shift-1 <= 23; so r = 0 is exact rounding here.
-  } else {
-    uint32_t whole = mant >> shift;
-    uint32_t rem = mant & ((1u << shift) - 1u);
-    uint32_t half = 1u << (shift - 1);
-    r = whole + ((rem > half || (rem == half && (whole & 1u))) ? 1u : 0u);
-  }
-  // r * 2^q is the rounded magnitude; encode it.
-  if (r == 0) return sign;
-  if (q == -9) {
-    // subnormal quantum: r in 1..8; r == 8 is the smallest normal 2^-6 (e=1, m=0)
-    if (r < 8) return (uint8_t)(sign | r);
-    return (uint8_t)(sign | 0x08);
-  }
-  // normal: r in 8..16 (16 means carry into the next binade)
-  int e = unbiased + 7;
-  if (r == 16) {
-    r = 8;
-    e += 1;
-  }
-  uint32_t code = ((uint32_t)e << 3) | (r - 8);
-  if (code > 0x7eu) code = 0x7eu;  // 464 and above round-to-nearest saturate to 448
-  return (uint8_t)(sign | code);
-}
+FE2O3_DEVICE uint8_t e4m3_from_f32(float v) { return e4m3_from_bits(__float_as_uint(v)); }
 
 // ---- wave64 reductions ---------------------------------------------------------------
 // Butterfly over the 64 lanes with DPP row operations for the in-row steps
@@ -112,10 +70,13 @@ FE2O3_DEVICE float wave_sum(float v) {
   return v;
 }
 
-// Exchange a value with lane (l ^ 32) using v_permlane32_swap.
+// Exchange a value with lane (l ^ 32) using v_permlane32_swap.  The
+// instruction swaps the upper half of its first operand with the lower half
+// of its second; with both operands = v, the first result holds v[l-32] in
+// lanes 32..63 and the second holds v[l+32] in lanes 0..31.
 FE2O3_DEVICE float swap_half(float v) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]);
+  return __uint_as_float((threadIdx.x & 32u) ? r[0] : r[1]);
 }
 
 // ---- explicit counter waits ---------------------------------------------------------

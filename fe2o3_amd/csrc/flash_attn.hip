@@ -1,0 +1,338 @@
+// flash_attn.hip -- flash-attention forward for gfx950.
+//
+// 1. The reference's exact profile (examples/flash_attention_v1/src/kernel.rs
+//    :36-169): causal, B1/H1/N8/D16, f32, scale 0.25, one wave64, lane l owns
+//    outputs 2l and 2l+1, sequential strict-f32 dot products and the online
+//    max/sum recurrence m' = max(m, s); w_prev = exp(m - m');
+//    w = exp(s - m'); l = l*w_prev + w; n = n*w_prev + v*w (kernel.rs:56-113),
+//    exp = OCML expf as the reference's DeviceMath::exp_f32.
+//
+// 2. The BASELINE shape: Q, K, V, O bf16 [B, H, S, 128], fp32 online softmax
+//    statistics, optional causal mask, LSE output.  Per workgroup: one (b, h)
+//    and 128 query rows; 4 waves x 32 query rows; K/V tiles of 64 keys,
+//    double-buffered in LDS.
+//    * S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (K tile rows as the first
+//      operand, the wave's Q rows -- held in registers for the whole loop --
+//      as the second), so lane l owns query row l%32 and 16 of the 32 keys of
+//      each key block; the other 16 sit in lane l^32.  Row max and row sum are
+//      in-lane reductions plus one v_permlane32_swap.
+//    * Softmax in the exp2 domain: p = exp2(s*c - m) with c = scale*log2(e)
+//      folded into one FMA before v_exp_f32; m and l are fp32 running
+//      statistics; O is rescaled by exp2(m_old - m_new) per tile.
+//    * O^T += V^T P^T: P (bf16) is the second operand straight from the S
+//      registers; V^T comes from an LDS copy of the V tile stored transposed
+//      ([d][key]) with the keys of each 16-key group in MFMA k-order (bits 2
+//      and 3 of the key index swapped), so every operand read is one 16-byte
+//      LDS access.
+//    * K tiles go global -> LDS with 16-byte global_load_lds (chunks
+//      XOR-permuted by row & 15 against bank conflicts); V tiles go through
+//      registers for the transpose.
+//    * Causal: query tiles are issued heaviest first; a wave skips the
+//      MFMAs of key tiles that lie entirely above its rows and masks the
+//      diagonal tile.
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace {
+
+using namespace fe2o3;
+
+// ---- exact profile ---------------------------------------------------------------------
+constexpr int P_N = 8, P_D = 16;
+
+__global__ void __launch_bounds__(64) flash_profile_kernel(const float* __restrict__ q,
+                                                           const float* __restrict__ k,
+                                                           const float* __restrict__ v,
+                                                           float* __restrict__ out) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x;
+  const int first = lane * 2;
+  const int row = first / P_D, col = first % P_D;
+  float m = 0.0f, l = 0.0f, n0 = 0.0f, n1 = 0.0f;
+  for (int kr = 0; kr <= row; ++kr) {
+    float dot = 0.0f;
+    for (int f = 0; f < P_D; ++f) {
+      const float p = q[row * P_D + f] * k[kr * P_D + f];
+      dot = dot + p;
+    }
+    const float s = dot * 0.25f;
+    const float v0 = v[kr * P_D + col], v1 = v[kr * P_D + col + 1];
+    if (kr == 0) {
+      m = s;
+      l = 1.0f;
+      n0 = v0;
+      n1 = v1;
+    } else {
+      const float nm = s > m ? s : m;
+      const float wp = expf(m - nm);
+      const float wc = expf(s - nm);
+      const float t0 = l * wp;
+      l = t0 + wc;
+      const float a0 = n0 * wp, b0 = v0 * wc;
+      n0 = a0 + b0;
+      const float a1 = n1 * wp, b1 = v1 * wc;
+      n1 = a1 + b1;
+      m = nm;
+    }
+  }
+  out[first] = n0 / l;
+  out[first + 1] = n1 / l;
+}
+
+// ---- BASELINE-shape kernel -------------------------------------------------------------------
+constexpr int D = 128;         // head dim
+constexpr int BQ = 128;        // query rows per workgroup
+constexpr int BKV = 64;        // keys per tile
+constexpr int K_TILE_BYTES = BKV * D * 2;   // 16 KiB, rows of 256 B
+constexpr int V_TILE_BYTES = D * BKV * 2;   // 16 KiB, rows (d) of 128 B
+constexpr int STAGE_BYTES = K_TILE_BYTES + V_TILE_BYTES;
+constexpr int SMEM_BYTES = 2 * STAGE_BYTES; // 64 KiB
+
+FE2O3_DEVICE uint32_t swz_k(uint32_t r) { return r & 15u; }
+FE2O3_DEVICE uint32_t swz_v(uint32_t d) { return (d ^ (d >> 3)) & 7u; }
+// key (0..63) -> position in the transposed V row: swap bits 2 and 3.
+FE2O3_DEVICE uint32_t vpos(uint32_t key) {
+  return (key & ~12u) | ((key & 4u) << 1) | ((key & 8u) >> 1);
+}
+
+// K tile: 16 instructions of 1 KiB (4 rows of 256 B); wave w issues 4.
+FE2O3_DEVICE void issue_k(const uint16_t* k_tile, uint8_t* lds) {
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t inst = 4u * j + w;
+    const uint32_t row = inst * 4u + (lane >> 4);
+    const uint32_t chunk = (lane & 15u) ^ swz_k(row);
+    g2l_b128(k_tile + row * D + chunk * 8u, lds + inst * 1024u);
+  }
+}
+
+// V tile: thread t loads 4 x 16 B: rows key = (t/16) + 16*i, d chunk t%16.
+FE2O3_DEVICE void load_v(const uint16_t* v_tile, u32x4_t regs[4]) {
+  const uint32_t t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t key = (t >> 4) + 16u * i, dc = t & 15u;
+    regs[i] = *reinterpret_cast<const u32x4_t*>(v_tile + key * D + dc * 8u);
+  }
+}
+
+FE2O3_DEVICE void store_vt(const u32x4_t regs[4], uint8_t* lds_v) {
+  const uint32_t t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t key = (t >> 4) + 16u * i, dc = t & 15u;
+    const uint32_t pos = vpos(key);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t d = dc * 8u + e;
+      const uint32_t word = regs[i][e >> 1];
+      const uint16_t val = (uint16_t)((e & 1) ? (word >> 16) : (word & 0xffffu));
+      const uint32_t off = d * 128u + (((pos >> 3) ^ swz_v(d)) << 4) + (pos & 7u) * 2u;
+      *reinterpret_cast<uint16_t*>(lds_v + off) = val;
+    }
+  }
+}
+
+template <bool CAUSAL>
+__global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse,
+    uint32_t seq, float scale_log2) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  const uint32_t lr = lane & 31u, g = lane >> 5;
+  const uint32_t nq = seq / BQ;
+  const uint32_t qt = CAUSAL ? (nq - 1u - blockIdx.x) : blockIdx.x;
+  const uint64_t head = (uint64_t)blockIdx.y * seq * D;
+  const uint16_t* qh = q + head;
+  const uint16_t* kh = k + head;
+  const uint16_t* vh = v + head;
+  const uint32_t q_row0 = qt * BQ + w * 32u;  // first query row of this wave
+  const uint32_t my_q = q_row0 + lr;
+
+  // Q fragments (second MFMA operand): lane holds row my_q, d = 16*ds + 8*g .. +7
+  bf16x8_t qf[8];
+#pragma unroll
+  for (int ds = 0; ds < 8; ++ds)
+    qf[ds] = *reinterpret_cast<const bf16x8_t*>(qh + (uint64_t)my_q * D + ds * 16 + g * 8);
+
+  f32x16_t acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+  float m_run = -INFINITY;  // running max of s*c (log2 domain)
+  float l_run = 0.0f;       // this lane's partial row sum
+
+  const uint32_t n_kv = CAUSAL ? (qt + 1u) * (BQ / BKV) : seq / BKV;
+  u32x4_t vregs[4];
+  issue_k(kh, smem);
+  load_v(vh, vregs);
+  store_vt(vregs, smem + K_TILE_BYTES);
+  wait_vmcnt0();
+  __syncthreads();
+
+  for (uint32_t j = 0; j < n_kv; ++j) {
+    uint8_t* cur = smem + (j & 1u) * STAGE_BYTES;
+    uint8_t* nxt = smem + ((j + 1u) & 1u) * STAGE_BYTES;
+    const bool more = j + 1u < n_kv;
+    if (more) {
+      issue_k(kh + (uint64_t)(j + 1u) * BKV * D, nxt);
+      load_v(vh + (uint64_t)(j + 1u) * BKV * D, vregs);
+    }
+    const uint32_t key0 = j * BKV;
+    // keys key0..key0+63 vs. rows q_row0..q_row0+31
+    const bool active = !CAUSAL || key0 <= q_row0 + 31u;
+    if (active) {
+      // S^T = K Q^T : two 32-key blocks
+      f32x16_t s[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
+        const uint32_t krow = kb * 32u + lr;
+#pragma unroll
+        for (int ds = 0; ds < 8; ++ds) {
+          const uint32_t c = 2u * ds + g;
+          const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(
+              cur + krow * 256u + ((c ^ swz_k(krow)) << 4));
+          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ds], s[kb], 0, 0, 0);
+        }
+      }
+      // mask the diagonal tile
+      if (CAUSAL && key0 + 63u > q_row0) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const uint32_t key = key0 + kb * 32u + 8u * (e >> 2) + 4u * g + (e & 3);
+            if (key > my_q) s[kb][e] = -INFINITY;
+          }
+      }
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[kb][e]);
+      mloc = fmaxf(mloc, swap_half(mloc));
+      const float m_new = fmaxf(m_run, mloc * scale_log2);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      bf16x8_t pf[2][2];
+      float psum = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float pv[8];
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) {
+            pv[jj] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][h * 8 + jj], scale_log2, -m_new));
+            psum += pv[jj];
+          }
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) pf[kb][h][jj] = (__bf16)pv[jj];
+        }
+      l_run = l_run * alpha + psum;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[db][e] *= alpha;
+      // O^T += V^T P^T
+      const uint8_t* vt = cur + K_TILE_BYTES;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const uint32_t d = db * 32u + lr;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const uint32_t c = (kb * 2u + h) * 2u + g;
+            const bf16x8_t vf = *reinterpret_cast<const bf16x8_t*>(
+                vt + d * 128u + ((c ^ swz_v(d)) << 4));
+            acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kb][h], acc[db], 0, 0, 0);
+          }
+      }
+    }
+    if (more) store_vt(vregs, nxt + K_TILE_BYTES);
+    wait_vmcnt0();
+    __syncthreads();
+  }
+
+  // finalize: full row sum across the lane pair, normalize, store
+  const float l_tot = l_run + swap_half(l_run);
+  const float inv = 1.0f / l_tot;
+  uint16_t* oh = o + head + (uint64_t)my_q * D;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const uint32_t d = db * 32u + 8u * qd + 4u * g;
+      u32x2_t packed;
+      packed[0] = pack_bf16x2(acc[db][4 * qd + 0] * inv, acc[db][4 * qd + 1] * inv);
+      packed[1] = pack_bf16x2(acc[db][4 * qd + 2] * inv, acc[db][4 * qd + 3] * inv);
+      *reinterpret_cast<u32x2_t*>(oh + d) = packed;
+    }
+  if (lse != nullptr && g == 0) {
+    // natural-log statistic: max(s)*scale + ln(sum) = (m_run + log2(sum)) * ln 2
+    lse[(uint64_t)blockIdx.y * seq + my_q] = (m_run + __log2f(l_tot)) * 0.69314718055994531f;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fe2o3_flash_attention_causal_f32_b1_h1_n8_d16_v1(const float* q, uint64_t q_len,
+                                                          const float* k, uint64_t k_len,
+                                                          const float* v, uint64_t v_len,
+                                                          float* output, uint64_t output_len,
+                                                          void* stream) {
+  FE2O3_FAULT("fe2o3_flash_attention_causal_f32_b1_h1_n8_d16_v1");
+  const uint64_t n = P_N * P_D;
+  if (q_len != n || k_len != n || v_len != n || output_len != n) return FE2O3_ERR_LENGTH;
+  if (!q || !k || !v || !output) return FE2O3_ERR_NULL;
+  flash_profile_kernel<<<1, 64, 0, (hipStream_t)stream>>>(q, k, v, output);
+  return fe2o3_host::after_launch();
+}
+
+int32_t fe2o3_flash_attention_fwd(const uint16_t* q, uint64_t q_len, const uint16_t* k,
+                                  uint64_t k_len, const uint16_t* v, uint64_t v_len, uint16_t* o,
+                                  uint64_t o_len, float* lse, uint64_t lse_len, uint32_t batch,
+                                  uint32_t heads, uint32_t seq, uint32_t head_dim, int32_t causal,
+                                  float scale, void* stream) {
+  FE2O3_FAULT("fe2o3_flash_attention_fwd");
+  if (head_dim != D) return FE2O3_ERR_SHAPE;
+  const uint64_t bh = (uint64_t)batch * heads;
+  const uint64_t n = bh * seq * head_dim;
+  if (q_len != n || k_len != n || v_len != n || o_len != n) return FE2O3_ERR_LENGTH;
+  if (lse != nullptr && lse_len != bh * seq) return FE2O3_ERR_LENGTH;
+  if (n == 0) return FE2O3_OK;
+  if (seq % BQ != 0 || bh > 65535u) return FE2O3_ERR_SHAPE;
+  if (!q || !k || !v || !o) return FE2O3_ERR_NULL;
+  if ((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) & 15u) != 0)
+    return FE2O3_ERR_ALIGNMENT;
+  if (!(scale > 0.0f) || !__builtin_isfinite(scale)) return FE2O3_ERR_SHAPE;
+  const float scale_log2 = scale * 1.4426950408889634f;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)flash_fwd_kernel<true>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, SMEM_BYTES);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void*)flash_fwd_kernel<false>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, SMEM_BYTES);
+    if (e != hipSuccess) return (int32_t)e;
+    attr_set = true;
+  }
+  const dim3 grid(seq / BQ, (unsigned)bh);
+  if (causal)
+    flash_fwd_kernel<true><<<grid, 256, SMEM_BYTES, (hipStream_t)stream>>>(q, k, v, o, lse, seq,
+                                                                            scale_log2);
+  else
+    flash_fwd_kernel<false><<<grid, 256, SMEM_BYTES, (hipStream_t)stream>>>(q, k, v, o, lse, seq,
+                                                                             scale_log2);
+  return fe2o3_host::after_launch();
+}
+
+}  // extern "C"

@@ -1,0 +1,156 @@
+// fp8.hip -- per-tensor-scaled OCP fp8 (E4M3FN) quantized GEMM path for
+// gfx950: amax reduction, scale = amax / 448, RNE/satfinite quantization,
+// and C (bf16) = (scale_a * scale_b) * (A_q . B_q^T) with fp32 accumulation.
+//
+// The reference has no gfx950 fp8 type (its Fp8E4M3Fnuz,
+// crates/fe2o3-device/src/fp8.rs:53-110, is gfx942's FNUZ encoding, bias 8);
+// this path follows the OCP 8-bit floating point specification: bias 7, no
+// infinities, max finite 448, NaN = S.1111.111, round-to-nearest-even with
+// saturation to +-448.
+//
+// The GEMM reuses the 256x256 tile machinery of the bf16 GEMM: one LDS stage
+// is 128 bytes of k per row, i.e. 128 fp8 values, and each substep of 64 k
+// issues v_mfma_scale_f32_32x32x64_f8f6f4 (5.0 PFLOP/s dense peak).
+#include "common.hpp"
+#include "gemm_core.hpp"
+#include "internal.hpp"
+
+namespace {
+
+using namespace fe2o3;
+
+__global__ void zero_f32_kernel(float* p) { *p = 0.0f; }
+
+__global__ void __launch_bounds__(256) amax_kernel(const float* __restrict__ x, uint64_t n,
+                                                   float* __restrict__ amax) {
+  float m = 0.0f;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  const uint64_t n4 = n / 4;
+  const f32x4_t* x4 = reinterpret_cast<const f32x4_t*>(x);
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    const f32x4_t v = __builtin_nontemporal_load(x4 + i);
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  }
+  for (uint64_t i = n4 * 4 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    m = fmaxf(m, fabsf(x[i]));
+  m = wave_max(m);
+  // |x| >= 0, so the IEEE bit patterns order like unsigned integers
+  if ((threadIdx.x & 63u) == 0) atomicMax(reinterpret_cast<unsigned int*>(amax), __float_as_uint(m));
+}
+
+__global__ void scale_kernel(const float* amax, float* scale) {
+  const float a = fmaxf(*amax, 1.17549435e-38f);
+  *scale = a / 448.0f;
+}
+
+__global__ void __launch_bounds__(256) quantize_kernel(const float* __restrict__ x, uint64_t n,
+                                                       const float* __restrict__ scale,
+                                                       uint8_t* __restrict__ q) {
+  const float s = *scale;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  const uint64_t n4 = n / 4;
+  const f32x4_t* x4 = reinterpret_cast<const f32x4_t*>(x);
+  uint32_t* q4 = reinterpret_cast<uint32_t*>(q);
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    const f32x4_t v = __builtin_nontemporal_load(x4 + i);
+    uint32_t packed = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) packed |= (uint32_t)e4m3_from_f32(v[e] / s) << (8 * e);
+    q4[i] = packed;
+  }
+  for (uint64_t i = n4 * 4 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    q[i] = e4m3_from_f32(x[i] / s);
+}
+
+__global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restrict__ a,
+                                                          const uint8_t* __restrict__ b,
+                                                          const float* __restrict__ scale_a,
+                                                          const float* __restrict__ scale_b,
+                                                          uint16_t* __restrict__ c, uint32_t m,
+                                                          uint32_t n, uint32_t k) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  uint32_t tm, tn;
+  gemm_core::xcd_tile_order(blockIdx.x, m / 256, n / 256, &tm, &tn);
+  const uint32_t k16 = k / 2;  // 16-bit units per row
+  const uint16_t* a16 = reinterpret_cast<const uint16_t*>(a + (uint64_t)tm * 256 * k);
+  const uint16_t* b16 = reinterpret_cast<const uint16_t*>(b + (uint64_t)tn * 256 * k);
+  const gemm_core::TileRows ar = gemm_core::dense_rows(a16, k16, 256);
+  const gemm_core::TileRows br = gemm_core::dense_rows(b16, k16, 256);
+  gemm_core::Acc256 acc;
+  gemm_core::zero(acc);
+  gemm_core::mainloop<gemm_core::MmaFp8>(ar, br, k16, smem, acc);
+  const float sab = scale_a[0] * scale_b[0];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc.v[i][j][e] *= sab;
+  gemm_core::store_bf16_256(acc, c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256, n);
+}
+
+unsigned grid_for(uint64_t n) {
+  uint64_t b = (n / 4 + 255) / 256;
+  if (b == 0) b = 1;
+  return (unsigned)(b < 8192 ? b : 8192);
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fe2o3_amax_f32(const float* x, uint64_t x_len, float* amax, void* stream) {
+  FE2O3_FAULT("fe2o3_amax_f32");
+  if (!amax || (x_len && !x)) return FE2O3_ERR_NULL;
+  if (((uintptr_t)x & 15u) != 0) return FE2O3_ERR_ALIGNMENT;
+  hipStream_t s = (hipStream_t)stream;
+  zero_f32_kernel<<<1, 1, 0, s>>>(amax);
+  if (x_len) amax_kernel<<<grid_for(x_len), 256, 0, s>>>(x, x_len, amax);
+  return fe2o3_host::after_launch();
+}
+
+int32_t fe2o3_fp8_scale_from_amax(const float* amax, float* scale, void* stream) {
+  FE2O3_FAULT("fe2o3_fp8_scale_from_amax");
+  if (!amax || !scale) return FE2O3_ERR_NULL;
+  scale_kernel<<<1, 1, 0, (hipStream_t)stream>>>(amax, scale);
+  return fe2o3_host::after_launch();
+}
+
+int32_t fe2o3_quantize_e4m3(const float* x, uint64_t x_len, const float* scale, uint8_t* q,
+                            uint64_t q_len, void* stream) {
+  FE2O3_FAULT("fe2o3_quantize_e4m3");
+  if (x_len != q_len) return FE2O3_ERR_LENGTH;
+  if (x_len == 0) return FE2O3_OK;
+  if (!x || !scale || !q) return FE2O3_ERR_NULL;
+  if (((uintptr_t)x & 15u) != 0 || ((uintptr_t)q & 3u) != 0) return FE2O3_ERR_ALIGNMENT;
+  quantize_kernel<<<grid_for(x_len), 256, 0, (hipStream_t)stream>>>(x, x_len, scale, q);
+  return fe2o3_host::after_launch();
+}
+
+int32_t fe2o3_gemm_fp8_nt(const uint8_t* a, uint64_t a_len, const uint8_t* b, uint64_t b_len,
+                          const float* scale_a, const float* scale_b, uint16_t* c, uint64_t c_len,
+                          uint32_t m, uint32_t n, uint32_t k, void* stream) {
+  FE2O3_FAULT("fe2o3_gemm_fp8_nt");
+  if (a_len != (uint64_t)m * k || b_len != (uint64_t)n * k || c_len != (uint64_t)m * n)
+    return FE2O3_ERR_LENGTH;
+  if (c_len == 0) return FE2O3_OK;
+  if (m % 256 != 0 || n % 256 != 0 || k % 128 != 0 || k == 0) return FE2O3_ERR_SHAPE;
+  if (128ull * k >= (1ull << 32)) return FE2O3_ERR_SHAPE;
+  if (!a || !b || !c || !scale_a || !scale_b) return FE2O3_ERR_NULL;
+  if ((((uintptr_t)a | (uintptr_t)b | (uintptr_t)c) & 15u) != 0) return FE2O3_ERR_ALIGNMENT;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)gemm_fp8_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       gemm_core::kSmemBytes256);
+    if (e != hipSuccess) return (int32_t)e;
+    attr_set = true;
+  }
+  const uint64_t tiles = (uint64_t)(m / 256) * (n / 256);
+  if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
+  gemm_fp8_kernel<<<(unsigned)tiles, 256, gemm_core::kSmemBytes256, (hipStream_t)stream>>>(
+      a, b, scale_a, scale_b, c, m, n, k);
+  return fe2o3_host::after_launch();
+}
+
+}  // extern "C"

@@ -62,27 +62,33 @@ FE2O3_DEVICE void xcd_tile_order(uint32_t pid, uint32_t tiles_m, uint32_t tiles_
   *tn = r / size_m;
 }
 
-// Per-thread source rows of one operand tile: a workgroup-uniform base and,
-// for instruction j, the 32-bit element offset of the 16-byte chunk this
-// thread moves (k offset 0).  Offsets stay below 2^32 elements for any tile
-// whose rows lie within 4 Gi elements of its base.
+// Per-thread source rows of one operand tile.  Instruction j moves tile rows
+// [32j, 32j+32) (rows (4j + w)*8 + lane/8 for wave w), so each instruction has
+// a workgroup-uniform base pointer base[j]; off[j] is the 32-bit element
+// offset from it of the 16-byte chunk this thread moves (k offset 0).
 struct TileRows {
-  const uint16_t* base;
+  const uint16_t* base[8];
   uint32_t off[8];
 };
+
+FE2O3_DEVICE uint32_t tile_row(int j) {
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  return (4u * j + w) * 8u + (lane >> 3);
+}
+
+FE2O3_DEVICE uint32_t tile_chunk(uint32_t row) { return ((threadIdx.x & 63u) & 7u) ^ swz(row); }
 
 // Dense operand: tile rows start at `base`, consecutive rows `ld` apart;
 // rows at or beyond `valid_rows` are clamped to the last valid row (their
 // values only feed outputs that are never stored).
 FE2O3_DEVICE TileRows dense_rows(const uint16_t* base, uint32_t ld, uint32_t valid_rows) {
   TileRows t;
-  t.base = base;
-  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    uint32_t row = (4u * j + w) * 8u + (lane >> 3);
-    const uint32_t chunk = (lane & 7u) ^ swz(row);
+    uint32_t row = tile_row(j);
+    const uint32_t chunk = tile_chunk(row);
     if (row >= valid_rows) row = valid_rows - 1u;
+    t.base[j] = base;
     t.off[j] = row * ld + chunk * 8u;
   }
   return t;
@@ -90,54 +96,103 @@ FE2O3_DEVICE TileRows dense_rows(const uint16_t* base, uint32_t ld, uint32_t val
 
 FE2O3_DEVICE void issue_tile(const TileRows& rows, uint32_t k0, uint8_t* lds_tile) {
   const uint32_t w = threadIdx.x >> 6;
-  const uint16_t* kbase = rows.base + k0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) g2l_b128(kbase + rows.off[j], lds_tile + (4u * j + w) * 1024u);
+  for (int j = 0; j < 8; ++j)
+    g2l_b128(rows.base[j] + k0 + rows.off[j], lds_tile + (4u * j + w) * 1024u);
 }
 
-// Operand fragments of one k-substep (16 k values) for one wave: 4 A and 4 B
-// 16-byte reads.
-struct Frags {
-  bf16x8_t a[4], b[4];
+// MFMA policies.  Each LDS stage holds 128 bytes of k per tile row: 64 bf16
+// or 128 fp8 values.  A policy knows how many k-substeps a stage has, how a
+// wave reads its operand fragments for one substep, and the MFMA it issues.
+
+// bf16: 4 substeps of 16 k; per substep 4 A and 4 B 16-byte reads and 16
+// v_mfma_f32_32x32x16_bf16 per wave.
+struct MmaBf16 {
+  static constexpr int kSubsteps = 4;
+  struct Frags {
+    bf16x8_t a[4], b[4];
+  };
+  static FE2O3_DEVICE void load(const uint8_t* stage, int s, Frags& f) {
+    const uint8_t* a_tile = stage;
+    const uint8_t* b_tile = stage + kTileBytes;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t wm = wave >> 1, wn = wave & 1u;
+    const uint32_t lr = lane & 31u, g = lane >> 5;
+    const uint32_t c = 2u * (uint32_t)s + g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t ra = wm * 128u + i * 32u + lr;
+      const uint32_t rb = wn * 128u + i * 32u + lr;
+      f.a[i] = *reinterpret_cast<const bf16x8_t*>(a_tile + ra * 128u + ((c ^ swz(ra)) << 4));
+      f.b[i] = *reinterpret_cast<const bf16x8_t*>(b_tile + rb * 128u + ((c ^ swz(rb)) << 4));
+    }
+  }
+  static FE2O3_DEVICE void mma(const Frags& f, Acc256& acc) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[j], f.a[i], acc.v[i][j], 0, 0, 0);
+  }
 };
 
-FE2O3_DEVICE void load_frags(const uint8_t* stage, int s, Frags& f) {
-  const uint8_t* a_tile = stage;
-  const uint8_t* b_tile = stage + kTileBytes;
-  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-  const uint32_t wm = wave >> 1, wn = wave & 1u;
-  const uint32_t lr = lane & 31u, g = lane >> 5;
-  const uint32_t c = 2u * (uint32_t)s + g;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t ra = wm * 128u + i * 32u + lr;
-    const uint32_t rb = wn * 128u + i * 32u + lr;
-    f.a[i] = *reinterpret_cast<const bf16x8_t*>(a_tile + ra * 128u + ((c ^ swz(ra)) << 4));
-    f.b[i] = *reinterpret_cast<const bf16x8_t*>(b_tile + rb * 128u + ((c ^ swz(rb)) << 4));
+// OCP fp8 e4m3: 2 substeps of 64 k; per substep each lane reads 32 bytes
+// (two 16-byte chunks) per operand fragment and the wave issues 16
+// v_mfma_scale_f32_32x32x64_f8f6f4 with both formats e4m3 (cbsz = blgp = 0)
+// and unit E8M0 block scales (127 = 2^0).
+struct MmaFp8 {
+  static constexpr int kSubsteps = 2;
+  struct Frags {
+    i32x8_t a[4], b[4];
+  };
+  static FE2O3_DEVICE i32x8_t read32(const uint8_t* tile, uint32_t r, uint32_t c0) {
+    const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(tile + r * 128u + ((c0 ^ swz(r)) << 4));
+    const i32x4_t hi =
+        *reinterpret_cast<const i32x4_t*>(tile + r * 128u + (((c0 + 1u) ^ swz(r)) << 4));
+    i32x8_t v;
+    v[0] = lo[0]; v[1] = lo[1]; v[2] = lo[2]; v[3] = lo[3];
+    v[4] = hi[0]; v[5] = hi[1]; v[6] = hi[2]; v[7] = hi[3];
+    return v;
   }
-}
-
-FE2O3_DEVICE void mma(const Frags& f, Acc256& acc) {
+  static FE2O3_DEVICE void load(const uint8_t* stage, int s, Frags& f) {
+    const uint8_t* a_tile = stage;
+    const uint8_t* b_tile = stage + kTileBytes;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t wm = wave >> 1, wn = wave & 1u;
+    const uint32_t lr = lane & 31u, g = lane >> 5;
+    const uint32_t c0 = 4u * (uint32_t)s + 2u * g;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
+      f.a[i] = read32(a_tile, wm * 128u + i * 32u + lr, c0);
+      f.b[i] = read32(b_tile, wn * 128u + i * 32u + lr, c0);
+    }
+  }
+  static FE2O3_DEVICE void mma(const Frags& f, Acc256& acc) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[j], f.a[i], acc.v[i][j], 0, 0, 0);
-}
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc.v[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[j], f.a[i], acc.v[i][j],
+                                                                      0, 0, 0, 127, 0, 127);
+  }
+};
 
-// Full K loop over k (multiple of 64) with two LDS stages and register
-// double-buffered fragments: the reads of substep s+1 are issued before the
-// MFMAs of substep s, and the per-step barrier sits before the last
-// substep's MFMAs so the first reads of the next stage overlap them.
-FE2O3_DEVICE void mainloop(const TileRows& a_rows, const TileRows& b_rows, uint32_t k,
+// Full K loop over `k16` 16-bit units of k per row (a multiple of 64: 128
+// bytes per stage) with two LDS stages and register double-buffered
+// fragments: the reads of substep s+1 are issued before the MFMAs of
+// substep s, and the per-step barrier sits before the last substep's MFMAs
+// so the first reads of the next stage overlap them.
+template <class Mma = MmaBf16>
+FE2O3_DEVICE void mainloop(const TileRows& a_rows, const TileRows& b_rows, uint32_t k16,
                            uint8_t* smem, Acc256& acc) {
-  const uint32_t steps = k / BK;
+  constexpr int S = Mma::kSubsteps;
+  const uint32_t steps = k16 / BK;
   issue_tile(a_rows, 0, smem);
   issue_tile(b_rows, 0, smem + kTileBytes);
   wait_vmcnt0();
   __syncthreads();
-  Frags f0, f1;
-  load_frags(smem, 0, f0);
+  typename Mma::Frags f[2];
+  Mma::load(smem, 0, f[0]);
   for (uint32_t kt = 0; kt < steps; ++kt) {
     const uint8_t* cur = smem + (kt & 1u) * kStageBytes;
     uint8_t* nxt = smem + ((kt + 1) & 1u) * kStageBytes;
@@ -146,16 +201,15 @@ FE2O3_DEVICE void mainloop(const TileRows& a_rows, const TileRows& b_rows, uint3
       issue_tile(a_rows, (kt + 1) * BK, nxt);
       issue_tile(b_rows, (kt + 1) * BK, nxt + kTileBytes);
     }
-    load_frags(cur, 1, f1);
-    mma(f0, acc);
-    load_frags(cur, 2, f0);
-    mma(f1, acc);
-    load_frags(cur, 3, f1);
-    mma(f0, acc);
+#pragma unroll
+    for (int s = 0; s + 1 < S; ++s) {
+      Mma::load(cur, s + 1, f[(s + 1) & 1]);
+      Mma::mma(f[s & 1], acc);
+    }
     wait_vmcnt0();
     __syncthreads();
-    if (more) load_frags(nxt, 0, f0);
-    mma(f1, acc);
+    if (more) Mma::load(nxt, 0, f[S & 1]);
+    Mma::mma(f[(S - 1) & 1], acc);
   }
 }
 
@@ -164,16 +218,30 @@ FE2O3_DEVICE void mainloop_nt_256(const uint16_t* a_tile_base, const uint16_t* b
                                   Acc256& acc) {
   const TileRows ar = dense_rows(a_tile_base, lda, 256);
   const TileRows br = dense_rows(b_tile_base, ldb, 256);
-  mainloop(ar, br, k, smem, acc);
+  mainloop<MmaBf16>(ar, br, k, smem, acc);
 }
 
-// bf16 epilogue for a full 256x256 tile at c_tile (row stride ldc).
-FE2O3_DEVICE void store_bf16_256(const Acc256& acc, uint16_t* c_tile, uint64_t ldc) {
+// Output coordinates of accumulator (i, j, e) for this lane: tile row
+// wm*128 + 32i + lane%32, tile column wn*128 + 32j + 8(e/4) + 4(lane/32) + e%4.
+FE2O3_DEVICE uint32_t acc_row(int i) {
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  return (wave >> 1) * 128u + i * 32u + (lane & 31u);
+}
+FE2O3_DEVICE uint32_t acc_col(int j, int q) {
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  return (wave & 1u) * 128u + j * 32u + 8u * q + 4u * (lane >> 5);
+}
+
+// bf16 epilogue for a 256x256 tile at c_tile (row stride ldc); rows at or
+// beyond valid_rows are not stored.
+FE2O3_DEVICE void store_bf16_256(const Acc256& acc, uint16_t* c_tile, uint64_t ldc,
+                                 uint32_t valid_rows = 256) {
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t wm = wave >> 1, wn = wave & 1u;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t row = wm * 128u + i * 32u + (lane & 31u);
+    if (row >= valid_rows) continue;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll

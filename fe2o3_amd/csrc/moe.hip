@@ -1,0 +1,473 @@
+// moe.hip -- top-2 mixture-of-experts for gfx950.
+//
+// Router (examples/moe_top2_v1/src/kernel.rs:25-202 semantics):
+//   1. route_select: one thread per token; running top-2 with
+//      candidate_precedes(score, id) = higher score, or equal score and lower
+//      id (kernel.rs:25-33); route r = 2*token + rank; gating weights
+//      w0 = 1/(1+exp(l1-l0)), w1 = 1 - w0 (w0 in [0.5,1], so the pair sums to
+//      exactly 1 as examples/moe_expert_v1/src/pipeline.rs:137-148 requires).
+//   2. route_assign: one 128-thread workgroup; thread t owns a contiguous
+//      block of routes; per-expert counts per thread in LDS, a per-expert
+//      exclusive scan over threads, requested = totals, admitted =
+//      min(requested, capacity), offsets = exclusive scan of admitted with the
+//      terminal total; then each route gets rank = number of earlier routes
+//      (lower route id) of its expert, slot = offset + rank when
+//      rank < capacity (stable prefix), permutation[slot] = route,
+//      inverse[route] = slot, DROP sentinels elsewhere.  Integer work only:
+//      bit-identical to the reference's sort-based oracle.
+//
+// Expert FFN at the BASELINE shape (gate/up SiLU, down, weighted combine):
+//   gather      Xc[slot] = X[permutation[slot] / 2]              (bf16 rows)
+//   gate/up     Hc = bf16(silu(Xc Wg_e^T) * (Xc Wu_e^T))  per expert e,
+//               one 256x256 MFMA tile whose B rows interleave 32 gate rows
+//               and the matching 32 up rows, so gate and up accumulators of
+//               the same (row, f) sit in the same lane for the fused epilogue
+//   down        Yc = Hc Wd_e^T (fp32)
+//   combine     out[t] = bf16((+0 + w0*Yc[inv[2t]]) + w1*Yc[inv[2t+1]]),
+//               dropped routes contribute nothing (moe_expert_v1 combine
+//               order, examples/moe_expert_v1/src/kernel.rs:98-157).
+// Expert row ranges come from the device-resident offsets, so the whole
+// layer runs without a host round trip: the grouped GEMM grids are sized
+// for the worst case and workgroups beyond the last expert tile exit.
+#include "common.hpp"
+#include "gemm_core.hpp"
+#include "internal.hpp"
+
+namespace {
+
+using namespace fe2o3;
+constexpr uint32_t DROP = 0xffffffffu;
+constexpr int MAX_EXPERTS = 64;
+constexpr int ASSIGN_THREADS = 128;  // 32 KiB of per-thread expert counters
+
+template <typename T>
+FE2O3_DEVICE float logit_at(const T* p, uint64_t i);
+template <>
+FE2O3_DEVICE float logit_at<float>(const float* p, uint64_t i) { return p[i]; }
+template <>
+FE2O3_DEVICE float logit_at<uint16_t>(const uint16_t* p, uint64_t i) {
+  return f32_from_bf16_bits(p[i]);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) route_select_kernel(const T* __restrict__ logits,
+                                                           uint32_t tokens, uint32_t experts,
+                                                           uint32_t* __restrict__ top2,
+                                                           float* __restrict__ weights) {
+#pragma clang fp contract(off)
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= tokens) return;
+  const T* row = logits + (uint64_t)t * experts;
+  uint32_t best = DROP, second = DROP;
+  float bs = 0.0f, ss = 0.0f;
+  for (uint32_t e = 0; e < experts; ++e) {
+    const float s = logit_at(row, e);
+    if (best == DROP || s > bs || (s == bs && e < best)) {
+      second = best;
+      ss = bs;
+      best = e;
+      bs = s;
+    } else if (second == DROP || s > ss || (s == ss && e < second)) {
+      second = e;
+      ss = s;
+    }
+  }
+  top2[2ull * t] = best;
+  top2[2ull * t + 1] = second;
+  if (weights != nullptr) {
+    const float w0 = 1.0f / (1.0f + expf(ss - bs));
+    weights[2ull * t] = w0;
+    weights[2ull * t + 1] = 1.0f - w0;
+  }
+}
+
+__global__ void __launch_bounds__(ASSIGN_THREADS) route_assign_kernel(
+    const uint32_t* __restrict__ top2, uint32_t routes, uint32_t experts, uint32_t capacity,
+    uint32_t* __restrict__ requested, uint32_t* __restrict__ admitted,
+    uint32_t* __restrict__ offsets, uint32_t* __restrict__ slots,
+    uint32_t* __restrict__ permutation, uint32_t* __restrict__ inverse) {
+  __shared__ uint32_t cnt[MAX_EXPERTS * ASSIGN_THREADS];
+  __shared__ uint32_t off_s[MAX_EXPERTS + 1];
+  const uint32_t t = threadIdx.x;
+  const uint32_t per = (routes + ASSIGN_THREADS - 1) / ASSIGN_THREADS;
+  const uint32_t r0 = t * per;
+  const uint32_t r1 = r0 + per < routes ? r0 + per : routes;
+  for (uint32_t e = 0; e < experts; ++e) cnt[e * ASSIGN_THREADS + t] = 0;
+  for (uint32_t r = r0; r < r1; ++r) cnt[top2[r] * ASSIGN_THREADS + t] += 1;
+  for (uint32_t r = t; r < routes; r += ASSIGN_THREADS) permutation[r] = DROP;
+  __syncthreads();
+  if (t < experts) {  // exclusive scan of expert t's counts over threads
+    uint32_t run = 0;
+    for (uint32_t i = 0; i < ASSIGN_THREADS; ++i) {
+      const uint32_t c = cnt[t * ASSIGN_THREADS + i];
+      cnt[t * ASSIGN_THREADS + i] = run;
+      run += c;
+    }
+    requested[t] = run;
+    off_s[t] = run;  // temporarily the requested count
+  }
+  __syncthreads();
+  if (t == 0) {
+    uint32_t run = 0;
+    for (uint32_t e = 0; e < experts; ++e) {
+      const uint32_t adm = off_s[e] < capacity ? off_s[e] : capacity;
+      admitted[e] = adm;
+      offsets[e] = run;
+      off_s[e] = run;
+      run += adm;
+    }
+    offsets[experts] = run;
+    off_s[experts] = run;
+  }
+  __syncthreads();
+  for (uint32_t r = r0; r < r1; ++r) {
+    const uint32_t e = top2[r];
+    const uint32_t rank = cnt[e * ASSIGN_THREADS + t]++;
+    if (rank < capacity) {
+      const uint32_t slot = off_s[e] + rank;
+      slots[r] = slot;
+      inverse[r] = slot;
+      permutation[slot] = r;
+    } else {
+      slots[r] = DROP;
+      inverse[r] = DROP;
+    }
+  }
+}
+
+// examples/moe_expert_v1/src/kernel.rs:104-157: T=8, K=2, O=16.
+__global__ void __launch_bounds__(128) combine_profile_kernel(const float* __restrict__ compact,
+                                                              const uint32_t* __restrict__ inverse,
+                                                              const float* __restrict__ weights,
+                                                              float* __restrict__ combined) {
+#pragma clang fp contract(off)
+  const uint32_t i = threadIdx.x;  // 0..127
+  const uint32_t t = i / 16, o = i % 16;
+  float acc = 0.0f;
+  for (uint32_t rank = 0; rank < 2; ++rank) {
+    const uint32_t route = t * 2 + rank;
+    const uint32_t slot = inverse[route];
+    if (slot < 16u) {
+      const float wv = weights[route] * compact[slot * 16 + o];
+      acc = acc + wv;
+    }
+  }
+  combined[i] = acc;
+}
+
+// ---- expert FFN -------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) gather_kernel(const uint16_t* __restrict__ x,
+                                                     const uint32_t* __restrict__ permutation,
+                                                     const uint32_t* __restrict__ offsets,
+                                                     uint32_t experts, uint32_t hidden,
+                                                     uint16_t* __restrict__ xc) {
+  const uint32_t slot = blockIdx.x;
+  if (slot >= offsets[experts]) return;
+  const uint32_t token = permutation[slot] >> 1;
+  const u32x4_t* src = reinterpret_cast<const u32x4_t*>(x + (uint64_t)token * hidden);
+  u32x4_t* dst = reinterpret_cast<u32x4_t*>(xc + (uint64_t)slot * hidden);
+  for (uint32_t i = threadIdx.x; i < hidden / 8; i += blockDim.x) dst[i] = src[i];
+}
+
+// Finds the (expert, m-tile) of workgroup `x` over experts' 256-row tiles.
+FE2O3_DEVICE bool expert_tile(const uint32_t* offsets, uint32_t experts, uint32_t x, uint32_t* e_out,
+                              uint32_t* row0, uint32_t* rows) {
+  for (uint32_t e = 0; e < experts; ++e) {
+    const uint32_t lo = offsets[e], n = offsets[e + 1] - lo;
+    const uint32_t tiles = (n + 255u) / 256u;
+    if (x < tiles) {
+      *e_out = e;
+      *row0 = lo + x * 256u;
+      const uint32_t left = n - x * 256u;
+      *rows = left < 256u ? left : 256u;
+      return true;
+    }
+    x -= tiles;
+  }
+  return false;
+}
+
+FE2O3_DEVICE float silu_mul(float g, float u) {
+  const float sg = g / (1.0f + expf(-g));
+  return sg * u;
+}
+
+__global__ void __launch_bounds__(256, 1) gate_up_kernel(
+    const uint16_t* __restrict__ xc, const uint16_t* __restrict__ wg,
+    const uint16_t* __restrict__ wu, const uint32_t* __restrict__ offsets, uint32_t experts,
+    uint32_t hidden, uint32_t ffn, uint16_t* __restrict__ hc) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  uint32_t e, row0, rows;
+  if (!expert_tile(offsets, experts, blockIdx.x, &e, &row0, &rows))
+    return;
+  const uint32_t f0 = blockIdx.y * 128u;
+  const gemm_core::TileRows ar = gemm_core::dense_rows(xc + (uint64_t)row0 * hidden, hidden, rows);
+  gemm_core::TileRows br;
+  const uint64_t wbase = (uint64_t)e * ffn * hidden;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t row = gemm_core::tile_row(j);  // 32j .. 32j+31
+    const uint32_t wn = j >> 2, jj = j & 3;
+    const uint16_t* mat = (jj & 1) ? wu : wg;
+    const uint32_t f = f0 + wn * 64u + (jj >> 1) * 32u;
+    br.base[j] = mat + wbase + (uint64_t)f * hidden;
+    br.off[j] = (row & 31u) * hidden + gemm_core::tile_chunk(row) * 8u;
+  }
+  gemm_core::Acc256 acc;
+  gemm_core::zero(acc);
+  gemm_core::mainloop(ar, br, hidden, smem, acc);
+  // epilogue: (j=0 gate, j=1 up) and (j=2 gate, j=3 up) pair up per lane
+  const uint32_t lane = threadIdx.x & 63u, wn = (threadIdx.x >> 6) & 1u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t r = gemm_core::acc_row(i);
+    if (r >= rows) continue;
+    uint16_t* out_row = hc + (uint64_t)(row0 + r) * ffn;
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t f = f0 + wn * 64u + half * 32u + 8u * q + 4u * (lane >> 5);
+        const f32x16_t& gv = acc.v[i][2 * half];
+        const f32x16_t& uv = acc.v[i][2 * half + 1];
+        u32x2_t packed;
+        packed[0] = pack_bf16x2(silu_mul(gv[4 * q + 0], uv[4 * q + 0]),
+                                silu_mul(gv[4 * q + 1], uv[4 * q + 1]));
+        packed[1] = pack_bf16x2(silu_mul(gv[4 * q + 2], uv[4 * q + 2]),
+                                silu_mul(gv[4 * q + 3], uv[4 * q + 3]));
+        *reinterpret_cast<u32x2_t*>(out_row + f) = packed;
+      }
+  }
+}
+
+__global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict__ hc,
+                                                      const uint16_t* __restrict__ wd,
+                                                      const uint32_t* __restrict__ offsets,
+                                                      uint32_t experts, uint32_t hidden,
+                                                      uint32_t ffn, float* __restrict__ yc) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  uint32_t e, row0, rows;
+  if (!expert_tile(offsets, experts, blockIdx.x, &e, &row0, &rows))
+    return;
+  const uint32_t n0 = blockIdx.y * 256u;
+  const gemm_core::TileRows ar = gemm_core::dense_rows(hc + (uint64_t)row0 * ffn, ffn, rows);
+  const gemm_core::TileRows br =
+      gemm_core::dense_rows(wd + (uint64_t)e * hidden * ffn + (uint64_t)n0 * ffn, ffn, 256);
+  gemm_core::Acc256 acc;
+  gemm_core::zero(acc);
+  gemm_core::mainloop(ar, br, ffn, smem, acc);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t r = gemm_core::acc_row(i);
+    if (r >= rows) continue;
+    float* out_row = yc + (uint64_t)(row0 + r) * hidden + n0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f32x4_t v;
+#pragma unroll
+        for (int z = 0; z < 4; ++z) v[z] = acc.v[i][j][4 * q + z];
+        *reinterpret_cast<f32x4_t*>(out_row + gemm_core::acc_col(j, q)) = v;
+      }
+  }
+}
+
+__global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ yc,
+                                                      const uint32_t* __restrict__ inverse,
+                                                      const float* __restrict__ weights,
+                                                      uint32_t tokens, uint32_t hidden,
+                                                      uint16_t* __restrict__ out) {
+#pragma clang fp contract(off)
+  const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 4 outputs each
+  const uint64_t per_token = hidden / 4u;
+  if (idx >= (uint64_t)tokens * per_token) return;
+  const uint32_t t = (uint32_t)(idx / per_token);
+  const uint32_t h = (uint32_t)(idx % per_token) * 4u;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t rank = 0; rank < 2; ++rank) {
+    const uint32_t route = 2u * t + rank;
+    const uint32_t slot = inverse[route];
+    if (slot == DROP) continue;
+    const float w = weights[route];
+    const f32x4_t y = *reinterpret_cast<const f32x4_t*>(yc + (uint64_t)slot * hidden + h);
+#pragma unroll
+    for (int z = 0; z < 4; ++z) {
+      const float wv = w * y[z];
+      acc[z] = acc[z] + wv;
+    }
+  }
+  u32x2_t packed;
+  packed[0] = pack_bf16x2(acc[0], acc[1]);
+  packed[1] = pack_bf16x2(acc[2], acc[3]);
+  *reinterpret_cast<u32x2_t*>(out + (uint64_t)t * hidden + h) = packed;
+}
+
+struct Workspace {
+  uint16_t* xc;
+  uint16_t* hc;
+  float* yc;
+  uint64_t bytes;
+};
+
+uint64_t align256(uint64_t v) { return (v + 255u) & ~255ull; }
+
+Workspace carve(void* base, uint32_t tokens, uint32_t hidden, uint32_t ffn) {
+  const uint64_t routes = 2ull * tokens;
+  Workspace w;
+  uint8_t* p = (uint8_t*)base;
+  const uint64_t xb = align256(routes * hidden * 2), hb = align256(routes * ffn * 2),
+                 yb = align256(routes * hidden * 4);
+  w.xc = (uint16_t*)p;
+  w.hc = (uint16_t*)(p + xb);
+  w.yc = (float*)(p + xb + hb);
+  w.bytes = xb + hb + yb;
+  return w;
+}
+
+int32_t route(const void* logits, uint64_t logits_len, uint32_t dtype, uint32_t* top2,
+              uint64_t top2_len, uint32_t* requested, uint64_t requested_len, uint32_t* admitted,
+              uint64_t admitted_len, uint32_t* offsets, uint64_t offsets_len, uint32_t* slots,
+              uint64_t slots_len, uint32_t* permutation, uint64_t permutation_len,
+              uint32_t* inverse, uint64_t inverse_len, float* weights, uint64_t weights_len,
+              uint32_t tokens, uint32_t experts, uint32_t capacity, void* stream) {
+  if (experts < 2 || experts > MAX_EXPERTS || dtype > 1) return FE2O3_ERR_SHAPE;
+  const uint64_t routes = 2ull * tokens;
+  if (routes > 0xfffffffeull) return FE2O3_ERR_OVERFLOW;
+  if (logits_len != (uint64_t)tokens * experts || top2_len != routes || slots_len != routes ||
+      permutation_len != routes || inverse_len != routes || requested_len != experts ||
+      admitted_len != experts || offsets_len != experts + 1ull ||
+      (weights && weights_len != routes))
+    return FE2O3_ERR_LENGTH;
+  if (!requested || !admitted || !offsets) return FE2O3_ERR_NULL;
+  if (routes && (!logits || !top2 || !slots || !permutation || !inverse)) return FE2O3_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  if (tokens) {
+    const unsigned blocks = (tokens + 255u) / 256u;
+    if (dtype == 0)
+      route_select_kernel<float><<<blocks, 256, 0, s>>>((const float*)logits, tokens, experts,
+                                                        top2, weights);
+    else
+      route_select_kernel<uint16_t><<<blocks, 256, 0, s>>>((const uint16_t*)logits, tokens,
+                                                           experts, top2, weights);
+  }
+  route_assign_kernel<<<1, ASSIGN_THREADS, 0, s>>>(top2, (uint32_t)routes, experts, capacity,
+                                                   requested, admitted, offsets, slots,
+                                                   permutation, inverse);
+  return fe2o3_host::after_launch();
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1(
+    const float* logits, uint64_t logits_len, uint32_t* top2_experts, uint64_t top2_len,
+    uint32_t* requested_counts, uint64_t requested_len, uint32_t* admitted_counts,
+    uint64_t admitted_len, uint32_t* expert_offsets, uint64_t offsets_len, uint32_t* route_slots,
+    uint64_t slots_len, uint32_t* permutation, uint64_t permutation_len, uint32_t* inverse,
+    uint64_t inverse_len, void* stream) {
+  FE2O3_FAULT("fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1");
+  // examples/moe_top2_v1/src/contract.rs:3-29: T=8, E=4, K=2, C=4
+  if (logits_len != 32 || top2_len != 16 || requested_len != 4 || admitted_len != 4 ||
+      offsets_len != 5 || slots_len != 16 || permutation_len != 16 || inverse_len != 16)
+    return FE2O3_ERR_LENGTH;
+  return route(logits, logits_len, 0, top2_experts, top2_len, requested_counts, requested_len,
+               admitted_counts, admitted_len, expert_offsets, offsets_len, route_slots, slots_len,
+               permutation, permutation_len, inverse, inverse_len, nullptr, 0, 8, 4, 4, stream);
+}
+
+int32_t fe2o3_moe_top2_route(const void* logits, uint64_t logits_len, uint32_t logits_dtype,
+                             uint32_t* top2_experts, uint64_t top2_len, uint32_t* requested_counts,
+                             uint64_t requested_len, uint32_t* admitted_counts,
+                             uint64_t admitted_len, uint32_t* expert_offsets, uint64_t offsets_len,
+                             uint32_t* route_slots, uint64_t slots_len, uint32_t* permutation,
+                             uint64_t permutation_len, uint32_t* inverse, uint64_t inverse_len,
+                             float* route_weights, uint64_t weights_len, uint32_t tokens,
+                             uint32_t experts, uint32_t capacity, void* stream) {
+  FE2O3_FAULT("fe2o3_moe_top2_route");
+  return route(logits, logits_len, logits_dtype, top2_experts, top2_len, requested_counts,
+               requested_len, admitted_counts, admitted_len, expert_offsets, offsets_len,
+               route_slots, slots_len, permutation, permutation_len, inverse, inverse_len,
+               route_weights, weights_len, tokens, experts, capacity, stream);
+}
+
+int32_t fe2o3_moe_expert_combine_f32_t8_k2_o16_v1(const float* compact_output,
+                                                  uint64_t compact_len, const uint32_t* inverse,
+                                                  uint64_t inverse_len,
+                                                  const float* route_weights, uint64_t weights_len,
+                                                  float* combined_output, uint64_t combined_len,
+                                                  void* stream) {
+  FE2O3_FAULT("fe2o3_moe_expert_combine_f32_t8_k2_o16_v1");
+  if (compact_len != 256 || inverse_len != 16 || weights_len != 16 || combined_len != 128)
+    return FE2O3_ERR_LENGTH;
+  if (!compact_output || !inverse || !route_weights || !combined_output) return FE2O3_ERR_NULL;
+  combine_profile_kernel<<<1, 128, 0, (hipStream_t)stream>>>(compact_output, inverse,
+                                                            route_weights, combined_output);
+  return fe2o3_host::after_launch();
+}
+
+uint64_t fe2o3_moe_ffn_workspace_bytes(uint32_t tokens, uint32_t hidden, uint32_t ffn,
+                                       uint32_t experts) {
+  (void)experts;
+  return carve(nullptr, tokens, hidden, ffn).bytes;
+}
+
+int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate,
+                           uint64_t w_gate_len, const uint16_t* w_up, uint64_t w_up_len,
+                           const uint16_t* w_down, uint64_t w_down_len,
+                           const uint32_t* top2_experts, uint64_t top2_len,
+                           const uint32_t* expert_offsets, uint64_t offsets_len,
+                           const uint32_t* permutation, uint64_t permutation_len,
+                           const uint32_t* inverse, uint64_t inverse_len,
+                           const float* route_weights, uint64_t weights_len, uint16_t* out,
+                           uint64_t out_len, void* workspace, uint64_t workspace_bytes,
+                           uint32_t tokens, uint32_t hidden, uint32_t ffn, uint32_t experts,
+                           void* stream) {
+  FE2O3_FAULT("fe2o3_moe_ffn_top2");
+  (void)top2_experts;
+  if (experts < 1 || experts > MAX_EXPERTS) return FE2O3_ERR_SHAPE;
+  if (hidden == 0 || ffn == 0 || hidden % 256 != 0 || ffn % 128 != 0) return FE2O3_ERR_SHAPE;
+  const uint64_t routes = 2ull * tokens;
+  const uint64_t wsz = (uint64_t)experts * ffn * hidden;
+  if (x_len != (uint64_t)tokens * hidden || w_gate_len != wsz || w_up_len != wsz ||
+      w_down_len != wsz || top2_len != routes || offsets_len != experts + 1ull ||
+      permutation_len != routes || inverse_len != routes || weights_len != routes ||
+      out_len != (uint64_t)tokens * hidden)
+    return FE2O3_ERR_LENGTH;
+  if (256ull * ffn >= (1ull << 32) || 256ull * hidden >= (1ull << 32)) return FE2O3_ERR_SHAPE;
+  if (tokens == 0) return FE2O3_OK;
+  const Workspace ws = carve(workspace, tokens, hidden, ffn);
+  if (workspace_bytes < ws.bytes) return FE2O3_ERR_WORKSPACE;
+  if (!x || !w_gate || !w_up || !w_down || !expert_offsets || !permutation || !inverse ||
+      !route_weights || !out || !workspace)
+    return FE2O3_ERR_NULL;
+  if ((((uintptr_t)x | (uintptr_t)w_gate | (uintptr_t)w_up | (uintptr_t)w_down |
+        (uintptr_t)out | (uintptr_t)workspace) & 15u) != 0)
+    return FE2O3_ERR_ALIGNMENT;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)gate_up_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       gemm_core::kSmemBytes256);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute((const void*)down_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              gemm_core::kSmemBytes256);
+    if (e != hipSuccess) return (int32_t)e;
+    attr_set = true;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  gather_kernel<<<(unsigned)routes, 256, 0, s>>>(x, permutation, expert_offsets, experts, hidden,
+                                                ws.xc);
+  const unsigned m_tiles = (unsigned)((routes + 255u) / 256u + experts);
+  gate_up_kernel<<<dim3(m_tiles, ffn / 128u), 256, gemm_core::kSmemBytes256, s>>>(
+      ws.xc, w_gate, w_up, expert_offsets, experts, hidden, ffn, ws.hc);
+  down_kernel<<<dim3(m_tiles, hidden / 256u), 256, gemm_core::kSmemBytes256, s>>>(
+      ws.hc, w_down, expert_offsets, experts, hidden, ffn, ws.yc);
+  const uint64_t threads = (uint64_t)tokens * (hidden / 4u);
+  combine_kernel<<<(unsigned)((threads + 255u) / 256u), 256, 0, s>>>(ws.yc, inverse, route_weights,
+                                                                    tokens, hidden, out);
+  return fe2o3_host::after_launch();
+}
+
+}  // extern "C"

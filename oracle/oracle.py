@@ -135,6 +135,16 @@ def _ptr(a):
     return a.ctypes.data if a.size else None
 
 
+def _threads() -> int:
+    """Default OpenMP width: the CPUs this process may run on, at most 16
+    (os.cpu_count() can report far more cores than a container grants)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
 def _c(a, dtype):
     return np.ascontiguousarray(a, dtype=dtype)
 
@@ -282,7 +292,7 @@ def scalar_gemm_inputs(a_len, b_len):
 def gemm_bf16_nt_rows(m, n, k, a, b, row_begin, row_end, threads=0):
     out = np.zeros((row_end - row_begin) * n, np.float32)
     lib().fe2o3o_gemm_bf16_nt_rows(m, n, k, _c(a, np.uint16).ravel(), _c(b, np.uint16).ravel(),
-                                   row_begin, row_end, out, threads or os.cpu_count())
+                                   row_begin, row_end, out, threads or _threads())
     return out
 
 
@@ -292,14 +302,14 @@ def gemm_bf16_nt_points(k, a_rows, b_cols, threads=0):
     pts = a_rows.shape[0]
     out = np.zeros(pts, np.float32)
     lib().fe2o3o_gemm_bf16_nt_points(k, a_rows.ravel(), b_cols.ravel(), pts, out,
-                                     threads or os.cpu_count())
+                                     threads or _threads())
     return out
 
 
 def gemm_f32_rows(m, n, k, a, b, row_begin, row_end, threads=0):
     out = np.zeros((row_end - row_begin) * n, np.float32)
     lib().fe2o3o_gemm_f32_rows(m, n, k, _c(a, np.float32).ravel(), _c(b, np.float32).ravel(),
-                               row_begin, row_end, out, threads or os.cpu_count())
+                               row_begin, row_end, out, threads or _threads())
     return out
 
 
@@ -322,7 +332,7 @@ def flash_attention_rows_bf16(q, k, v, s, d, causal, scale, bh, rows, threads=0)
     lse = np.zeros(rows.size, np.float32)
     rc = lib().fe2o3o_flash_attention_rows_bf16(
         _c(q, np.uint16).ravel(), _c(k, np.uint16).ravel(), _c(v, np.uint16).ravel(), s, d,
-        int(causal), scale, bh, rows, rows.size, out, lse, threads or os.cpu_count())
+        int(causal), scale, bh, rows, rows.size, out, lse, threads or _threads())
     return rc, out.reshape(rows.size, d), lse
 
 
@@ -359,7 +369,7 @@ def row_softmax_reference_v1(x):
 def row_softmax_rows(x, rows, cols, threads=0):
     x = _c(x, np.float32).ravel()
     out = np.zeros(rows * cols, np.float32)
-    rc = lib().fe2o3o_row_softmax_rows(x, rows, cols, out, threads or os.cpu_count())
+    rc = lib().fe2o3o_row_softmax_rows(x, rows, cols, out, threads or _threads())
     return rc, out.reshape(rows, cols)
 
 
@@ -457,13 +467,13 @@ def fp8_decode_table() -> np.ndarray:
 
 def amax_f32(x, threads=0):
     x = _c(x, np.float32).ravel()
-    return lib().fe2o3o_amax_f32(x, x.size, threads or os.cpu_count())
+    return lib().fe2o3o_amax_f32(x, x.size, threads or _threads())
 
 
 def quantize_e4m3(x, scale, threads=0):
     x = _c(x, np.float32).ravel()
     out = np.zeros(x.size, np.uint8)
-    lib().fe2o3o_quantize_e4m3(x, x.size, scale, out, threads or os.cpu_count())
+    lib().fe2o3o_quantize_e4m3(x, x.size, scale, out, threads or _threads())
     return out
 
 
@@ -473,5 +483,5 @@ def gemm_fp8_points(k, a_rows, b_cols, scale_ab, threads=0):
     of = np.zeros(p, np.float32)
     ob = np.zeros(p, np.uint16)
     lib().fe2o3o_gemm_fp8_points(k, a_rows.ravel(), b_cols.ravel(), p, scale_ab, of, ob,
-                                 threads or os.cpu_count())
+                                 threads or _threads())
     return of, ob

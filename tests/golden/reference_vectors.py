@@ -379,3 +379,23 @@ def moe_expert_weights(bf16_from_f32):
 
 def moe_expert_route_weights():
     return np.array([0.75 if r % 2 == 0 else 0.25 for r in range(16)], np.float32)
+
+
+# ---- crates/fe2o3-hsa-runtime/tests/flash_attention_v1_hardware.rs:94-117 --------
+def flash_hardware_vectors_v1():
+    """The hardware test's nominal / equal / dominant vectors (B1 H1 N8 D16)."""
+    n, d = 8, 16
+    e = n * d
+    f = np.float32
+    nominal = (np.array([(f(i % 13) - f(6.0)) / f(8.0) for i in range(e)], np.float32),
+               np.array([(f(i % 11) - f(5.0)) / f(7.0) for i in range(e)], np.float32),
+               np.array([(f(i % 17) - f(8.0)) / f(9.0) for i in range(e)], np.float32))
+    equal = (np.zeros(e, np.float32), np.ones(e, np.float32),
+             np.array([f(i // d) + f(i % d) / f(32.0) for i in range(e)], np.float32))
+    q = np.zeros(e, np.float32)
+    k = np.zeros(e, np.float32)
+    for r in range(n):
+        q[r * d] = 8.0
+        k[r * d] = 8.0 if r == 3 else -8.0
+    dominant = (q, k, np.array([(f(i % d) - f(7.0)) / f(4.0) for i in range(e)], np.float32))
+    return [("nominal", *nominal), ("equal", *equal), ("dominant", *dominant)]

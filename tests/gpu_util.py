@@ -60,3 +60,18 @@ def rel_err(got, ref) -> float:
 
 def bf16_to_f32(bits):
     return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def assert_same(got, ref, what=""):
+    """Bitwise equality of two arrays with a short report (never a full
+    element diff, which is slow for large arrays)."""
+    g = np.ascontiguousarray(got)
+    r = np.ascontiguousarray(ref)
+    assert g.shape == r.shape, (what, g.shape, r.shape)
+    gb = g.view(np.uint8).reshape(g.size, -1) if g.size else g
+    rb = r.view(np.uint8).reshape(r.size, -1) if r.size else r
+    bad = np.nonzero(np.any(gb != rb, axis=1))[0] if g.size else np.array([], int)
+    if bad.size:
+        i = int(bad[0])
+        raise AssertionError(f"{what}: {bad.size} of {g.size} elements differ; first at {i}: "
+                             f"got {g.ravel()[i]!r} want {r.ravel()[i]!r}")

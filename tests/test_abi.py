@@ -1,0 +1,92 @@
+"""CPU checks of the C-ABI boundary: the library loads (no GPU calls), exports
+every function include/fe2o3_mi355x.h declares, the ctypes table covers the
+same set, the 312-byte property record layout matches
+crates/fe2o3-hip-sys/src/lib.rs:190-214, and host-side validation fails
+closed before any launch."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    with open(os.path.join(ROOT, "include", "fe2o3_mi355x.h")) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fe2o3\w+|fe2o3HipGetDeviceProperties)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    names = _declared()
+    for required in ("fe2o3HipGetDeviceProperties", "fe2o3_tiled_gemm_lds_slice1_v1",
+                     "fe2o3_tiled_gemm_general_v1", "fe2o3_scalar_gemm_v1", "fe2o3_gemm_bf16_nt",
+                     "fe2o3_row_softmax_v1", "fe2o3_flash_attention_fwd",
+                     "fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1", "fe2o3_moe_ffn_top2",
+                     "fe2o3_gemm_fp8_nt"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    from fe2o3_amd import _lib
+    L = C.CDLL(_lib.LIB_PATH)
+    missing = [n for n in _declared() if not hasattr(L, n)]
+    assert missing == []
+
+
+def test_ctypes_table_matches_header():
+    from fe2o3_amd import _lib
+    assert sorted(_lib.SIGNATURES) == _declared()
+
+
+def test_property_record_layout():
+    from fe2o3_amd._lib import Fe2o3HipDeviceProperties as P
+    assert C.sizeof(P) == 312 and C.alignment(P) == 8
+    offsets = {"gcn_arch_name": 0, "warp_size": 256, "max_threads_per_block": 260,
+               "max_block_dim": 264, "max_grid_dim": 276, "shared_mem_per_block": 288,
+               "shared_mem_per_block_optin": 296, "architecture_features": 304}
+    for name, off in offsets.items():
+        assert getattr(P, name).offset == off
+
+
+# Host-side validation runs before any HIP call, so these need no GPU.
+def test_length_and_shape_validation_without_gpu():
+    from fe2o3_amd import _lib
+    L = _lib.lib()
+    assert L.fe2o3_tiled_gemm_lds_slice1_v1(None, 255, None, 256, None, 256, None) == -2
+    assert L.fe2o3_tiled_gemm_general_v1(None, 0, None, 0, None, 0, 4, 4, 4, 3, 4, 4, 1.0, 0.0,
+                                         None) == -4
+    assert L.fe2o3_gemm_bf16_nt(None, 10, None, 10, None, 10, 4, 4, 4, None) == -2
+    assert L.fe2o3_row_softmax(None, 0, None, 0, None, 0, 4, 0, None) == -3
+    assert L.fe2o3_flash_attention_fwd(None, 0, None, 0, None, 0, None, 0, None, 0, 1, 1, 128, 64,
+                                       0, 0.1, None) == -3
+    assert L.fe2o3_moe_top2_route(None, 0, 0, None, 0, None, 0, None, 0, None, 0, None, 0, None,
+                                  0, None, 0, None, 0, 0, 1, 0, None) == -3
+    assert L.fe2o3_gemm_fp8_nt(None, 256 * 100, None, 256 * 100, None, None, None, 256 * 256,
+                               256, 256, 100, None) == -3
+    assert L.fe2o3_moe_ffn_workspace_bytes(4096, 4096, 14336, 8) >= 8192 * (4096 * 6 + 14336 * 2)
+    assert b"length" in L.fe2o3_status_string(-2)
+
+
+def test_fault_point_fails_closed(monkeypatch):
+    """FE2O3_FAULT_POINT forces an entry point to fail before any launch."""
+    from fe2o3_amd import _lib
+    monkeypatch.setenv("FE2O3_FAULT_POINT", "fe2o3_gemm_bf16_nt")
+    L = _lib.lib()
+    assert L.fe2o3_gemm_bf16_nt(None, 0, None, 0, None, 0, 0, 0, 0, None) == -23
+
+
+def test_typed_prepare_rejects_wrong_element_type():
+    from fe2o3_amd import kernels
+    from fe2o3_amd.runtime import DeviceBuffer
+    import numpy as np
+    fake = DeviceBuffer.__new__(DeviceBuffer)
+    fake.dtype, fake.count, fake.ptr, fake.nbytes = np.dtype(np.float32), 256, None, 1024
+    k = kernels.tiled_gemm_lds_slice1_gpu.Kernel(ctx=None)
+    with pytest.raises(TypeError):
+        k.prepare(fake, fake, fake)
+    fake.ptr = None

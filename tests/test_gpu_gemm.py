@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from golden import reference_vectors as rv
-from gpu_util import Guarded, bf16_to_f32, rel_err
+from gpu_util import Guarded, assert_same, bf16_to_f32, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -101,7 +101,7 @@ def test_general_hardware_matrix_bit_exact(gpu, oracle, case):
     _kernels().tiled_gemm_general_v1_gpu.Kernel.load(gpu).prepare(
         ga.body, gb.body, gc.body, m, n, k, lda, ldb, ldc, alpha, beta).launch()
     got = gc.download()
-    assert got.view(np.uint32).tolist() == expected.view(np.uint32).tolist()
+    assert_same(got, expected, case)
     assert ga.unchanged() and gb.unchanged() and gc.guards_intact()
 
 
@@ -199,7 +199,7 @@ def test_config1_f32_gemm_256_bit_exact(gpu, oracle):
     c = gpu.alloc(m * n, np.float32)
     kern.scalar_gemm_v1_gpu.Kernel.load(gpu).prepare(da, db, c, m, n, k).launch()
     ref = oracle.scalar_gemm(m, n, k, a, b)
-    assert c.download().view(np.uint32).tolist() == ref.view(np.uint32).tolist()
+    assert_same(c.download(), ref, "config1")
 
 
 # ---- bf16 NT GEMM ---------------------------------------------------------------------------

@@ -1,0 +1,299 @@
+"""GPU parity tests for the top-2 MoE path and the fp8 quantized GEMM path,
+through the C-ABI, against the CPU oracle restatements.
+
+Routing (indices, counts, offsets, slots, permutation, inverse) is integer
+work and must be bit-exact; gating weights within 1e-6 relative with pairs
+summing to exactly 1; the expert FFN and fp8 GEMM outputs within rel-err
+1e-2 (bf16 outputs); fp8 encoding bit-exact.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from golden import reference_vectors as rv
+from gpu_util import Guarded, assert_same, bf16_to_f32, rel_err
+
+pytestmark = pytest.mark.gpu
+
+ROUTE_KEYS = ["top2_experts", "requested_counts", "admitted_counts", "expert_offsets",
+              "route_slots", "permutation", "inverse"]
+
+
+def _k():
+    from fe2o3_amd import kernels
+    return kernels
+
+
+# ---- router: exact profile -------------------------------------------------------------
+
+@pytest.mark.parametrize("name", list(rv.MOE_VECTORS))
+def test_route_profile_bit_exact(gpu, oracle, name):
+    """examples/moe_top2_v1/src/vectors.rs:14-117 through the fixed
+    T8/E4/K2/C4 entry point; every output array bit-equal to the oracle."""
+    logits = np.array(rv.MOE_VECTORS[name], np.float32)
+    rc, ref = oracle.moe_top2_route(logits, 8, 4, 4)
+    assert rc == 0
+    lens = [16, 4, 4, 5, 16, 16, 16]
+    outs = [Guarded(gpu, np.full(n, 0xABABABAB, np.uint32)) for n in lens]
+    gl = Guarded(gpu, logits)
+    _k().moe_top2_route_f32_t8_e4_k2_c4_v1_gpu.Kernel.load(gpu).prepare(
+        gl.body, *[o.body for o in outs]).launch()
+    assert gl.unchanged()
+    for key, o in zip(ROUTE_KEYS, outs):
+        assert o.guards_intact()
+        assert o.download().tolist() == ref[key].tolist(), key
+
+
+def test_route_profile_pins(gpu, oracle):
+    """The reference's pinned routing outcomes (tests/oracle.rs:33-89)."""
+    lens = [16, 4, 4, 5, 16, 16, 16]
+    K = _k().moe_top2_route_f32_t8_e4_k2_c4_v1_gpu.Kernel.load(gpu)
+
+    def run(name):
+        outs = [gpu.alloc(n, np.uint32) for n in lens]
+        K.prepare(gpu.to_device(np.array(rv.MOE_VECTORS[name], np.float32)), *outs).launch()
+        return {k: o.download() for k, o in zip(ROUTE_KEYS, outs)}
+
+    r = run("nominal-balanced")
+    assert r["requested_counts"].tolist() == [4, 4, 4, 4]
+    assert r["expert_offsets"].tolist() == [0, 4, 8, 12, 16]
+    r = run("all-equal-tie-break-and-empty-experts")
+    assert r["top2_experts"].tolist() == [0, 1] * 8
+    assert r["requested_counts"].tolist() == [8, 8, 0, 0]
+    assert r["admitted_counts"].tolist() == [4, 4, 0, 0]
+    assert r["expert_offsets"].tolist() == [0, 4, 8, 8, 8]
+    assert r["permutation"][8:].tolist() == [0xFFFFFFFF] * 8
+    r = run("stable-capacity-overflow")
+    assert r["requested_counts"][0] == 8
+    assert r["permutation"][:4].tolist() == [0, 2, 4, 6]
+    for route in (8, 10, 12, 14):
+        assert r["inverse"][route] == 0xFFFFFFFF and r["route_slots"][route] == 0xFFFFFFFF
+
+
+# ---- router: BASELINE scale ---------------------------------------------------------------
+
+def _route(gpu, logits_dev, tokens, experts, capacity):
+    out = {"top2": gpu.alloc(2 * tokens, np.uint32), "requested": gpu.alloc(experts, np.uint32),
+           "admitted": gpu.alloc(experts, np.uint32), "offsets": gpu.alloc(experts + 1, np.uint32),
+           "slots": gpu.alloc(2 * tokens, np.uint32),
+           "permutation": gpu.alloc(2 * tokens, np.uint32),
+           "inverse": gpu.alloc(2 * tokens, np.uint32), "weights": gpu.alloc(2 * tokens, np.float32)}
+    _k().moe_top2_route(logits_dev, out, tokens, experts, capacity)
+    return out
+
+
+@pytest.mark.parametrize("capacity", [0xFFFFFFFF, 1280, 700, 3])
+def test_route_config5_bf16_logits_bit_exact(gpu, oracle, capacity):
+    """Config 5 router: 4096 tokens x 8 experts, bf16 logits ~ N(0,1) (seed 5;
+    bf16 rounding makes ties frequent, exercising the lower-id rule), at
+    unbounded, 1.25x-balanced, tight and tiny capacities."""
+    tokens, experts = 4096, 8
+    lg = gpu.alloc(tokens * experts, np.uint16)
+    _k().fill_normal_bf16(lg, 5, 0x10617, 1.0)
+    host_bits = lg.download()
+    logits = bf16_to_f32(host_bits)
+    out = _route(gpu, lg, tokens, experts, capacity)
+    rc, ref = oracle.moe_top2_route(logits, tokens, experts, capacity)
+    assert rc == 0
+    names = dict(zip(["top2", "requested", "admitted", "offsets", "slots", "permutation",
+                      "inverse"], ROUTE_KEYS))
+    for mine, theirs in names.items():
+        assert_same(out[mine].download(), ref[theirs], mine)
+    w = out["weights"].download()
+    wref = oracle.moe_top2_weights(logits, tokens, experts, ref["top2_experts"])
+    assert np.all(np.abs(w - wref) <= 1e-6 * np.abs(wref))
+    assert np.all(w[0::2] + w[1::2] == np.float32(1.0))
+    # round trip: permutation and inverse are mutually inverse on admitted routes
+    perm, inv = ref["permutation"], ref["inverse"]
+    total = ref["expert_offsets"][-1]
+    assert all(inv[perm[s]] == s for s in range(total))
+
+
+def test_route_f32_logits_many_experts(gpu, oracle):
+    tokens, experts = 1000, 64
+    rng = np.random.default_rng(3)
+    logits = np.round(rng.standard_normal(tokens * experts) * 4).astype(np.float32)  # many ties
+    out = _route(gpu, gpu.to_device(logits), tokens, experts, 40)
+    rc, ref = oracle.moe_top2_route(logits, tokens, experts, 40)
+    assert rc == 0
+    assert_same(out["top2"].download(), ref["top2_experts"], "top2")
+    assert_same(out["inverse"].download(), ref["inverse"], "inverse")
+    assert_same(out["permutation"].download(), ref["permutation"], "permutation")
+
+
+# ---- expert combine: exact profile ----------------------------------------------------------
+
+@pytest.mark.parametrize("which", ["equal", "balanced"])
+def test_expert_combine_profile_bit_exact(gpu, oracle, which):
+    """examples/moe_expert_v1/tests/pipeline_oracle.rs:15-130: the combine of
+    the oracle pipeline's compact output, bit-equal."""
+    logits = np.array(rv.moe_expert_equal_logits() if which == "equal"
+                      else rv.moe_expert_balanced_logits(), np.float32)
+    rc, routing = oracle.moe_top2_route(logits, 8, 4, 4)
+    assert rc == 0
+    acts = rv.moe_expert_activations(oracle.bf16_from_f32)
+    weights = rv.moe_expert_weights(oracle.bf16_from_f32)
+    rw = rv.moe_expert_route_weights()
+    rc, pipe = oracle.moe_expert_pipeline_v1(logits, acts, weights, rw, routing)
+    assert rc == 0
+    compact = gpu.to_device(pipe["compact_output"])
+    out = Guarded(gpu, np.full(128, np.nan, np.float32))
+    _k().moe_expert_combine_f32_t8_k2_o16_v1_gpu.Kernel.load(gpu).prepare(
+        compact, gpu.to_device(routing["inverse"]), gpu.to_device(rw), out.body).launch()
+    assert out.download().view(np.uint32).tolist() == pipe["combined_output"].view(np.uint32).tolist()
+    assert out.guards_intact()
+
+
+# ---- expert FFN ------------------------------------------------------------------------------
+
+def _ffn_case(gpu, oracle, tokens, hidden, ffn, experts, capacity, sample_tokens):
+    kern = _k()
+    seed = 5
+    lg = gpu.alloc(tokens * experts, np.uint16)
+    kern.fill_normal_bf16(lg, seed, 0x10617, 1.0)
+    x = gpu.alloc(tokens * hidden, np.uint16)
+    kern.fill_normal_bf16(x, seed, 0xAC7, 1.0)
+    wsz = experts * ffn * hidden
+    wg, wu, wd = (gpu.alloc(wsz, np.uint16) for _ in range(3))
+    kern.fill_normal_bf16(wg, seed, 0x6A7E, 0.02)
+    kern.fill_normal_bf16(wu, seed, 0x0B0B, 0.02)
+    kern.fill_normal_bf16(wd, seed, 0xD0D0, 0.02)
+    routing = _route(gpu, lg, tokens, experts, capacity)
+    ws = gpu.alloc(kern.moe_ffn_workspace_bytes(tokens, hidden, ffn, experts), np.uint8)
+    out = Guarded(gpu, np.full(tokens * hidden, 0x7FDE, np.uint16))
+    kern.moe_ffn_top2(x, wg, wu, wd, routing, out.body, ws, tokens, hidden, ffn, experts)
+    assert out.guards_intact()
+    got = bf16_to_f32(out.download()).reshape(tokens, hidden)
+    top2 = routing["top2"].download()
+    inv = routing["inverse"].download()
+    w = routing["weights"].download()
+    xs = x.download().reshape(tokens, hidden)
+    worst = 0.0
+    cache = {}
+
+    def expert_weights(e):
+        if e not in cache:
+            off = e * ffn * hidden
+            cache[e] = tuple(t.view(off, ffn * hidden).download() for t in (wg, wu, wd))
+        return cache[e]
+
+    for t in sample_tokens:
+        ref = np.zeros(hidden, np.float32)
+        for rank in range(2):
+            r = 2 * t + rank
+            if inv[r] == 0xFFFFFFFF:
+                continue
+            g_, u_, d_ = expert_weights(int(top2[r]))
+            _, y = oracle.moe_ffn_route(xs[t], g_, u_, d_, hidden, ffn)
+            ref = ref + np.float32(w[r]) * y
+        worst = max(worst, rel_err(got[t], ref))
+    return worst, inv
+
+
+def test_moe_ffn_small_all_tokens(gpu, oracle):
+    tokens, hidden, ffn, experts = 256, 256, 512, 8
+    worst, inv = _ffn_case(gpu, oracle, tokens, hidden, ffn, experts, 0xFFFFFFFF, range(tokens))
+    assert worst <= 1e-2, worst
+
+
+def test_moe_ffn_small_with_drops(gpu, oracle):
+    """Capacity below demand: dropped routes contribute nothing."""
+    tokens, hidden, ffn, experts = 256, 256, 256, 8
+    worst, inv = _ffn_case(gpu, oracle, tokens, hidden, ffn, experts, 40, range(tokens))
+    assert (inv == 0xFFFFFFFF).any()
+    assert worst <= 1e-2, worst
+
+
+def test_moe_ffn_config5_sampled_tokens(gpu, oracle):
+    """4096 tokens, hidden 4096, 8 experts, FFN 14336,
+    weights N(0, 0.02), unbounded capacity; 12 tokens checked end to end."""
+    worst, _ = _ffn_case(gpu, oracle, 4096, 4096, 14336, 8, 0xFFFFFFFF,
+                         [0, 1, 511, 1024, 2047, 2048, 3000, 3333, 4000, 4093, 4094, 4095])
+    assert worst <= 1e-2, worst
+
+
+# ---- fp8 ------------------------------------------------------------------------------------
+
+def _edge_values():
+    v = [0.0, -0.0, 448.0, -448.0, 449.0, 463.99, 464.0, 464.01, 479.0, 480.0, 1e30, -1e30,
+         float("inf"), float("-inf"), 2.0 ** -9, 2.0 ** -10, 3 * 2.0 ** -11, 2.0 ** -6,
+         2.0 ** -6 * 1.0625, 2.0 ** -6 * 0.9375, 1.0625, 1.1875, 0.5 + 2.0 ** -5, 240.0, 1e-45,
+         -1e-40, 2.0 ** -7 * 15 / 16]
+    return np.array(v, np.float32)
+
+
+def test_e4m3_encoding_bit_exact(gpu, oracle):
+    """Device RNE/satfinite encoding equals the oracle's OCP closed form on
+    every bf16-representable value, edge cases and random f32 values."""
+    allbf = bf16_to_f32(np.arange(65536, dtype=np.uint16))
+    allbf = allbf[~np.isnan(allbf)]
+    rng = np.random.default_rng(0)
+    rand = (rng.standard_normal(1 << 20) * rng.choice([1e-3, 1.0, 30.0, 1000.0], 1 << 20)).astype(np.float32)
+    x = np.concatenate([allbf, _edge_values(), rand]).astype(np.float32)
+    x = np.concatenate([x, np.zeros((-x.size) % 4, np.float32)])
+    kern = _k()
+    dx = gpu.to_device(x)
+    one = gpu.to_device(np.array([1.0], np.float32))
+    dq = gpu.alloc(x.size, np.uint8)
+    kern.quantize_e4m3(dx, one, dq)
+    got = dq.download()
+    ref = oracle.quantize_e4m3(x, 1.0)
+    assert_same(got, ref, "e4m3 codes")
+
+
+def test_amax_scale_and_quantize_bit_exact(gpu, oracle):
+    kern = _k()
+    n = 1_000_003
+    xh = oracle.fill_normal_f32(n, 4, 0xA8A8, 1.0)
+    x = gpu.to_device(xh)
+    amax = gpu.alloc(1, np.float32)
+    scale = gpu.alloc(1, np.float32)
+    kern.amax_f32(x, amax)
+    kern.fp8_scale_from_amax(amax, scale)
+    a_ref = oracle.amax_f32(xh)
+    assert amax.download()[0] == np.float32(a_ref)
+    s_ref = np.float32(np.float32(a_ref) / np.float32(448.0))
+    assert scale.download()[0] == s_ref
+    q = gpu.alloc(n, np.uint8)
+    kern.quantize_e4m3(x, scale, q)
+    assert_same(q.download(), oracle.quantize_e4m3(xh, float(s_ref)), "quantized")
+
+
+def _fp8_case(gpu, oracle, m, n, k, points):
+    kern = _k()
+    a32 = gpu.alloc(m * k, np.float32)
+    b32 = gpu.alloc(n * k, np.float32)
+    kern.fill_normal_f32(a32, 4, 0xA, 1.0)
+    kern.fill_normal_f32(b32, 4, 0xB, 1.0)
+    sa, sb, am = gpu.alloc(1, np.float32), gpu.alloc(1, np.float32), gpu.alloc(1, np.float32)
+    aq, bq = gpu.alloc(m * k, np.uint8), gpu.alloc(n * k, np.uint8)
+    for src, s, q in ((a32, sa, aq), (b32, sb, bq)):
+        kern.amax_f32(src, am)
+        kern.fp8_scale_from_amax(am, s)
+        kern.quantize_e4m3(src, s, q)
+    c = Guarded(gpu, np.full(m * n, 0x7FDE, np.uint16))
+    kern.gemm_fp8_nt(aq, bq, sa, sb, c.body, m, n, k)
+    assert c.guards_intact()
+    got = bf16_to_f32(c.download()).reshape(m, n)
+    ah, bh = aq.download().reshape(m, k), bq.download().reshape(n, k)
+    sab = float(np.float32(sa.download()[0] * sb.download()[0]))
+    rows, cols = points
+    ref_f32, _ = oracle.gemm_fp8_points(k, ah[rows], bh[cols], sab)
+    return rel_err(got[rows, cols], ref_f32)
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (512, 768, 1024), (256, 512, 4096)])
+def test_gemm_fp8_all_outputs(gpu, oracle, m, n, k):
+    rr, cc = np.meshgrid(np.arange(m), np.arange(n), indexing="ij")
+    assert _fp8_case(gpu, oracle, m, n, k, (rr.ravel(), cc.ravel())) <= 1e-2
+
+
+def test_gemm_fp8_config4_sampled(gpu, oracle):
+    """8192^3 e4m3 with amax/448 per-tensor scales; 4096
+    sampled outputs at full K plus one full 128-row block."""
+    m = n = k = 8192
+    rng = np.random.default_rng(4)
+    rows = np.concatenate([rng.integers(0, m, 4096), np.repeat(np.arange(4096, 4096 + 128), 64)])
+    cols = np.concatenate([rng.integers(0, n, 4096), np.tile(rng.integers(0, n, 64), 128)])
+    assert _fp8_case(gpu, oracle, m, n, k, (rows, cols)) <= 1e-2
