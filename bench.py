@@ -130,17 +130,165 @@ def wl_gemm_bf16(ctx, stream, args):
     }
 
 
+def _timed(ctx, stream, fn, steps, warmup):
+    ms, _ = Timer(ctx, stream).run(fn, steps, warmup)
+    return ms
+
+
+def sec_flash(ctx, stream, causal, steps, warmup):
+    """Config 3a/3b: B8 H32 S4096 D128 bf16, scale 1/sqrt(128), LSE out."""
+    from fe2o3_amd import kernels
+    b, h, s, d = 8, 32, 4096, 128
+    n = b * h * s * d
+    q, k, v, o = (ctx.alloc(n, np.uint16) for _ in range(4))
+    lse = ctx.alloc(b * h * s, np.float32)
+    for i, t in enumerate((q, k, v)):
+        kernels.fill_normal_bf16(t, 2, 0xF100 + i, 1.0, stream=stream)
+    prep = kernels.flash_attention_fwd_gpu.Kernel.load(ctx).prepare(
+        q, k, v, o, lse, b, h, s, d, 1 if causal else 0, float(1.0 / np.sqrt(d)))
+    ms = _timed(ctx, stream, lambda: prep.launch_async(stream), steps, warmup)
+    flop = 4.0 * b * h * s * s * d * (0.5 if causal else 1.0)
+    tf = flop / (ms * 1e-3) / 1e12
+    return {"workload": f"flash-attn fwd {'causal' if causal else 'non-causal'} B8 H32 S4096 "
+                        f"D128 bf16 (config 3{'b' if causal else 'a'})",
+            "kernel": f"flash_fwd_kernel<{str(bool(causal)).lower()}>", "ms": ms,
+            "value": round(tf, 2), "unit": "TFLOP/s",
+            "roofline": {"bound": "mfma", "peak": PEAK["bf16"], "frac": round(tf / PEAK["bf16"], 4)}}
+
+
+def sec_softmax(ctx, stream, steps, warmup):
+    """Config 3c: 1,048,576 rows x 4096 fp32 in/out (HBM-bound)."""
+    from fe2o3_amd import kernels
+    rows, cols = 8 * 32 * 4096, 4096
+    x = ctx.alloc(rows * cols, np.float32)
+    y = ctx.alloc(rows * cols, np.float32)
+    kernels.fill_normal_f32(x, 3, 0x50F7, 1.0, stream=stream)
+    prep = kernels.row_softmax_gpu.Kernel.load(ctx).prepare(x, y, None, rows, cols)
+    ms = _timed(ctx, stream, lambda: prep.launch_async(stream), steps, warmup)
+    gbs = rows * cols * 8 / (ms * 1e-3) / 1e9
+    return {"workload": "row softmax 1048576 x 4096 fp32 (config 3c)",
+            "kernel": "softmax_reg_kernel<16,false>", "ms": ms, "value": round(gbs, 1),
+            "unit": "GB/s",
+            "roofline": {"bound": "hbm", "peak": PEAK["hbm_gbs"],
+                         "frac": round(gbs / PEAK["hbm_gbs"], 4)}}
+
+
+def sec_fp8(ctx, stream, steps, warmup):
+    """Config 4: fp8 e4m3 GEMM 8192^3, per-tensor amax/448 scales, bf16 out."""
+    from fe2o3_amd import kernels
+    m = n = k = 8192
+    a32, b32 = ctx.alloc(m * k, np.float32), ctx.alloc(n * k, np.float32)
+    kernels.fill_normal_f32(a32, 4, 0xA, 1.0, stream=stream)
+    kernels.fill_normal_f32(b32, 4, 0xB, 1.0, stream=stream)
+    sa, sb, am = ctx.alloc(1, np.float32), ctx.alloc(1, np.float32), ctx.alloc(1, np.float32)
+    aq, bq = ctx.alloc(m * k, np.uint8), ctx.alloc(n * k, np.uint8)
+    quant_ms = 0.0
+    for src, sc, q in ((a32, sa, aq), (b32, sb, bq)):
+        def quant(src=src, sc=sc, q=q):
+            kernels.amax_f32(src, am, stream=stream, sync=False)
+            kernels.fp8_scale_from_amax(am, sc, stream=stream, sync=False)
+            kernels.quantize_e4m3(src, sc, q, stream=stream, sync=False)
+        quant_ms += _timed(ctx, stream, quant, 5, 1)
+    c = ctx.alloc(m * n, np.uint16)
+    gemm = lambda: kernels.gemm_fp8_nt(aq, bq, sa, sb, c, m, n, k, stream=stream, sync=False)
+    ms = _timed(ctx, stream, gemm, steps, warmup)
+    tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    return {"workload": "fp8 e4m3 GEMM 8192^3, per-tensor scales, bf16 out (config 4)",
+            "kernel": "gemm_fp8_kernel", "ms": ms, "value": round(tf, 2), "unit": "TFLOP/s",
+            "quantize_ms_both_operands": round(quant_ms, 4),
+            "roofline": {"bound": "mfma", "peak": PEAK["fp8"], "frac": round(tf / PEAK["fp8"], 4)}}
+
+
+def sec_moe(ctx, stream, steps, warmup):
+    """Config 5: 4096 tokens, hidden 4096, 8 experts, FFN 14336, top-2."""
+    from fe2o3_amd import kernels
+    t, hdim, f, e = 4096, 4096, 14336, 8
+    lg = ctx.alloc(t * e, np.uint16)
+    x = ctx.alloc(t * hdim, np.uint16)
+    kernels.fill_normal_bf16(lg, 5, 0x10617, 1.0, stream=stream)
+    kernels.fill_normal_bf16(x, 5, 0xAC7, 1.0, stream=stream)
+    w = [ctx.alloc(e * f * hdim, np.uint16) for _ in range(3)]
+    for i, dom in enumerate((0x6A7E, 0x0B0B, 0xD0D0)):
+        kernels.fill_normal_bf16(w[i], 5, dom, 0.02, stream=stream)
+    r = {"top2": ctx.alloc(2 * t, np.uint32), "requested": ctx.alloc(e, np.uint32),
+         "admitted": ctx.alloc(e, np.uint32), "offsets": ctx.alloc(e + 1, np.uint32),
+         "slots": ctx.alloc(2 * t, np.uint32), "permutation": ctx.alloc(2 * t, np.uint32),
+         "inverse": ctx.alloc(2 * t, np.uint32), "weights": ctx.alloc(2 * t, np.float32)}
+    ws = ctx.alloc(kernels.moe_ffn_workspace_bytes(t, hdim, f, e), np.uint8)
+    out = ctx.alloc(t * hdim, np.uint16)
+
+    def layer():
+        kernels.moe_top2_route(lg, r, t, e, stream=stream, sync=False)
+        kernels.moe_ffn_top2(x, w[0], w[1], w[2], r, out, ws, t, hdim, f, e, stream=stream,
+                             sync=False)
+    ms = _timed(ctx, stream, layer, max(3, steps // 10), max(1, warmup // 10))
+    flop = 3.0 * 2.0 * hdim * f * 2 * t
+    tf = flop / (ms * 1e-3) / 1e12
+    return {"workload": "MoE top-2 layer: 4096 tokens, hidden 4096, 8 experts, FFN 14336, "
+                        "router + gather + gate/up SiLU + down + combine (config 5)",
+            "kernel": "gate_up_kernel + down_kernel", "ms": ms, "value": round(tf, 2),
+            "unit": "TFLOP/s",
+            "roofline": {"bound": "mfma", "peak": PEAK["bf16"], "frac": round(tf / PEAK["bf16"], 4)}}
+
+
+def sec_gemm_f32(ctx, stream, steps, warmup):
+    """Config 1: f32 GEMM 256^3, U[-1,1] seed 0, sequential unfused recurrence."""
+    from fe2o3_amd import kernels
+    m = n = k = 256
+    a, b, c = ctx.alloc(m * k, np.float32), ctx.alloc(k * n, np.float32), ctx.alloc(m * n, np.float32)
+    kernels.fill_uniform_f32(a, 0, 0xA, stream=stream)
+    kernels.fill_uniform_f32(b, 0, 0xB, stream=stream)
+    prep = kernels.scalar_gemm_v1_gpu.Kernel.load(ctx).prepare(a, b, c, m, n, k)
+    ms = _timed(ctx, stream, lambda: prep.launch_async(stream), steps, warmup)
+    tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    return {"workload": "f32 GEMM 256^3 bit-exact sequential recurrence (config 1)",
+            "kernel": "scalar_gemm_kernel", "ms": ms, "value": round(tf, 3), "unit": "TFLOP/s",
+            "roofline": {"bound": "fp32 VALU", "peak": PEAK["fp32"],
+                         "frac": round(tf / PEAK["fp32"], 5)}}
+
+
+SECONDARY = {
+    "flash_noncausal": lambda c, s, a: sec_flash(c, s, False, a.steps, a.warmup),
+    "flash_causal": lambda c, s, a: sec_flash(c, s, True, a.steps, a.warmup),
+    "softmax": lambda c, s, a: sec_softmax(c, s, max(5, a.steps // 10), max(2, a.warmup // 10)),
+    "fp8_gemm": lambda c, s, a: sec_fp8(c, s, a.steps, a.warmup),
+    "moe": lambda c, s, a: sec_moe(c, s, a.steps, a.warmup),
+    "gemm_f32": lambda c, s, a: sec_gemm_f32(c, s, a.steps, a.warmup),
+}
+
 WORKLOADS = {"gemm_bf16": wl_gemm_bf16}
+
+
+def calibrate_copy(ctx, stream, args):
+    """1 GiB device-to-device copy: 1 GiB read + 1 GiB written per launch."""
+    from fe2o3_amd import _lib
+    from fe2o3_amd.runtime import check
+    n = 1 << 30
+    src, dst = ctx.alloc(n, np.uint8), ctx.alloc(n, np.uint8)
+    copy = lambda: check(_lib.lib().fe2o3_rt_memcpy_async(dst.ptr, src.ptr, n, 3, stream.handle),
+                         "copy")
+    ms = _timed(ctx, stream, copy, args.steps, args.warmup)
+    print(json.dumps({"calibration": "d2d copy", "bytes_read": n, "bytes_written": n,
+                      "ms": round(ms, 5), "gbs": round(2 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
+    return 0
 
 
 def main() -> int:
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    # MI355X idles at a low clock and needs tens of milliseconds of load to
+    # reach its steady clock: the defaults warm up for ~30 ms and time ~70 ms
+    p.add_argument("--steps", type=int, default=500)
+    p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--workload", default="gemm_bf16", choices=sorted(WORKLOADS))
     p.add_argument("--cpu-seconds", type=float, default=20.0)
     p.add_argument("--no-cpu-baseline", dest="cpu_baseline", action="store_false")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only time a 1 GiB device-to-device copy (the reference kernel "
+                        "whose FETCH_SIZE/WRITE_SIZE calibrate the traffic counters)")
+    p.add_argument("--secondary", default="all",
+                   help="comma list of other configs to time after the main one "
+                        f"({','.join(SECONDARY)}), 'all' or 'none'")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not "
@@ -150,6 +298,8 @@ def main() -> int:
     from fe2o3_amd.runtime import GpuContext
     ctx = GpuContext.current(0)
     stream = ctx.stream()
+    if args.calibrate_copy:
+        return calibrate_copy(ctx, stream, args)
     r = WORKLOADS[args.workload](ctx, stream, args)
 
     value = r["flop"] / (r["ms"] * 1e-3) / 1e12
@@ -171,6 +321,14 @@ def main() -> int:
         "parity": r["parity"],
         "wall_s_timed_region": round(r["wall"], 4),
     }
+    names = list(SECONDARY) if args.secondary == "all" else \
+        [x for x in args.secondary.split(",") if x and x != "none"]
+    if names:
+        line["secondary"] = {}
+        for name in names:
+            res = SECONDARY[name](ctx, stream, args)
+            res["ms"] = round(res["ms"], 5)
+            line["secondary"][name] = res
     print(json.dumps(line), flush=True)
     ok = r["parity"]["max_rel_err"] <= r["parity"]["tolerance"]
     return 0 if ok else 1

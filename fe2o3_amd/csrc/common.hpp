@@ -83,6 +83,12 @@ FE2O3_DEVICE float swap_half(float v) {
 FE2O3_DEVICE void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 FE2O3_DEVICE void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Workgroup barrier that completes this wave's LDS operations first but,
+// unlike __syncthreads(), leaves its outstanding global loads (including
+// global->LDS copies of later pipeline stages) in flight.  Callers order
+// those copies with explicit s_waitcnt vmcnt(N) before the barrier.
+FE2O3_DEVICE void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // 16-byte global -> LDS copy (gfx950 global_load_lds_dwordx4): lane i of the
 // wave writes its 16 bytes to lds_base + 16*i.  lds_base must be uniform.
 FE2O3_DEVICE void g2l_b128(const void* gptr, void* lds_base) {

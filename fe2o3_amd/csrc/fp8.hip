@@ -13,6 +13,7 @@
 // issues v_mfma_scale_f32_32x32x64_f8f6f4 (5.0 PFLOP/s dense peak).
 #include "common.hpp"
 #include "gemm_core.hpp"
+#include "gemm_pipe.hpp"
 #include "internal.hpp"
 
 namespace {
@@ -62,6 +63,9 @@ __global__ void __launch_bounds__(256) quantize_kernel(const float* __restrict__
     q[i] = e4m3_from_f32(x[i] / s);
 }
 
+constexpr int kFp8RowBytes = 128, kFp8Stages = 2;
+constexpr int kFp8Smem = kFp8Stages * 2 * gemm_pipe::Geo<kFp8RowBytes>::kTileBytes;  // 128 KiB
+
 __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restrict__ a,
                                                           const uint8_t* __restrict__ b,
                                                           const float* __restrict__ scale_a,
@@ -71,14 +75,15 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   uint32_t tm, tn;
   gemm_core::xcd_tile_order(blockIdx.x, m / 256, n / 256, &tm, &tn);
-  const uint32_t k16 = k / 2;  // 16-bit units per row
+  const uint32_t k16 = k / 2;  // rows addressed in 16-bit units
   const uint16_t* a16 = reinterpret_cast<const uint16_t*>(a + (uint64_t)tm * 256 * k);
   const uint16_t* b16 = reinterpret_cast<const uint16_t*>(b + (uint64_t)tn * 256 * k);
-  const gemm_core::TileRows ar = gemm_core::dense_rows(a16, k16, 256);
-  const gemm_core::TileRows br = gemm_core::dense_rows(b16, k16, 256);
-  gemm_core::Acc256 acc;
-  gemm_core::zero(acc);
-  gemm_core::mainloop<gemm_core::MmaFp8>(ar, br, k16, smem, acc);
+  const auto ar = gemm_pipe::dense_rows<kFp8RowBytes>(a16, k16, 256);
+  const auto br = gemm_pipe::dense_rows<kFp8RowBytes>(b16, k16, 256);
+  gemm_pipe::Acc acc;
+  gemm_pipe::zero(acc);
+  gemm_pipe::mainloop<gemm_pipe::MmaFp8<kFp8RowBytes>, kFp8RowBytes, kFp8Stages>(ar, br, k16,
+                                                                                 smem, acc);
   const float sab = scale_a[0] * scale_b[0];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -86,7 +91,7 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc.v[i][j][e] *= sab;
-  gemm_core::store_bf16_256(acc, c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256, n);
+  gemm_pipe::store_bf16(acc, c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256, n);
 }
 
 unsigned grid_for(uint64_t n) {
@@ -142,13 +147,13 @@ int32_t fe2o3_gemm_fp8_nt(const uint8_t* a, uint64_t a_len, const uint8_t* b, ui
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)gemm_fp8_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       gemm_core::kSmemBytes256);
+                                       kFp8Smem);
     if (e != hipSuccess) return (int32_t)e;
     attr_set = true;
   }
   const uint64_t tiles = (uint64_t)(m / 256) * (n / 256);
   if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
-  gemm_fp8_kernel<<<(unsigned)tiles, 256, gemm_core::kSmemBytes256, (hipStream_t)stream>>>(
+  gemm_fp8_kernel<<<(unsigned)tiles, 256, kFp8Smem, (hipStream_t)stream>>>(
       a, b, scale_a, scale_b, c, m, n, k);
   return fe2o3_host::after_launch();
 }

@@ -30,7 +30,7 @@
 // layer runs without a host round trip: the grouped GEMM grids are sized
 // for the worst case and workgroups beyond the last expert tile exit.
 #include "common.hpp"
-#include "gemm_core.hpp"
+#include "gemm_pipe.hpp"
 #include "internal.hpp"
 
 namespace {
@@ -192,35 +192,41 @@ FE2O3_DEVICE float silu_mul(float g, float u) {
   return sg * u;
 }
 
+constexpr int kRowBytes = 128, kStages = 2;  // 64 k per LDS stage, two stages
+constexpr int kSmem = kStages * 2 * gemm_pipe::Geo<kRowBytes>::kTileBytes;  // 128 KiB
+using Pipe = gemm_pipe::Geo<kRowBytes>;
+using Mma = gemm_pipe::MmaBf16<kRowBytes>;
+
 __global__ void __launch_bounds__(256, 1) gate_up_kernel(
     const uint16_t* __restrict__ xc, const uint16_t* __restrict__ wg,
     const uint16_t* __restrict__ wu, const uint32_t* __restrict__ offsets, uint32_t experts,
     uint32_t hidden, uint32_t ffn, uint16_t* __restrict__ hc) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   uint32_t e, row0, rows;
-  if (!expert_tile(offsets, experts, blockIdx.x, &e, &row0, &rows))
-    return;
+  if (!expert_tile(offsets, experts, blockIdx.x, &e, &row0, &rows)) return;
   const uint32_t f0 = blockIdx.y * 128u;
-  const gemm_core::TileRows ar = gemm_core::dense_rows(xc + (uint64_t)row0 * hidden, hidden, rows);
-  gemm_core::TileRows br;
+  const auto ar = gemm_pipe::dense_rows<kRowBytes>(xc + (uint64_t)row0 * hidden, hidden, rows);
+  // B tile row r: 32-row block jb = r/32 belongs to wave column wn = jb/4;
+  // within a wave column the blocks are gate f, up f, gate f+32, up f+32 for
+  // f = f0 + 64*wn, so each lane's gate and up accumulators of one (row, f)
+  // pair up in the epilogue.
+  gemm_pipe::Rows<kRowBytes> br;
   const uint64_t wbase = (uint64_t)e * ffn * hidden;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t row = gemm_core::tile_row(j);  // 32j .. 32j+31
-    const uint32_t wn = j >> 2, jj = j & 3;
-    const uint16_t* mat = (jj & 1) ? wu : wg;
-    const uint32_t f = f0 + wn * 64u + (jj >> 1) * 32u;
-    br.base[j] = mat + wbase + (uint64_t)f * hidden;
-    br.off[j] = (row & 31u) * hidden + gemm_core::tile_chunk(row) * 8u;
+  for (int j = 0; j < Pipe::kInstPerWave; ++j) {
+    const uint32_t row = Pipe::inst_row(j);
+    const uint32_t jb = row >> 5, wn = jb >> 2, jj = jb & 3u;
+    const uint32_t f = f0 + wn * 64u + (jj >> 1) * 32u + (row & 31u);
+    br.base[j] = ((jj & 1u) ? wu : wg) + wbase;
+    br.off[j] = f * hidden + Pipe::inst_chunk(row) * 8u;
   }
-  gemm_core::Acc256 acc;
-  gemm_core::zero(acc);
-  gemm_core::mainloop(ar, br, hidden, smem, acc);
-  // epilogue: (j=0 gate, j=1 up) and (j=2 gate, j=3 up) pair up per lane
+  gemm_pipe::Acc acc;
+  gemm_pipe::zero(acc);
+  gemm_pipe::mainloop<Mma, kRowBytes, kStages>(ar, br, hidden, smem, acc);
   const uint32_t lane = threadIdx.x & 63u, wn = (threadIdx.x >> 6) & 1u;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t r = gemm_core::acc_row(i);
+    const uint32_t r = gemm_pipe::acc_row(i);
     if (r >= rows) continue;
     uint16_t* out_row = hc + (uint64_t)(row0 + r) * ffn;
 #pragma unroll
@@ -247,18 +253,17 @@ __global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict
                                                       uint32_t ffn, float* __restrict__ yc) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   uint32_t e, row0, rows;
-  if (!expert_tile(offsets, experts, blockIdx.x, &e, &row0, &rows))
-    return;
+  if (!expert_tile(offsets, experts, blockIdx.x, &e, &row0, &rows)) return;
   const uint32_t n0 = blockIdx.y * 256u;
-  const gemm_core::TileRows ar = gemm_core::dense_rows(hc + (uint64_t)row0 * ffn, ffn, rows);
-  const gemm_core::TileRows br =
-      gemm_core::dense_rows(wd + (uint64_t)e * hidden * ffn + (uint64_t)n0 * ffn, ffn, 256);
-  gemm_core::Acc256 acc;
-  gemm_core::zero(acc);
-  gemm_core::mainloop(ar, br, ffn, smem, acc);
+  const auto ar = gemm_pipe::dense_rows<kRowBytes>(hc + (uint64_t)row0 * ffn, ffn, rows);
+  const auto br = gemm_pipe::dense_rows<kRowBytes>(
+      wd + (uint64_t)e * hidden * ffn + (uint64_t)n0 * ffn, ffn, 256);
+  gemm_pipe::Acc acc;
+  gemm_pipe::zero(acc);
+  gemm_pipe::mainloop<Mma, kRowBytes, kStages>(ar, br, ffn, smem, acc);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t r = gemm_core::acc_row(i);
+    const uint32_t r = gemm_pipe::acc_row(i);
     if (r >= rows) continue;
     float* out_row = yc + (uint64_t)(row0 + r) * hidden + n0;
 #pragma unroll
@@ -268,7 +273,7 @@ __global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict
         f32x4_t v;
 #pragma unroll
         for (int z = 0; z < 4; ++z) v[z] = acc.v[i][j][4 * q + z];
-        *reinterpret_cast<f32x4_t*>(out_row + gemm_core::acc_col(j, q)) = v;
+        *reinterpret_cast<f32x4_t*>(out_row + gemm_pipe::acc_col(j, q)) = v;
       }
   }
 }
@@ -427,7 +432,7 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_
   FE2O3_FAULT("fe2o3_moe_ffn_top2");
   (void)top2_experts;
   if (experts < 1 || experts > MAX_EXPERTS) return FE2O3_ERR_SHAPE;
-  if (hidden == 0 || ffn == 0 || hidden % 256 != 0 || ffn % 128 != 0) return FE2O3_ERR_SHAPE;
+  if (hidden == 0 || ffn == 0 || hidden % 256 != 0 || ffn % 128 != 0) return FE2O3_ERR_SHAPE;  // K steps of 32
   const uint64_t routes = 2ull * tokens;
   const uint64_t wsz = (uint64_t)experts * ffn * hidden;
   if (x_len != (uint64_t)tokens * hidden || w_gate_len != wsz || w_up_len != wsz ||
@@ -449,10 +454,10 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)gate_up_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       gemm_core::kSmemBytes256);
+                                       kSmem);
     if (e == hipSuccess)
       e = hipFuncSetAttribute((const void*)down_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              gemm_core::kSmemBytes256);
+                              kSmem);
     if (e != hipSuccess) return (int32_t)e;
     attr_set = true;
   }
@@ -460,9 +465,9 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_
   gather_kernel<<<(unsigned)routes, 256, 0, s>>>(x, permutation, expert_offsets, experts, hidden,
                                                 ws.xc);
   const unsigned m_tiles = (unsigned)((routes + 255u) / 256u + experts);
-  gate_up_kernel<<<dim3(m_tiles, ffn / 128u), 256, gemm_core::kSmemBytes256, s>>>(
+  gate_up_kernel<<<dim3(m_tiles, ffn / 128u), 256, kSmem, s>>>(
       ws.xc, w_gate, w_up, expert_offsets, experts, hidden, ffn, ws.hc);
-  down_kernel<<<dim3(m_tiles, hidden / 256u), 256, gemm_core::kSmemBytes256, s>>>(
+  down_kernel<<<dim3(m_tiles, hidden / 256u), 256, kSmem, s>>>(
       ws.hc, w_down, expert_offsets, experts, hidden, ffn, ws.yc);
   const uint64_t threads = (uint64_t)tokens * (hidden / 4u);
   combine_kernel<<<(unsigned)((threads + 255u) / 256u), 256, 0, s>>>(ws.yc, inverse, route_weights,
