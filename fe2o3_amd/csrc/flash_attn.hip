@@ -17,16 +17,16 @@
 //      each key block; the other 16 sit in lane l^32.  Row max and row sum are
 //      in-lane reductions plus one v_permlane32_swap.
 //    * Softmax in the exp2 domain: p = exp2(s*c - m) with c = scale*log2(e)
-//      folded into one FMA before v_exp_f32; m and l are fp32 running
-//      statistics; O is rescaled by exp2(m_old - m_new) per tile.
+//      folded into one FMA before v_exp_f32.  The reference m is raised (and
+//      O, l rescaled by exp2(m_old - m_new)) only when some row's tile max
+//      exceeds it by 2^8, so most tiles skip the 64 rescale multiplies per
+//      lane; p stays <= 256, exact enough in bf16 and fp32.
 //    * O^T += V^T P^T: P (bf16) is the second operand straight from the S
-//      registers; V^T comes from an LDS copy of the V tile stored transposed
-//      ([d][key]) with the keys of each 16-key group in MFMA k-order (bits 2
-//      and 3 of the key index swapped), so every operand read is one 16-byte
-//      LDS access.
-//    * K tiles go global -> LDS with 16-byte global_load_lds (chunks
-//      XOR-permuted by row & 15 against bank conflicts); V tiles go through
-//      registers for the transpose.
+//      registers; the V^T operand is read from the row-major V tile with
+//      ds_read_b64_tr_b16 (the gfx950 transposing LDS read), two reads per
+//      MFMA, so V needs no register transpose.
+//    * K and V tiles go global -> LDS with 16-byte global_load_lds, chunks
+//      XOR-permuted per row against bank conflicts.
 //    * Causal: query tiles are issued heaviest first; a wave skips the
 //      MFMAs of key tiles that lie entirely above its rows and masks the
 //      diagonal tile.
@@ -83,55 +83,52 @@ __global__ void __launch_bounds__(64) flash_profile_kernel(const float* __restri
 constexpr int D = 128;         // head dim
 constexpr int BQ = 128;        // query rows per workgroup
 constexpr int BKV = 64;        // keys per tile
-constexpr int K_TILE_BYTES = BKV * D * 2;   // 16 KiB, rows of 256 B
-constexpr int V_TILE_BYTES = D * BKV * 2;   // 16 KiB, rows (d) of 128 B
-constexpr int STAGE_BYTES = K_TILE_BYTES + V_TILE_BYTES;
-constexpr int SMEM_BYTES = 2 * STAGE_BYTES; // 64 KiB
+constexpr int TILE_BYTES = BKV * D * 2;     // 16 KiB: 64 rows of 256 B
+constexpr int STAGE_BYTES = 2 * TILE_BYTES; // K tile then V tile
+constexpr int SMEM_BYTES = 2 * STAGE_BYTES; // 64 KiB: two stages
+constexpr float RESCALE_SLACK = 8.0f;       // log2 units: p may reach 2^8 before a rescale
 
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
+
+// Both tiles are [64 keys][128 d] bf16 rows of 256 B holding 16 chunks of
+// 16 B.  K chunk c of row r sits at c ^ (r & 15): the S^T operand reads (32
+// consecutive rows, one chunk) are conflict-free.  V chunk c of row r sits at
+// c ^ 2*(r & 3): the transposing reads below touch 4 consecutive rows x 32
+// bytes per 16 lanes, which this spreads over 8 distinct chunks.
 FE2O3_DEVICE uint32_t swz_k(uint32_t r) { return r & 15u; }
-FE2O3_DEVICE uint32_t swz_v(uint32_t d) { return (d ^ (d >> 3)) & 7u; }
-// key (0..63) -> position in the transposed V row: swap bits 2 and 3.
-FE2O3_DEVICE uint32_t vpos(uint32_t key) {
-  return (key & ~12u) | ((key & 4u) << 1) | ((key & 8u) >> 1);
-}
+FE2O3_DEVICE uint32_t swz_v(uint32_t r) { return (r & 3u) << 1; }
 
-// K tile: 16 instructions of 1 KiB (4 rows of 256 B); wave w issues 4.
-FE2O3_DEVICE void issue_k(const uint16_t* k_tile, uint8_t* lds) {
+// One tile: 16 instructions of 1 KiB (4 rows of 256 B); wave w issues 4.
+template <bool IS_V>
+FE2O3_DEVICE void issue_tile(const uint16_t* tile, uint8_t* lds) {
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t inst = 4u * j + w;
     const uint32_t row = inst * 4u + (lane >> 4);
-    const uint32_t chunk = (lane & 15u) ^ swz_k(row);
-    g2l_b128(k_tile + row * D + chunk * 8u, lds + inst * 1024u);
+    const uint32_t chunk = (lane & 15u) ^ (IS_V ? swz_v(row) : swz_k(row));
+    g2l_b128(tile + row * D + chunk * 8u, lds + inst * 1024u);
   }
 }
 
-// V tile: thread t loads 4 x 16 B: rows key = (t/16) + 16*i, d chunk t%16.
-FE2O3_DEVICE void load_v(const uint16_t* v_tile, u32x4_t regs[4]) {
-  const uint32_t t = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t key = (t >> 4) + 16u * i, dc = t & 15u;
-    regs[i] = *reinterpret_cast<const u32x4_t*>(v_tile + key * D + dc * 8u);
-  }
-}
-
-FE2O3_DEVICE void store_vt(const u32x4_t regs[4], uint8_t* lds_v) {
-  const uint32_t t = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t key = (t >> 4) + 16u * i, dc = t & 15u;
-    const uint32_t pos = vpos(key);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t d = dc * 8u + e;
-      const uint32_t word = regs[i][e >> 1];
-      const uint16_t val = (uint16_t)((e & 1) ? (word >> 16) : (word & 0xffffu));
-      const uint32_t off = d * 128u + (((pos >> 3) ^ swz_v(d)) << 4) + (pos & 7u) * 2u;
-      *reinterpret_cast<uint16_t*>(lds_v + off) = val;
-    }
-  }
+// V^T operand of one O^T MFMA (d rows 32*db.., keys of half h of 32-key block
+// kb) with ds_read_b64_tr_b16.  Within each 16-lane group the instruction
+// hands lane i the element M[4e + i/4][i%4] (e = 0..3) of the 16 x 4 block
+// whose row r is the 4 bf16 at lane r's address.  Lane i = l%16 of group
+// G = l/16 addresses V[kb0 + i/4][dg + 4*(i%4)] with dg = 32*db + 16*(G&1),
+// so it receives V[kb0 + e][dg + i]: one d per lane (l%32 over the half
+// wave) and 4 consecutive keys kb0 = 32kb + 16h + 4(G>>1) (+8 for the second
+// read) -- the keys the S^T registers hold for MFMA k-slots 8(l/32) + 0..7.
+FE2O3_DEVICE bf16x8_t read_vt(const uint8_t* vt, uint32_t db, uint32_t kb, uint32_t h) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t G = lane >> 4, i = lane & 15u;
+  const uint32_t d = db * 32u + 16u * (G & 1u) + 4u * (i & 3u);
+  const uint32_t key = kb * 32u + 16u * h + 4u * (G >> 1) + (i >> 2);
+  const uint32_t off0 = key * 256u + (((d >> 3) ^ swz_v(key)) << 4) + (d & 7u) * 2u;
+  const uint32_t off1 = (key + 8u) * 256u + (((d >> 3) ^ swz_v(key + 8u)) << 4) + (d & 7u) * 2u;
+  const bf16x4_t r0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(vt + off0));
+  const bf16x4_t r1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)(vt + off1));
+  return __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
 template <bool CAUSAL>
@@ -162,24 +159,21 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
-  float m_run = -INFINITY;  // running max of s*c (log2 domain)
-  float l_run = 0.0f;       // this lane's partial row sum
+  float m_ref = -INFINITY;  // exp reference, log2 domain (>= running max - slack)
+  float l_run = 0.0f;       // this lane's partial row sum of exp2(s*c - m_ref)
 
   const uint32_t n_kv = CAUSAL ? (qt + 1u) * (BQ / BKV) : seq / BKV;
-  u32x4_t vregs[4];
-  issue_k(kh, smem);
-  load_v(vh, vregs);
-  store_vt(vregs, smem + K_TILE_BYTES);
+  issue_tile<false>(kh, smem);
+  issue_tile<true>(vh, smem + TILE_BYTES);
   wait_vmcnt0();
-  __syncthreads();
+  lds_barrier();
 
   for (uint32_t j = 0; j < n_kv; ++j) {
-    uint8_t* cur = smem + (j & 1u) * STAGE_BYTES;
+    const uint8_t* cur = smem + (j & 1u) * STAGE_BYTES;
     uint8_t* nxt = smem + ((j + 1u) & 1u) * STAGE_BYTES;
-    const bool more = j + 1u < n_kv;
-    if (more) {
-      issue_k(kh + (uint64_t)(j + 1u) * BKV * D, nxt);
-      load_v(vh + (uint64_t)(j + 1u) * BKV * D, vregs);
+    if (j + 1u < n_kv) {
+      issue_tile<false>(kh + (uint64_t)(j + 1u) * BKV * D, nxt);
+      issue_tile<true>(vh + (uint64_t)(j + 1u) * BKV * D, nxt + TILE_BYTES);
     }
     const uint32_t key0 = j * BKV;
     // keys key0..key0+63 vs. rows q_row0..q_row0+31
@@ -189,15 +183,14 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
       f32x16_t s[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s[kb][e] = 0.0f;
         const uint32_t krow = kb * 32u + lr;
 #pragma unroll
         for (int ds = 0; ds < 8; ++ds) {
           const uint32_t c = 2u * ds + g;
           const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(
               cur + krow * 256u + ((c ^ swz_k(krow)) << 4));
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ds], s[kb], 0, 0, 0);
+          s[kb] = ds == 0 ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[0], f32x16_t{}, 0, 0, 0)
+                          : __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ds], s[kb], 0, 0, 0);
         }
       }
       // mask the diagonal tile
@@ -215,10 +208,18 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[kb][e]);
-      mloc = fmaxf(mloc, swap_half(mloc));
-      const float m_new = fmaxf(m_run, mloc * scale_log2);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
+      mloc = fmaxf(mloc, swap_half(mloc)) * scale_log2;
+      // rescale only when some row's tile max exceeds its reference by the slack
+      if (__any(mloc > m_ref + RESCALE_SLACK)) {
+        const float m_new = fmaxf(m_ref, mloc);
+        const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
+        m_ref = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[db][e] *= alpha;
+      }
       bf16x8_t pf[2][2];
       float psum = 0.0f;
 #pragma unroll
@@ -228,36 +229,26 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
           float pv[8];
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj) {
-            pv[jj] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][h * 8 + jj], scale_log2, -m_new));
+            pv[jj] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][h * 8 + jj], scale_log2, -m_ref));
             psum += pv[jj];
           }
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj) pf[kb][h][jj] = (__bf16)pv[jj];
         }
-      l_run = l_run * alpha + psum;
+      l_run += psum;
+      // O^T += V^T P^T
+      const uint8_t* vt = cur + TILE_BYTES;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[db][e] *= alpha;
-      // O^T += V^T P^T
-      const uint8_t* vt = cur + K_TILE_BYTES;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const uint32_t d = db * 32u + lr;
-#pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const uint32_t c = (kb * 2u + h) * 2u + g;
-            const bf16x8_t vf = *reinterpret_cast<const bf16x8_t*>(
-                vt + d * 128u + ((c ^ swz_v(d)) << 4));
-            acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kb][h], acc[db], 0, 0, 0);
-          }
-      }
+          for (int h = 0; h < 2; ++h)
+            acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(read_vt(vt, db, kb, h), pf[kb][h],
+                                                              acc[db], 0, 0, 0);
     }
-    if (more) store_vt(vregs, nxt + K_TILE_BYTES);
     wait_vmcnt0();
-    __syncthreads();
+    lds_barrier();
   }
 
   // finalize: full row sum across the lane pair, normalize, store
@@ -275,8 +266,8 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
       *reinterpret_cast<u32x2_t*>(oh + d) = packed;
     }
   if (lse != nullptr && g == 0) {
-    // natural-log statistic: max(s)*scale + ln(sum) = (m_run + log2(sum)) * ln 2
-    lse[(uint64_t)blockIdx.y * seq + my_q] = (m_run + __log2f(l_tot)) * 0.69314718055994531f;
+    // natural-log statistic: max(s)*scale + ln(sum) = (m_ref + log2(sum)) * ln 2
+    lse[(uint64_t)blockIdx.y * seq + my_q] = (m_ref + __log2f(l_tot)) * 0.69314718055994531f;
   }
 }
 
