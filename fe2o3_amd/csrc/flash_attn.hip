@@ -135,13 +135,27 @@ template <bool CAUSAL>
 __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse,
-    uint32_t seq, float scale_log2) {
+    uint32_t seq, uint32_t heads, float scale_log2) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
   const uint32_t lr = lane & 31u, g = lane >> 5;
+  // Workgroup order.  Workgroup id i runs on XCD i % 8.  When heads % 8 == 0
+  // the ids are laid out so that XCD x walks heads x, x+8, x+16, ... and,
+  // for each, all of its query tiles back to back: the tiles of one head run
+  // together on one XCD and share their K/V through that XCD's L2.  Within a
+  // head the causal order is heaviest tile (most key tiles) first.
   const uint32_t nq = seq / BQ;
-  const uint32_t qt = CAUSAL ? (nq - 1u - blockIdx.x) : blockIdx.x;
-  const uint64_t head = (uint64_t)blockIdx.y * seq * D;
+  uint32_t bh, rank;
+  if (heads % 8u == 0u) {
+    const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
+    bh = (slot / nq) * 8u + xcd;
+    rank = slot % nq;
+  } else {
+    bh = blockIdx.x / nq;
+    rank = blockIdx.x % nq;
+  }
+  const uint32_t qt = CAUSAL ? (nq - 1u - rank) : rank;
+  const uint64_t head = (uint64_t)bh * seq * D;
   const uint16_t* qh = q + head;
   const uint16_t* kh = k + head;
   const uint16_t* vh = v + head;
@@ -267,7 +281,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
     }
   if (lse != nullptr && g == 0) {
     // natural-log statistic: max(s)*scale + ln(sum) = (m_ref + log2(sum)) * ln 2
-    lse[(uint64_t)blockIdx.y * seq + my_q] = (m_ref + __log2f(l_tot)) * 0.69314718055994531f;
+    lse[(uint64_t)bh * seq + my_q] = (m_ref + __log2f(l_tot)) * 0.69314718055994531f;
   }
 }
 
@@ -300,7 +314,7 @@ int32_t fe2o3_flash_attention_fwd(const uint16_t* q, uint64_t q_len, const uint1
   if (q_len != n || k_len != n || v_len != n || o_len != n) return FE2O3_ERR_LENGTH;
   if (lse != nullptr && lse_len != bh * seq) return FE2O3_ERR_LENGTH;
   if (n == 0) return FE2O3_OK;
-  if (seq % BQ != 0 || bh > 65535u) return FE2O3_ERR_SHAPE;
+  if (seq % BQ != 0 || bh > 0xffffffffu) return FE2O3_ERR_SHAPE;
   if (!q || !k || !v || !o) return FE2O3_ERR_NULL;
   if ((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) & 15u) != 0)
     return FE2O3_ERR_ALIGNMENT;
@@ -316,13 +330,16 @@ int32_t fe2o3_flash_attention_fwd(const uint16_t* q, uint64_t q_len, const uint1
     if (e != hipSuccess) return (int32_t)e;
     attr_set = true;
   }
-  const dim3 grid(seq / BQ, (unsigned)bh);
+  // one linear workgroup id per (query tile, batch*head); see the kernel
+  const uint64_t wgs = (uint64_t)(seq / BQ) * bh;
+  if (wgs > 0x7fffffffu) return FE2O3_ERR_SHAPE;
+  const dim3 grid((unsigned)wgs);
   if (causal)
-    flash_fwd_kernel<true><<<grid, 256, SMEM_BYTES, (hipStream_t)stream>>>(q, k, v, o, lse, seq,
-                                                                            scale_log2);
+    flash_fwd_kernel<true><<<grid, 256, SMEM_BYTES, (hipStream_t)stream>>>(
+        q, k, v, o, lse, seq, (uint32_t)bh, scale_log2);
   else
-    flash_fwd_kernel<false><<<grid, 256, SMEM_BYTES, (hipStream_t)stream>>>(q, k, v, o, lse, seq,
-                                                                             scale_log2);
+    flash_fwd_kernel<false><<<grid, 256, SMEM_BYTES, (hipStream_t)stream>>>(
+        q, k, v, o, lse, seq, (uint32_t)bh, scale_log2);
   return fe2o3_host::after_launch();
 }
 
