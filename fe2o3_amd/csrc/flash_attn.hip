@@ -25,7 +25,8 @@
 //      registers; the V^T operand is read from the row-major V tile with
 //      ds_read_b64_tr_b16 (the gfx950 transposing LDS read), two reads per
 //      MFMA, so V needs no register transpose.
-//    * K and V tiles go global -> LDS with 16-byte global_load_lds, chunks
+//    * K and V tiles go global -> LDS with 16-byte buffer loads to LDS (one
+//      fixed VGPR offset per thread, tile offsets scalar), chunks
 //      XOR-permuted per row against bank conflicts.
 //    * Causal: query tiles are issued heaviest first; a wave skips the
 //      MFMAs of key tiles that lie entirely above its rows and masks the
@@ -93,22 +94,40 @@ typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
 // Both tiles are [64 keys][128 d] bf16 rows of 256 B holding 16 chunks of
 // 16 B.  K chunk c of row r sits at c ^ (r & 15): the S^T operand reads (32
 // consecutive rows, one chunk) are conflict-free.  V chunk c of row r sits at
-// c ^ 2*(r & 3): the transposing reads below touch 4 consecutive rows x 32
-// bytes per 16 lanes, which this spreads over 8 distinct chunks.
+// c ^ f(r & 3), f(j) = 2j ^ 4j: the transposing reads below touch 4
+// consecutive rows x 2 chunks per 16 lanes and 4 rows x 4 chunks per 32
+// lanes; f puts them in 8 distinct chunks mod 8 and 16 distinct chunks mod
+// 16, so they are conflict-free whether the LDS serves 128 or 256 bytes of
+// a read per cycle.
 FE2O3_DEVICE uint32_t swz_k(uint32_t r) { return r & 15u; }
-FE2O3_DEVICE uint32_t swz_v(uint32_t r) { return (r & 3u) << 1; }
+FE2O3_DEVICE uint32_t swz_v(uint32_t r) { return ((r & 3u) << 1) ^ ((r & 3u) << 2); }
 
-// One tile: 16 instructions of 1 KiB (4 rows of 256 B); wave w issues 4.
+// K and V of one head are read through buffer resources (base = the head,
+// range = its seq * 256 bytes).  One tile is 16 loads of 1 KiB (4 rows of
+// 256 B), wave w issuing loads j = 0..3 of rows 16j + 4w .. +3.  The chunk
+// swizzles depend on the row mod 16 only, so a thread's byte offset within
+// the tile is the same for every j up to the 4 KiB row-group step: one fixed
+// VGPR offset per thread, the rest is scalar (tile offset + 4096 j).
+FE2O3_DEVICE __amdgpu_buffer_rsrc_t head_rsrc(const uint16_t* base, uint32_t bytes) {
+  // word 3 = 0x00020000: 32-bit data format, the raw-buffer setting for CDNA
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, (int)bytes,
+                                           0x00020000);
+}
+
 template <bool IS_V>
-FE2O3_DEVICE void issue_tile(const uint16_t* tile, uint8_t* lds) {
+FE2O3_DEVICE uint32_t tile_voffset() {
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  const uint32_t row = 4u * w + (lane >> 4);
+  const uint32_t chunk = (lane & 15u) ^ (IS_V ? swz_v(row) : swz_k(row));
+  return row * 256u + chunk * 16u;
+}
+
+FE2O3_DEVICE void issue_tile(__amdgpu_buffer_rsrc_t src, uint32_t voff, uint32_t tile_byte,
+                             uint8_t* lds, uint32_t wave) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t inst = 4u * j + w;
-    const uint32_t row = inst * 4u + (lane >> 4);
-    const uint32_t chunk = (lane & 15u) ^ (IS_V ? swz_v(row) : swz_k(row));
-    g2l_b128(tile + row * D + chunk * 8u, lds + inst * 1024u);
-  }
+  for (int j = 0; j < 4; ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (lds_void_t*)(lds + (4u * j + wave) * 1024u),
+                                             16, voff, tile_byte + 4096u * j, 0, 0);
 }
 
 // V^T operand of one O^T MFMA (d rows 32*db.., keys of half h of 32-key block
@@ -177,8 +196,12 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
   float l_run = 0.0f;       // this lane's partial row sum of exp2(s*c - m_ref)
 
   const uint32_t n_kv = CAUSAL ? (qt + 1u) * (BQ / BKV) : seq / BKV;
-  issue_tile<false>(kh, smem);
-  issue_tile<true>(vh, smem + TILE_BYTES);
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(w);  // wave-uniform
+  const __amdgpu_buffer_rsrc_t ksrc = head_rsrc(kh, seq * (uint32_t)(D * 2));
+  const __amdgpu_buffer_rsrc_t vsrc = head_rsrc(vh, seq * (uint32_t)(D * 2));
+  const uint32_t k_off = tile_voffset<false>(), v_off = tile_voffset<true>();
+  issue_tile(ksrc, k_off, 0u, smem, wave);
+  issue_tile(vsrc, v_off, 0u, smem + TILE_BYTES, wave);
   wait_vmcnt0();
   lds_barrier();
 
@@ -186,8 +209,8 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
     const uint8_t* cur = smem + (j & 1u) * STAGE_BYTES;
     uint8_t* nxt = smem + ((j + 1u) & 1u) * STAGE_BYTES;
     if (j + 1u < n_kv) {
-      issue_tile<false>(kh + (uint64_t)(j + 1u) * BKV * D, nxt);
-      issue_tile<true>(vh + (uint64_t)(j + 1u) * BKV * D, nxt + TILE_BYTES);
+      issue_tile(ksrc, k_off, (j + 1u) * TILE_BYTES, nxt, wave);
+      issue_tile(vsrc, v_off, (j + 1u) * TILE_BYTES, nxt + TILE_BYTES, wave);
     }
     const uint32_t key0 = j * BKV;
     // keys key0..key0+63 vs. rows q_row0..q_row0+31
@@ -195,6 +218,10 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
     if (active) {
       // S^T = K Q^T : two 32-key blocks
       f32x16_t s[2];
+      // Each SIMD runs one wave of each of two workgroups.  A wave raises its
+      // issue priority while it issues MFMAs, so the matrix core is fed
+      // first and the other wave's softmax VALU work fills the gaps.
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const uint32_t krow = kb * 32u + lr;
@@ -207,6 +234,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
                           : __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ds], s[kb], 0, 0, 0);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
       // mask the diagonal tile
       if (CAUSAL && key0 + 63u > q_row0) {
 #pragma unroll
@@ -252,6 +280,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
       l_run += psum;
       // O^T += V^T P^T
       const uint8_t* vt = cur + TILE_BYTES;
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -260,6 +289,7 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
           for (int h = 0; h < 2; ++h)
             acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(read_vt(vt, db, kb, h), pf[kb][h],
                                                               acc[db], 0, 0, 0);
+      __builtin_amdgcn_s_setprio(0);
     }
     wait_vmcnt0();
     lds_barrier();
@@ -315,6 +345,8 @@ int32_t fe2o3_flash_attention_fwd(const uint16_t* q, uint64_t q_len, const uint1
   if (lse != nullptr && lse_len != bh * seq) return FE2O3_ERR_LENGTH;
   if (n == 0) return FE2O3_OK;
   if (seq % BQ != 0 || bh > 0xffffffffu) return FE2O3_ERR_SHAPE;
+  // K/V of one head are addressed through a 32-bit buffer range
+  if ((uint64_t)seq * D * 2 > 0x7fffffffu) return FE2O3_ERR_SHAPE;
   if (!q || !k || !v || !o) return FE2O3_ERR_NULL;
   if ((((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) & 15u) != 0)
     return FE2O3_ERR_ALIGNMENT;

@@ -64,6 +64,13 @@ def test_length_and_shape_validation_without_gpu():
     assert L.fe2o3_row_softmax(None, 0, None, 0, None, 0, 4, 0, None) == -3
     assert L.fe2o3_flash_attention_fwd(None, 0, None, 0, None, 0, None, 0, None, 0, 1, 1, 128, 64,
                                        0, 0.1, None) == -3
+    # one head's K/V must fit the kernel's 32-bit buffer range (seq * 256 B < 2^31)
+    big = (1 << 23) * 128
+    assert L.fe2o3_flash_attention_fwd(None, big, None, big, None, big, None, big, None, 0, 1, 1,
+                                       1 << 23, 128, 0, 0.1, None) == -3
+    ok = ((1 << 23) - 128) * 128  # largest seq that fits passes the shape checks
+    assert L.fe2o3_flash_attention_fwd(None, ok, None, ok, None, ok, None, ok, None, 0, 1, 1,
+                                       (1 << 23) - 128, 128, 0, 0.1, None) == -19
     assert L.fe2o3_moe_top2_route(None, 0, 0, None, 0, None, 0, None, 0, None, 0, None, 0, None,
                                   0, None, 0, None, 0, 0, 1, 0, None) == -3
     assert L.fe2o3_gemm_fp8_nt(None, 256 * 100, None, 256 * 100, None, None, None, 256 * 256,
