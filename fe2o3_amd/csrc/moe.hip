@@ -169,20 +169,36 @@ __global__ void __launch_bounds__(256) gather_kernel(const uint16_t* __restrict_
   for (uint32_t i = threadIdx.x; i < hidden / 8; i += blockDim.x) dst[i] = src[i];
 }
 
-// Finds the (expert, m-tile) of workgroup `x` over experts' 256-row tiles.
-FE2O3_DEVICE bool expert_tile(const uint32_t* offsets, uint32_t experts, uint32_t x, uint32_t* e_out,
-                              uint32_t* row0, uint32_t* rows) {
+// Work order of the expert GEMMs.  The tiles form one list: expert-major,
+// then n-block, then the expert's 256-row m-tiles, so consecutive entries
+// share a weight block and runs of entries share the expert's rows.
+// Workgroup id i runs on XCD i % 8; XCD x takes the x-th contiguous eighth of
+// the list in order, so the workgroups that share a weight block run at the
+// same time behind one L2.  The grid is sized for the most m-tiles routing can
+// produce; entries past the list's end exit at once.
+FE2O3_DEVICE bool expert_tile(const uint32_t* offsets, uint32_t experts, uint32_t n_blocks,
+                              uint32_t* e_out, uint32_t* row0, uint32_t* rows, uint32_t* nb) {
+  uint32_t total = 0;
+  for (uint32_t e = 0; e < experts; ++e)
+    total += (offsets[e + 1] - offsets[e] + 255u) / 256u * n_blocks;
+  const uint32_t chunk = (total + 7u) / 8u;
+  const uint32_t slot = blockIdx.x >> 3;
+  if (slot >= chunk) return false;
+  uint32_t x = (blockIdx.x & 7u) * chunk + slot;
+  if (x >= total) return false;
   for (uint32_t e = 0; e < experts; ++e) {
     const uint32_t lo = offsets[e], n = offsets[e + 1] - lo;
-    const uint32_t tiles = (n + 255u) / 256u;
-    if (x < tiles) {
+    const uint32_t m_tiles = (n + 255u) / 256u;
+    if (x < m_tiles * n_blocks) {
+      const uint32_t mt = x % m_tiles;
       *e_out = e;
-      *row0 = lo + x * 256u;
-      const uint32_t left = n - x * 256u;
+      *nb = x / m_tiles;
+      *row0 = lo + mt * 256u;
+      const uint32_t left = n - mt * 256u;
       *rows = left < 256u ? left : 256u;
       return true;
     }
-    x -= tiles;
+    x -= m_tiles * n_blocks;
   }
   return false;
 }
@@ -202,9 +218,9 @@ __global__ void __launch_bounds__(256, 1) gate_up_kernel(
     const uint16_t* __restrict__ wu, const uint32_t* __restrict__ offsets, uint32_t experts,
     uint32_t hidden, uint32_t ffn, uint16_t* __restrict__ hc) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  uint32_t e, row0, rows;
-  if (!expert_tile(offsets, experts, blockIdx.x, &e, &row0, &rows)) return;
-  const uint32_t f0 = blockIdx.y * 128u;
+  uint32_t e, row0, rows, nb;
+  if (!expert_tile(offsets, experts, ffn / 128u, &e, &row0, &rows, &nb)) return;
+  const uint32_t f0 = nb * 128u;
   const auto ar = gemm_pipe::dense_rows<kRowBytes>(xc + (uint64_t)row0 * hidden, hidden, rows);
   // B tile row r: 32-row block jb = r/32 belongs to wave column wn = jb/4;
   // within a wave column the blocks are gate f, up f, gate f+32, up f+32 for
@@ -250,22 +266,29 @@ __global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict
                                                       const uint16_t* __restrict__ wd,
                                                       const uint32_t* __restrict__ offsets,
                                                       uint32_t experts, uint32_t hidden,
-                                                      uint32_t ffn, float* __restrict__ yc) {
+                                                      uint32_t ffn, uint64_t routes,
+                                                      float* __restrict__ yc) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  uint32_t e, row0, rows;
-  if (!expert_tile(offsets, experts, blockIdx.x, &e, &row0, &rows)) return;
-  const uint32_t n0 = blockIdx.y * 256u;
-  const auto ar = gemm_pipe::dense_rows<kRowBytes>(hc + (uint64_t)row0 * ffn, ffn, rows);
+  // Split K in two: list entry nb = 2 * n-block + k-half.  Each half writes
+  // its own fp32 partial (yc, then yc + routes * hidden); the combine adds
+  // them.  Twice as many workgroups, each half as long, fill the last wave of
+  // the grid better at this kernel's few hundred tiles.
+  uint32_t e, row0, rows, nb;
+  if (!expert_tile(offsets, experts, 2u * (hidden / 256u), &e, &row0, &rows, &nb)) return;
+  const uint32_t n0 = (nb >> 1) * 256u, kh = nb & 1u, k_half = ffn / 2u;
+  const auto ar = gemm_pipe::dense_rows<kRowBytes>(hc + (uint64_t)row0 * ffn + kh * k_half, ffn,
+                                                   rows);
   const auto br = gemm_pipe::dense_rows<kRowBytes>(
-      wd + (uint64_t)e * hidden * ffn + (uint64_t)n0 * ffn, ffn, 256);
+      wd + (uint64_t)e * hidden * ffn + (uint64_t)n0 * ffn + kh * k_half, ffn, 256);
   gemm_pipe::Acc acc;
   gemm_pipe::zero(acc);
-  gemm_pipe::mainloop<Mma, kRowBytes, kStages>(ar, br, ffn, smem, acc);
+  gemm_pipe::mainloop<Mma, kRowBytes, kStages>(ar, br, k_half, smem, acc);
+  float* part = yc + (uint64_t)kh * routes * hidden;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t r = gemm_pipe::acc_row(i);
     if (r >= rows) continue;
-    float* out_row = yc + (uint64_t)(row0 + r) * hidden + n0;
+    float* out_row = part + (uint64_t)(row0 + r) * hidden + n0;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -282,7 +305,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
                                                       const uint32_t* __restrict__ inverse,
                                                       const float* __restrict__ weights,
                                                       uint32_t tokens, uint32_t hidden,
-                                                      uint16_t* __restrict__ out) {
+                                                      uint64_t routes, uint16_t* __restrict__ out) {
 #pragma clang fp contract(off)
   const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 4 outputs each
   const uint64_t per_token = hidden / 4u;
@@ -295,10 +318,13 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
     const uint32_t slot = inverse[route];
     if (slot == DROP) continue;
     const float w = weights[route];
-    const f32x4_t y = *reinterpret_cast<const f32x4_t*>(yc + (uint64_t)slot * hidden + h);
+    const f32x4_t y0 = *reinterpret_cast<const f32x4_t*>(yc + (uint64_t)slot * hidden + h);
+    const f32x4_t y1 = *reinterpret_cast<const f32x4_t*>(yc + routes * hidden +
+                                                         (uint64_t)slot * hidden + h);
 #pragma unroll
     for (int z = 0; z < 4; ++z) {
-      const float wv = w * y[z];
+      const float y = y0[z] + y1[z];  // the two k-halves of the down projection
+      const float wv = w * y;
       acc[z] = acc[z] + wv;
     }
   }
@@ -322,7 +348,7 @@ Workspace carve(void* base, uint32_t tokens, uint32_t hidden, uint32_t ffn) {
   Workspace w;
   uint8_t* p = (uint8_t*)base;
   const uint64_t xb = align256(routes * hidden * 2), hb = align256(routes * ffn * 2),
-                 yb = align256(routes * hidden * 4);
+                 yb = align256(2 * routes * hidden * 4);  // two k-half partials
   w.xc = (uint16_t*)p;
   w.hc = (uint16_t*)(p + xb);
   w.yc = (float*)(p + xb + hb);
@@ -432,7 +458,9 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_
   FE2O3_FAULT("fe2o3_moe_ffn_top2");
   (void)top2_experts;
   if (experts < 1 || experts > MAX_EXPERTS) return FE2O3_ERR_SHAPE;
-  if (hidden == 0 || ffn == 0 || hidden % 256 != 0 || ffn % 128 != 0) return FE2O3_ERR_SHAPE;  // K steps of 32
+  // hidden: 256-column output blocks of the down GEMM; ffn: 128-wide gate/up
+  // blocks, and each k-half of the down GEMM a whole number of 64-k stages
+  if (hidden == 0 || ffn == 0 || hidden % 256 != 0 || ffn % 128 != 0) return FE2O3_ERR_SHAPE;
   const uint64_t routes = 2ull * tokens;
   const uint64_t wsz = (uint64_t)experts * ffn * hidden;
   if (x_len != (uint64_t)tokens * hidden || w_gate_len != wsz || w_up_len != wsz ||
@@ -464,14 +492,19 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_
   hipStream_t s = (hipStream_t)stream;
   gather_kernel<<<(unsigned)routes, 256, 0, s>>>(x, permutation, expert_offsets, experts, hidden,
                                                 ws.xc);
-  const unsigned m_tiles = (unsigned)((routes + 255u) / 256u + experts);
-  gate_up_kernel<<<dim3(m_tiles, ffn / 128u), 256, kSmem, s>>>(
-      ws.xc, w_gate, w_up, expert_offsets, experts, hidden, ffn, ws.hc);
-  down_kernel<<<dim3(m_tiles, hidden / 256u), 256, kSmem, s>>>(
-      ws.hc, w_down, expert_offsets, experts, hidden, ffn, ws.yc);
+  // the most m-tiles any routing yields: routes/256 rounded up, plus one
+  // partial tile per expert
+  const uint64_t m_tiles = (routes + 255u) / 256u + experts;
+  const uint64_t gu_wgs = (m_tiles * (ffn / 128u) + 7u) / 8u * 8u;
+  const uint64_t dn_wgs = (m_tiles * 2u * (hidden / 256u) + 7u) / 8u * 8u;
+  if (gu_wgs > 0x7fffffffu || dn_wgs > 0x7fffffffu) return FE2O3_ERR_SHAPE;
+  gate_up_kernel<<<(unsigned)gu_wgs, 256, kSmem, s>>>(ws.xc, w_gate, w_up, expert_offsets,
+                                                      experts, hidden, ffn, ws.hc);
+  down_kernel<<<(unsigned)dn_wgs, 256, kSmem, s>>>(ws.hc, w_down, expert_offsets, experts,
+                                                   hidden, ffn, routes, ws.yc);
   const uint64_t threads = (uint64_t)tokens * (hidden / 4u);
   combine_kernel<<<(unsigned)((threads + 255u) / 256u), 256, 0, s>>>(ws.yc, inverse, route_weights,
-                                                                    tokens, hidden, out);
+                                                                    tokens, hidden, routes, out);
   return fe2o3_host::after_launch();
 }
 
