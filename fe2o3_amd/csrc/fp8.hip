@@ -34,9 +34,17 @@ __global__ void __launch_bounds__(256) amax_kernel(const float* __restrict__ x, 
   }
   for (uint64_t i = n4 * 4 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
     m = fmaxf(m, fabsf(x[i]));
+  // One device-scope atomic per workgroup: atomics on one address from every
+  // wave serialize and cost more than the read of the tensor.
+  __shared__ float wave_m[4];
   m = wave_max(m);
-  // |x| >= 0, so the IEEE bit patterns order like unsigned integers
-  if ((threadIdx.x & 63u) == 0) atomicMax(reinterpret_cast<unsigned int*>(amax), __float_as_uint(m));
+  if ((threadIdx.x & 63u) == 0) wave_m[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    m = fmaxf(fmaxf(wave_m[0], wave_m[1]), fmaxf(wave_m[2], wave_m[3]));
+    // |x| >= 0, so the IEEE bit patterns order like unsigned integers
+    atomicMax(reinterpret_cast<unsigned int*>(amax), __float_as_uint(m));
+  }
 }
 
 __global__ void scale_kernel(const float* amax, float* scale) {
@@ -110,7 +118,8 @@ int32_t fe2o3_amax_f32(const float* x, uint64_t x_len, float* amax, void* stream
   if (((uintptr_t)x & 15u) != 0) return FE2O3_ERR_ALIGNMENT;
   hipStream_t s = (hipStream_t)stream;
   zero_f32_kernel<<<1, 1, 0, s>>>(amax);
-  if (x_len) amax_kernel<<<grid_for(x_len), 256, 0, s>>>(x, x_len, amax);
+  // at most 1024 workgroups (4 per CU), each striding over the tensor
+  if (x_len) amax_kernel<<<std::min(grid_for(x_len), 1024u), 256, 0, s>>>(x, x_len, amax);
   return fe2o3_host::after_launch();
 }
 
