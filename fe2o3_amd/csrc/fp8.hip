@@ -86,8 +86,8 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
   const uint32_t k16 = k / 2;  // rows addressed in 16-bit units
   const uint16_t* a16 = reinterpret_cast<const uint16_t*>(a + (uint64_t)tm * 256 * k);
   const uint16_t* b16 = reinterpret_cast<const uint16_t*>(b + (uint64_t)tn * 256 * k);
-  const auto ar = gemm_pipe::dense_rows<kFp8RowBytes>(a16, k16, 256);
-  const auto br = gemm_pipe::dense_rows<kFp8RowBytes>(b16, k16, 256);
+  const auto ar = gemm_pipe::dense_rows<kFp8RowBytes>(a16, k16, 256, k16);
+  const auto br = gemm_pipe::dense_rows<kFp8RowBytes>(b16, k16, 256, k16);
   gemm_pipe::Acc acc;
   gemm_pipe::zero(acc);
   gemm_pipe::mainloop<gemm_pipe::MmaFp8<kFp8RowBytes>, kFp8RowBytes, kFp8Stages>(ar, br, k16,
@@ -149,7 +149,8 @@ int32_t fe2o3_gemm_fp8_nt(const uint8_t* a, uint64_t a_len, const uint8_t* b, ui
     return FE2O3_ERR_LENGTH;
   if (c_len == 0) return FE2O3_OK;
   if (m % 256 != 0 || n % 256 != 0 || k % 128 != 0 || k == 0) return FE2O3_ERR_SHAPE;
-  if (128ull * k >= (1ull << 32)) return FE2O3_ERR_SHAPE;
+  // a 256-row fp8 panel (256 * k bytes) within its buffer resource's 32-bit range
+  if (256ull * k >= (1ull << 31)) return FE2O3_ERR_SHAPE;
   if (!a || !b || !c || !scale_a || !scale_b) return FE2O3_ERR_NULL;
   if ((((uintptr_t)a | (uintptr_t)b | (uintptr_t)c) & 15u) != 0) return FE2O3_ERR_ALIGNMENT;
   static bool attr_set = false;

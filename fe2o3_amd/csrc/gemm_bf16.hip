@@ -2,9 +2,9 @@
 // A[m,k] (row-major) * B^T with B stored [n,k] (k contiguous, i.e. the
 // BASELINE's column-major B), fp32 accumulation, RNE bf16 output.
 //
-// Fast path (m, n multiples of 256, k multiple of 64, 16-byte aligned): the
-// 256x256 pipelined MFMA tile of gemm_pipe.hpp with 64 k per LDS stage and
-// two stages, workgroups ordered XCD-aware (gemm_core.hpp).
+// Fast path (m, n multiples of 256, k a multiple of 64 below 2^22, 16-byte
+// aligned): the 256x256 pipelined MFMA tile of gemm_pipe.hpp with 64 k per
+// LDS stage and two stages, workgroups ordered XCD-aware (gemm_core.hpp).
 // Any other shape uses a bounds-checked 64x64-tile MFMA kernel.
 #include "common.hpp"
 #include "gemm_core.hpp"
@@ -83,8 +83,8 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_nt_256_kernel(const uint16_t
   const uint32_t tiles_m = m / 256, tiles_n = n / 256;
   uint32_t tm, tn;
   gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
-  const auto ar = gemm_pipe::dense_rows<kRowBytes>(a + (uint64_t)tm * 256 * k, k, 256);
-  const auto br = gemm_pipe::dense_rows<kRowBytes>(b + (uint64_t)tn * 256 * k, k, 256);
+  const auto ar = gemm_pipe::dense_rows<kRowBytes>(a + (uint64_t)tm * 256 * k, k, 256, k);
+  const auto br = gemm_pipe::dense_rows<kRowBytes>(b + (uint64_t)tn * 256 * k, k, 256, k);
   gemm_pipe::Acc acc;
   gemm_pipe::zero(acc);
   gemm_pipe::mainloop<gemm_pipe::MmaBf16<kRowBytes>, kRowBytes, kStages>(ar, br, k, smem, acc);
@@ -104,8 +104,10 @@ extern "C" int32_t fe2o3_gemm_bf16_nt(const uint16_t* a, uint64_t a_len, const u
   if (c_len == 0) return FE2O3_OK;
   if ((a_len && !a) || (b_len && !b) || !c) return FE2O3_ERR_NULL;
   if (k == 0) return (int32_t)hipMemsetAsync(c, 0, c_len * 2, (hipStream_t)stream);
-  const bool fast = m % 256 == 0 && n % 256 == 0 && k % gemm_pipe::Geo<kRowBytes>::kK16 == 0 && aligned16(a) &&
-                    aligned16(b) && aligned16(c);
+  // fast path: whole tiles, whole stages, 16-byte rows, and a 256-row panel
+  // (512 * k bytes) inside the 32-bit range of its buffer resource
+  const bool fast = m % 256 == 0 && n % 256 == 0 && k % gemm_pipe::Geo<kRowBytes>::kK16 == 0 &&
+                    512ull * k < (1ull << 31) && aligned16(a) && aligned16(b) && aligned16(c);
   if (fast) {
     static bool attr_set = false;
     if (!attr_set) {

@@ -221,20 +221,25 @@ __global__ void __launch_bounds__(256, 1) gate_up_kernel(
   uint32_t e, row0, rows, nb;
   if (!expert_tile(offsets, experts, ffn / 128u, &e, &row0, &rows, &nb)) return;
   const uint32_t f0 = nb * 128u;
-  const auto ar = gemm_pipe::dense_rows<kRowBytes>(xc + (uint64_t)row0 * hidden, hidden, rows);
+  const auto ar = gemm_pipe::dense_rows<kRowBytes>(xc + (uint64_t)row0 * hidden, hidden, rows,
+                                                   hidden);
   // B tile row r: 32-row block jb = r/32 belongs to wave column wn = jb/4;
   // within a wave column the blocks are gate f, up f, gate f+32, up f+32 for
   // f = f0 + 64*wn, so each lane's gate and up accumulators of one (row, f)
   // pair up in the epilogue.
+  // (Load slot j moves rows 8(4j + w) .. +7, all in block jb = j, so the
+  // gate/up choice is per slot and wave-uniform.)  The buffers are the
+  // expert's gate and up matrices.
   gemm_pipe::Rows<kRowBytes> br;
   const uint64_t wbase = (uint64_t)e * ffn * hidden;
+  br.bytes = ffn * hidden * 2u;
 #pragma unroll
   for (int j = 0; j < Pipe::kInstPerWave; ++j) {
     const uint32_t row = Pipe::inst_row(j);
     const uint32_t jb = row >> 5, wn = jb >> 2, jj = jb & 3u;
     const uint32_t f = f0 + wn * 64u + (jj >> 1) * 32u + (row & 31u);
-    br.base[j] = ((jj & 1u) ? wu : wg) + wbase;
-    br.off[j] = f * hidden + Pipe::inst_chunk(row) * 8u;
+    br.base[j] = ((j & 1) ? wu : wg) + wbase;
+    br.voff[j] = (f * hidden + Pipe::inst_chunk(row) * 8u) * 2u;
   }
   gemm_pipe::Acc acc;
   gemm_pipe::zero(acc);
@@ -277,9 +282,9 @@ __global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict
   if (!expert_tile(offsets, experts, 2u * (hidden / 256u), &e, &row0, &rows, &nb)) return;
   const uint32_t n0 = (nb >> 1) * 256u, kh = nb & 1u, k_half = ffn / 2u;
   const auto ar = gemm_pipe::dense_rows<kRowBytes>(hc + (uint64_t)row0 * ffn + kh * k_half, ffn,
-                                                   rows);
+                                                   rows, k_half);
   const auto br = gemm_pipe::dense_rows<kRowBytes>(
-      wd + (uint64_t)e * hidden * ffn + (uint64_t)n0 * ffn + kh * k_half, ffn, 256);
+      wd + (uint64_t)e * hidden * ffn + (uint64_t)n0 * ffn + kh * k_half, ffn, 256, k_half);
   gemm_pipe::Acc acc;
   gemm_pipe::zero(acc);
   gemm_pipe::mainloop<Mma, kRowBytes, kStages>(ar, br, k_half, smem, acc);
@@ -468,7 +473,11 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_
       permutation_len != routes || inverse_len != routes || weights_len != routes ||
       out_len != (uint64_t)tokens * hidden)
     return FE2O3_ERR_LENGTH;
-  if (256ull * ffn >= (1ull << 32) || 256ull * hidden >= (1ull << 32)) return FE2O3_ERR_SHAPE;
+  // 256-row operand panels and one expert's gate/up matrix must fit the
+  // 32-bit range of a buffer resource
+  if (512ull * ffn >= (1ull << 31) || 512ull * hidden >= (1ull << 31) ||
+      2ull * ffn * hidden >= (1ull << 31))
+    return FE2O3_ERR_SHAPE;
   if (tokens == 0) return FE2O3_OK;
   const Workspace ws = carve(workspace, tokens, hidden, ffn);
   if (workspace_bytes < ws.bytes) return FE2O3_ERR_WORKSPACE;

@@ -243,8 +243,10 @@ def test_gemm_bf16_nt_generic_shapes(gpu, oracle, m, n, k):
     _nt_case(gpu, oracle, m, n, k, seed=3)
 
 
+# k = 64 is one K step (tail only); 192 and 320 are whole two-stage groups
+# plus a one-step tail
 @pytest.mark.parametrize("m,n,k", [(256, 256, 64), (256, 512, 256), (512, 768, 1024),
-                                   (1024, 256, 4096)])
+                                   (1024, 256, 4096), (256, 256, 320), (512, 256, 192)])
 def test_gemm_bf16_nt_fast_path(gpu, oracle, m, n, k):
     _nt_case(gpu, oracle, m, n, k, seed=1)
 

@@ -283,7 +283,8 @@ def _fp8_case(gpu, oracle, m, n, k, points):
     return rel_err(got[rows, cols], ref_f32)
 
 
-@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (512, 768, 1024), (256, 512, 4096)])
+@pytest.mark.parametrize("m,n,k", [(256, 256, 128), (512, 768, 1024), (256, 512, 4096),
+                                   (256, 256, 384)])
 def test_gemm_fp8_all_outputs(gpu, oracle, m, n, k):
     rr, cc = np.meshgrid(np.arange(m), np.arange(n), indexing="ij")
     assert _fp8_case(gpu, oracle, m, n, k, (rr.ravel(), cc.ravel())) <= 1e-2
