@@ -83,6 +83,9 @@ __global__ void __launch_bounds__(64) flash_profile_kernel(const float* __restri
 // ---- BASELINE-shape kernel -------------------------------------------------------------------
 constexpr int D = 128;         // head dim
 constexpr int BQ = 128;        // query rows per workgroup
+constexpr int WAVES = BQ / 32; // one wave per 32 query rows
+constexpr int THREADS = WAVES * 64;
+static_assert(16 % WAVES == 0 && (4 * WAVES) % 16 == 0, "tile copies split evenly over the waves");
 constexpr int BKV = 64;        // keys per tile
 constexpr int TILE_BYTES = BKV * D * 2;     // 16 KiB: 64 rows of 256 B
 constexpr int STAGE_BYTES = 2 * TILE_BYTES; // K tile then V tile
@@ -104,10 +107,11 @@ FE2O3_DEVICE uint32_t swz_v(uint32_t r) { return ((r & 3u) << 1) ^ ((r & 3u) << 
 
 // K and V of one head are read through buffer resources (base = the head,
 // range = its seq * 256 bytes).  One tile is 16 loads of 1 KiB (4 rows of
-// 256 B), wave w issuing loads j = 0..3 of rows 16j + 4w .. +3.  The chunk
-// swizzles depend on the row mod 16 only, so a thread's byte offset within
-// the tile is the same for every j up to the 4 KiB row-group step: one fixed
-// VGPR offset per thread, the rest is scalar (tile offset + 4096 j).
+// 256 B), wave w issuing loads j = 0 .. 16/WAVES - 1 of rows
+// 4 (WAVES j + w) .. +3.  The chunk swizzles depend on the row mod 16 only,
+// and 4 WAVES is a multiple of 16, so a thread's byte offset within the tile
+// is the same for every j up to the row-group step of 1024 WAVES bytes: one
+// fixed VGPR offset per thread, the rest is scalar.
 FE2O3_DEVICE __amdgpu_buffer_rsrc_t head_rsrc(const uint16_t* base, uint32_t bytes) {
   // word 3 = 0x00020000: 32-bit data format, the raw-buffer setting for CDNA
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, (int)bytes,
@@ -125,9 +129,10 @@ FE2O3_DEVICE uint32_t tile_voffset() {
 FE2O3_DEVICE void issue_tile(__amdgpu_buffer_rsrc_t src, uint32_t voff, uint32_t tile_byte,
                              uint8_t* lds, uint32_t wave) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (lds_void_t*)(lds + (4u * j + wave) * 1024u),
-                                             16, voff, tile_byte + 4096u * j, 0, 0);
+  for (int j = 0; j < 16 / WAVES; ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        src, (lds_void_t*)(lds + (WAVES * j + wave) * 1024u), 16, voff,
+        tile_byte + 1024u * WAVES * j, 0, 0);
 }
 
 // V^T operand of one O^T MFMA (d rows 32*db.., keys of half h of 32-key block
@@ -151,7 +156,7 @@ FE2O3_DEVICE bf16x8_t read_vt(const uint8_t* vt, uint32_t db, uint32_t kb, uint3
 }
 
 template <bool CAUSAL>
-__global__ void __launch_bounds__(256, 2) flash_fwd_kernel(
+__global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse,
     uint32_t seq, uint32_t heads, float scale_log2) {
@@ -367,10 +372,10 @@ int32_t fe2o3_flash_attention_fwd(const uint16_t* q, uint64_t q_len, const uint1
   if (wgs > 0x7fffffffu) return FE2O3_ERR_SHAPE;
   const dim3 grid((unsigned)wgs);
   if (causal)
-    flash_fwd_kernel<true><<<grid, 256, SMEM_BYTES, (hipStream_t)stream>>>(
+    flash_fwd_kernel<true><<<grid, THREADS, SMEM_BYTES, (hipStream_t)stream>>>(
         q, k, v, o, lse, seq, (uint32_t)bh, scale_log2);
   else
-    flash_fwd_kernel<false><<<grid, 256, SMEM_BYTES, (hipStream_t)stream>>>(
+    flash_fwd_kernel<false><<<grid, THREADS, SMEM_BYTES, (hipStream_t)stream>>>(
         q, k, v, o, lse, seq, (uint32_t)bh, scale_log2);
   return fe2o3_host::after_launch();
 }
