@@ -247,6 +247,48 @@ def sec_gemm_f32(ctx, stream, steps, warmup):
                          "frac": round(tf / PEAK["fp32"], 5)}}
 
 
+def sec_collectives(ctx, stream, steps, warmup):
+    """Wave64 collectives over 2^20 rows of 64 f32 with one mask per row:
+    4 bytes in and 12 bytes out per element plus 8 bytes per row (HBM-bound)."""
+    from fe2o3_amd import kernels
+    rows = 1 << 20
+    x = ctx.alloc(rows * 64, np.float32)
+    kernels.fill_normal_f32(x, 6, 0xC011, 1.0, stream=stream)
+    masks = ctx.to_device(np.random.default_rng(6).integers(0, 2**63, rows, dtype=np.uint64))
+    outs = [ctx.alloc(rows * 64, np.float32) for _ in range(3)]
+    ms = _timed(ctx, stream, lambda: kernels.wave64_collectives_rows(
+        x, masks, *outs, rows, stream=stream, sync=False), steps, warmup)
+    nbytes = rows * (64 * 16 + 8)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": "wave64 masked reduce + inclusive/exclusive scan, 2^20 rows x 64 f32",
+            "kernel": "wave64_collectives_rows_kernel", "ms": ms, "value": round(gbs, 1),
+            "unit": "GB/s",
+            "roofline": {"bound": "hbm", "peak": PEAK["hbm_gbs"],
+                         "frac": round(gbs / PEAK["hbm_gbs"], 4)}}
+
+
+def sec_routing_check(ctx, stream, steps, warmup):
+    """Routing-output consistency check of config 5's router output (4096
+    tokens, 8 experts, unbounded capacity): one workgroup, latency-bound."""
+    from fe2o3_amd import kernels
+    t, e = 4096, 8
+    lg = ctx.alloc(t * e, np.uint16)
+    kernels.fill_normal_bf16(lg, 5, 0x10617, 1.0, stream=stream)
+    r = {"top2": ctx.alloc(2 * t, np.uint32), "requested": ctx.alloc(e, np.uint32),
+         "admitted": ctx.alloc(e, np.uint32), "offsets": ctx.alloc(e + 1, np.uint32),
+         "slots": ctx.alloc(2 * t, np.uint32), "permutation": ctx.alloc(2 * t, np.uint32),
+         "inverse": ctx.alloc(2 * t, np.uint32), "weights": ctx.alloc(2 * t, np.float32)}
+    kernels.moe_top2_route(lg, r, t, e, stream=stream)
+    rec = ctx.alloc(4, np.uint32)
+    ms = _timed(ctx, stream, lambda: kernels.moe_routing_check(
+        r, t, e, 0xFFFFFFFF, rec, stream=stream, sync=False), steps, warmup)
+    kind = int(rec.download()[0])
+    return {"workload": "MoE routing-output consistency check, 4096 tokens x 8 experts",
+            "kernel": "routing_check_kernel", "ms": ms, "value": round(ms * 1e3, 2),
+            "unit": "us", "record_kind": kind,
+            "roofline": {"bound": "latency (one workgroup)", "peak": None, "frac": None}}
+
+
 SECONDARY = {
     "flash_noncausal": lambda c, s, a: sec_flash(c, s, False, a.steps, a.warmup),
     "flash_causal": lambda c, s, a: sec_flash(c, s, True, a.steps, a.warmup),
@@ -254,6 +296,10 @@ SECONDARY = {
     "fp8_gemm": lambda c, s, a: sec_fp8(c, s, a.steps, a.warmup),
     "moe": lambda c, s, a: sec_moe(c, s, a.steps, a.warmup),
     "gemm_f32": lambda c, s, a: sec_gemm_f32(c, s, a.steps, a.warmup),
+    "collectives": lambda c, s, a: sec_collectives(c, s, max(5, a.steps // 10),
+                                                   max(2, a.warmup // 10)),
+    "routing_check": lambda c, s, a: sec_routing_check(c, s, max(5, a.steps // 10),
+                                                       max(2, a.warmup // 10)),
 }
 
 WORKLOADS = {"gemm_bf16": wl_gemm_bf16}

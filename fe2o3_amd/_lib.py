@@ -94,6 +94,14 @@ SIGNATURES = {
     "fe2o3_fp8_scale_from_amax": (i32, [vp, vp, vp]),
     "fe2o3_quantize_e4m3": (i32, [vp, u64, vp, vp, u64, vp]),
     "fe2o3_gemm_fp8_nt": (i32, [vp, u64, vp, u64, vp, vp, vp, u64, u32, u32, u32, vp]),
+    "fe2o3_moe_routing_check": (
+        i32, [vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, u32, u32, u32, vp,
+              u64, vp]),
+    "fe2o3_wave64_collectives_v1": (i32, [vp, u64, u64, vp, u64, vp, u64, vp, u64, vp]),
+    "fe2o3_wave64_collectives_rows": (
+        i32, [vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, u64, vp]),
+    "fe2o3_lds_reduce_i32_v1": (i32, [vp, u64, vp, u64, vp]),
+    "fe2o3_scoped_atomic_add_u32_v1": (i32, [vp, u64, vp, u64, vp, vp]),
 }
 
 

@@ -395,6 +395,170 @@ int32_t route(const void* logits, uint64_t logits_len, uint32_t dtype, uint32_t*
 
 }  // namespace
 
+// ---- routing output consistency -------------------------------------------------------
+// crates/fe2o3-host/src/moe_routing_expert_bridge_v1.rs:220-389 and the
+// compact pack plan (crates/fe2o3-host/src/generated_moe_expert_v1.rs:159-
+// 190), over T tokens, E experts and capacity C, on the device.  Each check
+// site has a 64-bit key (phase << 58 | position << 3 | sub-check) that
+// orders it as the reference's sequential check does; the smallest failing
+// key is the reference's first error, and its site writes the record
+// {kind, index, expected, actual}.  Exactness for the parallel form: when
+// site k is the first failure, every earlier site passed, so what k reads
+// (stable ranks from all earlier routes, the slots earlier routes claimed)
+// is what the sequential check sees at k.  Every read is bounds-guarded, so
+// arbitrary payloads are safe.
+enum : uint32_t {
+  RC_OK = 0, RC_EXPERT_OUT_OF_RANGE, RC_DUPLICATE_TOKEN_EXPERT, RC_REQUESTED_COUNT, RC_CAPACITY,
+  RC_ADMITTED_COUNT, RC_FIRST_OFFSET, RC_NONMONOTONE_OFFSETS, RC_OFFSET_MISMATCH,
+  RC_PLAN_OFFSET_ORDER, RC_PLAN_CAPACITY, RC_SLOT_OUT_OF_RANGE, RC_DUPLICATE_SLOT,
+  RC_STABLE_SLOT, RC_INVERSE, RC_PERMUTATION, RC_PREFIX_HOLE, RC_PERMUTATION_ROUTE,
+  RC_PERMUTATION_TAIL
+};
+constexpr uint32_t CHECK_MAX_ROUTES = 24576;  // claimed-slot table: 96 KiB of LDS
+
+struct Site {
+  uint64_t key = ~0ull;
+  uint32_t rec[4] = {0, 0, 0, 0};
+  FE2O3_DEVICE void fail(uint64_t k, uint32_t kind, uint32_t index, uint32_t expected,
+                         uint32_t actual) {
+    if (k < key) {
+      key = k;
+      rec[0] = kind;
+      rec[1] = index;
+      rec[2] = expected;
+      rec[3] = actual;
+    }
+  }
+};
+FE2O3_DEVICE uint64_t site_key(uint32_t phase, uint64_t pos, uint32_t sub) {
+  return ((uint64_t)phase << 58) | (pos << 3) | sub;
+}
+
+__global__ void __launch_bounds__(ASSIGN_THREADS) routing_check_kernel(
+    const uint32_t* __restrict__ top2, const uint32_t* __restrict__ requested,
+    const uint32_t* __restrict__ admitted, const uint32_t* __restrict__ offsets,
+    const uint32_t* __restrict__ slots, const uint32_t* __restrict__ permutation,
+    const uint32_t* __restrict__ inverse, uint32_t tokens, uint32_t experts, uint32_t capacity,
+    uint32_t* __restrict__ record) {
+  __shared__ uint32_t cnt[MAX_EXPERTS * ASSIGN_THREADS];
+  __shared__ unsigned long long best;
+  extern __shared__ uint32_t claimant[];  // per slot: the smallest route claiming it
+  const uint32_t t = threadIdx.x, routes = 2u * tokens;
+  const uint32_t per = (routes + ASSIGN_THREADS - 1) / ASSIGN_THREADS;
+  const uint32_t r0 = t * per, r1 = r0 + per < routes ? r0 + per : routes;
+  Site site;
+  if (t == 0) best = ~0ull;
+  for (uint32_t e = 0; e < experts; ++e) cnt[e * ASSIGN_THREADS + t] = 0;
+  for (uint32_t s = t; s < routes; s += ASSIGN_THREADS) claimant[s] = DROP;
+  __syncthreads();
+  // phase 1: top-2 ids in range and distinct per token; per-thread counts
+  for (uint32_t tk = t; tk < tokens; tk += ASSIGN_THREADS) {
+    const uint32_t a = top2[2 * tk], b = top2[2 * tk + 1];
+    if (a >= experts) site.fail(site_key(1, tk, 0), RC_EXPERT_OUT_OF_RANGE, 2 * tk, 0, a);
+    else if (b >= experts) site.fail(site_key(1, tk, 1), RC_EXPERT_OUT_OF_RANGE, 2 * tk + 1, 0, b);
+    else if (a == b) site.fail(site_key(1, tk, 2), RC_DUPLICATE_TOKEN_EXPERT, tk, 0, a);
+  }
+  for (uint32_t r = r0; r < r1; ++r) {
+    const uint32_t e = top2[r];
+    if (e < experts) cnt[e * ASSIGN_THREADS + t] += 1;
+  }
+  // the slots routes claim (the reference's seen set), smallest route first
+  const uint32_t accepted = offsets[experts];
+  for (uint32_t r = r0; r < r1; ++r) {
+    const uint32_t slot = slots[r];
+    if (slot != DROP && slot < accepted && slot < routes) atomicMin(&claimant[slot], r);
+  }
+  __syncthreads();
+  // phases 2-6: counts, capacity, offsets, pack plan (E <= 64, one thread
+  // each for the scan of its expert's counts, then one thread in order)
+  __shared__ uint32_t total[MAX_EXPERTS];
+  if (t < experts) {
+    uint32_t run = 0;
+    for (uint32_t i = 0; i < ASSIGN_THREADS; ++i) {
+      const uint32_t c = cnt[t * ASSIGN_THREADS + i];
+      cnt[t * ASSIGN_THREADS + i] = run;  // exclusive prefix: the stable-rank base
+      run += c;
+    }
+    total[t] = run;
+  }
+  __syncthreads();
+  if (t == 0) {
+    Site s0;
+    for (uint32_t e = 0; e < experts && s0.key == ~0ull; ++e)
+      if (requested[e] != total[e]) s0.fail(site_key(2, e, 0), RC_REQUESTED_COUNT, e, total[e], requested[e]);
+    for (uint32_t e = 0; e < experts && s0.key == ~0ull; ++e) {
+      const uint32_t want = requested[e] < capacity ? requested[e] : capacity;
+      if (admitted[e] > capacity) s0.fail(site_key(3, e, 0), RC_CAPACITY, e, 0, admitted[e]);
+      else if (admitted[e] != want) s0.fail(site_key(3, e, 1), RC_ADMITTED_COUNT, e, want, admitted[e]);
+    }
+    if (s0.key == ~0ull && offsets[0] != 0) s0.fail(site_key(4, 0, 0), RC_FIRST_OFFSET, 0, 0, offsets[0]);
+    uint32_t cum = 0;
+    for (uint32_t e = 0; e < experts && s0.key == ~0ull; ++e) {
+      const uint32_t start = offsets[e], end = offsets[e + 1];
+      cum += admitted[e];
+      if (start > end) s0.fail(site_key(5, e, 0), RC_NONMONOTONE_OFFSETS, e, start, end);
+      else if (end != cum) s0.fail(site_key(5, e, 1), RC_OFFSET_MISMATCH, e + 1, cum, end);
+    }
+    for (uint32_t e = 0; e < experts && s0.key == ~0ull; ++e) {
+      const uint32_t start = offsets[e], end = offsets[e + 1];
+      if (start > end || end > routes) s0.fail(site_key(6, e, 0), RC_PLAN_OFFSET_ORDER, e, 0, end);
+      else if (end - start > capacity) s0.fail(site_key(6, e, 1), RC_PLAN_CAPACITY, e, 0, end - start);
+    }
+    if (s0.key < site.key) site = s0;
+  }
+  // phase 7: per route in order -- slot range, duplicate, stable slot,
+  // inverse, permutation entry
+  for (uint32_t r = r0; r < r1; ++r) {
+    const uint32_t e = top2[r];
+    if (e >= experts) break;  // phase 1 reports it, and ranks stop being defined
+    const uint32_t rank = cnt[e * ASSIGN_THREADS + t]++;
+    const uint32_t want = rank < capacity ? offsets[e] + rank : DROP;
+    const uint32_t slot = slots[r];
+    if (slot != DROP && slot >= accepted) {
+      site.fail(site_key(7, r, 0), RC_SLOT_OUT_OF_RANGE, r, accepted, slot);
+      break;
+    }
+    if (slot != DROP && slot < routes && claimant[slot] < r) {
+      site.fail(site_key(7, r, 1), RC_DUPLICATE_SLOT, r, 0, slot);
+      break;
+    }
+    if (slot != want) {
+      site.fail(site_key(7, r, 2), RC_STABLE_SLOT, r, want, slot);
+      break;
+    }
+    if (inverse[r] != want) {
+      site.fail(site_key(7, r, 3), RC_INVERSE, r, want, inverse[r]);
+      break;
+    }
+    if (want != DROP && want < routes && permutation[want] != r) {
+      site.fail(site_key(7, r, 4), RC_PERMUTATION, want, r, permutation[want]);
+      break;
+    }
+  }
+  // phase 8: every accepted slot claimed, its permutation entry consistent;
+  // phase 9: the permutation tail holds the drop sentinel
+  const uint32_t acc = accepted < routes ? accepted : routes;
+  for (uint32_t s = t; s < acc; s += ASSIGN_THREADS) {
+    if (claimant[s] == DROP) { site.fail(site_key(8, s, 0), RC_PREFIX_HOLE, s, 0, 0); continue; }
+    const uint32_t r = permutation[s];
+    if (r >= routes) site.fail(site_key(8, s, 1), RC_PERMUTATION_ROUTE, s, 0, r);
+    else if (slots[r] != s || inverse[r] != s) site.fail(site_key(8, s, 2), RC_PERMUTATION, s, r, r);
+  }
+  for (uint32_t s = acc; s < routes; s += ASSIGN_THREADS)
+    if (s >= accepted && permutation[s] != DROP)
+      site.fail(site_key(9, s, 0), RC_PERMUTATION_TAIL, s, 0, permutation[s]);
+  if (site.key != ~0ull) atomicMin(&best, (unsigned long long)site.key);
+  __syncthreads();
+  if (best == ~0ull) {
+    if (t == 0) record[0] = record[1] = record[2] = record[3] = 0;
+  } else if (site.key == best) {
+    record[0] = site.rec[0];
+    record[1] = site.rec[1];
+    record[2] = site.rec[2];
+    record[3] = site.rec[3];
+  }
+}
+
 extern "C" {
 
 int32_t fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1(
@@ -514,6 +678,41 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_
   const uint64_t threads = (uint64_t)tokens * (hidden / 4u);
   combine_kernel<<<(unsigned)((threads + 255u) / 256u), 256, 0, s>>>(ws.yc, inverse, route_weights,
                                                                     tokens, hidden, routes, out);
+  return fe2o3_host::after_launch();
+}
+
+int32_t fe2o3_moe_routing_check(const uint32_t* top2_experts, uint64_t top2_len,
+                                const uint32_t* requested_counts, uint64_t requested_len,
+                                const uint32_t* admitted_counts, uint64_t admitted_len,
+                                const uint32_t* expert_offsets, uint64_t offsets_len,
+                                const uint32_t* route_slots, uint64_t slots_len,
+                                const uint32_t* permutation, uint64_t permutation_len,
+                                const uint32_t* inverse, uint64_t inverse_len, uint32_t tokens,
+                                uint32_t experts, uint32_t capacity, uint32_t* record,
+                                uint64_t record_len, void* stream) {
+  FE2O3_FAULT("fe2o3_moe_routing_check");
+  if (experts < 1 || experts > MAX_EXPERTS) return FE2O3_ERR_SHAPE;
+  const uint64_t routes = 2ull * tokens;
+  if (routes > CHECK_MAX_ROUTES) return FE2O3_ERR_SHAPE;
+  if (top2_len != routes || slots_len != routes || permutation_len != routes ||
+      inverse_len != routes || requested_len != experts || admitted_len != experts ||
+      offsets_len != experts + 1ull || record_len != 4)
+    return FE2O3_ERR_LENGTH;
+  if (!requested_counts || !admitted_counts || !expert_offsets || !record ||
+      (routes && (!top2_experts || !route_slots || !permutation || !inverse)))
+    return FE2O3_ERR_NULL;
+  const size_t lds = (size_t)(routes ? routes : 1) * sizeof(uint32_t);
+  static bool attr_set = false;
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute((const void*)routing_check_kernel,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             CHECK_MAX_ROUTES * sizeof(uint32_t));
+    if (e != hipSuccess) return (int32_t)e;
+    attr_set = true;
+  }
+  routing_check_kernel<<<1, ASSIGN_THREADS, lds, (hipStream_t)stream>>>(
+      top2_experts, requested_counts, admitted_counts, expert_offsets, route_slots, permutation,
+      inverse, tokens, experts, capacity, record);
   return fe2o3_host::after_launch();
 }
 

@@ -198,6 +198,45 @@ def gemm_fp8_nt(a, b, scale_a, scale_b, c, m, n, k, stream=None, sync=True) -> N
           c.ptr, c.count, m, n, k, stream=stream, sync=sync)
 
 
+# examples/wave64_collectives_v1/src/kernel.rs:18-67 (the mask is a scalar
+# between the input slice and the three output slices)
+def wave64_collectives_v1(input: DeviceBuffer, active_mask: int, reduction: DeviceBuffer,
+                          inclusive: DeviceBuffer, exclusive: DeviceBuffer, stream=None,
+                          sync=True) -> None:
+    _call("fe2o3_wave64_collectives_v1", *_ps(input), C.c_uint64(active_mask & (2**64 - 1)),
+          *_ps(reduction), *_ps(inclusive), *_ps(exclusive), stream=stream, sync=sync)
+
+
+def wave64_collectives_rows(input: DeviceBuffer, masks: DeviceBuffer, reduction: DeviceBuffer,
+                            inclusive: DeviceBuffer, exclusive: DeviceBuffer, rows: int,
+                            stream=None, sync=True) -> None:
+    _call("fe2o3_wave64_collectives_rows", *_ps(input), *_ps(masks), *_ps(reduction),
+          *_ps(inclusive), *_ps(exclusive), rows, stream=stream, sync=sync)
+
+
+# examples/workgroup_sync_v1/src/kernel.rs:18-78
+def lds_reduce_i32_v1(values: DeviceBuffer, output: DeviceBuffer, stream=None,
+                      sync=True) -> None:
+    _call("fe2o3_lds_reduce_i32_v1", *_ps(values), *_ps(output), stream=stream, sync=sync)
+
+
+# examples/workgroup_sync_v1/src/scoped_atomic.rs:11-32 (target: one u32)
+def scoped_atomic_add_u32_v1(values: DeviceBuffer, eligible: DeviceBuffer,
+                             target: DeviceBuffer, stream=None, sync=True) -> None:
+    _call("fe2o3_scoped_atomic_add_u32_v1", *_ps(values), *_ps(eligible), target.ptr,
+          stream=stream, sync=sync)
+
+
+# crates/fe2o3-host/src/moe_routing_expert_bridge_v1.rs:220-389 on the device;
+# record: 4 x u32 {kind, index, expected, actual}
+def moe_routing_check(routing: dict, tokens: int, experts: int, capacity: int,
+                      record: DeviceBuffer, stream=None, sync=True) -> None:
+    _call("fe2o3_moe_routing_check", *_ps(routing["top2"]), *_ps(routing["requested"]),
+          *_ps(routing["admitted"]), *_ps(routing["offsets"]), *_ps(routing["slots"]),
+          *_ps(routing["permutation"]), *_ps(routing["inverse"]), tokens, experts, capacity,
+          *_ps(record), stream=stream, sync=sync)
+
+
 def fill_normal_bf16(buf: DeviceBuffer, seed: int, domain: int, scale: float, first: int = 0,
                      stream=None, sync=True) -> None:
     _call("fe2o3_fill_normal_bf16", buf.ptr, buf.count, seed, domain, scale, first,

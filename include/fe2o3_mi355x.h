@@ -339,6 +339,88 @@ int32_t fe2o3_gemm_fp8_nt(const uint8_t *a, uint64_t a_len, const uint8_t *b,
                           const float *scale_b, uint16_t *c, uint64_t c_len,
                           uint32_t m, uint32_t n, uint32_t k, void *stream);
 
+/* crates/fe2o3-host/src/moe_routing_expert_bridge_v1.rs:220-389
+ * (check_host_observed_moe_routing_output_v1) with the compact pack plan of
+ * crates/fe2o3-host/src/generated_moe_expert_v1.rs:159-190, on the device
+ * and for any tokens (at most 12288), experts (1..64) and capacity
+ * (0xFFFFFFFF = unbounded).  Checks a complete routing output (the seven
+ * arrays of fe2o3_moe_top2_route) and writes the reference's FIRST failing
+ * relation to record[0..3] = {kind, index, expected, actual}, kind
+ * FE2O3_RC_OK (0) when every relation holds.  Lengths as
+ * fe2o3_moe_top2_route; record 4. */
+enum {
+  FE2O3_RC_OK = 0,
+  FE2O3_RC_EXPERT_OUT_OF_RANGE = 1,    /* index route, actual expert            */
+  FE2O3_RC_DUPLICATE_TOKEN_EXPERT = 2, /* index token, actual expert            */
+  FE2O3_RC_REQUESTED_COUNT = 3,        /* index expert, expected, actual        */
+  FE2O3_RC_CAPACITY = 4,               /* index expert, actual admitted         */
+  FE2O3_RC_ADMITTED_COUNT = 5,         /* index expert, expected, actual        */
+  FE2O3_RC_FIRST_OFFSET = 6,           /* actual offsets[0]                     */
+  FE2O3_RC_NONMONOTONE_OFFSETS = 7,    /* index expert, expected start, actual end */
+  FE2O3_RC_OFFSET_MISMATCH = 8,        /* index expert + 1, expected, actual    */
+  FE2O3_RC_PLAN_OFFSET_ORDER = 9,      /* index expert, actual end              */
+  FE2O3_RC_PLAN_CAPACITY = 10,         /* index expert, actual rows             */
+  FE2O3_RC_SLOT_OUT_OF_RANGE = 11,     /* index route, expected accepted, actual slot */
+  FE2O3_RC_DUPLICATE_SLOT = 12,        /* index route, actual slot              */
+  FE2O3_RC_STABLE_SLOT = 13,           /* index route, expected, actual         */
+  FE2O3_RC_INVERSE = 14,               /* index route, expected, actual         */
+  FE2O3_RC_PERMUTATION = 15,           /* index slot, expected route, actual    */
+  FE2O3_RC_PREFIX_HOLE = 16,           /* index slot                            */
+  FE2O3_RC_PERMUTATION_ROUTE = 17,     /* index slot, actual route              */
+  FE2O3_RC_PERMUTATION_TAIL = 18       /* index slot, actual                    */
+};
+int32_t fe2o3_moe_routing_check(const uint32_t *top2_experts, uint64_t top2_len,
+                                const uint32_t *requested_counts, uint64_t requested_len,
+                                const uint32_t *admitted_counts, uint64_t admitted_len,
+                                const uint32_t *expert_offsets, uint64_t offsets_len,
+                                const uint32_t *route_slots, uint64_t slots_len,
+                                const uint32_t *permutation, uint64_t permutation_len,
+                                const uint32_t *inverse, uint64_t inverse_len,
+                                uint32_t tokens, uint32_t experts, uint32_t capacity,
+                                uint32_t *record, uint64_t record_len, void *stream);
+
+/* ---- collectives and workgroup synchronization ----------------------------------------- */
+
+/* examples/wave64_collectives_v1/src/kernel.rs:18-67 (wave64_collectives_v1).
+ * One wave64: lane l contributes input[l] if bit l of active_mask is set,
+ * else +0.  Active lanes publish the full masked sum, the inclusive and the
+ * exclusive prefix sums in physical lane order; inactive lanes publish +0
+ * in all three.  The sum is six XOR-butterfly rounds and the scans six
+ * Hillis-Steele rounds (examples/wave64_collectives_v1/src/oracle.rs:150-172),
+ * so every bit matches the reference's oracle for any finite input.  All
+ * four lengths 64. */
+int32_t fe2o3_wave64_collectives_v1(const float *input, uint64_t input_len,
+                                    uint64_t active_mask, float *reduction,
+                                    uint64_t reduction_len, float *inclusive,
+                                    uint64_t inclusive_len, float *exclusive,
+                                    uint64_t exclusive_len, void *stream);
+
+/* The same collectives over `rows` independent 64-element rows (row r =
+ * elements 64r .. 64r+63, mask masks[r]); the reference has only the single
+ * wave.  input/reduction/inclusive/exclusive rows*64, masks rows. */
+int32_t fe2o3_wave64_collectives_rows(const float *input, uint64_t input_len,
+                                      const uint64_t *masks, uint64_t masks_len,
+                                      float *reduction, uint64_t reduction_len,
+                                      float *inclusive, uint64_t inclusive_len,
+                                      float *exclusive, uint64_t exclusive_len,
+                                      uint64_t rows, void *stream);
+
+/* examples/workgroup_sync_v1/src/kernel.rs:18-78 (lds_publish_read_reduce_i32_v1).
+ * output[0] = sum of values[0..63]: each lane publishes one value to its own
+ * LDS slot, uniform barriers around a halving tree, lane 0 writes.  The
+ * addition wraps; the result is the exact sum whenever it fits in int32
+ * (the reference admits only such inputs).  Lengths 64 and 1. */
+int32_t fe2o3_lds_reduce_i32_v1(const int32_t *values, uint64_t values_len,
+                                int32_t *output, uint64_t output_len, void *stream);
+
+/* examples/workgroup_sync_v1/src/scoped_atomic.rs:11-32 (scoped_atomic_add_u32_v1).
+ * For each lane l with eligible[l] != 0, one relaxed system-scope atomic
+ * add of values[l] to *target (which keeps its prior contents as the
+ * initial value).  Lengths 64; target 4-byte aligned. */
+int32_t fe2o3_scoped_atomic_add_u32_v1(const uint32_t *values, uint64_t values_len,
+                                       const uint32_t *eligible, uint64_t eligible_len,
+                                       uint32_t *target, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -243,6 +243,64 @@ void fe2o3o_gemm_fp8_points(uint32_t k, const uint8_t *a_rows,
                             float scale_ab, float *out_f32, uint16_t *out_bf16,
                             int32_t threads);
 
+/* ---- collectives, workgroup sync, routing consistency (sync.c) ---- */
+
+void fe2o3o_wave64_collectives_compute(const float *input, uint64_t mask, float *reduction,
+                                       float *inclusive, float *exclusive);
+int32_t fe2o3o_wave64_collectives_v1(const float *input, uint64_t mask, float *reduction,
+                                     float *inclusive, float *exclusive);
+int32_t fe2o3o_lds_reduce_i32_v1(const int32_t *values, int32_t *output);
+int32_t fe2o3o_atomic_add_u32_v1(uint32_t initial, const uint32_t *values,
+                                 const uint32_t *eligible, uint32_t *result);
+
+/* Routing consistency record kinds, in the order the reference checks them
+ * (crates/fe2o3-host/src/moe_routing_expert_bridge_v1.rs:67-140); record =
+ * {kind, index, expected, actual}:
+ *   EXPERT_OUT_OF_RANGE   index route, actual expert
+ *   DUPLICATE_TOKEN_EXPERT index token, actual expert
+ *   REQUESTED_COUNT       index expert, expected, actual
+ *   CAPACITY              index expert, actual admitted
+ *   ADMITTED_COUNT        index expert, expected, actual
+ *   FIRST_OFFSET          actual offsets[0]
+ *   NONMONOTONE_OFFSETS   index expert, expected = start, actual = end
+ *   OFFSET_MISMATCH       index expert + 1, expected, actual
+ *   PLAN_OFFSET_ORDER     index expert, actual end        (compact pack plan)
+ *   PLAN_CAPACITY         index expert, actual rows       (compact pack plan)
+ *   SLOT_OUT_OF_RANGE     index route, expected = accepted routes, actual slot
+ *   DUPLICATE_SLOT        index route, actual slot
+ *   STABLE_SLOT           index route, expected, actual
+ *   INVERSE               index route, expected, actual
+ *   PERMUTATION           index slot, expected route, actual permutation[slot]
+ *   PREFIX_HOLE           index slot
+ *   PERMUTATION_ROUTE     index slot, actual route
+ *   PERMUTATION_TAIL      index slot, actual */
+enum {
+  FE2O3O_RC_OK = 0,
+  FE2O3O_RC_EXPERT_OUT_OF_RANGE = 1,
+  FE2O3O_RC_DUPLICATE_TOKEN_EXPERT = 2,
+  FE2O3O_RC_REQUESTED_COUNT = 3,
+  FE2O3O_RC_CAPACITY = 4,
+  FE2O3O_RC_ADMITTED_COUNT = 5,
+  FE2O3O_RC_FIRST_OFFSET = 6,
+  FE2O3O_RC_NONMONOTONE_OFFSETS = 7,
+  FE2O3O_RC_OFFSET_MISMATCH = 8,
+  FE2O3O_RC_PLAN_OFFSET_ORDER = 9,
+  FE2O3O_RC_PLAN_CAPACITY = 10,
+  FE2O3O_RC_SLOT_OUT_OF_RANGE = 11,
+  FE2O3O_RC_DUPLICATE_SLOT = 12,
+  FE2O3O_RC_STABLE_SLOT = 13,
+  FE2O3O_RC_INVERSE = 14,
+  FE2O3O_RC_PERMUTATION = 15,
+  FE2O3O_RC_PREFIX_HOLE = 16,
+  FE2O3O_RC_PERMUTATION_ROUTE = 17,
+  FE2O3O_RC_PERMUTATION_TAIL = 18
+};
+int32_t fe2o3o_moe_routing_check(const uint32_t *top2, const uint32_t *requested,
+                                 const uint32_t *admitted, const uint32_t *offsets,
+                                 const uint32_t *slots, const uint32_t *permutation,
+                                 const uint32_t *inverse, uint32_t tokens, uint32_t experts,
+                                 uint32_t capacity, uint32_t *record);
+
 #ifdef __cplusplus
 }
 #endif

@@ -120,6 +120,12 @@ def _declare(L):
         "fe2o3o_amax_f32": (f32, [f32p, u64, i32]),
         "fe2o3o_quantize_e4m3": (None, [f32p, u64, f32, u8p, i32]),
         "fe2o3o_gemm_fp8_points": (None, [u32, u8p, u8p, u64, f32, f32p, u16p, i32]),
+        "fe2o3o_wave64_collectives_compute": (None, [f32p, u64, f32p, f32p, f32p]),
+        "fe2o3o_wave64_collectives_v1": (i32, [f32p, u64, f32p, f32p, f32p]),
+        "fe2o3o_lds_reduce_i32_v1": (i32, [vp, vp]),
+        "fe2o3o_atomic_add_u32_v1": (i32, [u32, u32p, u32p, u32p]),
+        "fe2o3o_moe_routing_check": (
+            i32, [u32p, u32p, u32p, u32p, u32p, u32p, u32p, u32, u32, u32, u32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -485,3 +491,54 @@ def gemm_fp8_points(k, a_rows, b_cols, scale_ab, threads=0):
     lib().fe2o3o_gemm_fp8_points(k, a_rows.ravel(), b_cols.ravel(), p, scale_ab, of, ob,
                                  threads or _threads())
     return of, ob
+
+
+# ---- collectives, workgroup sync, routing consistency (sync.c) ----------------------------
+
+ROUTING_CHECK_KINDS = (
+    "ok", "expert_out_of_range", "duplicate_token_expert", "requested_count", "capacity",
+    "admitted_count", "first_offset", "nonmonotone_offsets", "offset_mismatch",
+    "plan_offset_order", "plan_capacity", "slot_out_of_range", "duplicate_slot", "stable_slot",
+    "inverse", "permutation", "prefix_hole", "permutation_route", "permutation_tail")
+
+
+def wave64_collectives(x, mask, admit=True):
+    """(rc, reduction, inclusive, exclusive) for 64 f32 inputs.  admit=True
+    applies the reference's exact-corpus admission (finite integers in
+    [-1024, 1024]); admit=False computes the fixed-order rounds for any
+    input.  Outputs are NaN-filled when rejected."""
+    x = _c(x, np.float32)
+    outs = [np.full(64, np.nan, np.float32) for _ in range(3)]
+    if admit:
+        rc = lib().fe2o3o_wave64_collectives_v1(x, int(mask) & 0xFFFFFFFFFFFFFFFF, *outs)
+    else:
+        lib().fe2o3o_wave64_collectives_compute(x, int(mask) & 0xFFFFFFFFFFFFFFFF, *outs)
+        rc = OK
+    return rc, outs[0], outs[1], outs[2]
+
+
+def lds_reduce_i32(values):
+    v = _c(values, np.int32)
+    out = np.zeros(1, np.int32)
+    rc = lib().fe2o3o_lds_reduce_i32_v1(v.ctypes.data, out.ctypes.data)
+    return rc, int(out[0])
+
+
+def atomic_add_u32(initial, values, eligible):
+    out = np.zeros(1, np.uint32)
+    rc = lib().fe2o3o_atomic_add_u32_v1(initial, _c(values, np.uint32),
+                                        _c(eligible, np.uint32), out)
+    return rc, int(out[0])
+
+
+def moe_routing_check(outs, tokens, experts, capacity=DROP_ROUTE):
+    """First inconsistency of a routing output (dict as moe_top2_route
+    returns) as (kind name, index, expected, actual)."""
+    rec = np.zeros(4, np.uint32)
+    rc = lib().fe2o3o_moe_routing_check(
+        *(_c(outs[k], np.uint32) for k in ("top2_experts", "requested_counts", "admitted_counts",
+                                           "expert_offsets", "route_slots", "permutation",
+                                           "inverse")),
+        tokens, experts, capacity, rec)
+    assert rc == OK
+    return ROUTING_CHECK_KINDS[rec[0]], int(rec[1]), int(rec[2]), int(rec[3])

@@ -18,6 +18,8 @@ def guard_pattern(dtype, n):
         return np.full(n, 0x7FDE, np.uint16)
     if dtype == np.uint32:
         return np.full(n, 0xDEADBEEF, np.uint32)
+    if dtype == np.int32:
+        return np.full(n, 0xDEADBEEF, np.uint32).view(np.int32)
     if dtype == np.uint8:
         return np.full(n, 0xA5, np.uint8)
     raise TypeError(dtype)
