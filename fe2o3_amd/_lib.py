@@ -37,6 +37,20 @@ class Fe2o3HipDeviceProperties(C.Structure):
     ]
 
 
+class Fe2o3KernelResources(C.Structure):
+    """Resource record of one kernel behind an entry point (120 bytes)."""
+
+    _fields_ = [
+        ("kernel", C.c_char * 96),
+        ("workgroup_size", C.c_uint32),
+        ("static_lds_bytes", C.c_uint32),
+        ("dynamic_lds_bytes", C.c_uint32),
+        ("private_segment_bytes", C.c_uint32),
+        ("vgprs", C.c_uint32),
+        ("max_threads_per_workgroup", C.c_uint32),
+    ]
+
+
 # name -> (restype, argtypes).  Order and meaning follow the header.
 SIGNATURES = {
     "fe2o3_status_string": (C.c_char_p, [i32]),
@@ -97,6 +111,8 @@ SIGNATURES = {
     "fe2o3_moe_routing_check": (
         i32, [vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, u32, u32, u32, vp,
               u64, vp]),
+    "fe2o3_kernel_resources": (
+        i32, [C.c_char_p, u32, C.POINTER(Fe2o3KernelResources), C.POINTER(u32)]),
     "fe2o3_wave64_collectives_v1": (i32, [vp, u64, u64, vp, u64, vp, u64, vp, u64, vp]),
     "fe2o3_wave64_collectives_rows": (
         i32, [vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, u64, vp]),

@@ -91,6 +91,13 @@ __global__ void __launch_bounds__(64) scoped_atomic_add_kernel(const uint32_t* _
     __hip_atomic_fetch_add(target, values[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// kernels behind each entry point (fe2o3_kernel_resources)
+const fe2o3_host::KernelRegistrar kRegistered[] = {
+    fe2o3_host::KernelRegistrar({"fe2o3_wave64_collectives_v1", "wave64_collectives_kernel", (const void*)wave64_collectives_kernel, 64, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_wave64_collectives_rows", "wave64_collectives_rows_kernel", (const void*)wave64_collectives_rows_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_lds_reduce_i32_v1", "lds_reduce_i32_kernel", (const void*)lds_reduce_i32_kernel, 64, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_scoped_atomic_add_u32_v1", "scoped_atomic_add_kernel", (const void*)scoped_atomic_add_kernel, 64, 0})};
+
 }  // namespace
 
 extern "C" {

@@ -71,6 +71,12 @@ unsigned fill_blocks(uint64_t n) {
   return (unsigned)(b < 16384 ? (b ? b : 1) : 16384);
 }
 
+// kernels behind each entry point (fe2o3_kernel_resources)
+const fe2o3_host::KernelRegistrar kRegistered[] = {
+    fe2o3_host::KernelRegistrar({"fe2o3_fill_normal_bf16", "fill_normal_bf16_kernel", (const void*)fill_normal_bf16_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_fill_normal_f32", "fill_normal_f32_kernel", (const void*)fill_normal_f32_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_fill_uniform_f32", "fill_uniform_f32_kernel", (const void*)fill_uniform_f32_kernel, 256, 0})};
+
 }  // namespace
 
 extern "C" {

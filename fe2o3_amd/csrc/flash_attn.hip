@@ -320,6 +320,12 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
   }
 }
 
+// kernels behind each entry point (fe2o3_kernel_resources)
+const fe2o3_host::KernelRegistrar kRegistered[] = {
+    fe2o3_host::KernelRegistrar({"fe2o3_flash_attention_causal_f32_b1_h1_n8_d16_v1", "flash_profile_kernel", (const void*)flash_profile_kernel, 64, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_flash_attention_fwd", "flash_fwd_kernel<false>", (const void*)flash_fwd_kernel<false>, THREADS, SMEM_BYTES}),
+    fe2o3_host::KernelRegistrar({"fe2o3_flash_attention_fwd", "flash_fwd_kernel<true>", (const void*)flash_fwd_kernel<true>, THREADS, SMEM_BYTES})};
+
 }  // namespace
 
 extern "C" {

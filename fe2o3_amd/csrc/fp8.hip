@@ -108,6 +108,14 @@ unsigned grid_for(uint64_t n) {
   return (unsigned)(b < 8192 ? b : 8192);
 }
 
+// kernels behind each entry point (fe2o3_kernel_resources)
+const fe2o3_host::KernelRegistrar kRegistered[] = {
+    fe2o3_host::KernelRegistrar({"fe2o3_amax_f32", "zero_f32_kernel", (const void*)zero_f32_kernel, 1, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_amax_f32", "amax_kernel", (const void*)amax_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_fp8_scale_from_amax", "scale_kernel", (const void*)scale_kernel, 1, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_quantize_e4m3", "quantize_kernel", (const void*)quantize_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel", (const void*)gemm_fp8_kernel, 256, kFp8Smem})};
+
 }  // namespace
 
 extern "C" {

@@ -93,6 +93,11 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_nt_256_kernel(const uint16_t
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// kernels behind each entry point (fe2o3_kernel_resources)
+const fe2o3_host::KernelRegistrar kRegistered[] = {
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel", (const void*)gemm_bf16_nt_256_kernel, 256, kFastSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_generic_kernel", (const void*)gemm_bf16_nt_generic_kernel, 256, 0})};
+
 }  // namespace
 
 extern "C" int32_t fe2o3_gemm_bf16_nt(const uint16_t* a, uint64_t a_len, const uint16_t* b,

@@ -218,6 +218,13 @@ int32_t tile16(const uint16_t* a, uint64_t a_len, const uint16_t* b, uint64_t b_
   return fe2o3_host::after_launch();
 }
 
+// kernels behind each entry point (fe2o3_kernel_resources)
+const fe2o3_host::KernelRegistrar kRegistered[] = {
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_lds_slice1_v1", "tile16_bf16_kernel", (const void*)tile16_bf16_kernel, 64, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_expert_gemm_bf16_m16_n16_k16_v1", "tile16_bf16_kernel", (const void*)tile16_bf16_kernel, 64, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_kernel", (const void*)gemm_general_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_scalar_gemm_v1", "scalar_gemm_kernel", (const void*)scalar_gemm_kernel, 256, 0})};
+
 }  // namespace
 
 extern "C" {

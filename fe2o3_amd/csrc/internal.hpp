@@ -18,6 +18,21 @@ inline int32_t after_launch() {
   return (int32_t)e;
 }
 
+// One kernel launched by a C-ABI entry point, with the launch facts the
+// runtime cannot report (workgroup size, dynamic LDS requested).  Each
+// source file registers its kernels with a static table of KernelRegistrar;
+// fe2o3_kernel_resources adds what HIP reports for the loaded code object.
+struct KernelInfo {
+  const char* entry;     // C-ABI entry point
+  const char* kernel;    // kernel name
+  const void* fn;        // host launch stub
+  uint32_t threads;      // workgroup size of its launch
+  uint32_t dynamic_lds;  // dynamic LDS bytes of its launch (largest)
+};
+struct KernelRegistrar {
+  explicit KernelRegistrar(const KernelInfo& k);
+};
+
 }  // namespace fe2o3_host
 
 #define FE2O3_FAULT(entry)                                   \

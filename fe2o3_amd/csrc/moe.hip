@@ -393,8 +393,6 @@ int32_t route(const void* logits, uint64_t logits_len, uint32_t dtype, uint32_t*
   return fe2o3_host::after_launch();
 }
 
-}  // namespace
-
 // ---- routing output consistency -------------------------------------------------------
 // crates/fe2o3-host/src/moe_routing_expert_bridge_v1.rs:220-389 and the
 // compact pack plan (crates/fe2o3-host/src/generated_moe_expert_v1.rs:159-
@@ -558,6 +556,22 @@ __global__ void __launch_bounds__(ASSIGN_THREADS) routing_check_kernel(
     record[3] = site.rec[3];
   }
 }
+
+// kernels behind each entry point (fe2o3_kernel_resources)
+const fe2o3_host::KernelRegistrar kRegistered[] = {
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1", "route_select_kernel<float>", (const void*)route_select_kernel<float>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1", "route_assign_kernel", (const void*)route_assign_kernel, ASSIGN_THREADS, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_select_kernel<float>", (const void*)route_select_kernel<float>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_select_kernel<uint16_t>", (const void*)route_select_kernel<uint16_t>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_assign_kernel", (const void*)route_assign_kernel, ASSIGN_THREADS, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_expert_combine_f32_t8_k2_o16_v1", "combine_profile_kernel", (const void*)combine_profile_kernel, 128, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "gather_kernel", (const void*)gather_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "gate_up_kernel", (const void*)gate_up_kernel, 256, kSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "down_kernel", (const void*)down_kernel, 256, kSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "combine_kernel", (const void*)combine_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_routing_check", "routing_check_kernel", (const void*)routing_check_kernel, ASSIGN_THREADS, CHECK_MAX_ROUTES * 4})};
+
+}  // namespace
 
 extern "C" {
 

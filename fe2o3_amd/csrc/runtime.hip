@@ -24,7 +24,26 @@ bool fault_point(const char* entry) {
   return env != nullptr && strcmp(env, entry) == 0;
 }
 
+// Registered kernels, filled by the static tables of every source file when
+// the library loads (a function-local static, so registration order across
+// files does not matter).
+static constexpr int kMaxKernels = 128;
+struct Registry {
+  KernelInfo k[kMaxKernels];
+  int n = 0;
+};
+static Registry& registry() {
+  static Registry r;
+  return r;
+}
+KernelRegistrar::KernelRegistrar(const KernelInfo& k) {
+  Registry& r = registry();
+  if (r.n < kMaxKernels) r.k[r.n++] = k;
+}
+
 }  // namespace fe2o3_host
+
+static_assert(sizeof(Fe2o3KernelResources) == 120, "resource record is 120 bytes");
 
 extern "C" {
 
@@ -188,6 +207,34 @@ int32_t fe2o3_rt_memcpy(void* dst, const void* src, size_t bytes, uint32_t kind)
 
 int32_t fe2o3_rt_memset_async(void* dst, int32_t value, size_t bytes, void* stream) {
   return (int32_t)hipMemsetAsync(dst, value, bytes, (hipStream_t)stream);
+}
+
+int32_t fe2o3_kernel_resources(const char* entry, uint32_t index, Fe2o3KernelResources* out,
+                               uint32_t* count) {
+  if (!entry || !count) return FE2O3_ERR_NULL;
+  const fe2o3_host::Registry& r = fe2o3_host::registry();
+  const fe2o3_host::KernelInfo* hit = nullptr;
+  uint32_t n = 0;
+  for (int i = 0; i < r.n; ++i)
+    if (strcmp(r.k[i].entry, entry) == 0) {
+      if (n == index) hit = &r.k[i];
+      ++n;
+    }
+  *count = n;
+  if (!hit) return FE2O3_ERR_LENGTH;
+  if (!out) return FE2O3_ERR_NULL;
+  hipFuncAttributes attr;
+  const hipError_t e = hipFuncGetAttributes(&attr, hit->fn);
+  if (e != hipSuccess) return (int32_t)e;
+  memset(out, 0, sizeof *out);
+  strncpy(out->kernel, hit->kernel, sizeof out->kernel - 1);
+  out->workgroup_size = hit->threads;
+  out->static_lds_bytes = (uint32_t)attr.sharedSizeBytes;
+  out->dynamic_lds_bytes = hit->dynamic_lds;
+  out->private_segment_bytes = (uint32_t)attr.localSizeBytes;
+  out->vgprs = (uint32_t)attr.numRegs;
+  out->max_threads_per_workgroup = (uint32_t)attr.maxThreadsPerBlock;
+  return FE2O3_OK;
 }
 
 }  // extern "C"

@@ -136,6 +136,23 @@ int32_t row_softmax(const float* input, uint64_t input_len, float* output, uint6
   return fe2o3_host::after_launch();
 }
 
+// kernels behind each entry point (fe2o3_kernel_resources)
+const fe2o3_host::KernelRegistrar kRegistered[] = {
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax_v1", "softmax_strided_kernel", (const void*)softmax_strided_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax", "softmax_reg_kernel<1, false>", (const void*)softmax_reg_kernel<1, false>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax", "softmax_reg_kernel<1, true>", (const void*)softmax_reg_kernel<1, true>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax", "softmax_reg_kernel<2, false>", (const void*)softmax_reg_kernel<2, false>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax", "softmax_reg_kernel<2, true>", (const void*)softmax_reg_kernel<2, true>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax", "softmax_reg_kernel<4, false>", (const void*)softmax_reg_kernel<4, false>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax", "softmax_reg_kernel<4, true>", (const void*)softmax_reg_kernel<4, true>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax", "softmax_reg_kernel<8, false>", (const void*)softmax_reg_kernel<8, false>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax", "softmax_reg_kernel<8, true>", (const void*)softmax_reg_kernel<8, true>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax", "softmax_reg_kernel<16, false>", (const void*)softmax_reg_kernel<16, false>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax", "softmax_reg_kernel<16, true>", (const void*)softmax_reg_kernel<16, true>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax", "softmax_reg_kernel<32, false>", (const void*)softmax_reg_kernel<32, false>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax", "softmax_reg_kernel<32, true>", (const void*)softmax_reg_kernel<32, true>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_row_softmax", "softmax_strided_kernel", (const void*)softmax_strided_kernel, 256, 0})};
+
 }  // namespace
 
 extern "C" {

@@ -237,6 +237,25 @@ def moe_routing_check(routing: dict, tokens: int, experts: int, capacity: int,
           *_ps(record), stream=stream, sync=sync)
 
 
+def kernel_resources(entry: str) -> list[dict]:
+    """Every kernel behind C-ABI entry point `entry` with its launch facts and
+    the resources the runtime reports for the loaded code object
+    (fe2o3_kernel_resources)."""
+    L = _lib.lib()
+    count = C.c_uint32(0)
+    rc = L.fe2o3_kernel_resources(entry.encode(), 0xFFFFFFFF, None, C.byref(count))
+    if rc not in (0, -2):
+        check(rc, "fe2o3_kernel_resources")
+    out = []
+    for i in range(count.value):
+        rec = _lib.Fe2o3KernelResources()
+        check(L.fe2o3_kernel_resources(entry.encode(), i, C.byref(rec), C.byref(count)),
+              "fe2o3_kernel_resources")
+        out.append({name: (getattr(rec, name).decode() if name == "kernel" else getattr(rec, name))
+                    for name, _ in rec._fields_})
+    return out
+
+
 def fill_normal_bf16(buf: DeviceBuffer, seed: int, domain: int, scale: float, first: int = 0,
                      stream=None, sync=True) -> None:
     _call("fe2o3_fill_normal_bf16", buf.ptr, buf.count, seed, domain, scale, first,

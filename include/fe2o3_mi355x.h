@@ -379,6 +379,29 @@ int32_t fe2o3_moe_routing_check(const uint32_t *top2_experts, uint64_t top2_len,
                                 uint32_t tokens, uint32_t experts, uint32_t capacity,
                                 uint32_t *record, uint64_t record_len, void *stream);
 
+/* ---- kernel resource observation ------------------------------------------------------- */
+
+/* crates/fe2o3-host/src/generated_lds_gemm_lifecycle.rs:47-120
+ * (ExactLdsGemmKernelResourceObservationV1: group and private segment
+ * sizes observed from the loaded code object).  Kernel `index` of those
+ * that C-ABI entry point `entry` launches: its workgroup size and dynamic
+ * LDS (launch facts), its static LDS (group segment), private segment
+ * bytes per lane (0 = no scratch, no register spills) and registers as the
+ * runtime reports them for the loaded code object.  *count is always set
+ * to the number of kernels behind `entry`; FE2O3_ERR_LENGTH when
+ * index >= *count (0 for an unknown entry).  120-byte record. */
+typedef struct Fe2o3KernelResources {
+  char kernel[96];
+  uint32_t workgroup_size;
+  uint32_t static_lds_bytes;
+  uint32_t dynamic_lds_bytes;
+  uint32_t private_segment_bytes;
+  uint32_t vgprs;
+  uint32_t max_threads_per_workgroup;
+} Fe2o3KernelResources;
+int32_t fe2o3_kernel_resources(const char *entry, uint32_t index, Fe2o3KernelResources *out,
+                               uint32_t *count);
+
 /* ---- collectives and workgroup synchronization ----------------------------------------- */
 
 /* examples/wave64_collectives_v1/src/kernel.rs:18-67 (wave64_collectives_v1).

@@ -79,6 +79,36 @@ def test_length_and_shape_validation_without_gpu():
     assert b"length" in L.fe2o3_status_string(-2)
 
 
+def test_kernel_resource_record_and_registry_without_gpu():
+    """The record layout, and the per-entry kernel counts: the lookup needs
+    no GPU; only the resource query itself does."""
+    import ctypes
+    from fe2o3_amd import _lib
+    R = _lib.Fe2o3KernelResources
+    assert ctypes.sizeof(R) == 120
+    offsets = {"kernel": 0, "workgroup_size": 96, "static_lds_bytes": 100,
+               "dynamic_lds_bytes": 104, "private_segment_bytes": 108, "vgprs": 112,
+               "max_threads_per_workgroup": 116}
+    for name, off in offsets.items():
+        assert getattr(R, name).offset == off
+    L = _lib.lib()
+    expected = {"fe2o3_gemm_bf16_nt": 2, "fe2o3_flash_attention_fwd": 2, "fe2o3_moe_ffn_top2": 4,
+                "fe2o3_gemm_fp8_nt": 1, "fe2o3_row_softmax": 13, "fe2o3_moe_routing_check": 1,
+                "fe2o3_wave64_collectives_v1": 1, "no_such_entry": 0}
+    for entry, n in expected.items():
+        count = ctypes.c_uint32(12345)
+        assert L.fe2o3_kernel_resources(entry.encode(), 10**6, None, ctypes.byref(count)) == -2
+        assert count.value == n, entry
+    # every declared kernel entry point (not the runtime seam) registers a kernel
+    kernel_entries = [n for n in _declared() if not n.startswith(("fe2o3_rt_", "fe2o3Hip"))
+                      and n not in ("fe2o3_status_string", "fe2o3_kernel_resources",
+                                    "fe2o3_moe_ffn_workspace_bytes")]
+    for entry in kernel_entries:
+        count = ctypes.c_uint32(0)
+        L.fe2o3_kernel_resources(entry.encode(), 10**6, None, ctypes.byref(count))
+        assert count.value >= 1, entry
+
+
 def test_fault_point_fails_closed(monkeypatch):
     """FE2O3_FAULT_POINT forces an entry point to fail before any launch."""
     from fe2o3_amd import _lib
