@@ -28,7 +28,8 @@
 //    * K and V tiles go global -> LDS with 16-byte buffer loads to LDS (one
 //      fixed VGPR offset per thread, tile offsets scalar), chunks
 //      XOR-permuted per row against bank conflicts.
-//    * Causal: query tiles are issued heaviest first; a wave skips the
+//    * Causal: a workgroup runs query tiles r and nq-1-r of one head in
+//      turn, so every workgroup does nq+1 key tiles; a wave skips the
 //      MFMAs of key tiles that lie entirely above its rows and masks the
 //      diagonal tile.
 #include "common.hpp"
@@ -159,7 +160,7 @@ template <bool CAUSAL>
 __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse,
-    uint32_t seq, uint32_t heads, float scale_log2) {
+    uint32_t seq, uint32_t heads, float scale_log2, uint32_t paired) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
   const uint32_t lr = lane & 31u, g = lane >> 5;
@@ -168,21 +169,31 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
   // for each, all of its query tiles back to back: the tiles of one head run
   // together on one XCD and share their K/V through that XCD's L2.  Within a
   // head the causal order is heaviest tile (most key tiles) first.
+  // With `paired`, a workgroup runs two query tiles of one head, r then
+  // nq-1-r, so every causal workgroup does the same nq+1 key tiles.
   const uint32_t nq = seq / BQ;
+  const uint32_t per_head = paired ? nq / 2u : nq;
   uint32_t bh, rank;
   if (heads % 8u == 0u) {
     const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
-    bh = (slot / nq) * 8u + xcd;
-    rank = slot % nq;
+    bh = (slot / per_head) * 8u + xcd;
+    rank = slot % per_head;
   } else {
-    bh = blockIdx.x / nq;
-    rank = blockIdx.x % nq;
+    bh = blockIdx.x / per_head;
+    rank = blockIdx.x % per_head;
   }
-  const uint32_t qt = CAUSAL ? (nq - 1u - rank) : rank;
   const uint64_t head = (uint64_t)bh * seq * D;
   const uint16_t* qh = q + head;
   const uint16_t* kh = k + head;
   const uint16_t* vh = v + head;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(w);  // wave-uniform
+  const __amdgpu_buffer_rsrc_t ksrc = head_rsrc(kh, seq * (uint32_t)(D * 2));
+  const __amdgpu_buffer_rsrc_t vsrc = head_rsrc(vh, seq * (uint32_t)(D * 2));
+  const uint32_t k_off = tile_voffset<false>(), v_off = tile_voffset<true>();
+  for (uint32_t item = 0; item < (paired ? 2u : 1u); ++item) {
+  // heaviest first: the higher query tile of the pair, or rank order reversed
+  const uint32_t qt = paired ? (item == 0u ? nq - 1u - rank : rank)
+                             : (CAUSAL ? nq - 1u - rank : rank);
   const uint32_t q_row0 = qt * BQ + w * 32u;  // first query row of this wave
   const uint32_t my_q = q_row0 + lr;
 
@@ -201,10 +212,6 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
   float l_run = 0.0f;       // this lane's partial row sum of exp2(s*c - m_ref)
 
   const uint32_t n_kv = CAUSAL ? (qt + 1u) * (BQ / BKV) : seq / BKV;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(w);  // wave-uniform
-  const __amdgpu_buffer_rsrc_t ksrc = head_rsrc(kh, seq * (uint32_t)(D * 2));
-  const __amdgpu_buffer_rsrc_t vsrc = head_rsrc(vh, seq * (uint32_t)(D * 2));
-  const uint32_t k_off = tile_voffset<false>(), v_off = tile_voffset<true>();
   issue_tile(ksrc, k_off, 0u, smem, wave);
   issue_tile(vsrc, v_off, 0u, smem + TILE_BYTES, wave);
   wait_vmcnt0();
@@ -318,6 +325,7 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
     // natural-log statistic: max(s)*scale + ln(sum) = (m_ref + log2(sum)) * ln 2
     lse[(uint64_t)bh * seq + my_q] = (m_ref + __log2f(l_tot)) * 0.69314718055994531f;
   }
+  }  // item
 }
 
 // kernels behind each entry point (fe2o3_kernel_resources)
@@ -374,15 +382,18 @@ int32_t fe2o3_flash_attention_fwd(const uint16_t* q, uint64_t q_len, const uint1
     attr_set = true;
   }
   // one linear workgroup id per (query tile, batch*head); see the kernel
-  const uint64_t wgs = (uint64_t)(seq / BQ) * bh;
+  // causal: pairs of query tiles per workgroup (every workgroup the same
+  // work) when the tile count is even; non-causal tiles are equal already
+  const uint32_t paired = causal && (seq / BQ) % 2u == 0u ? 1u : 0u;
+  const uint64_t wgs = (uint64_t)(seq / BQ) / (paired ? 2u : 1u) * bh;
   if (wgs > 0x7fffffffu) return FE2O3_ERR_SHAPE;
   const dim3 grid((unsigned)wgs);
   if (causal)
     flash_fwd_kernel<true><<<grid, THREADS, SMEM_BYTES, (hipStream_t)stream>>>(
-        q, k, v, o, lse, seq, (uint32_t)bh, scale_log2);
+        q, k, v, o, lse, seq, (uint32_t)bh, scale_log2, paired);
   else
     flash_fwd_kernel<false><<<grid, THREADS, SMEM_BYTES, (hipStream_t)stream>>>(
-        q, k, v, o, lse, seq, (uint32_t)bh, scale_log2);
+        q, k, v, o, lse, seq, (uint32_t)bh, scale_log2, paired);
   return fe2o3_host::after_launch();
 }
 
