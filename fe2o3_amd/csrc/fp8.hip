@@ -88,7 +88,7 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
   const uint16_t* b16 = reinterpret_cast<const uint16_t*>(b + (uint64_t)tn * 256 * k);
   const auto ar = gemm_pipe::dense_rows<kFp8RowBytes>(a16, k16, 256, k16);
   const auto br = gemm_pipe::dense_rows<kFp8RowBytes>(b16, k16, 256, k16);
-  gemm_pipe::Acc acc;
+  gemm_pipe::Acc32 acc;
   gemm_pipe::zero(acc);
   gemm_pipe::mainloop<gemm_pipe::MmaFp8<kFp8RowBytes>, kFp8RowBytes, kFp8Stages>(ar, br, k16,
                                                                                  smem, acc);

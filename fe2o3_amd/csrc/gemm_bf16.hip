@@ -69,8 +69,8 @@ __global__ void __launch_bounds__(256) gemm_bf16_nt_generic_kernel(
 }
 
 // ---- fast path ----------------------------------------------------------------------------
-// 256x256 tiles, 64 k per LDS stage (128-byte rows), two stages: the faster
-// choice in steady state on MI355X (1150 vs 1111 TFLOP/s for 32 k x 4 stages).
+// 256x256 tiles, 64 k per LDS stage (128-byte rows), two stages, 16x16x32
+// MFMAs in a fixed issue order (gemm_pipe.hpp).
 constexpr int kRowBytes = 128, kStages = 2;
 constexpr int kFastSmem = kStages * 2 * gemm_pipe::Geo<kRowBytes>::kTileBytes;  // 128 KiB
 
@@ -85,9 +85,8 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_nt_256_kernel(const uint16_t
   gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
   const auto ar = gemm_pipe::dense_rows<kRowBytes>(a + (uint64_t)tm * 256 * k, k, 256, k);
   const auto br = gemm_pipe::dense_rows<kRowBytes>(b + (uint64_t)tn * 256 * k, k, 256, k);
-  gemm_pipe::Acc acc;
-  gemm_pipe::zero(acc);
-  gemm_pipe::mainloop<gemm_pipe::MmaBf16<kRowBytes>, kRowBytes, kStages>(ar, br, k, smem, acc);
+  gemm_pipe::Acc16 acc;
+  gemm_pipe::mainloop_bf16<kRowBytes, kStages>(ar, br, k, smem, acc);
   gemm_pipe::store_bf16(acc, c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256, n);
 }
 

@@ -211,7 +211,6 @@ FE2O3_DEVICE float silu_mul(float g, float u) {
 constexpr int kRowBytes = 128, kStages = 2;  // 64 k per LDS stage, two stages
 constexpr int kSmem = kStages * 2 * gemm_pipe::Geo<kRowBytes>::kTileBytes;  // 128 KiB
 using Pipe = gemm_pipe::Geo<kRowBytes>;
-using Mma = gemm_pipe::MmaBf16<kRowBytes>;
 
 __global__ void __launch_bounds__(256, 1) gate_up_kernel(
     const uint16_t* __restrict__ xc, const uint16_t* __restrict__ wg,
@@ -241,28 +240,29 @@ __global__ void __launch_bounds__(256, 1) gate_up_kernel(
     br.base[j] = ((j & 1) ? wu : wg) + wbase;
     br.voff[j] = (f * hidden + Pipe::inst_chunk(row) * 8u) * 2u;
   }
-  gemm_pipe::Acc acc;
-  gemm_pipe::zero(acc);
-  gemm_pipe::mainloop<Mma, kRowBytes, kStages>(ar, br, hidden, smem, acc);
-  const uint32_t lane = threadIdx.x & 63u, wn = (threadIdx.x >> 6) & 1u;
+  gemm_pipe::Acc16 acc;
+  gemm_pipe::mainloop_bf16<kRowBytes, kStages>(ar, br, hidden, smem, acc);
+  // accumulator column j (16 B rows each) of wave column wn: j = 0,1 gate
+  // f .. f+31, j = 2,3 up f .. f+31, j = 4,5 gate f+32 .., j = 6,7 up f+32 ..
+  // (f = f0 + 64 wn); gate j pairs with up j + 2
+  const uint32_t r0 = gemm_pipe::acc16_row0();
+  const uint32_t c0 = gemm_pipe::acc16_col0();                // 128 wn + 4 (lane / 16)
+  const uint32_t fl = f0 + ((c0 & 128u) >> 1) + (c0 & 127u);  // f0 + 64 wn + 4 (lane / 16)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t r = gemm_pipe::acc_row(i);
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t r = r0 + 16u * i;
     if (r >= rows) continue;
     uint16_t* out_row = hc + (uint64_t)(row0 + r) * ffn;
 #pragma unroll
     for (int half = 0; half < 2; ++half)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t f = f0 + wn * 64u + half * 32u + 8u * q + 4u * (lane >> 5);
-        const f32x16_t& gv = acc.v[i][2 * half];
-        const f32x16_t& uv = acc.v[i][2 * half + 1];
+      for (int sub = 0; sub < 2; ++sub) {
+        const f32x4_t& gv = acc.v[i][4 * half + sub];
+        const f32x4_t& uv = acc.v[i][4 * half + sub + 2];
         u32x2_t packed;
-        packed[0] = pack_bf16x2(silu_mul(gv[4 * q + 0], uv[4 * q + 0]),
-                                silu_mul(gv[4 * q + 1], uv[4 * q + 1]));
-        packed[1] = pack_bf16x2(silu_mul(gv[4 * q + 2], uv[4 * q + 2]),
-                                silu_mul(gv[4 * q + 3], uv[4 * q + 3]));
-        *reinterpret_cast<u32x2_t*>(out_row + f) = packed;
+        packed[0] = pack_bf16x2(silu_mul(gv[0], uv[0]), silu_mul(gv[1], uv[1]));
+        packed[1] = pack_bf16x2(silu_mul(gv[2], uv[2]), silu_mul(gv[3], uv[3]));
+        *reinterpret_cast<u32x2_t*>(out_row + fl + half * 32u + sub * 16u) = packed;
       }
   }
 }
@@ -285,24 +285,17 @@ __global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict
                                                    rows, k_half);
   const auto br = gemm_pipe::dense_rows<kRowBytes>(
       wd + (uint64_t)e * hidden * ffn + (uint64_t)n0 * ffn + kh * k_half, ffn, 256, k_half);
-  gemm_pipe::Acc acc;
-  gemm_pipe::zero(acc);
-  gemm_pipe::mainloop<Mma, kRowBytes, kStages>(ar, br, k_half, smem, acc);
+  gemm_pipe::Acc16 acc;
+  gemm_pipe::mainloop_bf16<kRowBytes, kStages>(ar, br, k_half, smem, acc);
   float* part = yc + (uint64_t)kh * routes * hidden;
+  const uint32_t r0 = gemm_pipe::acc16_row0(), c0 = gemm_pipe::acc16_col0();
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t r = gemm_pipe::acc_row(i);
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t r = r0 + 16u * i;
     if (r >= rows) continue;
-    float* out_row = part + (uint64_t)(row0 + r) * hidden + n0;
+    float* out_row = part + (uint64_t)(row0 + r) * hidden + n0 + c0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        f32x4_t v;
-#pragma unroll
-        for (int z = 0; z < 4; ++z) v[z] = acc.v[i][j][4 * q + z];
-        *reinterpret_cast<f32x4_t*>(out_row + gemm_pipe::acc_col(j, q)) = v;
-      }
+    for (int j = 0; j < 8; ++j) *reinterpret_cast<f32x4_t*>(out_row + 16u * j) = acc.v[i][j];
   }
 }
 

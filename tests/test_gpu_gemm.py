@@ -243,12 +243,21 @@ def test_gemm_bf16_nt_generic_shapes(gpu, oracle, m, n, k):
     _nt_case(gpu, oracle, m, n, k, seed=3)
 
 
-# k = 64 is one K step (tail only); 192 and 320 are whole two-stage groups
-# plus a one-step tail
-@pytest.mark.parametrize("m,n,k", [(256, 256, 64), (256, 512, 256), (512, 768, 1024),
-                                   (1024, 256, 4096), (256, 256, 320), (512, 256, 192)])
+# K steps of 64: k = 64 is the first step alone (tail only), 128 the first
+# two-step group alone, 192 and 320 whole groups plus a one-step tail
+@pytest.mark.parametrize("m,n,k", [(256, 256, 64), (256, 256, 128), (256, 512, 256),
+                                   (512, 768, 1024), (1024, 256, 4096), (256, 256, 320),
+                                   (512, 256, 192)])
 def test_gemm_bf16_nt_fast_path(gpu, oracle, m, n, k):
     _nt_case(gpu, oracle, m, n, k, seed=1)
+
+
+def test_gemm_bf16_nt_more_tiles_than_cus(gpu, oracle):
+    """264 output tiles (more than one per CU): sampled rows of every tile
+    row against the oracle."""
+    m, n, k = 2048, 8448, 640
+    rows = [t * 256 + (t * 53) % 256 for t in range(8)] + [0, 2047]
+    _nt_case(gpu, oracle, m, n, k, seed=4, rows=rows)
 
 
 def test_gemm_bf16_nt_config2_4096(gpu, oracle):
