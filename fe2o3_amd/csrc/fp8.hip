@@ -89,8 +89,7 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
   const auto ar = gemm_pipe::dense_rows<kFp8RowBytes>(a16, k16, 256, k16);
   const auto br = gemm_pipe::dense_rows<kFp8RowBytes>(b16, k16, 256, k16);
   gemm_pipe::Acc32 acc;
-  gemm_pipe::zero(acc);
-  gemm_pipe::mainloop<gemm_pipe::MmaFp8<kFp8RowBytes>, kFp8RowBytes, kFp8Stages>(ar, br, k16,
+  gemm_pipe::mainloop<gemm_pipe::Fp8Mma<kFp8RowBytes>, kFp8RowBytes, kFp8Stages>(ar, br, k16,
                                                                                  smem, acc);
   const float sab = scale_a[0] * scale_b[0];
 #pragma unroll

@@ -86,7 +86,7 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_nt_256_kernel(const uint16_t
   const auto ar = gemm_pipe::dense_rows<kRowBytes>(a + (uint64_t)tm * 256 * k, k, 256, k);
   const auto br = gemm_pipe::dense_rows<kRowBytes>(b + (uint64_t)tn * 256 * k, k, 256, k);
   gemm_pipe::Acc16 acc;
-  gemm_pipe::mainloop_bf16<kRowBytes, kStages>(ar, br, k, smem, acc);
+  gemm_pipe::mainloop<gemm_pipe::Bf16Mma<kRowBytes>, kRowBytes, kStages>(ar, br, k, smem, acc);
   gemm_pipe::store_bf16(acc, c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256, n);
 }
 

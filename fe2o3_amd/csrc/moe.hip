@@ -241,7 +241,8 @@ __global__ void __launch_bounds__(256, 1) gate_up_kernel(
     br.voff[j] = (f * hidden + Pipe::inst_chunk(row) * 8u) * 2u;
   }
   gemm_pipe::Acc16 acc;
-  gemm_pipe::mainloop_bf16<kRowBytes, kStages>(ar, br, hidden, smem, acc);
+  gemm_pipe::mainloop<gemm_pipe::Bf16Mma<kRowBytes>, kRowBytes, kStages>(ar, br, hidden, smem,
+                                                                        acc);
   // accumulator column j (16 B rows each) of wave column wn: j = 0,1 gate
   // f .. f+31, j = 2,3 up f .. f+31, j = 4,5 gate f+32 .., j = 6,7 up f+32 ..
   // (f = f0 + 64 wn); gate j pairs with up j + 2
@@ -286,7 +287,8 @@ __global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict
   const auto br = gemm_pipe::dense_rows<kRowBytes>(
       wd + (uint64_t)e * hidden * ffn + (uint64_t)n0 * ffn + kh * k_half, ffn, 256, k_half);
   gemm_pipe::Acc16 acc;
-  gemm_pipe::mainloop_bf16<kRowBytes, kStages>(ar, br, k_half, smem, acc);
+  gemm_pipe::mainloop<gemm_pipe::Bf16Mma<kRowBytes>, kRowBytes, kStages>(ar, br, k_half, smem,
+                                                                        acc);
   float* part = yc + (uint64_t)kh * routes * hidden;
   const uint32_t r0 = gemm_pipe::acc16_row0(), c0 = gemm_pipe::acc16_col0();
 #pragma unroll
