@@ -18,10 +18,12 @@
 // LDS layout.  The A tiles of all stages come first, then the B tiles (A of
 // stage p at p * T, B at (STAGES + p) * T, T = 256 * ROW_BYTES).  16-byte
 // chunk c of row r is stored at position c ^ swz(r):
-//   ROW_BYTES 128: swz(r) = (r ^ (r >> 3)) & 7
+//   ROW_BYTES 128: swz(r) = (r ^ (r >> 2)) & 7
 //   ROW_BYTES  64: swz(r) = ((r >> 1) ^ (r >> 3)) & 3
-// Both keep the MFMA operand reads (16 or 32 consecutive rows, one chunk)
-// free of bank conflicts (measured: SQ_LDS_BANK_CONFLICT = 0).
+// The 128-byte form keeps both operand read patterns free of bank conflicts
+// (measured, SQ_LDS_BANK_CONFLICT = 0): 16 rows x chunks 4s + l/16 (bf16
+// 16x16x32) and 32 rows x chunks 4s + 2(l/32) + h (fp8 32x32x64).  The
+// earlier (r ^ (r >> 3)) & 7 is conflict-free for the second only.
 //
 // Fragment reads.  The K loop is unrolled over the STAGES buffers, so the
 // stage, tile and row-block offsets of every ds_read are compile-time
@@ -47,7 +49,7 @@ struct Geo {
   static constexpr int kK16 = ROW_BYTES / 2;                 // 16-bit k units per stage
 
   static FE2O3_DEVICE uint32_t swz(uint32_t r) {
-    if (ROW_BYTES == 128) return (r ^ (r >> 3)) & 7u;
+    if (ROW_BYTES == 128) return (r ^ (r >> 2)) & 7u;
     return ((r >> 1) ^ (r >> 3)) & 3u;
   }
   // tile row moved by this thread in load j; the instruction covers rows
