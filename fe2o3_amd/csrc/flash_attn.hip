@@ -27,7 +27,9 @@
 //      MFMA, so V needs no register transpose.
 //    * K and V tiles go global -> LDS with 16-byte buffer loads to LDS (one
 //      fixed VGPR offset per thread, tile offsets scalar), chunks
-//      XOR-permuted per row against bank conflicts.
+//      XOR-permuted per row against bank conflicts.  The next tile's loads
+//      are spread one per two S^T MFMAs rather than issued as a burst
+//      (+3%).
 //    * Causal: a workgroup runs query tiles r and nq-1-r of one head in
 //      turn, so every workgroup does nq+1 key tiles; a wave skips the
 //      MFMAs of key tiles that lie entirely above its rows and masks the
@@ -127,13 +129,19 @@ FE2O3_DEVICE uint32_t tile_voffset() {
   return row * 256u + chunk * 16u;
 }
 
+constexpr int kLoadsPerTile = 16 / WAVES;  // 1 KiB loads per wave and tile
+static_assert(16 % (2 * kLoadsPerTile) == 0, "a tile's copies spread evenly over 16 MFMAs");
+
+FE2O3_DEVICE void copy_load(__amdgpu_buffer_rsrc_t src, uint32_t voff, uint32_t tile_byte,
+                            uint8_t* lds, uint32_t wave, int j) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (lds_void_t*)(lds + (WAVES * j + wave) * 1024u),
+                                           16, voff, tile_byte + 1024u * WAVES * j, 0, 0);
+}
+
 FE2O3_DEVICE void issue_tile(__amdgpu_buffer_rsrc_t src, uint32_t voff, uint32_t tile_byte,
                              uint8_t* lds, uint32_t wave) {
 #pragma unroll
-  for (int j = 0; j < 16 / WAVES; ++j)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        src, (lds_void_t*)(lds + (WAVES * j + wave) * 1024u), 16, voff,
-        tile_byte + 1024u * WAVES * j, 0, 0);
+  for (int j = 0; j < kLoadsPerTile; ++j) copy_load(src, voff, tile_byte, lds, wave, j);
 }
 
 // V^T operand of one O^T MFMA (d rows 32*db.., keys of half h of 32-key block
@@ -220,20 +228,20 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
   for (uint32_t j = 0; j < n_kv; ++j) {
     const uint8_t* cur = smem + (j & 1u) * STAGE_BYTES;
     uint8_t* nxt = smem + ((j + 1u) & 1u) * STAGE_BYTES;
-    if (j + 1u < n_kv) {
-      issue_tile(ksrc, k_off, (j + 1u) * TILE_BYTES, nxt, wave);
-      issue_tile(vsrc, v_off, (j + 1u) * TILE_BYTES, nxt + TILE_BYTES, wave);
-    }
+    // next tile's k offset; the last tile copies itself again (into a buffer
+    // nobody reads) so that every tile issues the same copies
+    const uint32_t nt =
+        __builtin_amdgcn_readfirstlane((j + 1u < n_kv ? j + 1u : j) * (uint32_t)TILE_BYTES);
     const uint32_t key0 = j * BKV;
     // keys key0..key0+63 vs. rows q_row0..q_row0+31
     const bool active = !CAUSAL || key0 <= q_row0 + 31u;
+    if (!active) {
+      issue_tile(ksrc, k_off, nt, nxt, wave);
+      issue_tile(vsrc, v_off, nt, nxt + TILE_BYTES, wave);
+    }
     if (active) {
       // S^T = K Q^T : two 32-key blocks
       f32x16_t s[2];
-      // Each SIMD runs one wave of each of two workgroups.  A wave raises its
-      // issue priority while it issues MFMAs, so the matrix core is fed
-      // first and the other wave's softmax VALU work fills the gaps.
-      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const uint32_t krow = kb * 32u + lr;
@@ -244,9 +252,17 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
               cur + krow * 256u + ((c ^ swz_k(krow)) << 4));
           s[kb] = ds == 0 ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[0], f32x16_t{}, 0, 0, 0)
                           : __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ds], s[kb], 0, 0, 0);
+          // the next tile's copies, spread over these 16 MFMAs (K loads, then V)
+          constexpr int kCopyEvery = 16 / (2 * kLoadsPerTile);
+          const int slot = kb * 8 + ds;
+          if (slot % kCopyEvery == 0) {
+            const int n = slot / kCopyEvery, jj = n % kLoadsPerTile;
+            const bool is_v = n >= kLoadsPerTile;
+            copy_load(is_v ? vsrc : ksrc, is_v ? v_off : k_off, nt,
+                      nxt + (is_v ? TILE_BYTES : 0), wave, jj);
+          }
         }
       }
-      __builtin_amdgcn_s_setprio(0);
       // mask the diagonal tile
       if (CAUSAL && key0 + 63u > q_row0) {
 #pragma unroll
@@ -290,7 +306,11 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
           for (int jj = 0; jj < 8; ++jj) pf[kb][h][jj] = (__bf16)pv[jj];
         }
       l_run += psum;
-      // O^T += V^T P^T
+      // O^T += V^T P^T.  Each SIMD runs one wave of each of two workgroups; a
+      // wave raises its issue priority while it issues these MFMAs, so the
+      // matrix core is fed first and the other wave's softmax fills the gaps
+      // (measured: +1% over raising it for the S^T MFMAs as well, +2% over
+      // not raising it).
       const uint8_t* vt = cur + TILE_BYTES;
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
