@@ -169,6 +169,9 @@ def _ffn_case(gpu, oracle, tokens, hidden, ffn, experts, capacity, sample_tokens
     inv = routing["inverse"].download()
     w = routing["weights"].download()
     xs = x.download().reshape(tokens, hidden)
+    if callable(sample_tokens):
+        sample_tokens = sample_tokens(routing["offsets"].download(),
+                                      routing["permutation"].download())
     worst = 0.0
     cache = {}
 
@@ -202,6 +205,34 @@ def test_moe_ffn_small_with_drops(gpu, oracle):
     tokens, hidden, ffn, experts = 256, 256, 256, 8
     worst, inv = _ffn_case(gpu, oracle, tokens, hidden, ffn, experts, 40, range(tokens))
     assert (inv == 0xFFFFFFFF).any()
+    assert worst <= 1e-2, worst
+
+
+def _tail_tokens(offsets, permutation):
+    """Tokens routed to rows of each expert's short last m-tile (at most 64
+    rows) and to the last rows of its full m-tiles, plus its first row."""
+    rows = set()
+    tails = mains = 0
+    for e in range(len(offsets) - 1):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        full, rem = divmod(hi - lo, 256)
+        if 0 < rem <= 64:
+            tails += 1
+            rows.update(range(lo + full * 256, hi))
+        if full:
+            mains += 1
+            rows.update(range(lo + full * 256 - 8, lo + full * 256))
+        rows.add(lo)
+    assert tails >= 2 and mains >= 2, (tails, mains)
+    return sorted({int(permutation[r]) >> 1 for r in rows if r < int(offsets[-1])})
+
+
+def test_moe_ffn_short_last_tiles(gpu, oracle):
+    """Experts of 256-300 rows: one full m-tile plus a last m-tile of at most
+    64 rows; every token routed into such a row is checked, with the last
+    rows of each full tile."""
+    tokens, hidden, ffn, experts = 1100, 512, 1024, 8
+    worst, _ = _ffn_case(gpu, oracle, tokens, hidden, ffn, experts, 0xFFFFFFFF, _tail_tokens)
     assert worst <= 1e-2, worst
 
 
