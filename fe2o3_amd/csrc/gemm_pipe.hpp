@@ -357,11 +357,18 @@ struct Substep {
   using G = Geo<ROW_BYTES>;
   using L = Lay<ROW_BYTES, STAGES>;
   static constexpr int S = M::kSubsteps, MF = M::kMfma;
-  static constexpr int NC = 2 * G::kInstPerWave;  // copies per stage and wave (16)
+  static constexpr int NC = 2 * G::kInstPerWave;  // copies per stage and wave
   static constexpr int kEarly = NC / 2;           // copies started at the barrier
   static constexpr int PN = (P + 1) % STAGES;     // buffer of the next step
+  static constexpr int PL = (P + STAGES - 1) % STAGES;  // buffer of the late copies' stage
   static constexpr bool LAST = S_ + 1 == S;
   static constexpr int kBarrierAt = MF / 2;
+  // late copies: all of substep 0, or its first half when it is also the
+  // last substep (every late copy precedes the barrier, every early one
+  // follows it, which keeps the wait counts exact)
+  static constexpr int kLateTo = LAST ? kBarrierAt : MF;
+  // fragment buffers alternate by substep over the whole K loop
+  static constexpr int FC = (P * S + S_) & 1, FN = FC ^ 1;
   static constexpr int kReadFrom = LAST ? MF / 2 : MF / 8;
   static constexpr int kReadTo = LAST ? MF : MF - MF / 8;
   // fragments read here: the next substep's, or in the last substep the next stage's first
@@ -376,22 +383,22 @@ struct Substep {
                                 typename M::Acc& acc) {
     if constexpr (I < MF) {
       if constexpr (LAST && I == kBarrierAt) {
-        static_assert(STAGES == 2, "the stage waited for holds every outstanding copy");
-        __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
+        // stage t+1 landed: later stages' copies may still be in flight
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm((STAGES - 2) * NC, 0));
         __builtin_amdgcn_s_barrier();
       }
-      M::template mfma<FIRST && S_ == 0, I>(acc, f[S_ & 1]);
-      if constexpr (LAST)  // early copies: stage t+2 into buffer P
+      M::template mfma<FIRST && S_ == 0, I>(acc, f[FC]);
+      if constexpr (LAST)  // early copies: stage t+STAGES into buffer P
         Spread<kEarly, kBarrierAt, MF>::template at<I>([&](auto n) {
           copy_one<ROW_BYTES, STAGES, decltype(n)::value>(ar, br, k_next2, smem, wave, P);
         });
-      if constexpr (S_ == 0)  // late copies: the rest of stage t+1 into the other buffer
-        Spread<NC - kEarly, 0, MF>::template at<I>([&](auto n) {
+      if constexpr (S_ == 0)  // late copies: the rest of stage t+STAGES-1
+        Spread<NC - kEarly, 0, kLateTo>::template at<I>([&](auto n) {
           copy_one<ROW_BYTES, STAGES, kEarly + decltype(n)::value>(ar, br, k_next, smem, wave,
-                                                                   PN);
+                                                                   PL);
         });
       Spread<M::kReads, kReadFrom, kReadTo>::template at<I>([&](auto n) {
-        M::template read<RA, RB, RS, decltype(n)::value>(smem, ln, f[(S_ + 1) & 1]);
+        M::template read<RA, RB, RS, decltype(n)::value>(smem, ln, f[FN]);
       });
       __builtin_amdgcn_sched_barrier(0);
       slot<I + 1>(ar, br, k_next, k_next2, smem, wave, ln, f, acc);
@@ -424,7 +431,8 @@ struct Steps {
                                typename M::Acc& acc) {
     if (TAIL && kt >= steps) return;
     Substep<M, ROW_BYTES, STAGES, P, 0, FIRST && P == 0>::run(
-        ar, br, stage_k(kt + 1, steps), stage_k(kt + 2, steps), smem, wave, ln, f, acc);
+        ar, br, stage_k(kt + STAGES - 1, steps), stage_k(kt + STAGES, steps), smem, wave, ln, f,
+        acc);
     if constexpr (P + 1 < STAGES)
       Steps<M, ROW_BYTES, STAGES, P + 1, TAIL, FIRST>::run(ar, br, kt + 1, steps, smem, wave, ln,
                                                            f, acc);
@@ -439,19 +447,28 @@ FE2O3_DEVICE void mainloop(const Rows<ROW_BYTES>& ar, const Rows<ROW_BYTES>& br,
   using G = Geo<ROW_BYTES>;
   using L = Lay<ROW_BYTES, STAGES>;
   using Sub = Substep<M, ROW_BYTES, STAGES, 0, 0, false>;
-  static_assert(ROW_BYTES == 128 && STAGES == 2, "the slot plan is for two stages of 128-byte rows");
-  static_assert(M::kSubsteps % 2 == 0, "fragment buffers alternate within a stage");
+  static_assert((ROW_BYTES == 128 && STAGES == 2) || (ROW_BYTES == 64 && STAGES == 4),
+                "two 64-k or four 32-k stages");
+  static_assert(M::kSubsteps % 2 == 0 || STAGES % 2 == 0,
+                "fragment buffers alternate across the unrolled steps");
   constexpr int NJ = G::kInstPerWave;
   const int steps = (int)(k16 / G::kK16);
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const typename M::Lanes ln = M::lanes(L::b_region);
-  // stage 0 whole, and stage 1's early copies (those a step -1 would issue)
-  issue_part<ROW_BYTES, 0, NJ>(ar, 0u, smem, L::a(0), wave);
-  issue_part<ROW_BYTES, 0, NJ>(br, 0u, smem, L::b_region + L::b(0), wave);
-  const uint32_t k1 = Steps<M, ROW_BYTES, STAGES, 0, false, false>::stage_k(1, steps);
-  issue_part<ROW_BYTES, 0, Sub::kEarly / 2>(ar, k1, smem, L::a(1), wave);
-  issue_part<ROW_BYTES, 0, Sub::kEarly / 2>(br, k1, smem, L::b_region + L::b(1), wave);
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm(Sub::kEarly, 0));  // stage 0 landed
+  // stages 0 .. STAGES-2 whole, and stage STAGES-1's early copies (those a
+  // step -1 would issue)
+  using St = Steps<M, ROW_BYTES, STAGES, 0, false, false>;
+#pragma unroll
+  for (int st = 0; st + 1 < STAGES; ++st) {
+    const uint32_t kb = st == 0 ? 0u : St::stage_k(st, steps);
+    issue_part<ROW_BYTES, 0, NJ>(ar, kb, smem, L::a(st), wave);
+    issue_part<ROW_BYTES, 0, NJ>(br, kb, smem, L::b_region + L::b(st), wave);
+  }
+  const uint32_t kl = St::stage_k(STAGES - 1, steps);
+  issue_part<ROW_BYTES, 0, Sub::kEarly / 2>(ar, kl, smem, L::a(STAGES - 1), wave);
+  issue_part<ROW_BYTES, 0, Sub::kEarly / 2>(br, kl, smem, L::b_region + L::b(STAGES - 1), wave);
+  // stage 0 landed
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm((STAGES - 2) * Sub::NC + Sub::kEarly, 0));
   __builtin_amdgcn_s_barrier();
   typename M::Frags f[2];
   Spread<M::kReads, 0, 1>::template at<0>([&](auto n) {

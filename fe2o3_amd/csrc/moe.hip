@@ -226,18 +226,18 @@ __global__ void __launch_bounds__(256, 1) gate_up_kernel(
   // within a wave column the blocks are gate f, up f, gate f+32, up f+32 for
   // f = f0 + 64*wn, so each lane's gate and up accumulators of one (row, f)
   // pair up in the epilogue.
-  // (Load slot j moves rows 8(4j + w) .. +7, all in block jb = j, so the
-  // gate/up choice is per slot and wave-uniform.)  The buffers are the
-  // expert's gate and up matrices.
+  // The buffers are the expert's gate and up matrices.
   gemm_pipe::Rows<kRowBytes> br;
   const uint64_t wbase = (uint64_t)e * ffn * hidden;
   br.bytes = ffn * hidden * 2u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
   for (int j = 0; j < Pipe::kInstPerWave; ++j) {
     const uint32_t row = Pipe::inst_row(j);
-    const uint32_t jb = row >> 5, wn = jb >> 2, jj = jb & 3u;
+    // the load's rows lie in one 32-row block: gate or up is wave-uniform
+    const uint32_t jb = ((4u * j + wave) * Pipe::kRowsPerInst) >> 5, wn = jb >> 2, jj = jb & 3u;
     const uint32_t f = f0 + wn * 64u + (jj >> 1) * 32u + (row & 31u);
-    br.base[j] = ((j & 1) ? wu : wg) + wbase;
+    br.base[j] = ((jj & 1u) ? wu : wg) + wbase;
     br.voff[j] = (f * hidden + Pipe::inst_chunk(row) * 8u) * 2u;
   }
   gemm_pipe::Acc16 acc;
