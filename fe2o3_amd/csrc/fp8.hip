@@ -74,6 +74,9 @@ __global__ void __launch_bounds__(256) quantize_kernel(const float* __restrict__
 constexpr int kFp8RowBytes = 128, kFp8Stages = 2;
 constexpr int kFp8Smem = kFp8Stages * 2 * gemm_pipe::Geo<kFp8RowBytes>::kTileBytes;  // 128 KiB
 
+// STAGED: C leaves through LDS in whole rows with nontemporal stores
+// (gemm_pipe::store_bf16_staged), for operands that stream from HBM.
+template <bool STAGED>
 __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restrict__ a,
                                                           const uint8_t* __restrict__ b,
                                                           const float* __restrict__ scale_a,
@@ -98,7 +101,11 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc.v[i][j][e] *= sab;
-  gemm_pipe::store_bf16(acc, c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256, n);
+  uint16_t* c_tile = c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256;
+  if constexpr (STAGED)
+    gemm_pipe::store_bf16_staged(acc, smem, c_tile, n);
+  else
+    gemm_pipe::store_bf16(acc, c_tile, n);
 }
 
 unsigned grid_for(uint64_t n) {
@@ -113,7 +120,8 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_amax_f32", "amax_kernel", (const void*)amax_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_fp8_scale_from_amax", "scale_kernel", (const void*)scale_kernel, 1, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_quantize_e4m3", "quantize_kernel", (const void*)quantize_kernel, 256, 0}),
-    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel", (const void*)gemm_fp8_kernel, 256, kFp8Smem})};
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel", (const void*)gemm_fp8_kernel<false>, 256, kFp8Smem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel<staged>", (const void*)gemm_fp8_kernel<true>, 256, kFp8Smem})};
 
 }  // namespace
 
@@ -162,16 +170,20 @@ int32_t fe2o3_gemm_fp8_nt(const uint8_t* a, uint64_t a_len, const uint8_t* b, ui
   if ((((uintptr_t)a | (uintptr_t)b | (uintptr_t)c) & 15u) != 0) return FE2O3_ERR_ALIGNMENT;
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)gemm_fp8_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       kFp8Smem);
-    if (e != hipSuccess) return (int32_t)e;
+    for (const void* f : {(const void*)gemm_fp8_kernel<false>, (const void*)gemm_fp8_kernel<true>}) {
+      hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kFp8Smem);
+      if (e != hipSuccess) return (int32_t)e;
+    }
     attr_set = true;
   }
   const uint64_t tiles = (uint64_t)(m / 256) * (n / 256);
   if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
-  gemm_fp8_kernel<<<(unsigned)tiles, 256, kFp8Smem, (hipStream_t)stream>>>(
-      a, b, scale_a, scale_b, c, m, n, k);
+  if (gemm_core::staged_epilogue(((uint64_t)m + n) * k))
+    gemm_fp8_kernel<true><<<(unsigned)tiles, 256, kFp8Smem, (hipStream_t)stream>>>(
+        a, b, scale_a, scale_b, c, m, n, k);
+  else
+    gemm_fp8_kernel<false><<<(unsigned)tiles, 256, kFp8Smem, (hipStream_t)stream>>>(
+        a, b, scale_a, scale_b, c, m, n, k);
   return fe2o3_host::after_launch();
 }
 

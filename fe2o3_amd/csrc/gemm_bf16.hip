@@ -74,6 +74,9 @@ __global__ void __launch_bounds__(256) gemm_bf16_nt_generic_kernel(
 constexpr int kRowBytes = 128, kStages = 2;
 constexpr int kFastSmem = kStages * 2 * gemm_pipe::Geo<kRowBytes>::kTileBytes;  // 128 KiB
 
+// STAGED: C leaves through LDS in whole rows with nontemporal stores
+// (gemm_pipe::store_bf16_staged), for operands that stream from HBM.
+template <bool STAGED>
 __global__ void __launch_bounds__(256, 1) gemm_bf16_nt_256_kernel(const uint16_t* __restrict__ a,
                                                                    const uint16_t* __restrict__ b,
                                                                    uint16_t* __restrict__ c,
@@ -87,14 +90,19 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_nt_256_kernel(const uint16_t
   const auto br = gemm_pipe::dense_rows<kRowBytes>(b + (uint64_t)tn * 256 * k, k, 256, k);
   gemm_pipe::Acc16 acc;
   gemm_pipe::mainloop<gemm_pipe::Bf16Mma<kRowBytes>, kRowBytes, kStages>(ar, br, k, smem, acc);
-  gemm_pipe::store_bf16(acc, c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256, n);
+  uint16_t* c_tile = c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256;
+  if constexpr (STAGED)
+    gemm_pipe::store_bf16_staged(acc, smem, c_tile, n);
+  else
+    gemm_pipe::store_bf16(acc, c_tile, n);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // kernels behind each entry point (fe2o3_kernel_resources)
 const fe2o3_host::KernelRegistrar kRegistered[] = {
-    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel", (const void*)gemm_bf16_nt_256_kernel, 256, kFastSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel", (const void*)gemm_bf16_nt_256_kernel<false>, 256, kFastSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel<staged>", (const void*)gemm_bf16_nt_256_kernel<true>, 256, kFastSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_generic_kernel", (const void*)gemm_bf16_nt_generic_kernel, 256, 0})};
 
 }  // namespace
@@ -115,16 +123,22 @@ extern "C" int32_t fe2o3_gemm_bf16_nt(const uint16_t* a, uint64_t a_len, const u
   if (fast) {
     static bool attr_set = false;
     if (!attr_set) {
-      hipError_t e = hipFuncSetAttribute((const void*)gemm_bf16_nt_256_kernel,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         kFastSmem);
-      if (e != hipSuccess) return (int32_t)e;
+      for (const void* f : {(const void*)gemm_bf16_nt_256_kernel<false>,
+                            (const void*)gemm_bf16_nt_256_kernel<true>}) {
+        hipError_t e =
+            hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kFastSmem);
+        if (e != hipSuccess) return (int32_t)e;
+      }
       attr_set = true;
     }
     const uint64_t tiles = (uint64_t)(m / 256) * (n / 256);
     if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
-    gemm_bf16_nt_256_kernel<<<(unsigned)tiles, 256, kFastSmem,
-                              (hipStream_t)stream>>>(a, b, c, m, n, k);
+    if (gemm_core::staged_epilogue(((uint64_t)m + n) * k * 2u))
+      gemm_bf16_nt_256_kernel<true><<<(unsigned)tiles, 256, kFastSmem, (hipStream_t)stream>>>(
+          a, b, c, m, n, k);
+    else
+      gemm_bf16_nt_256_kernel<false><<<(unsigned)tiles, 256, kFastSmem, (hipStream_t)stream>>>(
+          a, b, c, m, n, k);
     return fe2o3_host::after_launch();
   }
   dim3 grid((n + N_BN - 1) / N_BN, (m + N_BM - 1) / N_BM);

@@ -526,6 +526,67 @@ FE2O3_DEVICE void store_bf16(const Acc16& acc, uint16_t* c_tile, uint64_t ldc) {
     }
 }
 
+// Staged stores. Straight from the accumulators, one store instruction writes
+// 32 (Acc16) or 16 (Acc32) bytes into each of 16 or 32 rows, parts of cache
+// lines. Here each wave first writes its 128x128 block as bf16 into its own
+// 32 KiB of the idle stage buffers (row-major, 256 bytes a row, the 16-byte
+// chunks of row r XOR-permuted by r & 15 so that the 16-byte reads are
+// conflict-free), then reads 16 bytes per lane, so that one nontemporal store
+// writes four whole 256-byte row segments. The detour costs ~1 us per tile;
+// it pays where C would otherwise evict operands from the last-level cache
+// (gemm_core::staged_epilogue).
+FE2O3_DEVICE void stage_bf16(const Acc16& acc, uint8_t* region) {
+  const uint32_t l = lane_id(), s = l & 15u;
+  const uint32_t wr = s * 256u + ((l >> 4) & 1u) * 8u;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      u32x2_t packed;
+      packed[0] = pack_bf16x2(acc.v[i][j][0], acc.v[i][j][1]);
+      packed[1] = pack_bf16x2(acc.v[i][j][2], acc.v[i][j][3]);
+      const uint32_t chunk = ((2u * j) | (l >> 5)) ^ s;
+      *reinterpret_cast<u32x2_t*>(region + 4096u * i + wr + chunk * 16u) = packed;
+    }
+}
+
+FE2O3_DEVICE void stage_bf16(const Acc32& acc, uint8_t* region) {
+  const uint32_t l = lane_id(), s = l & 15u;
+  const uint32_t wr = (l & 31u) * 256u + (l >> 5) * 8u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        u32x2_t packed;
+        packed[0] = pack_bf16x2(acc.v[i][j][4 * q + 0], acc.v[i][j][4 * q + 1]);
+        packed[1] = pack_bf16x2(acc.v[i][j][4 * q + 2], acc.v[i][j][4 * q + 3]);
+        const uint32_t chunk = (4u * j + q) ^ s;
+        *reinterpret_cast<u32x2_t*>(region + 8192u * i + wr + chunk * 16u) = packed;
+      }
+}
+
+// `smem` needs 128 KiB, and the caller's copies must all have landed.
+template <class Acc>
+FE2O3_DEVICE void store_bf16_staged(const Acc& acc, uint8_t* smem, uint16_t* c_tile,
+                                    uint64_t ldc) {
+  const uint32_t l = lane_id(), w = wave_id();
+  uint8_t* region = smem + w * 32768u;
+  __syncthreads();  // every wave is past its last fragment read and copy
+  stage_bf16(acc, region);
+  __syncthreads();  // the wave's lanes read what other lanes wrote
+  const uint32_t rr = l >> 4, cc = l & 15u;
+  uint16_t* out = c_tile + (uint64_t)((w >> 1) * 128u + rr) * ldc + (w & 1u) * 128u + 8u * cc;
+#pragma unroll
+  for (int p = 0; p < 32; ++p) {
+    const uint32_t r = 4u * p + rr;
+    const u32x4_t v =
+        *reinterpret_cast<const u32x4_t*>(region + r * 256u + ((cc ^ (r & 15u)) << 4));
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(out + (uint64_t)(4u * p) * ldc));
+  }
+}
+
 FE2O3_DEVICE void store_bf16(const Acc32& acc, uint16_t* c_tile, uint64_t ldc) {
   const uint32_t row0 = acc32_row0(), col0 = acc32_col0();
 #pragma unroll

@@ -260,6 +260,14 @@ def test_gemm_bf16_nt_more_tiles_than_cus(gpu, oracle):
     _nt_case(gpu, oracle, m, n, k, seed=4, rows=rows)
 
 
+def test_gemm_bf16_nt_staged_epilogue(gpu, oracle):
+    """Operands of 243 MB, above the size at which C leaves through LDS with
+    nontemporal stores: whole rows of every tile row against the oracle."""
+    m, n, k = 1024, 28672, 4096
+    rows = [t * 256 + (t * 97) % 256 for t in range(4)] + [0, 511, 1023]
+    _nt_case(gpu, oracle, m, n, k, seed=5, rows=rows)
+
+
 def test_gemm_bf16_nt_config2_4096(gpu, oracle):
     """BASELINE config 2 (bf16 4096^3, A row-major, B column-major,
     N(0,1)/sqrt(K), seed 1): 64 full output rows spread over every tile row

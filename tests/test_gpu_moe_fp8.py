@@ -329,3 +329,15 @@ def test_gemm_fp8_config4_sampled(gpu, oracle):
     rows = np.concatenate([rng.integers(0, m, 4096), np.repeat(np.arange(4096, 4096 + 128), 64)])
     cols = np.concatenate([rng.integers(0, n, 4096), np.tile(rng.integers(0, n, 64), 128)])
     assert _fp8_case(gpu, oracle, m, n, k, (rows, cols)) <= 1e-2
+
+
+def test_gemm_fp8_staged_epilogue(gpu, oracle):
+    """Operands of 192 MiB, the size from which C leaves through LDS with
+    nontemporal stores: four rows over the first four column tiles plus 4096
+    random outputs."""
+    m, n, k = 256, 24576, 8192
+    rng = np.random.default_rng(5)
+    full = np.array([0, 97, 130, 255])
+    rows = np.concatenate([np.repeat(full, 1024), rng.integers(0, m, 4096)])
+    cols = np.concatenate([np.tile(np.arange(1024), len(full)), rng.integers(0, n, 4096)])
+    assert _fp8_case(gpu, oracle, m, n, k, (rows, cols)) <= 1e-2

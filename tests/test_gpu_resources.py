@@ -36,7 +36,9 @@ def test_every_kernel_is_spill_free_and_fits(gpu):
 
 @pytest.mark.parametrize("entry,kernel,dynamic_lds,threads", [
     ("fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel", 128 * 1024, 256),
+    ("fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel<staged>", 128 * 1024, 256),
     ("fe2o3_gemm_fp8_nt", "gemm_fp8_kernel", 128 * 1024, 256),
+    ("fe2o3_gemm_fp8_nt", "gemm_fp8_kernel<staged>", 128 * 1024, 256),
     ("fe2o3_flash_attention_fwd", "flash_fwd_kernel<false>", 64 * 1024, 256),
     ("fe2o3_flash_attention_fwd", "flash_fwd_kernel<true>", 64 * 1024, 256),
     ("fe2o3_moe_ffn_top2", "gate_up_kernel", 128 * 1024, 256),
