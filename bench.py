@@ -120,7 +120,7 @@ def wl_gemm_bf16(ctx, stream, args):
     return {
         "metric": "bf16 GEMM TFLOP/s (M=N=K=4096) on 1 MI355X",
         "unit": "TFLOP/s", "dtype": "bf16", "flop": flop, "ms": ms, "wall": wall,
-        "peak_key": "bf16", "kernel": "gemm_bf16_nt_256_kernel",
+        "peak_key": "bf16", "kernel": "gemm_bf16_nt_256_kernel<false>",
         "config": {"workload": "bf16 GEMM C=A.B^T, M=N=K=4096, A row-major, B column-major "
                                "([N,K] K-contiguous), A,B ~ N(0,1)/sqrt(K) seed 1, fp32 "
                                "accumulate, bf16 out (BASELINE config 2)",
@@ -194,7 +194,7 @@ def sec_fp8(ctx, stream, steps, warmup):
     ms = _timed(ctx, stream, gemm, steps, warmup)
     tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     return {"workload": "fp8 e4m3 GEMM 8192^3, per-tensor scales, bf16 out (config 4)",
-            "kernel": "gemm_fp8_kernel", "ms": ms, "value": round(tf, 2), "unit": "TFLOP/s",
+            "kernel": "gemm_fp8_kernel<false>", "ms": ms, "value": round(tf, 2), "unit": "TFLOP/s",
             "quantize_ms_both_operands": round(quant_ms, 4),
             "roofline": {"bound": "mfma", "peak": PEAK["fp8"], "frac": round(tf / PEAK["fp8"], 4)}}
 
