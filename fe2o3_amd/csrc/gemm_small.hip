@@ -140,71 +140,65 @@ __global__ void __launch_bounds__(256) gemm_general_kernel(
 }
 
 // ---- scalar f32 GEMM (sequential, unfused) -----------------------------------------
-// Workgroup tile 64x64, 256 threads, each thread a 4x4 block of outputs whose
-// accumulators each follow acc = acc + a*b over t = 0..k-1 in order.
-constexpr int S_BM = 64, S_BN = 64, S_BK = 16;
+// Workgroup tile 16x16, 256 threads, one output per thread, whose accumulator
+// follows acc = acc + a*b over t = 0..k-1 in order.  One output per thread
+// (rather than a register block) spreads a 256^3 problem over 256 workgroups;
+// the k loop runs in LDS chunks of 256, so k <= 256 waits for global memory
+// once.
+constexpr int S_BM = 16, S_BN = 16, S_BK = 256;
 
 __global__ void __launch_bounds__(256) scalar_gemm_kernel(const float* __restrict__ a,
                                                           const float* __restrict__ b,
                                                           float* __restrict__ c, uint32_t m,
                                                           uint32_t n, uint32_t k) {
 #pragma clang fp contract(off)
-  __shared__ float a_lds[S_BK][S_BM + 4];  // [depth][row]
-  __shared__ float b_lds[S_BK][S_BN + 4];  // [depth][col]
+  // Both tiles k-contiguous per row (B transposed on the way in), rows padded
+  // to 260 floats: 16-byte reads of 4 consecutive depths, conflict-free.
+  constexpr int LD = S_BK + 4;
+  __shared__ __attribute__((aligned(16))) float a_lds[S_BM][LD];   // [row][depth]
+  __shared__ __attribute__((aligned(16))) float bt_lds[S_BN][LD];  // [col][depth]
   const int t = threadIdx.x;
-  const int tr = t >> 4, tc = t & 15;  // thread owns rows tr+16*i, cols tc+16*j
-  const uint64_t row0 = (uint64_t)blockIdx.y * S_BM, col0 = (uint64_t)blockIdx.x * S_BN;
-  float acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+  const int tr = t >> 4, tc = t & 15;  // thread owns output (row0 + tr, col0 + tc)
+  // linear workgroup id over (row tile, column tile), column tiles fastest
+  const uint32_t tiles_n = (uint32_t)(((uint64_t)n + S_BN - 1) / S_BN);
+  const uint64_t row0 = (uint64_t)(blockIdx.x / tiles_n) * S_BM;
+  const uint64_t col0 = (uint64_t)(blockIdx.x % tiles_n) * S_BN;
+  float acc = 0.0f;
   for (uint64_t k0 = 0; k0 < k; k0 += S_BK) {
-    // A tile 64 rows x 16 depths: thread t loads row t/4, depths (t%4)*4..+3
-    {
-      const int r = t >> 2, d0 = (t & 3) * 4;
-      const uint64_t gr = row0 + r;
+    // A tile 16 rows x 256 depths and B tile 256 depths x 16 cols, 16 values each per thread
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint64_t gd = k0 + d0 + e;
-        a_lds[d0 + e][r] = (gr < m && gd < k) ? a[gr * k + gd] : 0.0f;
-      }
-    }
-    // B tile 16 depths x 64 cols: thread t loads depth t/16, cols (t%16)*4..+3
-    {
-      const int d = t >> 4, c0 = (t & 15) * 4;
-      const uint64_t gd = k0 + d;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint64_t gc = col0 + c0 + e;
-        b_lds[d][c0 + e] = (gd < k && gc < n) ? b[gd * n + gc] : 0.0f;
-      }
+    for (int e = 0; e < 16; ++e) {
+      const int i = t + 256 * e;
+      const int ar = i >> 8, ad = i & 255;
+      const uint64_t gr = row0 + ar, gd = k0 + ad;
+      a_lds[ar][ad] = (gr < m && gd < k) ? a[gr * k + gd] : 0.0f;
+      const int bd = i >> 4, bc = i & 15;
+      const uint64_t gbd = k0 + bd, gc = col0 + bc;
+      bt_lds[bc][bd] = (gbd < k && gc < n) ? b[gbd * n + gc] : 0.0f;
     }
     __syncthreads();
     const int depth = (k - k0) < (uint64_t)S_BK ? (int)(k - k0) : S_BK;
-    for (int d = 0; d < depth; ++d) {
-      float av[4], bv[4];
+    if (depth == S_BK) {
+#pragma unroll 16
+      for (int d = 0; d < S_BK; d += 4) {
+        const f32x4_t av = *reinterpret_cast<const f32x4_t*>(&a_lds[tr][d]);
+        const f32x4_t bv = *reinterpret_cast<const f32x4_t*>(&bt_lds[tc][d]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = a_lds[d][tr + 16 * i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = b_lds[d][tc + 16 * j];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float p = av[i] * bv[j];
-          acc[i][j] = acc[i][j] + p;
+        for (int e = 0; e < 4; ++e) {
+          const float p = av[e] * bv[e];
+          acc = acc + p;
         }
+      }
+    } else {
+      for (int d = 0; d < depth; ++d) {
+        const float p = a_lds[tr][d] * bt_lds[tc][d];
+        acc = acc + p;
+      }
     }
     __syncthreads();
   }
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint64_t gr = row0 + tr + 16 * i, gc = col0 + tc + 16 * j;
-      if (gr < m && gc < n) c[gr * n + gc] = acc[i][j];
-    }
+  const uint64_t gr = row0 + tr, gc = col0 + tc;
+  if (gr < m && gc < n) c[gr * n + gc] = acc;
 }
 
 bool aligned(const void* p, uintptr_t bytes) { return ((uintptr_t)p & (bytes - 1)) == 0; }
@@ -275,9 +269,9 @@ int32_t fe2o3_scalar_gemm_v1(const float* a, uint64_t a_len, const float* b, uin
   if (a_len < ea || b_len < eb || c_len < ec) return FE2O3_ERR_LENGTH;
   if (ec == 0) return FE2O3_OK;
   if ((ea && !a) || (eb && !b) || !c) return FE2O3_ERR_NULL;
-  dim3 grid((n + S_BN - 1) / S_BN, (m + S_BM - 1) / S_BM);
-  if (grid.y > 65535u) return FE2O3_ERR_SHAPE;
-  scalar_gemm_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(a, b, c, m, n, k);
+  const uint64_t tiles = (((uint64_t)m + S_BM - 1) / S_BM) * (((uint64_t)n + S_BN - 1) / S_BN);
+  if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
+  scalar_gemm_kernel<<<(unsigned)tiles, 256, 0, (hipStream_t)stream>>>(a, b, c, m, n, k);
   return fe2o3_host::after_launch();
 }
 
