@@ -203,8 +203,13 @@ FE2O3_DEVICE bool expert_tile(const uint32_t* offsets, uint32_t experts, uint32_
   return false;
 }
 
+// silu(g) * u = g / (1 + e^-g) * u with the hardware exp2 and reciprocal
+// (about one ulp each, far below the bf16 rounding of the product); the
+// library expf and IEEE divide cost ~30 instructions per output, a few
+// percent of a 256x128 tile.  Limits: g -> +inf gives g, g -> -inf gives -0.
 FE2O3_DEVICE float silu_mul(float g, float u) {
-  const float sg = g / (1.0f + expf(-g));
+  const float e = __builtin_amdgcn_exp2f(-g * 1.4426950408889634f);
+  const float sg = g * __builtin_amdgcn_rcpf(1.0f + e);
   return sg * u;
 }
 
