@@ -29,6 +29,8 @@
 // Expert row ranges come from the device-resident offsets, so the whole
 // layer runs without a host round trip: the grouped GEMM grids are sized
 // for the worst case and workgroups beyond the last expert tile exit.
+#include <mutex>
+
 #include "common.hpp"
 #include "gemm_pipe.hpp"
 #include "internal.hpp"
@@ -176,17 +178,18 @@ __global__ void __launch_bounds__(256) gather_kernel(const uint16_t* __restrict_
 // the list in order, so the workgroups that share a weight block run at the
 // same time behind one L2.  The grid is sized for the most m-tiles routing can
 // produce; entries past the list's end exit at once.
-FE2O3_DEVICE bool expert_tile(const uint32_t* offsets, uint32_t experts, uint32_t n_blocks,
-                              uint32_t* e_out, uint32_t* row0, uint32_t* rows, uint32_t* nb) {
+FE2O3_DEVICE bool expert_tile(const uint32_t* offsets, uint32_t e_begin, uint32_t e_end,
+                              uint32_t n_blocks, uint32_t* e_out, uint32_t* row0, uint32_t* rows,
+                              uint32_t* nb) {
   uint32_t total = 0;
-  for (uint32_t e = 0; e < experts; ++e)
+  for (uint32_t e = e_begin; e < e_end; ++e)
     total += (offsets[e + 1] - offsets[e] + 255u) / 256u * n_blocks;
   const uint32_t chunk = (total + 7u) / 8u;
   const uint32_t slot = blockIdx.x >> 3;
   if (slot >= chunk) return false;
   uint32_t x = (blockIdx.x & 7u) * chunk + slot;
   if (x >= total) return false;
-  for (uint32_t e = 0; e < experts; ++e) {
+  for (uint32_t e = e_begin; e < e_end; ++e) {
     const uint32_t lo = offsets[e], n = offsets[e + 1] - lo;
     const uint32_t m_tiles = (n + 255u) / 256u;
     if (x < m_tiles * n_blocks) {
@@ -219,11 +222,11 @@ using Pipe = gemm_pipe::Geo<kRowBytes>;
 
 __global__ void __launch_bounds__(256, 1) gate_up_kernel(
     const uint16_t* __restrict__ xc, const uint16_t* __restrict__ wg,
-    const uint16_t* __restrict__ wu, const uint32_t* __restrict__ offsets, uint32_t experts,
-    uint32_t hidden, uint32_t ffn, uint16_t* __restrict__ hc) {
+    const uint16_t* __restrict__ wu, const uint32_t* __restrict__ offsets, uint32_t e_begin,
+    uint32_t e_end, uint32_t hidden, uint32_t ffn, uint16_t* __restrict__ hc) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   uint32_t e, row0, rows, nb;
-  if (!expert_tile(offsets, experts, ffn / 128u, &e, &row0, &rows, &nb)) return;
+  if (!expert_tile(offsets, e_begin, e_end, ffn / 128u, &e, &row0, &rows, &nb)) return;
   const uint32_t f0 = nb * 128u;
   const auto ar = gemm_pipe::dense_rows<kRowBytes>(xc + (uint64_t)row0 * hidden, hidden, rows,
                                                    hidden);
@@ -276,16 +279,16 @@ __global__ void __launch_bounds__(256, 1) gate_up_kernel(
 __global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict__ hc,
                                                       const uint16_t* __restrict__ wd,
                                                       const uint32_t* __restrict__ offsets,
-                                                      uint32_t experts, uint32_t hidden,
-                                                      uint32_t ffn, uint64_t routes,
-                                                      float* __restrict__ yc) {
+                                                      uint32_t e_begin, uint32_t e_end,
+                                                      uint32_t hidden, uint32_t ffn,
+                                                      uint64_t routes, float* __restrict__ yc) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   // Split K in two: list entry nb = 2 * n-block + k-half.  Each half writes
   // its own fp32 partial (yc, then yc + routes * hidden); the combine adds
   // them.  Twice as many workgroups, each half as long, fill the last wave of
   // the grid better at this kernel's few hundred tiles.
   uint32_t e, row0, rows, nb;
-  if (!expert_tile(offsets, experts, 2u * (hidden / 256u), &e, &row0, &rows, &nb)) return;
+  if (!expert_tile(offsets, e_begin, e_end, 2u * (hidden / 256u), &e, &row0, &rows, &nb)) return;
   const uint32_t n0 = (nb >> 1) * 256u, kh = nb & 1u, k_half = ffn / 2u;
   const auto ar = gemm_pipe::dense_rows<kRowBytes>(hc + (uint64_t)row0 * ffn + kh * k_half, ffn,
                                                    rows, k_half);
@@ -571,6 +574,34 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "combine_kernel", (const void*)combine_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_routing_check", "routing_check_kernel", (const void*)routing_check_kernel, ASSIGN_THREADS, CHECK_MAX_ROUTES * 4})};
 
+// The expert FFN's second stream, one per device, created on first use and
+// kept for the life of the process (default priority, non-blocking so that it
+// also runs beside a caller's null stream).
+struct SideStream {
+  std::mutex mu;
+  hipStream_t stream = nullptr;
+  hipEvent_t gathered = nullptr, done = nullptr;
+  bool ok = false;
+};
+
+SideStream* side_stream() {
+  static constexpr int kMaxDevices = 64;
+  static SideStream sides[kMaxDevices];
+  static std::mutex create_mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  SideStream& sd = sides[dev];
+  std::lock_guard<std::mutex> lock(create_mu);
+  if (!sd.ok) {
+    if (hipStreamCreateWithFlags(&sd.stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&sd.gathered, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&sd.done, hipEventDisableTiming) != hipSuccess)
+      return nullptr;
+    sd.ok = true;
+  }
+  return &sd;
+}
+
 }  // namespace
 
 extern "C" {
@@ -677,18 +708,44 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_
     attr_set = true;
   }
   hipStream_t s = (hipStream_t)stream;
+  // the most m-tiles any routing yields for experts [b, e): routes/256
+  // rounded up, plus one partial tile per expert
+  auto grids = [&](uint32_t n_experts, uint64_t* gu, uint64_t* dn) {
+    const uint64_t m_tiles = (routes + 255u) / 256u + n_experts;
+    *gu = (m_tiles * (ffn / 128u) + 7u) / 8u * 8u;
+    *dn = (m_tiles * 2u * (hidden / 256u) + 7u) / 8u * 8u;
+    return *gu <= 0x7fffffffu && *dn <= 0x7fffffffu;
+  };
+  auto experts_ffn = [&](uint32_t b, uint32_t e, hipStream_t st) {
+    uint64_t gu, dn;
+    grids(e - b, &gu, &dn);
+    gate_up_kernel<<<(unsigned)gu, 256, kSmem, st>>>(ws.xc, w_gate, w_up, expert_offsets, b, e,
+                                                     hidden, ffn, ws.hc);
+    down_kernel<<<(unsigned)dn, 256, kSmem, st>>>(ws.hc, w_down, expert_offsets, b, e, hidden,
+                                                  ffn, routes, ws.yc);
+  };
+  uint64_t gu_all, dn_all;
+  if (!grids(experts, &gu_all, &dn_all)) return FE2O3_ERR_SHAPE;
   gather_kernel<<<(unsigned)routes, 256, 0, s>>>(x, permutation, expert_offsets, experts, hidden,
                                                 ws.xc);
-  // the most m-tiles any routing yields: routes/256 rounded up, plus one
-  // partial tile per expert
-  const uint64_t m_tiles = (routes + 255u) / 256u + experts;
-  const uint64_t gu_wgs = (m_tiles * (ffn / 128u) + 7u) / 8u * 8u;
-  const uint64_t dn_wgs = (m_tiles * 2u * (hidden / 256u) + 7u) / 8u * 8u;
-  if (gu_wgs > 0x7fffffffu || dn_wgs > 0x7fffffffu) return FE2O3_ERR_SHAPE;
-  gate_up_kernel<<<(unsigned)gu_wgs, 256, kSmem, s>>>(ws.xc, w_gate, w_up, expert_offsets,
-                                                      experts, hidden, ffn, ws.hc);
-  down_kernel<<<(unsigned)dn_wgs, 256, kSmem, s>>>(ws.hc, w_down, expert_offsets, experts,
-                                                   hidden, ffn, routes, ws.yc);
+  // Two halves of the experts, each gate/up then down, on the caller's
+  // stream and on a side stream: each grouped GEMM ends in a partly filled
+  // round of tiles, which the other half's tiles fill.
+  SideStream* side = experts >= 2 ? side_stream() : nullptr;
+  if (side != nullptr) {
+    std::lock_guard<std::mutex> lock(side->mu);  // keeps one call's event waits its own
+    const uint32_t half = experts / 2u;
+    hipError_t e = hipEventRecord(side->gathered, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->gathered, 0);
+    if (e != hipSuccess) return (int32_t)e;
+    experts_ffn(0u, half, s);
+    experts_ffn(half, experts, side->stream);
+    e = hipEventRecord(side->done, side->stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(s, side->done, 0);
+    if (e != hipSuccess) return (int32_t)e;
+  } else {
+    experts_ffn(0u, experts, s);
+  }
   const uint64_t threads = (uint64_t)tokens * (hidden / 4u);
   combine_kernel<<<(unsigned)((threads + 255u) / 256u), 256, 0, s>>>(ws.yc, inverse, route_weights,
                                                                     tokens, hidden, routes, out);
