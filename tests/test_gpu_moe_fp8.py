@@ -200,6 +200,15 @@ def test_moe_ffn_small_all_tokens(gpu, oracle):
     assert worst <= 1e-2, worst
 
 
+@pytest.mark.parametrize("experts", [2, 3])
+def test_moe_ffn_few_experts(gpu, oracle, experts):
+    """Two and three experts: the expert halves that run on the caller's
+    stream and on the side stream are 1 + 1 and 1 + 2 experts."""
+    tokens, hidden, ffn = 256, 256, 256
+    worst, _ = _ffn_case(gpu, oracle, tokens, hidden, ffn, experts, 0xFFFFFFFF, range(tokens))
+    assert worst <= 1e-2, worst
+
+
 def test_moe_ffn_small_with_drops(gpu, oracle):
     """Capacity below demand: dropped routes contribute nothing."""
     tokens, hidden, ffn, experts = 256, 256, 256, 8
