@@ -510,7 +510,6 @@ FE2O3_DEVICE uint32_t acc16_col0() { return (wave_id() & 1u) * 128u + 4u * (lane
 // Acc32 (i, j, e): tile row wm*128 + 32i + lane%32, tile column
 // wn*128 + 32j + 8(e/4) + 4(lane/32) + e%4.
 FE2O3_DEVICE uint32_t acc32_row0() { return (wave_id() >> 1) * 128u + (lane_id() & 31u); }
-FE2O3_DEVICE uint32_t acc32_col0() { return (wave_id() & 1u) * 128u + 4u * (lane_id() >> 5); }
 
 FE2O3_DEVICE void store_bf16(const Acc16& acc, uint16_t* c_tile, uint64_t ldc) {
   const uint32_t row0 = acc16_row0(), col0 = acc16_col0();
@@ -527,7 +526,7 @@ FE2O3_DEVICE void store_bf16(const Acc16& acc, uint16_t* c_tile, uint64_t ldc) {
 }
 
 // Staged stores. Straight from the accumulators, one store instruction writes
-// 32 (Acc16) or 16 (Acc32) bytes into each of 16 or 32 rows, parts of cache
+// 32 bytes into each of 16 (Acc16) or 32 (Acc32) rows, parts of cache
 // lines. Here each wave first writes its 128x128 block as bf16 into its own
 // 32 KiB of the idle stage buffers (row-major, 256 bytes a row, the 16-byte
 // chunks of row r XOR-permuted by r & 15 so that the 16-byte reads are
@@ -587,20 +586,37 @@ FE2O3_DEVICE void store_bf16_staged(const Acc& acc, uint8_t* smem, uint16_t* c_t
   }
 }
 
+// Acc32 (i, j, e) holds columns 32j + 8(e/4) + 4h + e%4 (h = lane/32), so
+// the two lane halves own alternating 4-column pieces.  One v_permlane32_swap
+// of the even-e/4 and odd-e/4 registers gives lanes 0-31 columns 32j + 16p +
+// 0..7 and lanes 32-63 columns 32j + 16p + 8..15: 16 bytes per lane and 32
+// bytes per row per store, twice the run and half the stores of storing the
+// 8-byte pieces in place.
 FE2O3_DEVICE void store_bf16(const Acc32& acc, uint16_t* c_tile, uint64_t ldc) {
-  const uint32_t row0 = acc32_row0(), col0 = acc32_col0();
+  const uint32_t row0 = acc32_row0();
+  const uint32_t col0 = (wave_id() & 1u) * 128u + 8u * (lane_id() >> 5);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        u32x2_t packed;
-        packed[0] = pack_bf16x2(acc.v[i][j][4 * q + 0], acc.v[i][j][4 * q + 1]);
-        packed[1] = pack_bf16x2(acc.v[i][j][4 * q + 2], acc.v[i][j][4 * q + 3]);
-        *reinterpret_cast<u32x2_t*>(c_tile + (uint64_t)(row0 + 32u * i) * ldc + col0 + 32u * j +
-                                    8u * q) = packed;
+      for (int p = 0; p < 2; ++p) {
+        const int qe = 2 * p, qo = 2 * p + 1;
+        const uint32_t y0 = pack_bf16x2(acc.v[i][j][4 * qe + 0], acc.v[i][j][4 * qe + 1]);
+        const uint32_t y1 = pack_bf16x2(acc.v[i][j][4 * qe + 2], acc.v[i][j][4 * qe + 3]);
+        const uint32_t x0 = pack_bf16x2(acc.v[i][j][4 * qo + 0], acc.v[i][j][4 * qo + 1]);
+        const uint32_t x1 = pack_bf16x2(acc.v[i][j][4 * qo + 2], acc.v[i][j][4 * qo + 3]);
+        const auto s0 = __builtin_amdgcn_permlane32_swap(y0, x0, false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(y1, x1, false, false);
+        u32x4_t packed;
+        packed[0] = s0[0];
+        packed[1] = s1[0];
+        packed[2] = s0[1];
+        packed[3] = s1[1];
+        *reinterpret_cast<u32x4_t*>(c_tile + (uint64_t)(row0 + 32u * i) * ldc + col0 + 32u * j +
+                                    16u * p) = packed;
       }
 }
+
 
 }  // namespace gemm_pipe
