@@ -338,7 +338,8 @@ def main() -> int:
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not "
-              "supported (the path would shard as described in DESIGN.md)", file=sys.stderr)
+              "supported (across GPUs the GEMM would shard by output tile rows, flash "
+              "attention by (batch, head), the MoE layer by expert)", file=sys.stderr)
         return 2
 
     from fe2o3_amd.runtime import GpuContext
