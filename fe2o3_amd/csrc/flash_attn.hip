@@ -391,16 +391,9 @@ int32_t fe2o3_flash_attention_fwd(const uint16_t* q, uint64_t q_len, const uint1
     return FE2O3_ERR_ALIGNMENT;
   if (!(scale > 0.0f) || !__builtin_isfinite(scale)) return FE2O3_ERR_SHAPE;
   const float scale_log2 = scale * 1.4426950408889634f;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)flash_fwd_kernel<true>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, SMEM_BYTES);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute((const void*)flash_fwd_kernel<false>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, SMEM_BYTES);
-    if (e != hipSuccess) return (int32_t)e;
-    attr_set = true;
-  }
+  static const int32_t lds_rc = fe2o3_host::set_dynamic_lds(
+      {(const void*)flash_fwd_kernel<true>, (const void*)flash_fwd_kernel<false>}, SMEM_BYTES);
+  if (lds_rc != FE2O3_OK) return lds_rc;
   // one linear workgroup id per (query tile, batch*head); see the kernel
   // causal: pairs of query tiles per workgroup (every workgroup the same
   // work) when the tile count is even; non-causal tiles are equal already

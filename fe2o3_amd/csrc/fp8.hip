@@ -168,14 +168,9 @@ int32_t fe2o3_gemm_fp8_nt(const uint8_t* a, uint64_t a_len, const uint8_t* b, ui
   if (256ull * k >= (1ull << 31)) return FE2O3_ERR_SHAPE;
   if (!a || !b || !c || !scale_a || !scale_b) return FE2O3_ERR_NULL;
   if ((((uintptr_t)a | (uintptr_t)b | (uintptr_t)c) & 15u) != 0) return FE2O3_ERR_ALIGNMENT;
-  static bool attr_set = false;
-  if (!attr_set) {
-    for (const void* f : {(const void*)gemm_fp8_kernel<false>, (const void*)gemm_fp8_kernel<true>}) {
-      hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kFp8Smem);
-      if (e != hipSuccess) return (int32_t)e;
-    }
-    attr_set = true;
-  }
+  static const int32_t lds_rc = fe2o3_host::set_dynamic_lds(
+      {(const void*)gemm_fp8_kernel<false>, (const void*)gemm_fp8_kernel<true>}, kFp8Smem);
+  if (lds_rc != FE2O3_OK) return lds_rc;
   const uint64_t tiles = (uint64_t)(m / 256) * (n / 256);
   if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
   if (gemm_core::staged_epilogue(((uint64_t)m + n) * k))

@@ -121,16 +121,10 @@ extern "C" int32_t fe2o3_gemm_bf16_nt(const uint16_t* a, uint64_t a_len, const u
   const bool fast = m % 256 == 0 && n % 256 == 0 && k % gemm_pipe::Geo<kRowBytes>::kK16 == 0 &&
                     512ull * k < (1ull << 31) && aligned16(a) && aligned16(b) && aligned16(c);
   if (fast) {
-    static bool attr_set = false;
-    if (!attr_set) {
-      for (const void* f : {(const void*)gemm_bf16_nt_256_kernel<false>,
-                            (const void*)gemm_bf16_nt_256_kernel<true>}) {
-        hipError_t e =
-            hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kFastSmem);
-        if (e != hipSuccess) return (int32_t)e;
-      }
-      attr_set = true;
-    }
+    static const int32_t lds_rc = fe2o3_host::set_dynamic_lds(
+        {(const void*)gemm_bf16_nt_256_kernel<false>, (const void*)gemm_bf16_nt_256_kernel<true>},
+        kFastSmem);
+    if (lds_rc != FE2O3_OK) return lds_rc;
     const uint64_t tiles = (uint64_t)(m / 256) * (n / 256);
     if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
     if (gemm_core::staged_epilogue(((uint64_t)m + n) * k * 2u))

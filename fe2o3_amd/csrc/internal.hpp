@@ -3,6 +3,8 @@
 
 #include <stdint.h>
 
+#include <initializer_list>
+
 #include <hip/hip_runtime.h>
 
 namespace fe2o3_host {
@@ -11,6 +13,17 @@ namespace fe2o3_host {
 // entry point then fails with FE2O3_ERR_INJECTED before any launch.  This is
 // the host-forced failure path used by the failure-handling tests.
 bool fault_point(const char* entry);
+
+// Raises the dynamic-LDS limit of each kernel in `fns` to `bytes` and returns
+// 0 or the first hipError_t.  Call sites keep the result in a function-local
+// static, so this runs once per process, thread-safely.
+inline int32_t set_dynamic_lds(std::initializer_list<const void*> fns, int bytes) {
+  for (const void* f : fns) {
+    const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e != hipSuccess) return (int32_t)e;
+  }
+  return 0;
+}
 
 // Enqueue status: 0, or the hipError_t of the launch just made.
 inline int32_t after_launch() {

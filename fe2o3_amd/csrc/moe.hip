@@ -696,17 +696,9 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_
   if ((((uintptr_t)x | (uintptr_t)w_gate | (uintptr_t)w_up | (uintptr_t)w_down |
         (uintptr_t)out | (uintptr_t)workspace) & 15u) != 0)
     return FE2O3_ERR_ALIGNMENT;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)gate_up_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       kSmem);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute((const void*)down_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              kSmem);
-    if (e != hipSuccess) return (int32_t)e;
-    attr_set = true;
-  }
+  static const int32_t lds_rc = fe2o3_host::set_dynamic_lds(
+      {(const void*)gate_up_kernel, (const void*)down_kernel}, kSmem);
+  if (lds_rc != FE2O3_OK) return lds_rc;
   hipStream_t s = (hipStream_t)stream;
   // the most m-tiles any routing yields for experts [b, e): routes/256
   // rounded up, plus one partial tile per expert
@@ -773,14 +765,9 @@ int32_t fe2o3_moe_routing_check(const uint32_t* top2_experts, uint64_t top2_len,
       (routes && (!top2_experts || !route_slots || !permutation || !inverse)))
     return FE2O3_ERR_NULL;
   const size_t lds = (size_t)(routes ? routes : 1) * sizeof(uint32_t);
-  static bool attr_set = false;
-  if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute((const void*)routing_check_kernel,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             CHECK_MAX_ROUTES * sizeof(uint32_t));
-    if (e != hipSuccess) return (int32_t)e;
-    attr_set = true;
-  }
+  static const int32_t lds_rc = fe2o3_host::set_dynamic_lds(
+      {(const void*)routing_check_kernel}, (int)(CHECK_MAX_ROUTES * sizeof(uint32_t)));
+  if (lds_rc != FE2O3_OK) return lds_rc;
   routing_check_kernel<<<1, ASSIGN_THREADS, lds, (hipStream_t)stream>>>(
       top2_experts, requested_counts, admitted_counts, expert_offsets, route_slots, permutation,
       inverse, tokens, experts, capacity, record);
