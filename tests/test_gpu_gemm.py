@@ -175,6 +175,20 @@ def test_scalar_hardware_cases_bit_exact(gpu, oracle, case):
         assert got.view(np.uint32)[0] == 0
 
 
+def test_scalar_gemm_multi_chunk_bit_exact(gpu, oracle):
+    """k over several 256-deep LDS chunks (256 + 256 + 88) and m, n that are
+    not multiples of the 16 x 16 workgroup tile: bit equality with the
+    sequential unfused oracle, guard bands intact."""
+    m, n, k = 33, 47, 600
+    a, b = oracle.scalar_gemm_inputs(m * k, k * n)
+    ref = oracle.scalar_gemm(m, n, k, a, b)
+    gc = Guarded(gpu, np.full(m * n, np.nan, np.float32))
+    ga, gb = Guarded(gpu, a), Guarded(gpu, b)
+    _kernels().scalar_gemm_v1_gpu.Kernel.load(gpu).prepare(ga.body, gb.body, gc.body, m, n, k).launch()
+    assert gc.download().view(np.uint32).tolist() == ref.view(np.uint32).tolist()
+    assert gc.guards_intact() and ga.unchanged() and gb.unchanged()
+
+
 def test_scalar_kat(gpu):
     a = gpu.to_device(np.array(rv.SCALAR_KAT["a"], np.float32))
     b = gpu.to_device(np.array(rv.SCALAR_KAT["b"], np.float32))
