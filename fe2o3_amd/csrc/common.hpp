@@ -79,6 +79,22 @@ FE2O3_DEVICE float swap_half(float v) {
   return __uint_as_float((threadIdx.x & 32u) ? r[0] : r[1]);
 }
 
+// ---- finiteness -----------------------------------------------------------------------
+// fma(x, 0, acc) leaves acc unchanged (0) for every finite x and makes it NaN
+// for a NaN or an infinity (inf * 0 = NaN, and NaN propagates), so one FMA
+// per element carries "some element was not finite" through a loop that
+// already touches every element.
+FE2O3_DEVICE float finite_probe(float acc, float x) { return __builtin_fmaf(x, 0.0f, acc); }
+
+// Marks the device's contract-status word (fe2o3_host::status_word) with a
+// vector atomic; only the rejecting path calls it.
+FE2O3_DEVICE void mark_nonfinite(uint32_t* status) {
+  __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Canonical quiet NaN, the sentinel output of a rejected row or tile.
+FE2O3_DEVICE float quiet_nan() { return __uint_as_float(0x7fc00000u); }
+
 // ---- explicit counter waits ---------------------------------------------------------
 FE2O3_DEVICE void wait_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 FE2O3_DEVICE void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }

@@ -44,14 +44,28 @@ using namespace fe2o3;
 // ---- exact profile ---------------------------------------------------------------------
 constexpr int P_N = 8, P_D = 16;
 
+// A NaN or an infinity anywhere in Q, K or V rejects the whole launch, as
+// the reference's kernel traps (kernel.rs:143-146): every output is written
+// as quiet NaN and the device's contract-status word is marked.  Lane l
+// probes elements 2l and 2l+1 of each input; a ballot combines the lanes.
 __global__ void __launch_bounds__(64) flash_profile_kernel(const float* __restrict__ q,
                                                            const float* __restrict__ k,
                                                            const float* __restrict__ v,
-                                                           float* __restrict__ out) {
+                                                           float* __restrict__ out,
+                                                           uint32_t* __restrict__ status) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x;
   const int first = lane * 2;
   const int row = first / P_D, col = first % P_D;
+  float probe = 0.0f;
+  for (int i = first; i < first + 2; ++i)
+    probe = finite_probe(finite_probe(finite_probe(probe, q[i]), k[i]), v[i]);
+  if (__ballot(probe != probe) != 0ull) {
+    if (lane == 0) mark_nonfinite(status);
+    out[first] = quiet_nan();
+    out[first + 1] = quiet_nan();
+    return;
+  }
   float m = 0.0f, l = 0.0f, n0 = 0.0f, n1 = 0.0f;
   for (int kr = 0; kr <= row; ++kr) {
     float dot = 0.0f;
@@ -367,7 +381,9 @@ int32_t fe2o3_flash_attention_causal_f32_b1_h1_n8_d16_v1(const float* q, uint64_
   const uint64_t n = P_N * P_D;
   if (q_len != n || k_len != n || v_len != n || output_len != n) return FE2O3_ERR_LENGTH;
   if (!q || !k || !v || !output) return FE2O3_ERR_NULL;
-  flash_profile_kernel<<<1, 64, 0, (hipStream_t)stream>>>(q, k, v, output);
+  uint32_t* status = fe2o3_host::status_word();
+  if (status == nullptr) return (int32_t)hipErrorInvalidSymbol;
+  flash_profile_kernel<<<1, 64, 0, (hipStream_t)stream>>>(q, k, v, output, status);
   return fe2o3_host::after_launch();
 }
 

@@ -25,6 +25,14 @@ inline int32_t set_dynamic_lds(std::initializer_list<const void*> fns, int bytes
   return 0;
 }
 
+// The current device's contract-status word: a device address that kernels
+// admitting only finite inputs receive as an argument and mark (atomic OR of
+// kStatusNonFinite) when they find a NaN or an infinity.  Each device has its
+// own copy of the word (a file-scope __device__ variable of runtime.hip,
+// located once per device with hipGetSymbolAddress).  nullptr on failure.
+constexpr uint32_t kStatusNonFinite = 1u;
+uint32_t* status_word();
+
 // Enqueue status: 0, or the hipError_t of the launch just made.
 inline int32_t after_launch() {
   hipError_t e = hipGetLastError();

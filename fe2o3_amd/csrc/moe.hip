@@ -34,6 +34,7 @@
 #include "common.hpp"
 #include "gemm_pipe.hpp"
 #include "internal.hpp"
+#include "moe_tiles.hpp"
 
 namespace {
 
@@ -51,17 +52,29 @@ FE2O3_DEVICE float logit_at<uint16_t>(const uint16_t* p, uint64_t i) {
   return f32_from_bf16_bits(p[i]);
 }
 
+// A token with a NaN or infinite logit is written as top2 = (DROP, DROP)
+// and marks the contract-status word; route_assign then rejects the whole
+// launch (see there), as the reference's kernel traps on any non-finite
+// logit (kernel.rs:118-128).
 template <typename T>
 __global__ void __launch_bounds__(256) route_select_kernel(const T* __restrict__ logits,
                                                            uint32_t tokens, uint32_t experts,
                                                            uint32_t* __restrict__ top2,
-                                                           float* __restrict__ weights) {
+                                                           float* __restrict__ weights,
+                                                           uint32_t* __restrict__ status) {
 #pragma clang fp contract(off)
   const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= tokens) return;
   const T* row = logits + (uint64_t)t * experts;
   uint32_t best = DROP, second = DROP;
-  float bs = 0.0f, ss = 0.0f;
+  float bs = 0.0f, ss = 0.0f, probe = 0.0f;
+  for (uint32_t e = 0; e < experts; ++e) probe = finite_probe(probe, logit_at(row, e));
+  if (probe != probe) {
+    mark_nonfinite(status);
+    top2[2ull * t] = DROP;
+    top2[2ull * t + 1] = DROP;
+    return;
+  }
   for (uint32_t e = 0; e < experts; ++e) {
     const float s = logit_at(row, e);
     if (best == DROP || s > bs || (s == bs && e < best)) {
@@ -83,11 +96,16 @@ __global__ void __launch_bounds__(256) route_select_kernel(const T* __restrict__
   }
 }
 
+// A launch whose route_select rejected any token (an expert id out of
+// range in top2) is rejected as a whole: every output takes its sentinel --
+// top2, slots, permutation and inverse DROP, route weights +0, requested,
+// admitted and offsets 0 -- so no expert receives a route.
 __global__ void __launch_bounds__(ASSIGN_THREADS) route_assign_kernel(
-    const uint32_t* __restrict__ top2, uint32_t routes, uint32_t experts, uint32_t capacity,
+    uint32_t* __restrict__ top2, uint32_t routes, uint32_t experts, uint32_t capacity,
     uint32_t* __restrict__ requested, uint32_t* __restrict__ admitted,
     uint32_t* __restrict__ offsets, uint32_t* __restrict__ slots,
-    uint32_t* __restrict__ permutation, uint32_t* __restrict__ inverse) {
+    uint32_t* __restrict__ permutation, uint32_t* __restrict__ inverse,
+    float* __restrict__ weights) {
   __shared__ uint32_t cnt[MAX_EXPERTS * ASSIGN_THREADS];
   __shared__ uint32_t off_s[MAX_EXPERTS + 1];
   const uint32_t t = threadIdx.x;
@@ -95,9 +113,24 @@ __global__ void __launch_bounds__(ASSIGN_THREADS) route_assign_kernel(
   const uint32_t r0 = t * per;
   const uint32_t r1 = r0 + per < routes ? r0 + per : routes;
   for (uint32_t e = 0; e < experts; ++e) cnt[e * ASSIGN_THREADS + t] = 0;
-  for (uint32_t r = r0; r < r1; ++r) cnt[top2[r] * ASSIGN_THREADS + t] += 1;
+  int rejected = 0;
+  for (uint32_t r = r0; r < r1; ++r) {
+    const uint32_t e = top2[r];
+    if (e < experts) cnt[e * ASSIGN_THREADS + t] += 1;
+    else rejected = 1;
+  }
   for (uint32_t r = t; r < routes; r += ASSIGN_THREADS) permutation[r] = DROP;
-  __syncthreads();
+  if (__syncthreads_or(rejected)) {
+    for (uint32_t r = t; r < routes; r += ASSIGN_THREADS) {
+      top2[r] = DROP;
+      slots[r] = DROP;
+      inverse[r] = DROP;
+      if (weights != nullptr) weights[r] = 0.0f;
+    }
+    if (t < experts) requested[t] = admitted[t] = offsets[t] = 0;
+    if (t == 0) offsets[experts] = 0;
+    return;
+  }
   if (t < experts) {  // exclusive scan of expert t's counts over threads
     uint32_t run = 0;
     for (uint32_t i = 0; i < ASSIGN_THREADS; ++i) {
@@ -158,52 +191,34 @@ __global__ void __launch_bounds__(128) combine_profile_kernel(const float* __res
 }
 
 // ---- expert FFN -------------------------------------------------------------------------
+// Routing arrays live in device memory, where the host cannot validate them
+// (fe2o3_moe_routing_check does); every kernel of the FFN clamps what it
+// reads from them, so an inconsistent routing gives unspecified outputs but
+// no access outside the caller's buffers and the workspace.  A slot whose
+// permutation entry is not a route gathers a zero row.
 __global__ void __launch_bounds__(256) gather_kernel(const uint16_t* __restrict__ x,
                                                      const uint32_t* __restrict__ permutation,
                                                      const uint32_t* __restrict__ offsets,
                                                      uint32_t experts, uint32_t hidden,
+                                                     uint32_t routes,
                                                      uint16_t* __restrict__ xc) {
   const uint32_t slot = blockIdx.x;
   if (slot >= offsets[experts]) return;
-  const uint32_t token = permutation[slot] >> 1;
-  const u32x4_t* src = reinterpret_cast<const u32x4_t*>(x + (uint64_t)token * hidden);
+  const uint32_t route = permutation[slot];
   u32x4_t* dst = reinterpret_cast<u32x4_t*>(xc + (uint64_t)slot * hidden);
+  if (route >= routes) {
+    for (uint32_t i = threadIdx.x; i < hidden / 8; i += blockDim.x) dst[i] = u32x4_t{0, 0, 0, 0};
+    return;
+  }
+  const u32x4_t* src = reinterpret_cast<const u32x4_t*>(x + (uint64_t)(route >> 1) * hidden);
   for (uint32_t i = threadIdx.x; i < hidden / 8; i += blockDim.x) dst[i] = src[i];
 }
 
-// Work order of the expert GEMMs.  The tiles form one list: expert-major,
-// then n-block, then the expert's 256-row m-tiles, so consecutive entries
-// share a weight block and runs of entries share the expert's rows.
-// Workgroup id i runs on XCD i % 8; XCD x takes the x-th contiguous eighth of
-// the list in order, so the workgroups that share a weight block run at the
-// same time behind one L2.  The grid is sized for the most m-tiles routing can
-// produce; entries past the list's end exit at once.
 FE2O3_DEVICE bool expert_tile(const uint32_t* offsets, uint32_t e_begin, uint32_t e_end,
-                              uint32_t n_blocks, uint32_t* e_out, uint32_t* row0, uint32_t* rows,
-                              uint32_t* nb) {
-  uint32_t total = 0;
-  for (uint32_t e = e_begin; e < e_end; ++e)
-    total += (offsets[e + 1] - offsets[e] + 255u) / 256u * n_blocks;
-  const uint32_t chunk = (total + 7u) / 8u;
-  const uint32_t slot = blockIdx.x >> 3;
-  if (slot >= chunk) return false;
-  uint32_t x = (blockIdx.x & 7u) * chunk + slot;
-  if (x >= total) return false;
-  for (uint32_t e = e_begin; e < e_end; ++e) {
-    const uint32_t lo = offsets[e], n = offsets[e + 1] - lo;
-    const uint32_t m_tiles = (n + 255u) / 256u;
-    if (x < m_tiles * n_blocks) {
-      const uint32_t mt = x % m_tiles;
-      *e_out = e;
-      *nb = x / m_tiles;
-      *row0 = lo + mt * 256u;
-      const uint32_t left = n - mt * 256u;
-      *rows = left < 256u ? left : 256u;
-      return true;
-    }
-    x -= m_tiles * n_blocks;
-  }
-  return false;
+                              uint32_t routes, uint32_t n_blocks, uint32_t* e_out, uint32_t* row0,
+                              uint32_t* rows, uint32_t* nb) {
+  return expert_tile_at(offsets, e_begin, e_end, routes, n_blocks, blockIdx.x, e_out, row0, rows,
+                        nb);
 }
 
 // silu(g) * u = g / (1 + e^-g) * u with the hardware exp2 and reciprocal
@@ -223,10 +238,10 @@ using Pipe = gemm_pipe::Geo<kRowBytes>;
 __global__ void __launch_bounds__(256, 1) gate_up_kernel(
     const uint16_t* __restrict__ xc, const uint16_t* __restrict__ wg,
     const uint16_t* __restrict__ wu, const uint32_t* __restrict__ offsets, uint32_t e_begin,
-    uint32_t e_end, uint32_t hidden, uint32_t ffn, uint16_t* __restrict__ hc) {
+    uint32_t e_end, uint32_t hidden, uint32_t ffn, uint32_t routes, uint16_t* __restrict__ hc) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   uint32_t e, row0, rows, nb;
-  if (!expert_tile(offsets, e_begin, e_end, ffn / 128u, &e, &row0, &rows, &nb)) return;
+  if (!expert_tile(offsets, e_begin, e_end, routes, ffn / 128u, &e, &row0, &rows, &nb)) return;
   const uint32_t f0 = nb * 128u;
   const auto ar = gemm_pipe::dense_rows<kRowBytes>(xc + (uint64_t)row0 * hidden, hidden, rows,
                                                    hidden);
@@ -288,7 +303,9 @@ __global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict
   // them.  Twice as many workgroups, each half as long, fill the last wave of
   // the grid better at this kernel's few hundred tiles.
   uint32_t e, row0, rows, nb;
-  if (!expert_tile(offsets, e_begin, e_end, 2u * (hidden / 256u), &e, &row0, &rows, &nb)) return;
+  if (!expert_tile(offsets, e_begin, e_end, (uint32_t)routes, 2u * (hidden / 256u), &e, &row0,
+                   &rows, &nb))
+    return;
   const uint32_t n0 = (nb >> 1) * 256u, kh = nb & 1u, k_half = ffn / 2u;
   const auto ar = gemm_pipe::dense_rows<kRowBytes>(hc + (uint64_t)row0 * ffn + kh * k_half, ffn,
                                                    rows, k_half);
@@ -324,7 +341,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
   for (uint32_t rank = 0; rank < 2; ++rank) {
     const uint32_t route = 2u * t + rank;
     const uint32_t slot = inverse[route];
-    if (slot == DROP) continue;
+    if (slot >= routes) continue;  // DROP, or not a slot
     const float w = weights[route];
     const f32x4_t y0 = *reinterpret_cast<const f32x4_t*>(yc + (uint64_t)slot * hidden + h);
     const f32x4_t y1 = *reinterpret_cast<const f32x4_t*>(yc + routes * hidden +
@@ -381,18 +398,20 @@ int32_t route(const void* logits, uint64_t logits_len, uint32_t dtype, uint32_t*
   if (!requested || !admitted || !offsets) return FE2O3_ERR_NULL;
   if (routes && (!logits || !top2 || !slots || !permutation || !inverse)) return FE2O3_ERR_NULL;
   hipStream_t s = (hipStream_t)stream;
+  uint32_t* status = fe2o3_host::status_word();
+  if (status == nullptr) return (int32_t)hipErrorInvalidSymbol;
   if (tokens) {
     const unsigned blocks = (tokens + 255u) / 256u;
     if (dtype == 0)
       route_select_kernel<float><<<blocks, 256, 0, s>>>((const float*)logits, tokens, experts,
-                                                        top2, weights);
+                                                        top2, weights, status);
     else
       route_select_kernel<uint16_t><<<blocks, 256, 0, s>>>((const uint16_t*)logits, tokens,
-                                                           experts, top2, weights);
+                                                           experts, top2, weights, status);
   }
   route_assign_kernel<<<1, ASSIGN_THREADS, 0, s>>>(top2, (uint32_t)routes, experts, capacity,
                                                    requested, admitted, offsets, slots,
-                                                   permutation, inverse);
+                                                   permutation, inverse, weights);
   return fe2o3_host::after_launch();
 }
 
@@ -545,7 +564,7 @@ __global__ void __launch_bounds__(ASSIGN_THREADS) routing_check_kernel(
     if (r >= routes) site.fail(site_key(8, s, 1), RC_PERMUTATION_ROUTE, s, 0, r);
     else if (slots[r] != s || inverse[r] != s) site.fail(site_key(8, s, 2), RC_PERMUTATION, s, r, r);
   }
-  for (uint32_t s = acc; s < routes; s += ASSIGN_THREADS)
+  for (uint32_t s = acc + t; s < routes; s += ASSIGN_THREADS)
     if (s >= accepted && permutation[s] != DROP)
       site.fail(site_key(9, s, 0), RC_PERMUTATION_TAIL, s, 0, permutation[s]);
   if (site.key != ~0ull) atomicMin(&best, (unsigned long long)site.key);
@@ -703,23 +722,22 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_
   // the most m-tiles any routing yields for experts [b, e): routes/256
   // rounded up, plus one partial tile per expert
   auto grids = [&](uint32_t n_experts, uint64_t* gu, uint64_t* dn) {
-    const uint64_t m_tiles = (routes + 255u) / 256u + n_experts;
-    *gu = (m_tiles * (ffn / 128u) + 7u) / 8u * 8u;
-    *dn = (m_tiles * 2u * (hidden / 256u) + 7u) / 8u * 8u;
+    *gu = expert_grid(routes, n_experts, ffn / 128u);
+    *dn = expert_grid(routes, n_experts, 2u * (hidden / 256u));
     return *gu <= 0x7fffffffu && *dn <= 0x7fffffffu;
   };
   auto experts_ffn = [&](uint32_t b, uint32_t e, hipStream_t st) {
     uint64_t gu, dn;
     grids(e - b, &gu, &dn);
     gate_up_kernel<<<(unsigned)gu, 256, kSmem, st>>>(ws.xc, w_gate, w_up, expert_offsets, b, e,
-                                                     hidden, ffn, ws.hc);
+                                                     hidden, ffn, (uint32_t)routes, ws.hc);
     down_kernel<<<(unsigned)dn, 256, kSmem, st>>>(ws.hc, w_down, expert_offsets, b, e, hidden,
                                                   ffn, routes, ws.yc);
   };
   uint64_t gu_all, dn_all;
   if (!grids(experts, &gu_all, &dn_all)) return FE2O3_ERR_SHAPE;
   gather_kernel<<<(unsigned)routes, 256, 0, s>>>(x, permutation, expert_offsets, experts, hidden,
-                                                ws.xc);
+                                                (uint32_t)routes, ws.xc);
   // Two halves of the experts, each gate/up then down, on the caller's
   // stream and on a side stream: each grouped GEMM ends in a partly filled
   // round of tiles, which the other half's tiles fill.

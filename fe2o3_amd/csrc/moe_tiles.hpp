@@ -1,0 +1,78 @@
+// moe_tiles.hpp -- the work list of the MoE expert GEMMs.
+//
+// The tiles of experts [e_begin, e_end) form one list: expert-major, then
+// n-block, then the expert's 256-row m-tiles, so consecutive entries share a
+// weight block and runs of entries share the expert's rows.  Workgroup id i
+// runs on XCD i % 8; XCD x takes the x-th contiguous eighth of the list in
+// order, so the workgroups that share a weight block run at the same time
+// behind one L2.  The grid is sized for the most m-tiles routing can produce;
+// entries past the list's end exit at once.
+//
+// Expert e's rows are offsets[e] .. offsets[e+1] clamped to [0, routes]
+// (empty when the offsets decrease): the offsets are device data the host
+// cannot validate, and the clamp keeps every tile inside the workspace rows
+// [0, routes) for any offsets.
+//
+// Plain C++ so the same functions compile for gfx950 and for the host (a CPU
+// test sweeps arbitrary offsets over every workgroup of the grid).
+#pragma once
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define FE2O3_HD __host__ __device__ __forceinline__
+#else
+#define FE2O3_HD inline
+#endif
+
+namespace fe2o3 {
+
+FE2O3_HD void expert_rows(const uint32_t* offsets, uint32_t e, uint32_t routes, uint32_t* lo,
+                          uint32_t* n) {
+  const uint32_t a = offsets[e] < routes ? offsets[e] : routes;
+  const uint32_t b = offsets[e + 1] < routes ? offsets[e + 1] : routes;
+  *lo = a;
+  *n = b > a ? b - a : 0u;
+}
+
+// Entry of workgroup `block` in the list: expert, first row, row count
+// (1..256) and n-block; false when the workgroup has no entry.
+FE2O3_HD bool expert_tile_at(const uint32_t* offsets, uint32_t e_begin, uint32_t e_end,
+                             uint32_t routes, uint32_t n_blocks, uint32_t block, uint32_t* e_out,
+                             uint32_t* row0, uint32_t* rows, uint32_t* nb) {
+  uint32_t total = 0, lo, n;
+  for (uint32_t e = e_begin; e < e_end; ++e) {
+    expert_rows(offsets, e, routes, &lo, &n);
+    total += (n + 255u) / 256u * n_blocks;
+  }
+  const uint32_t chunk = (total + 7u) / 8u;
+  const uint32_t slot = block >> 3;
+  if (slot >= chunk) return false;
+  uint32_t x = (block & 7u) * chunk + slot;
+  if (x >= total) return false;
+  for (uint32_t e = e_begin; e < e_end; ++e) {
+    expert_rows(offsets, e, routes, &lo, &n);
+    const uint32_t m_tiles = (n + 255u) / 256u;
+    if (x < m_tiles * n_blocks) {
+      const uint32_t mt = x % m_tiles;
+      *e_out = e;
+      *nb = x / m_tiles;
+      *row0 = lo + mt * 256u;
+      const uint32_t left = n - mt * 256u;
+      *rows = left < 256u ? left : 256u;
+      return true;
+    }
+    x -= m_tiles * n_blocks;
+  }
+  return false;
+}
+
+// Grid sizes (workgroups, a multiple of 8) of the gate/up and down launches
+// for experts [e_begin, e_end): routes/256 rounded up plus one partial tile
+// per expert bounds the m-tiles of any consistent routing.
+FE2O3_HD uint64_t expert_grid(uint64_t routes, uint32_t n_experts, uint32_t n_blocks) {
+  const uint64_t m_tiles = (routes + 255u) / 256u + n_experts;
+  return (m_tiles * n_blocks + 7u) / 8u * 8u;
+}
+
+}  // namespace fe2o3

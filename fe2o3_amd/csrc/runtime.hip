@@ -5,6 +5,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -39,6 +41,46 @@ static Registry& registry() {
 KernelRegistrar::KernelRegistrar(const KernelInfo& k) {
   Registry& r = registry();
   if (r.n < kMaxKernels) r.k[r.n++] = k;
+}
+
+// One contract-status word per device.  The reference's kernels trap on a
+// non-finite input and the fault surfaces when the host synchronizes; here
+// the kernel marks this word instead, writes its documented sentinel
+// outputs and exits normally, and the next fe2o3_rt_stream_synchronize or
+// fe2o3_rt_device_synchronize on the device reports FE2O3_ERR_NONFINITE.
+static __device__ __align__(256) uint32_t status_word_dev;
+
+static constexpr int kMaxDevices = 64;
+static std::mutex status_mu;
+static uint32_t* status_ptrs[kMaxDevices];
+
+uint32_t* status_word() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(status_mu);
+  if (status_ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(status_word_dev)) != hipSuccess) return nullptr;
+    status_ptrs[dev] = (uint32_t*)p;
+  }
+  return status_ptrs[dev];
+}
+
+// Reads and clears the current device's status word after a successful
+// synchronize.  The word is per device: a report from a kernel that finished
+// on another stream of the device is returned here too.
+static int32_t take_status(hipStream_t s) {
+  uint32_t* p = status_word();
+  if (p == nullptr) return (int32_t)hipErrorInvalidSymbol;
+  uint32_t v = 0;
+  hipError_t e = hipMemcpyAsync(&v, p, sizeof v, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return (int32_t)e;
+  if (v == 0) return FE2O3_OK;
+  e = hipMemsetAsync(p, 0, sizeof v, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return (int32_t)e;
+  return (v & kStatusNonFinite) ? FE2O3_ERR_NONFINITE : FE2O3_OK;
 }
 
 }  // namespace fe2o3_host
@@ -135,7 +177,11 @@ int32_t fe2o3_rt_require_gfx950(int32_t device_id) {
   return strncmp(p.gcnArchName, "gfx950", 6) == 0 ? FE2O3_OK : FE2O3_ERR_DEVICE;
 }
 
-int32_t fe2o3_rt_device_synchronize(void) { return (int32_t)hipDeviceSynchronize(); }
+int32_t fe2o3_rt_device_synchronize(void) {
+  const hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return (int32_t)e;
+  return fe2o3_host::take_status(nullptr);
+}
 
 int32_t fe2o3_rt_stream_create(void** stream) {
   if (stream == nullptr) return FE2O3_ERR_NULL;
@@ -150,7 +196,9 @@ int32_t fe2o3_rt_stream_destroy(void* stream) {
 }
 
 int32_t fe2o3_rt_stream_synchronize(void* stream) {
-  return (int32_t)hipStreamSynchronize((hipStream_t)stream);
+  const hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+  if (e != hipSuccess) return (int32_t)e;
+  return fe2o3_host::take_status((hipStream_t)stream);
 }
 
 int32_t fe2o3_rt_event_create(void** event, uint32_t flags) {

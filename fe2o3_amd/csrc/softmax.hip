@@ -6,6 +6,13 @@
 //   reference's DeviceMath::exp_f32), sum of w, out_i = w_i / sum (correctly
 //   rounded f32 division); masked elements -> +0.  A row without an active
 //   element is written as all +0.
+//   Non-finite input: the reference's contract rejects a row holding a NaN
+//   or an infinity anywhere, masked elements included
+//   (examples/row_softmax_v1/src/numerical_contract.rs:145-151).  Such a row
+//   is written as all quiet NaN (0x7fc00000) and the device's contract-status
+//   word is marked, so the host's next synchronize reports
+//   FE2O3_ERR_NONFINITE; other rows are unaffected.  The check is one FMA per
+//   element folded into the pass that already holds the row.
 //
 // One wave64 per row.  Rows of 256*NV columns (NV <= 32) live in registers:
 // each lane holds NV float4 chunks loaded with coalesced 16-byte accesses
@@ -26,7 +33,8 @@ template <int NV, bool MASK>
 __global__ void __launch_bounds__(256) softmax_reg_kernel(const float* __restrict__ in,
                                                           float* __restrict__ out,
                                                           const uint8_t* __restrict__ mask,
-                                                          uint64_t rows) {
+                                                          uint64_t rows,
+                                                          uint32_t* __restrict__ status) {
   const uint64_t row = (uint64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
   if (row >= rows) return;
   const uint32_t lane = threadIdx.x & 63u;
@@ -45,13 +53,18 @@ __global__ void __launch_bounds__(256) softmax_reg_kernel(const float* __restric
     return !MASK || ((act[j] >> (8 * e)) & 0xffu) != 0u;
   };
   float mx = -INFINITY;
+  f32x4_t probe = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
+    for (int e = 0; e < 4; ++e) {
+      probe[e] = finite_probe(probe[e], x[j][e]);
       if (active(j, e)) mx = fmaxf(mx, x[j][e]);
+    }
   }
   mx = wave_max(mx);
+  const float pr = (probe[0] + probe[1]) + (probe[2] + probe[3]);
+  const bool rejected = __ballot(pr != pr) != 0ull;
   float sum = 0.0f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
@@ -62,6 +75,13 @@ __global__ void __launch_bounds__(256) softmax_reg_kernel(const float* __restric
   sum = wave_sum(sum);
   const bool any = mx != -INFINITY;
   f32x4_t* dst = reinterpret_cast<f32x4_t*>(out + row * cols) + lane;
+  if (rejected) {
+    if (lane == 0) mark_nonfinite(status);
+    const float nan = quiet_nan();
+#pragma unroll
+    for (int j = 0; j < NV; ++j) __builtin_nontemporal_store(f32x4_t{nan, nan, nan, nan}, dst + 64 * j);
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     f32x4_t y;
@@ -74,33 +94,41 @@ __global__ void __launch_bounds__(256) softmax_reg_kernel(const float* __restric
 __global__ void __launch_bounds__(256) softmax_strided_kernel(const float* __restrict__ in,
                                                               float* __restrict__ out,
                                                               const uint8_t* __restrict__ mask,
-                                                              uint64_t rows, uint64_t cols) {
+                                                              uint64_t rows, uint64_t cols,
+                                                              uint32_t* __restrict__ status) {
   const uint64_t row = (uint64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
   if (row >= rows) return;
   const uint32_t lane = threadIdx.x & 63u;
   const float* x = in + row * cols;
   const uint8_t* m = mask ? mask + row * cols : nullptr;
-  float mx = -INFINITY;
-  for (uint64_t c = lane; c < cols; c += 64)
+  float* y = out + row * cols;
+  float mx = -INFINITY, probe = 0.0f;
+  for (uint64_t c = lane; c < cols; c += 64) {
+    probe = finite_probe(probe, x[c]);
     if (!m || m[c]) mx = fmaxf(mx, x[c]);
+  }
+  if (__ballot(probe != probe) != 0ull) {
+    if (lane == 0) mark_nonfinite(status);
+    for (uint64_t c = lane; c < cols; c += 64) y[c] = quiet_nan();
+    return;
+  }
   mx = wave_max(mx);
   float sum = 0.0f;
   for (uint64_t c = lane; c < cols; c += 64)
     if (!m || m[c]) sum += expf(x[c] - mx);
   sum = wave_sum(sum);
   const bool any = mx != -INFINITY;
-  float* y = out + row * cols;
   for (uint64_t c = lane; c < cols; c += 64)
     y[c] = (any && (!m || m[c])) ? expf(x[c] - mx) / sum : 0.0f;
 }
 
 template <int NV>
 void launch_reg(const float* in, float* out, const uint8_t* mask, uint64_t rows, dim3 grid,
-                hipStream_t s) {
+                uint32_t* status, hipStream_t s) {
   if (mask)
-    softmax_reg_kernel<NV, true><<<grid, 256, 0, s>>>(in, out, mask, rows);
+    softmax_reg_kernel<NV, true><<<grid, 256, 0, s>>>(in, out, mask, rows, status);
   else
-    softmax_reg_kernel<NV, false><<<grid, 256, 0, s>>>(in, out, mask, rows);
+    softmax_reg_kernel<NV, false><<<grid, 256, 0, s>>>(in, out, mask, rows, status);
 }
 
 int32_t row_softmax(const float* input, uint64_t input_len, float* output, uint64_t output_len,
@@ -116,22 +144,24 @@ int32_t row_softmax(const float* input, uint64_t input_len, float* output, uint6
   if (blocks > 0x7fffffffu) return FE2O3_ERR_SHAPE;
   const dim3 grid((unsigned)blocks);
   hipStream_t s = (hipStream_t)stream;
+  uint32_t* status = fe2o3_host::status_word();
+  if (status == nullptr) return (int32_t)hipErrorInvalidSymbol;
   const bool aligned = ((uintptr_t)input & 15u) == 0 && ((uintptr_t)output & 15u) == 0 &&
                        (!mask || ((uintptr_t)mask & 3u) == 0);
   if (aligned && cols % 256 == 0 && cols <= 256 * 32) {
     switch (cols / 256) {
-      case 1: launch_reg<1>(input, output, mask, rows, grid, s); break;
-      case 2: launch_reg<2>(input, output, mask, rows, grid, s); break;
-      case 4: launch_reg<4>(input, output, mask, rows, grid, s); break;
-      case 8: launch_reg<8>(input, output, mask, rows, grid, s); break;
-      case 16: launch_reg<16>(input, output, mask, rows, grid, s); break;
-      case 32: launch_reg<32>(input, output, mask, rows, grid, s); break;
+      case 1: launch_reg<1>(input, output, mask, rows, grid, status, s); break;
+      case 2: launch_reg<2>(input, output, mask, rows, grid, status, s); break;
+      case 4: launch_reg<4>(input, output, mask, rows, grid, status, s); break;
+      case 8: launch_reg<8>(input, output, mask, rows, grid, status, s); break;
+      case 16: launch_reg<16>(input, output, mask, rows, grid, status, s); break;
+      case 32: launch_reg<32>(input, output, mask, rows, grid, status, s); break;
       default:
-        softmax_strided_kernel<<<grid, 256, 0, s>>>(input, output, mask, rows, cols);
+        softmax_strided_kernel<<<grid, 256, 0, s>>>(input, output, mask, rows, cols, status);
         break;
     }
   } else {
-    softmax_strided_kernel<<<grid, 256, 0, s>>>(input, output, mask, rows, cols);
+    softmax_strided_kernel<<<grid, 256, 0, s>>>(input, output, mask, rows, cols, status);
   }
   return fe2o3_host::after_launch();
 }

@@ -103,6 +103,20 @@ int32_t fe2o3_rt_device_rates(int32_t device_id, int32_t *compute_units,
                               int32_t *memory_bus_bits);
 /* Fails with FE2O3_ERR_DEVICE unless the device's arch name starts "gfx950". */
 int32_t fe2o3_rt_require_gfx950(int32_t device_id);
+/* Non-finite inputs.  The reference's kernels that admit only finite inputs
+ * trap, and the fault surfaces when the host synchronizes
+ * (examples/moe_top2_v1/src/kernel.rs:126-128,
+ * examples/flash_attention_v1/src/kernel.rs:143-146; the row-softmax
+ * contract rejects them, examples/row_softmax_v1/src/numerical_contract.rs:149).
+ * Here such a kernel (fe2o3_row_softmax_v1, fe2o3_row_softmax,
+ * fe2o3_flash_attention_causal_f32_b1_h1_n8_d16_v1, both top-2 routers)
+ * writes the sentinel outputs its declaration states, marks the device's
+ * contract-status word and exits normally; the next successful
+ * fe2o3_rt_device_synchronize or fe2o3_rt_stream_synchronize on that device
+ * returns FE2O3_ERR_NONFINITE and clears the word.  The word is per device,
+ * like the reference's context-wide fault: a synchronize reports what any
+ * kernel that finished before it on the device found, whichever stream
+ * launched it.  Event synchronization does not read the word. */
 int32_t fe2o3_rt_device_synchronize(void);
 
 /* lib.rs:109-111: hipStreamCreate / Destroy / Synchronize. */
@@ -299,9 +313,14 @@ int32_t fe2o3_moe_expert_combine_f32_t8_k2_o16_v1(
  * and out[t] = bf16( sum over ranks of w_r * y_r ) (dropped routes add 0).
  * x [tokens, hidden] bf16; w_gate, w_up [experts, ffn, hidden] bf16;
  * w_down [experts, hidden, ffn] bf16; routing arrays as produced by
- * fe2o3_moe_top2_route; out [tokens, hidden] bf16.  hidden and ffn must be
- * multiples of 256.  workspace: device scratch of at least
- * fe2o3_moe_ffn_workspace_bytes(tokens, hidden, ffn, experts) bytes. */
+ * fe2o3_moe_top2_route; out [tokens, hidden] bf16.  hidden must be a
+ * multiple of 256 and ffn a multiple of 128.  workspace: device scratch of
+ * at least fe2o3_moe_ffn_workspace_bytes(tokens, hidden, ffn, experts)
+ * bytes.  The routing arrays are device data the host cannot validate: a
+ * routing that fails fe2o3_moe_routing_check gives unspecified outputs, but
+ * every access stays inside the caller's buffers and the workspace (offsets
+ * are clamped to [0, 2*tokens]; slot and permutation entries out of range
+ * count as dropped). */
 uint64_t fe2o3_moe_ffn_workspace_bytes(uint32_t tokens, uint32_t hidden,
                                        uint32_t ffn, uint32_t experts);
 int32_t fe2o3_moe_ffn_top2(const uint16_t *x, uint64_t x_len,

@@ -229,6 +229,14 @@ int32_t fe2o3o_moe_expert_pipeline_v1(
 void fe2o3o_moe_ffn_route(const uint16_t *x, const uint16_t *w_gate,
                           const uint16_t *w_up, const uint16_t *w_down,
                           uint32_t h, uint32_t f, uint16_t *hidden, float *y);
+/* The same for n (token, expert) pairs, OpenMP over pairs (hidden not
+ * kept): x [tokens, H]; weights as above with a leading expert index;
+ * y [n, H]. */
+void fe2o3o_moe_ffn_routes(const uint16_t *x, const uint16_t *w_gate,
+                           const uint16_t *w_up, const uint16_t *w_down,
+                           uint32_t h, uint32_t f, const uint32_t *tokens,
+                           const uint32_t *experts, uint64_t n, float *y,
+                           int32_t threads);
 
 /* ---- OCP FP8 E4M3FN ------------------------------------------------------ */
 uint8_t fe2o3o_fp8e4m3_from_f32(float value);

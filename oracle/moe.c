@@ -293,37 +293,61 @@ int32_t fe2o3o_moe_expert_pipeline_v1(
 /* SiLU expert FFN (not in the reference): g = x.Wg^T, u = x.Wu^T in
  * sequential f32 (same recurrence as the expert GEMM oracle above),
  * hidden = bf16(silu(g) * u) with silu(g) = g / (1 + exp(-g)), then
- * y = hidden.Wd^T in sequential f32. */
+ * y = hidden.Wd^T in sequential f32.  FB outputs are computed side by side
+ * (independent accumulators, each still summed over i = 0, 1, ... in
+ * order), which vectorises across outputs without changing any result. */
+#define FFN_FB 8
 void fe2o3o_moe_ffn_route(const uint16_t *x, const uint16_t *w_gate,
                           const uint16_t *w_up, const uint16_t *w_down,
                           uint32_t h, uint32_t f, uint16_t *hidden, float *y) {
   float *xf = (float *)malloc(sizeof(float) * h);
   float *hf = (float *)malloc(sizeof(float) * f);
   for (uint32_t i = 0; i < h; ++i) xf[i] = fe2o3o_bf16_to_f32(x[i]);
-  for (uint32_t j = 0; j < f; ++j) {
-    const uint16_t *wg = w_gate + (uint64_t)j * h;
-    const uint16_t *wu = w_up + (uint64_t)j * h;
-    float g = 0.0f, u = 0.0f;
+  for (uint32_t j0 = 0; j0 < f; j0 += FFN_FB) {
+    const uint32_t nb = f - j0 < FFN_FB ? f - j0 : FFN_FB;
+    float g[FFN_FB] = {0}, u[FFN_FB] = {0};
     for (uint32_t i = 0; i < h; ++i) {
-      float pg = xf[i] * fe2o3o_bf16_to_f32(wg[i]);
-      g = g + pg;
-      float pu = xf[i] * fe2o3o_bf16_to_f32(wu[i]);
-      u = u + pu;
+      for (uint32_t jj = 0; jj < nb; ++jj) {
+        float pg = xf[i] * fe2o3o_bf16_to_f32(w_gate[(uint64_t)(j0 + jj) * h + i]);
+        g[jj] = g[jj] + pg;
+        float pu = xf[i] * fe2o3o_bf16_to_f32(w_up[(uint64_t)(j0 + jj) * h + i]);
+        u[jj] = u[jj] + pu;
+      }
     }
-    float sg = g / (1.0f + expf(-g));
-    uint16_t hb = fe2o3o_bf16_from_f32(sg * u);
-    hidden[j] = hb;
-    hf[j] = fe2o3o_bf16_to_f32(hb);
+    for (uint32_t jj = 0; jj < nb; ++jj) {
+      float sg = g[jj] / (1.0f + expf(-g[jj]));
+      uint16_t hb = fe2o3o_bf16_from_f32(sg * u[jj]);
+      if (hidden) hidden[j0 + jj] = hb;
+      hf[j0 + jj] = fe2o3o_bf16_to_f32(hb);
+    }
   }
-  for (uint32_t i = 0; i < h; ++i) {
-    const uint16_t *wd = w_down + (uint64_t)i * f;
-    float acc = 0.0f;
+  for (uint32_t i0 = 0; i0 < h; i0 += FFN_FB) {
+    const uint32_t nb = h - i0 < FFN_FB ? h - i0 : FFN_FB;
+    float acc[FFN_FB] = {0};
     for (uint32_t j = 0; j < f; ++j) {
-      float p = hf[j] * fe2o3o_bf16_to_f32(wd[j]);
-      acc = acc + p;
+      for (uint32_t ii = 0; ii < nb; ++ii) {
+        float p = hf[j] * fe2o3o_bf16_to_f32(w_down[(uint64_t)(i0 + ii) * f + j]);
+        acc[ii] = acc[ii] + p;
+      }
     }
-    y[i] = acc;
+    for (uint32_t ii = 0; ii < nb; ++ii) y[i0 + ii] = acc[ii];
   }
   free(xf);
   free(hf);
+}
+
+/* fe2o3o_moe_ffn_route for n (token, expert) pairs at once, spread over
+ * `threads` OpenMP threads: x [tokens, h]; w_gate, w_up [E, F, H];
+ * w_down [E, H, F]; y [n, h] receives each pair's f32 expert output. */
+void fe2o3o_moe_ffn_routes(const uint16_t *x, const uint16_t *w_gate,
+                           const uint16_t *w_up, const uint16_t *w_down,
+                           uint32_t h, uint32_t f, const uint32_t *tokens,
+                           const uint32_t *experts, uint64_t n, float *y,
+                           int32_t threads) {
+  const uint64_t wsz = (uint64_t)f * h;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
+  for (uint64_t r = 0; r < n; ++r)
+    fe2o3o_moe_ffn_route(x + (uint64_t)tokens[r] * h, w_gate + experts[r] * wsz,
+                         w_up + experts[r] * wsz, w_down + experts[r] * wsz, h, f, NULL,
+                         y + r * h);
 }

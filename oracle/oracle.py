@@ -115,6 +115,8 @@ def _declare(L):
         "fe2o3o_moe_expert_pipeline_v1": (
             i32, [vp, vp, u64, vp, u64, vp, u64, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
         "fe2o3o_moe_ffn_route": (None, [u16p, u16p, u16p, u16p, u32, u32, u16p, f32p]),
+        "fe2o3o_moe_ffn_routes": (None, [u16p, u16p, u16p, u16p, u32, u32, u32p, u32p, u64, f32p,
+                                         i32]),
         "fe2o3o_fp8e4m3_from_f32": (C.c_uint8, [f32]),
         "fe2o3o_fp8e4m3_to_f32": (f32, [C.c_uint8]),
         "fe2o3o_amax_f32": (f32, [f32p, u64, i32]),
@@ -455,6 +457,17 @@ def moe_ffn_route(x, w_gate, w_up, w_down, h, f):
                                _c(w_up, np.uint16).ravel(), _c(w_down, np.uint16).ravel(), h, f,
                                hidden, y)
     return hidden, y
+
+
+def moe_ffn_routes(x, w_gate, w_up, w_down, h, f, tokens, experts, threads=0):
+    """Expert outputs y [n, h] (f32) of the (token, expert) pairs; x is
+    [tokens, h] bf16 bits, weights [E, F, H] / [E, H, F]."""
+    tok, exp = _c(tokens, np.uint32).ravel(), _c(experts, np.uint32).ravel()
+    y = np.zeros((tok.size, h), np.float32)
+    lib().fe2o3o_moe_ffn_routes(_c(x, np.uint16).ravel(), _c(w_gate, np.uint16).ravel(),
+                                _c(w_up, np.uint16).ravel(), _c(w_down, np.uint16).ravel(), h, f,
+                                tok, exp, tok.size, y.ravel(), threads or _threads())
+    return y
 
 
 # ---- fp8 -------------------------------------------------------------------------

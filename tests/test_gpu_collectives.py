@@ -223,11 +223,36 @@ def test_routing_check_reference_mutations(gpu, oracle):
     cases = [("expert_offsets", 2, 3), ("admitted_counts", 0, 5), ("route_slots", 8, 0),
              ("inverse", 8, 0), ("permutation", 8, 0), ("route_slots", 0, 16),
              ("permutation", 0, 2), ("inverse", 0, 1), ("requested_counts", 0, 7),
-             ("top2_experts", 5, 4), ("top2_experts", 5, 0)]
+             ("top2_experts", 5, 4), ("top2_experts", 5, 0),
+             ("permutation", 9, 0), ("permutation", 15, 0)]
     for key, i, value in cases:
         m = {k: np.array(v, np.uint32) for k, v in base.items()}
         m[key][i] = value
-        assert _device_check(gpu, m, 8, 4, 4) == _oracle_check(oracle, m, 8, 4, 4), (key, i)
+        want = _oracle_check(oracle, m, 8, 4, 4)
+        assert want[0] != 0, (key, i)
+        assert _device_check(gpu, m, 8, 4, 4) == want, (key, i)
+
+
+def test_routing_check_every_permutation_tail_slot(gpu, oracle):
+    """A capacity-limited routing (4096 tokens, 8 experts, capacity 700, so
+    the permutation has a long sentinel tail): a non-sentinel value planted
+    in each tail slot in turn is reported as PermutationTail at that slot,
+    as the oracle reports it."""
+    tokens, experts, capacity = 4096, 8, 700
+    rng = np.random.default_rng(11)
+    rc, base = oracle.moe_top2_route(rng.standard_normal((tokens, experts)).astype(np.float32),
+                                     tokens, experts, capacity)
+    assert rc == 0
+    accepted = int(base["expert_offsets"][-1])
+    assert accepted < 2 * tokens - 200
+    tail = list(range(accepted, 2 * tokens))
+    picks = tail[:130] + tail[-130:] + [int(x) for x in rng.choice(tail, 40, replace=False)]
+    for s in picks:
+        m = {k: np.array(v, np.uint32) for k, v in base.items()}
+        m["permutation"][s] = 3
+        want = _oracle_check(oracle, m, tokens, experts, capacity)
+        assert want[0] == 18 and want[1] == s, (s, want)
+        assert _device_check(gpu, m, tokens, experts, capacity) == want, s
 
 
 def test_routing_check_garbage_payloads_are_safe(gpu, oracle):

@@ -209,6 +209,52 @@ def test_moe_ffn_few_experts(gpu, oracle, experts):
     assert worst <= 1e-2, worst
 
 
+@pytest.mark.parametrize("ffn", [384, 640])
+def test_moe_ffn_odd_128_blocks(gpu, oracle, ffn):
+    """ffn an odd multiple of 128 (the smallest granule the entry point
+    admits): an odd number of 128-wide gate/up blocks, and down-projection
+    k-halves of 192 or 320, an odd number of 64-k pipeline stages."""
+    tokens, hidden, experts = 300, 256, 4
+    worst, _ = _ffn_case(gpu, oracle, tokens, hidden, ffn, experts, 0xFFFFFFFF, range(tokens))
+    assert worst <= 1e-2, worst
+
+
+def test_moe_ffn_garbage_routing_stays_in_bounds(gpu, oracle):
+    """Routing arrays that fail the consistency check (random offsets, some
+    decreasing or beyond 2*tokens; permutation and inverse entries out of
+    range) give unspecified outputs, but every access stays inside the
+    caller's buffers: the output and workspace guards stay intact and the
+    inputs unchanged.  (Bounds of the tile list for any offsets are shown on
+    the CPU by tests/test_moe_tiles.py.)"""
+    kern = _k()
+    tokens, hidden, ffn, experts = 200, 256, 256, 8
+    rng = np.random.default_rng(17)
+    routes = 2 * tokens
+    x = Guarded(gpu, oracle.bf16_from_f32(rng.standard_normal(tokens * hidden)))
+    w = [Guarded(gpu, oracle.bf16_from_f32(rng.standard_normal(experts * ffn * hidden) * 0.02))
+         for _ in range(3)]
+    wsb = kern.moe_ffn_workspace_bytes(tokens, hidden, ffn, experts)
+    for trial in range(6):
+        offsets = rng.integers(0, routes + 300, experts + 1).astype(np.uint32)
+        if trial % 2:
+            offsets = np.sort(offsets)
+        routing = {
+            "top2": Guarded(gpu, rng.integers(0, 2**32, routes, dtype=np.uint64).astype(np.uint32)),
+            "offsets": Guarded(gpu, offsets),
+            "permutation": Guarded(gpu, rng.integers(0, routes + 50, routes).astype(np.uint32)),
+            "inverse": Guarded(gpu, rng.integers(0, routes + 50, routes).astype(np.uint32)),
+            "weights": Guarded(gpu, rng.random(routes).astype(np.float32)),
+        }
+        out = Guarded(gpu, np.full(tokens * hidden, 0x7FDE, np.uint16))
+        ws = Guarded(gpu, np.zeros(wsb, np.uint8))
+        kern.moe_ffn_top2(x.body, w[0].body, w[1].body, w[2].body,
+                          {k: v.body for k, v in routing.items()}, out.body, ws.body, tokens,
+                          hidden, ffn, experts)
+        assert out.guards_intact() and ws.guards_intact(), trial
+        assert x.unchanged() and all(t.unchanged() for t in w)
+        assert all(v.unchanged() for v in routing.values())
+
+
 def test_moe_ffn_small_with_drops(gpu, oracle):
     """Capacity below demand: dropped routes contribute nothing."""
     tokens, hidden, ffn, experts = 256, 256, 256, 8
