@@ -82,6 +82,7 @@ SIGNATURES = {
     "fe2o3_fill_normal_f32": (i32, [vp, u64, u64, u64, f32, u64, vp]),
     "fe2o3_fill_uniform_f32": (i32, [vp, u64, u64, u64, u64, vp]),
     "fe2o3_tiled_gemm_lds_slice1_v1": (i32, [vp, u64, vp, u64, vp, u64, vp]),
+    "fe2o3_tiled_gemm_v1": (i32, [vp, u64, vp, u64, vp, u64, u32, u32, u32, vp]),
     "fe2o3_tiled_gemm_general_v1": (
         i32, [vp, u64, vp, u64, vp, u64, u32, u32, u32, u32, u32, u32, f32, f32, vp]),
     "fe2o3_scalar_gemm_v1": (i32, [vp, u64, vp, u64, vp, u64, u32, u32, u32, vp]),

@@ -55,6 +55,50 @@ __global__ void __launch_bounds__(64) tile16_bf16_kernel(const uint16_t* __restr
   for (int i = 0; i < 4; ++i) c[(row0 + i) * 16 + col] = acc[i];
 }
 
+// ---- exact-tile multi-tile GEMM (tiled_gemm_v1 plan) ---------------------------------
+// C[M,N] f32 = A[M,K] bf16 (row-major) * B[K,N] bf16 (row-major), M, N, K
+// multiples of 16.  One wave64 per 16x16 output tile, as the reference's plan
+// assigns (examples/tiled_gemm_v1/src/contract.rs:387-427); workgroup id ->
+// (tile column, tile row) = (id % tile_cols, id / tile_cols).  Each
+// v_mfma_f32_16x16x32_bf16 consumes two 16-deep reduction tiles; with an odd
+// count the last MFMA's upper half is zero.  Operand lanes: A row l%16 and
+// B column l%16, k chunk 8*(l/16) .. +7 of the 32-deep step, read straight
+// from global memory (a chunk lies wholly inside or wholly past K).  The
+// output lane map is tile16_bf16_kernel's.
+__global__ void __launch_bounds__(64) tiled_v1_kernel(const uint16_t* __restrict__ a,
+                                                      const uint16_t* __restrict__ b,
+                                                      float* __restrict__ c, uint32_t n,
+                                                      uint32_t k, uint32_t tile_cols) {
+  const uint32_t l = threadIdx.x;
+  const uint32_t tr = blockIdx.x / tile_cols, tc = blockIdx.x % tile_cols;
+  const uint32_t rc = l & 15u, chunk = l >> 4;
+  const uint16_t* arow = a + (uint64_t)(tr * 16u + rc) * k;
+  const uint16_t* bcol = b + tc * 16u + rc;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (uint32_t kk = 0; kk < k; kk += 32u) {
+    const uint32_t k0 = kk + 8u * chunk;
+    bf16x8_t af = {}, bf = {};
+    if (k0 < k) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        af[i] = __builtin_bit_cast(__bf16, arow[k0 + i]);
+        bf[i] = __builtin_bit_cast(__bf16, bcol[(uint64_t)(k0 + i) * n]);
+      }
+    }
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf, acc, 0, 0, 0);
+  }
+  float* ctile = c + (uint64_t)(tr * 16u + 4u * chunk) * n + tc * 16u + rc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ctile[(uint64_t)i * n] = acc[i];
+}
+
+// +0 fill of the plan's K = 0 case (a kernel rather than a memset, so the
+// call can sit inside a captured graph).
+__global__ void __launch_bounds__(256) zero_fill_kernel(float* __restrict__ c, uint64_t n) {
+  for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256u)
+    c[i] = 0.0f;
+}
+
 // ---- general bf16 GEMM with alpha/beta -----------------------------------------------
 // C[r*ldc+j] = alpha * (A B)[r][j] + beta * C[r*ldc+j] for r < m, j < n.
 // A row-major (lda), B row-major [k][n] (ldb).  Workgroup tile 64x64, K step
@@ -216,6 +260,8 @@ int32_t tile16(const uint16_t* a, uint64_t a_len, const uint16_t* b, uint64_t b_
 const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_lds_slice1_v1", "tile16_bf16_kernel", (const void*)tile16_bf16_kernel, 64, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_expert_gemm_bf16_m16_n16_k16_v1", "tile16_bf16_kernel", (const void*)tile16_bf16_kernel, 64, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_v1", "tiled_v1_kernel", (const void*)tiled_v1_kernel, 64, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_v1", "zero_fill_kernel", (const void*)zero_fill_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_kernel", (const void*)gemm_general_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_scalar_gemm_v1", "scalar_gemm_kernel", (const void*)scalar_gemm_kernel, 256, 0})};
 
@@ -236,6 +282,37 @@ int32_t fe2o3_moe_expert_gemm_bf16_m16_n16_k16_v1(const uint16_t* activations,
                                                   void* stream) {
   FE2O3_FAULT("fe2o3_moe_expert_gemm_bf16_m16_n16_k16_v1");
   return tile16(activations, activations_len, weights, weights_len, output, output_len, stream);
+}
+
+int32_t fe2o3_tiled_gemm_v1(const uint16_t* a, uint64_t a_len, const uint16_t* b, uint64_t b_len,
+                            float* c, uint64_t c_len, uint32_t m, uint32_t n, uint32_t k,
+                            void* stream) {
+  FE2O3_FAULT("fe2o3_tiled_gemm_v1");
+  // ShapeV1::checked (contract.rs:145-179): an empty output needs no
+  // operand buffers; otherwise byte extents of A, B, C in that order
+  if (m == 0 || n == 0) {
+    if (a_len != 0 || b_len != 0 || c_len != 0) return FE2O3_ERR_LENGTH;
+    return FE2O3_OK;  // NoDispatchEmptyOutput
+  }
+  const uint64_t ea = (uint64_t)m * k, eb = (uint64_t)k * n, ec = (uint64_t)m * n;
+  if (ea > UINT64_MAX / 2 || eb > UINT64_MAX / 2 || ec > UINT64_MAX / 4) return FE2O3_ERR_OVERFLOW;
+  if (a_len != ea || b_len != eb || c_len != ec) return FE2O3_ERR_LENGTH;
+  // plan_v1 (contract.rs:387-427), in its order
+  if (m % 16u != 0) return FE2O3_ERR_M_TAIL;
+  if (n % 16u != 0) return FE2O3_ERR_N_TAIL;
+  if (k != 0 && k % 16u != 0) return FE2O3_ERR_K_TAIL;
+  if ((uint64_t)(n / 16u) * 64u > UINT32_MAX) return FE2O3_ERR_OVERFLOW;  // AQL grid x
+  if (!c || (k != 0 && (!a || !b))) return FE2O3_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  if (k == 0) {  // HostFillPositiveZero
+    const uint64_t blocks = (ec + 255u) / 256u;
+    zero_fill_kernel<<<(unsigned)(blocks < 4096u ? blocks : 4096u), 256, 0, s>>>(c, ec);
+    return fe2o3_host::after_launch();
+  }
+  const uint64_t tiles = (uint64_t)(m / 16u) * (n / 16u);
+  if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
+  tiled_v1_kernel<<<(unsigned)tiles, 64, 0, s>>>(a, b, c, n, k, n / 16u);
+  return fe2o3_host::after_launch();
 }
 
 int32_t fe2o3_tiled_gemm_general_v1(const uint16_t* a, uint64_t a_len, const uint16_t* b,

@@ -103,6 +103,9 @@ const char* fe2o3_status_string(int32_t status) {
     case FE2O3_ERR_ALIGNMENT: return "pointer misaligned for this entry point";
     case FE2O3_ERR_WORKSPACE: return "workspace too small";
     case FE2O3_ERR_INJECTED: return "failure injected by FE2O3_FAULT_POINT";
+    case FE2O3_ERR_M_TAIL: return "M is not a multiple of the 16-row tile";
+    case FE2O3_ERR_N_TAIL: return "N is not a multiple of the 16-column tile";
+    case FE2O3_ERR_K_TAIL: return "K is not a multiple of the 16-deep reduction tile";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);

@@ -94,6 +94,10 @@ u32, i32, f32 = C.c_uint32, C.c_int32, C.c_float
 # examples/tiled_gemm_v1/src/kernel.rs:63-67
 tiled_gemm_lds_slice1_gpu = _typed(
     "fe2o3_tiled_gemm_lds_slice1_v1", [("a", U16, 256), ("b", U16, 256), ("c", F32, 256)])
+# examples/tiled_gemm_v1/src/contract.rs:387-427 (the multi-tile plan)
+tiled_gemm_v1_gpu = _typed(
+    "fe2o3_tiled_gemm_v1", [("a", U16, None), ("b", U16, None), ("c", F32, None)],
+    [("m", u32), ("n", u32), ("k", u32)])
 # examples/tiled_gemm_general_v1/src/kernel.rs:67-79
 tiled_gemm_general_v1_gpu = _typed(
     "fe2o3_tiled_gemm_general_v1", [("a", U16, None), ("b", U16, None), ("c", F32, None)],

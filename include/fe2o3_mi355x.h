@@ -60,6 +60,9 @@ extern "C" {
 #define FE2O3_ERR_ALIGNMENT (-21)    /* pointer misaligned for the fast path   */
 #define FE2O3_ERR_WORKSPACE (-22)    /* workspace too small                    */
 #define FE2O3_ERR_INJECTED (-23)     /* FE2O3_FAULT_POINT forced a failure     */
+#define FE2O3_ERR_M_TAIL (-24)       /* M not a multiple of the 16-row tile    */
+#define FE2O3_ERR_N_TAIL (-25)       /* N not a multiple of the 16-column tile */
+#define FE2O3_ERR_K_TAIL (-26)       /* K not a multiple of the 16-deep tile   */
 
 /* Human-readable text for any status (HIP codes included).  Never NULL. */
 const char *fe2o3_status_string(int32_t status);
@@ -169,6 +172,25 @@ int32_t fe2o3_fill_uniform_f32(float *out, uint64_t n, uint64_t seed,
 int32_t fe2o3_tiled_gemm_lds_slice1_v1(const uint16_t *a, uint64_t a_len,
                                        const uint16_t *b, uint64_t b_len,
                                        float *c, uint64_t c_len, void *stream);
+
+/* The multi-tile LDS GEMM of examples/tiled_gemm_v1 under its checked plan
+ * (ShapeV1::checked and plan_v1, examples/tiled_gemm_v1/src/contract.rs:
+ * 145-179, 387-427): C[m,n] f32 = A[m,k] bf16 (row-major) * B[k,n] bf16
+ * (row-major), fp32 accumulation, one wave64 per 16x16 output tile.  The
+ * plan's outcomes, in its order:
+ *   m == 0 or n == 0  -> NoDispatchEmptyOutput: FE2O3_OK, nothing launched;
+ *                        the three lengths must be 0 (no operand buffers);
+ *   byte extents of A, B, C overflowing u64 -> FE2O3_ERR_OVERFLOW;
+ *   lengths other than m*k, k*n, m*n -> FE2O3_ERR_LENGTH;
+ *   m % 16 -> FE2O3_ERR_M_TAIL; n % 16 -> FE2O3_ERR_N_TAIL;
+ *   k == 0 -> HostFillPositiveZero: C is filled with +0 (by a kernel);
+ *   k % 16 -> FE2O3_ERR_K_TAIL; 64 * n/16 above u32 -> FE2O3_ERR_OVERFLOW;
+ *   otherwise Dispatch.
+ * On every error nothing is launched and C is untouched. */
+int32_t fe2o3_tiled_gemm_v1(const uint16_t *a, uint64_t a_len,
+                            const uint16_t *b, uint64_t b_len, float *c,
+                            uint64_t c_len, uint32_t m, uint32_t n, uint32_t k,
+                            void *stream);
 
 /* examples/tiled_gemm_general_v1/src/kernel.rs:67-79 tiled_gemm_general_v1:
  * c[r*ldc+j] = alpha * sum_d A[r*lda+d]*B[d*ldb+j] + beta * c[r*ldc+j] for

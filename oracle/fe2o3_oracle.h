@@ -250,6 +250,10 @@ void fe2o3o_gemm_fp8_points(uint32_t k, const uint8_t *a_rows,
                             const uint8_t *b_cols, uint64_t points,
                             float scale_ab, float *out_f32, uint16_t *out_bf16,
                             int32_t threads);
+/* Whole rows of the same product (f32 values before narrowing). */
+void fe2o3o_gemm_fp8_nt_rows(uint32_t n, uint32_t k, const uint8_t *a, const uint8_t *b,
+                             float scale_ab, uint32_t row_begin, uint32_t row_end,
+                             float *out_f32, int32_t threads);
 
 /* ---- collectives, workgroup sync, routing consistency (sync.c) ---- */
 

@@ -10,6 +10,7 @@
  * TEST INFRASTRUCTURE ONLY (the checker, never the product).
  */
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "fe2o3_oracle.h"
@@ -96,5 +97,49 @@ void fe2o3o_gemm_fp8_points(uint32_t k, const uint8_t *a_rows,
     float c = acc * scale_ab;
     if (out_f32) out_f32[p] = c;
     if (out_bf16) out_bf16[p] = fe2o3o_bf16_from_f32(c);
+  }
+}
+
+/* Whole output rows row_begin .. row_end-1 of the same recurrence as
+ * fe2o3o_gemm_fp8_points (A [m,k], B stored [n,k], both e4m3 bytes):
+ * FB8 outputs of a row are accumulated side by side, each from +0 over
+ * increasing depth with separate rounding, so every output equals the
+ * points form bit for bit.  out_f32 [(row_end-row_begin), n]. */
+#define FB8 16
+void fe2o3o_gemm_fp8_nt_rows(uint32_t n, uint32_t k, const uint8_t *a, const uint8_t *b,
+                             float scale_ab, uint32_t row_begin, uint32_t row_end,
+                             float *out_f32, int32_t threads) {
+  if (row_end <= row_begin) return;
+  float lut[256];
+  for (int i = 0; i < 256; ++i) lut[i] = fe2o3o_fp8e4m3_to_f32((uint8_t)i);
+  const uint32_t col_blocks = (n + FB8 - 1) / FB8;
+#pragma omp parallel num_threads(threads > 0 ? threads : 1)
+  {
+    float *bt = (float *)malloc(sizeof(float) * (size_t)k * FB8);
+    float *arow = (float *)malloc(sizeof(float) * (size_t)k);
+#pragma omp for schedule(dynamic, 1)
+    for (uint32_t cb = 0; cb < col_blocks; ++cb) {
+      const uint32_t c0 = cb * FB8, w = (n - c0) < FB8 ? (n - c0) : FB8;
+      for (uint32_t d = 0; d < k; ++d)
+        for (uint32_t j = 0; j < FB8; ++j)
+          bt[(size_t)d * FB8 + j] = j < w ? lut[b[(size_t)(c0 + j) * k + d]] : 0.0f;
+      for (uint32_t row = row_begin; row < row_end; ++row) {
+        for (uint32_t d = 0; d < k; ++d) arow[d] = lut[a[(size_t)row * k + d]];
+        float acc[FB8];
+        for (int j = 0; j < FB8; ++j) acc[j] = 0.0f;
+        for (uint32_t d = 0; d < k; ++d) {
+          const float av = arow[d];
+          const float *bv = bt + (size_t)d * FB8;
+          for (int j = 0; j < FB8; ++j) {
+            float p = av * bv[j];
+            acc[j] = acc[j] + p;
+          }
+        }
+        float *o = out_f32 + (size_t)(row - row_begin) * n + c0;
+        for (uint32_t j = 0; j < w; ++j) o[j] = acc[j] * scale_ab;
+      }
+    }
+    free(bt);
+    free(arow);
   }
 }

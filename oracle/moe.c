@@ -338,16 +338,95 @@ void fe2o3o_moe_ffn_route(const uint16_t *x, const uint16_t *w_gate,
 
 /* fe2o3o_moe_ffn_route for n (token, expert) pairs at once, spread over
  * `threads` OpenMP threads: x [tokens, h]; w_gate, w_up [E, F, H];
- * w_down [E, H, F]; y [n, h] receives each pair's f32 expert output. */
+ * w_down [E, H, F]; y [n, h] receives each pair's f32 expert output.  The
+ * pairs are grouped by expert and each expert's matrices are walked in
+ * panels of FFN_PB rows, transposed once to f32, so FFN_PB outputs of a
+ * route are accumulated side by side; every output keeps the single-route
+ * order (+0, then i = 0, 1, ... with separate rounding), so the results are
+ * those of fe2o3o_moe_ffn_route bit for bit. */
+#define FFN_PB 16
 void fe2o3o_moe_ffn_routes(const uint16_t *x, const uint16_t *w_gate,
                            const uint16_t *w_up, const uint16_t *w_down,
                            uint32_t h, uint32_t f, const uint32_t *tokens,
                            const uint32_t *experts, uint64_t n, float *y,
                            int32_t threads) {
   const uint64_t wsz = (uint64_t)f * h;
-#pragma omp parallel for schedule(dynamic, 1) num_threads(threads > 0 ? threads : 1)
-  for (uint64_t r = 0; r < n; ++r)
-    fe2o3o_moe_ffn_route(x + (uint64_t)tokens[r] * h, w_gate + experts[r] * wsz,
-                         w_up + experts[r] * wsz, w_down + experts[r] * wsz, h, f, NULL,
-                         y + r * h);
+  uint32_t max_e = 0;
+  for (uint64_t r = 0; r < n; ++r) max_e = experts[r] > max_e ? experts[r] : max_e;
+  uint64_t *idx = (uint64_t *)malloc(sizeof(uint64_t) * (n ? n : 1));
+  for (uint32_t e = 0; e <= max_e && n; ++e) {
+    uint64_t cnt = 0;
+    for (uint64_t r = 0; r < n; ++r)
+      if (experts[r] == e) idx[cnt++] = r;
+    if (cnt == 0) continue;
+    const uint16_t *wg = w_gate + e * wsz, *wu = w_up + e * wsz, *wd = w_down + e * wsz;
+    float *xf = (float *)malloc(sizeof(float) * cnt * h);
+    float *hf = (float *)malloc(sizeof(float) * cnt * f);
+    for (uint64_t t = 0; t < cnt; ++t)
+      for (uint32_t i = 0; i < h; ++i)
+        xf[t * h + i] = fe2o3o_bf16_to_f32(x[(uint64_t)tokens[idx[t]] * h + i]);
+#pragma omp parallel num_threads(threads > 0 ? threads : 1)
+    {
+      float *pg = (float *)malloc(sizeof(float) * (size_t)h * FFN_PB);
+      float *pu = (float *)malloc(sizeof(float) * (size_t)h * FFN_PB);
+      float *pd = (float *)malloc(sizeof(float) * (size_t)f * FFN_PB);
+#pragma omp for schedule(dynamic, 1)
+      for (uint32_t j0 = 0; j0 < f; j0 += FFN_PB) {
+        const uint32_t nb = f - j0 < FFN_PB ? f - j0 : FFN_PB;
+        for (uint32_t i = 0; i < h; ++i)
+          for (uint32_t jj = 0; jj < FFN_PB; ++jj) {
+            const uint64_t at = (uint64_t)(j0 + jj) * h + i;
+            pg[(size_t)i * FFN_PB + jj] = jj < nb ? fe2o3o_bf16_to_f32(wg[at]) : 0.0f;
+            pu[(size_t)i * FFN_PB + jj] = jj < nb ? fe2o3o_bf16_to_f32(wu[at]) : 0.0f;
+          }
+        for (uint64_t t = 0; t < cnt; ++t) {
+          float g[FFN_PB], u[FFN_PB];
+          for (int jj = 0; jj < FFN_PB; ++jj) g[jj] = u[jj] = 0.0f;
+          const float *xr = xf + t * h;
+          for (uint32_t i = 0; i < h; ++i) {
+            const float xv = xr[i];
+            const float *gv = pg + (size_t)i * FFN_PB, *uv = pu + (size_t)i * FFN_PB;
+            for (int jj = 0; jj < FFN_PB; ++jj) {
+              float a = xv * gv[jj];
+              g[jj] = g[jj] + a;
+              float b = xv * uv[jj];
+              u[jj] = u[jj] + b;
+            }
+          }
+          for (uint32_t jj = 0; jj < nb; ++jj) {
+            float sg = g[jj] / (1.0f + expf(-g[jj]));
+            hf[t * f + j0 + jj] = fe2o3o_bf16_to_f32(fe2o3o_bf16_from_f32(sg * u[jj]));
+          }
+        }
+      }
+#pragma omp for schedule(dynamic, 1)
+      for (uint32_t i0 = 0; i0 < h; i0 += FFN_PB) {
+        const uint32_t nb = h - i0 < FFN_PB ? h - i0 : FFN_PB;
+        for (uint32_t j = 0; j < f; ++j)
+          for (uint32_t ii = 0; ii < FFN_PB; ++ii)
+            pd[(size_t)j * FFN_PB + ii] =
+                ii < nb ? fe2o3o_bf16_to_f32(wd[(uint64_t)(i0 + ii) * f + j]) : 0.0f;
+        for (uint64_t t = 0; t < cnt; ++t) {
+          float acc[FFN_PB];
+          for (int ii = 0; ii < FFN_PB; ++ii) acc[ii] = 0.0f;
+          const float *hr = hf + t * f;
+          for (uint32_t j = 0; j < f; ++j) {
+            const float hv = hr[j];
+            const float *dv = pd + (size_t)j * FFN_PB;
+            for (int ii = 0; ii < FFN_PB; ++ii) {
+              float p = hv * dv[ii];
+              acc[ii] = acc[ii] + p;
+            }
+          }
+          for (uint32_t ii = 0; ii < nb; ++ii) y[idx[t] * h + i0 + ii] = acc[ii];
+        }
+      }
+      free(pg);
+      free(pu);
+      free(pd);
+    }
+    free(xf);
+    free(hf);
+  }
+  free(idx);
 }

@@ -122,6 +122,7 @@ def _declare(L):
         "fe2o3o_amax_f32": (f32, [f32p, u64, i32]),
         "fe2o3o_quantize_e4m3": (None, [f32p, u64, f32, u8p, i32]),
         "fe2o3o_gemm_fp8_points": (None, [u32, u8p, u8p, u64, f32, f32p, u16p, i32]),
+        "fe2o3o_gemm_fp8_nt_rows": (None, [u32, u32, u8p, u8p, f32, u32, u32, f32p, i32]),
         "fe2o3o_wave64_collectives_compute": (None, [f32p, u64, f32p, f32p, f32p]),
         "fe2o3o_wave64_collectives_v1": (i32, [f32p, u64, f32p, f32p, f32p]),
         "fe2o3o_lds_reduce_i32_v1": (i32, [vp, vp]),
@@ -504,6 +505,15 @@ def gemm_fp8_points(k, a_rows, b_cols, scale_ab, threads=0):
     lib().fe2o3o_gemm_fp8_points(k, a_rows.ravel(), b_cols.ravel(), p, scale_ab, of, ob,
                                  threads or _threads())
     return of, ob
+
+
+def gemm_fp8_nt_rows(n, k, a, b, scale_ab, row_begin, row_end, threads=0):
+    """f32 values (before bf16 narrowing) of output rows row_begin..row_end-1
+    of (sa*sb) * A_q B_q^T; a is [m, k], b [n, k] e4m3 bytes."""
+    out = np.zeros((row_end - row_begin) * n, np.float32)
+    lib().fe2o3o_gemm_fp8_nt_rows(n, k, _c(a, np.uint8).ravel(), _c(b, np.uint8).ravel(),
+                                  scale_ab, row_begin, row_end, out, threads or _threads())
+    return out.reshape(row_end - row_begin, n)
 
 
 # ---- collectives, workgroup sync, routing consistency (sync.c) ----------------------------

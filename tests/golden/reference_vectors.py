@@ -399,3 +399,29 @@ def flash_hardware_vectors_v1():
         k[r * d] = 8.0 if r == 3 else -8.0
     dominant = (q, k, np.array([(f(i % d) - f(7.0)) / f(4.0) for i in range(e)], np.float32))
     return [("nominal", *nominal), ("equal", *equal), ("dominant", *dominant)]
+
+
+# examples/tiled_gemm_v1/src/contract.rs:458-536 (EDGE_CASES_V1): name, m, n,
+# k and the required plan outcome ("no-dispatch", "host-fill", "dispatch", or
+# the rejection "m-tail" / "n-tail" / "k-tail")
+EDGE_CASES_V1 = [
+    ("all-zero", 0, 0, 0, "no-dispatch"),
+    ("zero-m-with-k-tail", 0, 17, 3, "no-dispatch"),
+    ("zero-n", 32, 0, 16, "no-dispatch"),
+    ("zero-k", 16, 32, 0, "host-fill"),
+    ("single-tile", 16, 16, 16, "dispatch"),
+    ("rectangular-multi-tile", 32, 48, 32, "dispatch"),
+    ("three-reduction-tiles", 16, 16, 48, "dispatch"),
+    ("m-tail", 17, 16, 16, "m-tail"),
+    ("n-tail", 16, 31, 16, "n-tail"),
+    ("k-tail-below-one-tile", 16, 16, 15, "k-tail"),
+    ("k-tail-after-one-tile", 16, 16, 17, "k-tail"),
+]
+
+# examples/tiled_gemm_v1/tests/contract.rs:64-101: empty outputs with extreme
+# unused extents plan no dispatch; nonempty extremes overflow the byte
+# accounting of A, then B, then C
+EXTREME_EMPTY_V1 = [(0, 0xFFFFFFFF, 0xFFFFFFFF), (0xFFFFFFFF, 0, 0xFFFFFFFF),
+                    (0, 0, 0xFFFFFFFF), (0, 1, 1), (1, 0, 1), (0, 17, 3), (31, 0, 17)]
+BYTE_OVERFLOW_V1 = [(0xFFFFFFFF, 1, 0xFFFFFFFF, "A"), (1, 0xFFFFFFFF, 0xFFFFFFFF, "B"),
+                    (0xFFFFFFFF, 0xFFFFFFFF, 1, "C")]

@@ -127,3 +127,39 @@ def test_typed_prepare_rejects_wrong_element_type():
     with pytest.raises(TypeError):
         k.prepare(fake, fake, fake)
     fake.ptr = None
+
+
+def test_tiled_gemm_v1_plan_without_gpu():
+    """examples/tiled_gemm_v1's plan_v1 outcomes that launch nothing, through
+    the C-ABI entry point (validation runs before any HIP call): every
+    EDGE_CASES_V1 row that plans no dispatch or a rejection, the extreme
+    empty shapes (no operand buffers), the A/B/C byte-overflow order, wrong
+    lengths, and empty outputs that name operand buffers."""
+    from golden import reference_vectors as rv
+    from fe2o3_amd import _lib
+    L = _lib.lib()
+    code = {"m-tail": -24, "n-tail": -25, "k-tail": -26, "no-dispatch": 0}
+    seen = set()
+    for name, m, n, k, outcome in rv.EDGE_CASES_V1:
+        if outcome not in code:
+            continue
+        empty = m == 0 or n == 0
+        la, lb, lc = (0, 0, 0) if empty else (m * k, k * n, m * n)
+        assert L.fe2o3_tiled_gemm_v1(None, la, None, lb, None, lc, m, n, k, None) == code[outcome], name
+        seen.add(outcome)
+    assert seen == set(code)
+    for m, n, k in rv.EXTREME_EMPTY_V1:
+        assert L.fe2o3_tiled_gemm_v1(None, 0, None, 0, None, 0, m, n, k, None) == 0
+        # an empty output requires zero-length operands
+        assert L.fe2o3_tiled_gemm_v1(None, 1, None, 0, None, 0, m, n, k, None) == -2
+    for m, n, k, _ in rv.BYTE_OVERFLOW_V1:
+        assert L.fe2o3_tiled_gemm_v1(None, 0, None, 0, None, 0, m, n, k, None) == -16
+    assert L.fe2o3_tiled_gemm_v1(None, 255, None, 256, None, 256, 16, 16, 16, None) == -2
+    # a tail is reported after the lengths are checked, M before N before K
+    assert L.fe2o3_tiled_gemm_v1(None, 17 * 15, None, 15 * 31, None, 17 * 31, 17, 31, 15,
+                                 None) == -24
+    assert L.fe2o3_tiled_gemm_v1(None, 16 * 15, None, 15 * 31, None, 16 * 31, 16, 31, 15,
+                                 None) == -25
+    # K = 0 with tails in M or N still rejects; K = 0 itself is a host fill
+    assert L.fe2o3_tiled_gemm_v1(None, 0, None, 0, None, 17 * 16, 17, 16, 0, None) == -24
+    assert b"16-row tile" in L.fe2o3_status_string(-24)

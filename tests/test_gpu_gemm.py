@@ -284,11 +284,10 @@ def test_gemm_bf16_nt_staged_epilogue(gpu, oracle):
 
 def test_gemm_bf16_nt_config2_4096(gpu, oracle):
     """BASELINE config 2 (bf16 4096^3, A row-major, B column-major,
-    N(0,1)/sqrt(K), seed 1): 64 full output rows spread over every tile row
-    and a column sample checked against the sequential fp32 oracle."""
+    N(0,1)/sqrt(K), seed 1): every one of the 16.8M outputs against the
+    sequential fp32 oracle (rel-err and per-element bounds)."""
     m = n = k = 4096
-    rows = [t * 256 + (t * 37) % 256 for t in range(16)] + [0, 255, 4095, 2048]
-    _nt_case(gpu, oracle, m, n, k, seed=1, rows=rows)
+    _nt_case(gpu, oracle, m, n, k, seed=1)
 
 
 def test_gemm_bf16_nt_rejects_bad_lengths(gpu):

@@ -172,25 +172,17 @@ def _ffn_case(gpu, oracle, tokens, hidden, ffn, experts, capacity, sample_tokens
     if callable(sample_tokens):
         sample_tokens = sample_tokens(routing["offsets"].download(),
                                       routing["permutation"].download())
-    worst = 0.0
-    cache = {}
-
-    def expert_weights(e):
-        if e not in cache:
-            off = e * ffn * hidden
-            cache[e] = tuple(t.view(off, ffn * hidden).download() for t in (wg, wu, wd))
-        return cache[e]
-
-    for t in sample_tokens:
-        ref = np.zeros(hidden, np.float32)
-        for rank in range(2):
-            r = 2 * t + rank
-            if inv[r] == 0xFFFFFFFF:
-                continue
-            g_, u_, d_ = expert_weights(int(top2[r]))
-            _, y = oracle.moe_ffn_route(xs[t], g_, u_, d_, hidden, ffn)
-            ref = ref + np.float32(w[r]) * y
-        worst = max(worst, rel_err(got[t], ref))
+    toks = np.array(list(sample_tokens), np.int64)
+    hw = [t.download() for t in (wg, wu, wd)]
+    pairs = [(int(t), 2 * int(t) + rank) for t in toks for rank in range(2)
+             if inv[2 * int(t) + rank] != 0xFFFFFFFF]
+    y = oracle.moe_ffn_routes(xs, hw[0], hw[1], hw[2], hidden, ffn,
+                              np.array([p[0] for p in pairs], np.uint32),
+                              np.array([top2[p[1]] for p in pairs], np.uint32))
+    refs = {int(t): np.zeros(hidden, np.float32) for t in toks}
+    for (t, r), yr in zip(pairs, y):  # +0, then each admitted rank in order
+        refs[t] = refs[t] + np.float32(w[r]) * yr
+    worst = max(rel_err(got[t], refs[int(t)]) for t in toks)
     return worst, inv
 
 
@@ -291,11 +283,24 @@ def test_moe_ffn_short_last_tiles(gpu, oracle):
     assert worst <= 1e-2, worst
 
 
+def _per_expert_tokens(per):
+    """Tokens of the first `per` slots of every expert plus those of its last
+    `per` slots (so each expert's first and last m-tiles are covered)."""
+    def pick(offsets, permutation):
+        rows = set()
+        for e in range(len(offsets) - 1):
+            lo, hi = int(offsets[e]), int(offsets[e + 1])
+            rows.update(range(lo, min(hi, lo + per)))
+            rows.update(range(max(lo, hi - per), hi))
+        return sorted({int(permutation[r]) >> 1 for r in rows})
+    return pick
+
+
 def test_moe_ffn_config5_sampled_tokens(gpu, oracle):
     """4096 tokens, hidden 4096, 8 experts, FFN 14336,
-    weights N(0, 0.02), unbounded capacity; 12 tokens checked end to end."""
-    worst, _ = _ffn_case(gpu, oracle, 4096, 4096, 14336, 8, 0xFFFFFFFF,
-                         [0, 1, 511, 1024, 2047, 2048, 3000, 3333, 4000, 4093, 4094, 4095])
+    weights N(0, 0.02), unbounded capacity; the tokens of the first 64 and
+    the last 64 slots of every expert (both routes of each) end to end."""
+    worst, _ = _ffn_case(gpu, oracle, 4096, 4096, 14336, 8, 0xFFFFFFFF, _per_expert_tokens(64))
     assert worst <= 1e-2, worst
 
 
@@ -346,7 +351,10 @@ def test_amax_scale_and_quantize_bit_exact(gpu, oracle):
     assert_same(q.download(), oracle.quantize_e4m3(xh, float(s_ref)), "quantized")
 
 
-def _fp8_case(gpu, oracle, m, n, k, points):
+def _fp8_case(gpu, oracle, m, n, k, points, block=None):
+    """rel-err of the device GEMM at `points` (rows, cols); the outputs of
+    whole rows block[0]..block[1]-1 among them come from the row-block form
+    of the oracle, the rest from the per-point form."""
     kern = _k()
     a32 = gpu.alloc(m * k, np.float32)
     b32 = gpu.alloc(n * k, np.float32)
@@ -365,8 +373,15 @@ def _fp8_case(gpu, oracle, m, n, k, points):
     ah, bh = aq.download().reshape(m, k), bq.download().reshape(n, k)
     sab = float(np.float32(sa.download()[0] * sb.download()[0]))
     rows, cols = points
-    ref_f32, _ = oracle.gemm_fp8_points(k, ah[rows], bh[cols], sab)
-    return rel_err(got[rows, cols], ref_f32)
+    if block is None:
+        ref_f32, _ = oracle.gemm_fp8_points(k, ah[rows], bh[cols], sab)
+        return rel_err(got[rows, cols], ref_f32)
+    inb = (rows >= block[0]) & (rows < block[1])
+    ref_blk = oracle.gemm_fp8_nt_rows(n, k, ah, bh, sab, block[0], block[1])
+    ref_pts, _ = oracle.gemm_fp8_points(k, ah[rows[~inb]], bh[cols[~inb]], sab)
+    got_all = np.concatenate([got[rows[~inb], cols[~inb]], got[rows[inb], cols[inb]]])
+    ref_all = np.concatenate([ref_pts, ref_blk[rows[inb] - block[0], cols[inb]]])
+    return rel_err(got_all, ref_all)
 
 
 @pytest.mark.parametrize("m,n,k", [(256, 256, 128), (512, 768, 1024), (256, 512, 4096),
@@ -377,13 +392,15 @@ def test_gemm_fp8_all_outputs(gpu, oracle, m, n, k):
 
 
 def test_gemm_fp8_config4_sampled(gpu, oracle):
-    """8192^3 e4m3 with amax/448 per-tensor scales; 4096
-    sampled outputs at full K plus one full 128-row block."""
+    """8192^3 e4m3 with amax/448 per-tensor scales; one
+    whole 128-row block (rows 4096..4223, all 8192 columns: 1M outputs at
+    full K) plus 4096 random outputs."""
     m = n = k = 8192
     rng = np.random.default_rng(4)
-    rows = np.concatenate([rng.integers(0, m, 4096), np.repeat(np.arange(4096, 4096 + 128), 64)])
-    cols = np.concatenate([rng.integers(0, n, 4096), np.tile(rng.integers(0, n, 64), 128)])
-    assert _fp8_case(gpu, oracle, m, n, k, (rows, cols)) <= 1e-2
+    rr, cc = np.meshgrid(np.arange(4096, 4096 + 128), np.arange(n), indexing="ij")
+    rows = np.concatenate([rng.integers(0, m, 4096), rr.ravel()])
+    cols = np.concatenate([rng.integers(0, n, 4096), cc.ravel()])
+    assert _fp8_case(gpu, oracle, m, n, k, (rows, cols), block=(4096, 4096 + 128)) <= 1e-2
 
 
 def test_gemm_fp8_staged_epilogue(gpu, oracle):

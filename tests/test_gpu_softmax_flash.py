@@ -100,22 +100,34 @@ def test_row_softmax_rows_against_oracle(gpu, oracle, rows, cols, masked):
 
 
 def test_row_softmax_config3c_rows_sum_to_one(gpu, oracle):
-    """Config 3c distribution (N(0,1) logits, 4096 columns) at 65536 rows:
-    every row sums to 1 within the reference's 6e-5 and a row sample
-    matches the oracle under the OCML policy."""
-    rows, cols = 65536, 4096
+    """BASELINE config 3c at full size: 1,048,576 rows x 4096 fp32 (the
+    bench's N(0,1) input, seed 3).  Every row sums to 1 within the
+    reference's 6e-5 (read back in 1 GiB chunks), and 1024 rows spread over
+    all chunks, first and last rows included, match the oracle element by
+    element under the OCML policy."""
+    rows, cols = 8 * 32 * 4096, 4096
     kern = _k()
     x = gpu.alloc(rows * cols, np.float32)
     kern.fill_normal_f32(x, 3, 0x50F7, 1.0)
     y = gpu.alloc(rows * cols, np.float32)
     kern.row_softmax_gpu.Kernel.load(gpu).prepare(x, y, None, rows, cols).launch()
-    out = y.download().reshape(rows, cols)
-    sums = out.astype(np.float64).sum(axis=1)
-    assert np.all(np.abs(sums - 1.0) <= 6e-5)
-    xs = oracle.fill_normal_f32(rows * cols, 3, 0x50F7, 1.0).reshape(rows, cols)
-    for r in (0, 1, 4097, rows - 1):
-        rc, ref, _ = oracle.row_softmax_oracle_v1(xs[r])
-        assert oracle.compare_row_softmax_v1(ref, out[r], **oracle.GFX_SOFTMAX_POLICY)[0] == 0
+    chunk = 65536
+    checked = 0
+    for c0 in range(0, rows, chunk):
+        out = y.view(c0 * cols, chunk * cols).download().reshape(chunk, cols)
+        sums = np.sum(out, axis=1, dtype=np.float64)
+        bad = np.nonzero(np.abs(sums - 1.0) > 6e-5)[0]
+        assert bad.size == 0, (c0 + int(bad[0]), float(sums[bad[0]]))
+        picks = sorted({0, chunk - 1} | {int(v) for v in np.random.default_rng(c0).choice(
+            np.arange(1, chunk - 1), 62, replace=False)})
+        xs = x.view(c0 * cols, chunk * cols).download().reshape(chunk, cols)[picks]
+        rc, ref = oracle.row_softmax_rows(xs, len(picks), cols)
+        assert rc == 0
+        for i, r in enumerate(picks):
+            assert oracle.compare_row_softmax_v1(ref[i], out[r], **oracle.GFX_SOFTMAX_POLICY)[0] == 0, \
+                c0 + r
+        checked += len(picks)
+    assert checked >= 1024
 
 
 def test_row_softmax_rejects_zero_cols(gpu):
@@ -196,25 +208,33 @@ def test_flash_small_all_rows(gpu, oracle, b, h, s, causal):
     assert rc == 0
     got = out.reshape(-1, 128)
     assert rel_err(got, ref) <= 1e-2
-    assert np.max(np.abs(lse - ref_lse)) <= 1e-3
+    assert rel_err(lse, ref_lse) <= 1e-5  # fp32 output: the 1e-5 bar
 
 
 @pytest.mark.parametrize("causal", [False, True])
 def test_flash_config3_sampled_rows(gpu, oracle, causal):
     """B8 H32 S4096 D128, Q/K/V ~ N(0,1) bf16, scale
-    1/sqrt(128); 8 query rows (incl. first, last and tile edges) in each of
-    16 heads spread over every batch, against the two-pass f64 oracle."""
+    1/sqrt(128), against the two-pass f64 oracle with the LSE: 8 query rows
+    in every one of the 256 (batch, head), one per 512-row band at a
+    position that varies with the head, plus 64 rows (first, last and
+    128-row tile edges among them) in 16 heads spread over every batch."""
     b, h, s = 8, 32, 4096
     (q, k, v), out, lse, scale = _flash(gpu, b, h, s, causal, seed=2)
+    per = 8
+    bh_all = np.repeat(np.arange(b * h, dtype=np.uint32), per)
+    band = np.tile(np.arange(per, dtype=np.uint32), b * h)
+    rows_all = band * (s // per) + (bh_all * 67 + band * 131) % (s // per)
     heads = [i * 16 + (i * 5) % 16 for i in range(16)]
-    qrows = [0, 1, 127, 128, 2047, 2048, 4094, 4095]
-    bh = np.array([hh for hh in heads for _ in qrows], np.uint32)
-    rows = np.array(qrows * len(heads), np.uint32)
+    qrows = sorted({0, 1, 127, 128, 2047, 2048, 4094, 4095} |
+                   {int(r) for r in np.random.default_rng(3).integers(0, s, 56)})
+    qrows = (qrows + [255, 256, 383, 384, 511, 512, 3967, 3968])[:64]
+    bh = np.concatenate([bh_all, np.array([hh for hh in heads for _ in qrows], np.uint32)])
+    rows = np.concatenate([rows_all, np.array(qrows * len(heads), np.uint32)]).astype(np.uint32)
     rc, ref, ref_lse = oracle.flash_attention_rows_bf16(q, k, v, s, 128, causal, scale, bh, rows)
     assert rc == 0
     got = out.reshape(b * h, s, 128)[bh, rows]
     assert rel_err(got, ref) <= 1e-2
-    assert np.max(np.abs(lse.reshape(b * h, s)[bh, rows] - ref_lse)) <= 1e-3
+    assert rel_err(lse.reshape(b * h, s)[bh, rows], ref_lse) <= 1e-5  # fp32 output: the 1e-5 bar
 
 
 def test_flash_causal_ignores_future_keys(gpu):

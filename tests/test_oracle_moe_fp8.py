@@ -226,3 +226,44 @@ def test_fp8_gemm_points_closed_form(oracle):
     exact = (table[qa] @ table[qb].T)[ii, jj] * float(sa * sb)
     assert np.allclose(of, exact, rtol=1e-5, atol=1e-4)
     assert np.array_equal(ob, oracle.bf16_from_f32(of))
+
+
+def test_fp8_rows_equal_points_form(oracle):
+    """The row-block fp8 GEMM oracle (used for whole-row parity at config 4)
+    equals the per-point form bit for bit, on a tail column block too."""
+    rng = np.random.default_rng(1)
+    m, n, k = 5, 37, 300
+    a = rng.integers(0, 256, m * k).astype(np.uint8)
+    b = rng.integers(0, 256, n * k).astype(np.uint8)
+    a[(a & 0x7F) == 0x7F] = 0  # no NaN encodings
+    b[(b & 0x7F) == 0x7F] = 0
+    rows = oracle.gemm_fp8_nt_rows(n, k, a, b, 0.37, 1, 4)
+    ii, jj = np.meshgrid(np.arange(1, 4), np.arange(n), indexing="ij")
+    of, _ = oracle.gemm_fp8_points(k, a.reshape(m, k)[ii.ravel()], b.reshape(n, k)[jj.ravel()],
+                                   0.37)
+    assert rows.ravel().view(np.uint32).tolist() == of.view(np.uint32).tolist()
+
+
+def test_moe_ffn_routes_equal_single_route(oracle):
+    """The OpenMP batch of expert FFN routes equals the single-route form
+    bit for bit, and the single-route form equals a float64 evaluation of
+    silu(x Wg^T) * (x Wu^T) then Wd within the bf16 rounding of the hidden
+    activation."""
+    rng = np.random.default_rng(2)
+    tokens, h, f, e = 6, 64, 40, 3
+    x = oracle.bf16_from_f32(rng.standard_normal(tokens * h)).reshape(tokens, h)
+    wg, wu, wd = (oracle.bf16_from_f32(rng.standard_normal(e * f * h) * 0.1) for _ in range(3))
+    tok = np.array([0, 5, 2, 2, 4], np.uint32)
+    exp_ = np.array([1, 0, 2, 1, 2], np.uint32)
+    y = oracle.moe_ffn_routes(x, wg, wu, wd, h, f, tok, exp_)
+    for r, (t, ex) in enumerate(zip(tok, exp_)):
+        sl = slice(int(ex) * f * h, (int(ex) + 1) * f * h)
+        hid, y1 = oracle.moe_ffn_route(x[t], wg[sl], wu[sl], wd[sl], h, f)
+        assert y[r].view(np.uint32).tolist() == y1.view(np.uint32).tolist()
+        xf = oracle.bf16_to_f32(x[t]).astype(np.float64)
+        g = oracle.bf16_to_f32(wg[sl]).reshape(f, h).astype(np.float64) @ xf
+        u = oracle.bf16_to_f32(wu[sl]).reshape(f, h).astype(np.float64) @ xf
+        hv = g / (1.0 + np.exp(-g)) * u
+        assert np.max(np.abs(oracle.bf16_to_f32(hid) - hv)) <= 2.0 ** -7 * np.max(np.abs(hv))
+        ref = oracle.bf16_to_f32(wd[sl]).reshape(h, f).astype(np.float64) @ oracle.bf16_to_f32(hid)
+        assert np.max(np.abs(y1 - ref)) <= 1e-5 * np.max(np.abs(ref))
