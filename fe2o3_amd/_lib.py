@@ -105,6 +105,9 @@ SIGNATURES = {
     "fe2o3_moe_ffn_top2": (
         i32, [vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64,
               vp, u64, vp, u64, u32, u32, u32, u32, vp]),
+    "fe2o3_moe_ffn_top2_noalloc": (
+        i32, [vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64,
+              vp, u64, u32, u32, u32, u32, vp]),
     "fe2o3_amax_f32": (i32, [vp, u64, vp, vp]),
     "fe2o3_fp8_scale_from_amax": (i32, [vp, vp, vp]),
     "fe2o3_quantize_e4m3": (i32, [vp, u64, vp, vp, u64, vp]),

@@ -591,6 +591,10 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "gate_up_kernel", (const void*)gate_up_kernel, 256, kSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "down_kernel", (const void*)down_kernel, 256, kSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "combine_kernel", (const void*)combine_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2_noalloc", "gather_kernel", (const void*)gather_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2_noalloc", "gate_up_kernel", (const void*)gate_up_kernel, 256, kSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2_noalloc", "down_kernel", (const void*)down_kernel, 256, kSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2_noalloc", "combine_kernel", (const void*)combine_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_routing_check", "routing_check_kernel", (const void*)routing_check_kernel, ASSIGN_THREADS, CHECK_MAX_ROUTES * 4})};
 
 // The expert FFN's second stream, one per device, created on first use and
@@ -677,19 +681,22 @@ uint64_t fe2o3_moe_ffn_workspace_bytes(uint32_t tokens, uint32_t hidden, uint32_
   return carve(nullptr, tokens, hidden, ffn).bytes;
 }
 
-int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate,
-                           uint64_t w_gate_len, const uint16_t* w_up, uint64_t w_up_len,
-                           const uint16_t* w_down, uint64_t w_down_len,
-                           const uint32_t* top2_experts, uint64_t top2_len,
-                           const uint32_t* expert_offsets, uint64_t offsets_len,
-                           const uint32_t* permutation, uint64_t permutation_len,
-                           const uint32_t* inverse, uint64_t inverse_len,
-                           const float* route_weights, uint64_t weights_len, uint16_t* out,
-                           uint64_t out_len, void* workspace, uint64_t workspace_bytes,
-                           uint32_t tokens, uint32_t hidden, uint32_t ffn, uint32_t experts,
-                           void* stream) {
-  FE2O3_FAULT("fe2o3_moe_ffn_top2");
-  (void)top2_experts;
+}  // extern "C"
+
+namespace {
+
+// The expert FFN behind both C-ABI entry points.  `split_streams` runs the
+// second half of the experts on the per-device side stream (created on
+// first use); without it every kernel runs on the caller's stream and the
+// call creates nothing.
+int32_t ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate, uint64_t w_gate_len,
+                 const uint16_t* w_up, uint64_t w_up_len, const uint16_t* w_down,
+                 uint64_t w_down_len, uint64_t top2_len, const uint32_t* expert_offsets,
+                 uint64_t offsets_len, const uint32_t* permutation, uint64_t permutation_len,
+                 const uint32_t* inverse, uint64_t inverse_len, const float* route_weights,
+                 uint64_t weights_len, uint16_t* out, uint64_t out_len, void* workspace,
+                 uint64_t workspace_bytes, uint32_t tokens, uint32_t hidden, uint32_t ffn,
+                 uint32_t experts, bool split_streams, void* stream) {
   if (experts < 1 || experts > MAX_EXPERTS) return FE2O3_ERR_SHAPE;
   // hidden: 256-column output blocks of the down GEMM; ffn: 128-wide gate/up
   // blocks, and each k-half of the down GEMM a whole number of 64-k stages
@@ -741,7 +748,7 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_
   // Two halves of the experts, each gate/up then down, on the caller's
   // stream and on a side stream: each grouped GEMM ends in a partly filled
   // round of tiles, which the other half's tiles fill.
-  SideStream* side = experts >= 2 ? side_stream() : nullptr;
+  SideStream* side = split_streams && experts >= 2 ? side_stream() : nullptr;
   if (side != nullptr) {
     std::lock_guard<std::mutex> lock(side->mu);  // keeps one call's event waits its own
     const uint32_t half = experts / 2u;
@@ -760,6 +767,74 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_
   combine_kernel<<<(unsigned)((threads + 255u) / 256u), 256, 0, s>>>(ws.yc, inverse, route_weights,
                                                                     tokens, hidden, routes, out);
   return fe2o3_host::after_launch();
+}
+
+// Scratch of the allocation-free FFN entry point: a file-scope device array,
+// one copy per device, held from library load to process end.  Host code
+// uses only the address hipGetSymbolAddress returns for the current device
+// (the array's name on the host is a stand-in, not a device address).
+constexpr uint64_t kNoAllocScratchBytes = FE2O3_MOE_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+void* noalloc_scratch() {
+  static constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate,
+                           uint64_t w_gate_len, const uint16_t* w_up, uint64_t w_up_len,
+                           const uint16_t* w_down, uint64_t w_down_len,
+                           const uint32_t* top2_experts, uint64_t top2_len,
+                           const uint32_t* expert_offsets, uint64_t offsets_len,
+                           const uint32_t* permutation, uint64_t permutation_len,
+                           const uint32_t* inverse, uint64_t inverse_len,
+                           const float* route_weights, uint64_t weights_len, uint16_t* out,
+                           uint64_t out_len, void* workspace, uint64_t workspace_bytes,
+                           uint32_t tokens, uint32_t hidden, uint32_t ffn, uint32_t experts,
+                           void* stream) {
+  FE2O3_FAULT("fe2o3_moe_ffn_top2");
+  (void)top2_experts;
+  return ffn_top2(x, x_len, w_gate, w_gate_len, w_up, w_up_len, w_down, w_down_len, top2_len,
+                  expert_offsets, offsets_len, permutation, permutation_len, inverse, inverse_len,
+                  route_weights, weights_len, out, out_len, workspace, workspace_bytes, tokens,
+                  hidden, ffn, experts, true, stream);
+}
+
+int32_t fe2o3_moe_ffn_top2_noalloc(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate,
+                                   uint64_t w_gate_len, const uint16_t* w_up, uint64_t w_up_len,
+                                   const uint16_t* w_down, uint64_t w_down_len,
+                                   const uint32_t* top2_experts, uint64_t top2_len,
+                                   const uint32_t* expert_offsets, uint64_t offsets_len,
+                                   const uint32_t* permutation, uint64_t permutation_len,
+                                   const uint32_t* inverse, uint64_t inverse_len,
+                                   const float* route_weights, uint64_t weights_len,
+                                   uint16_t* out, uint64_t out_len, uint32_t tokens,
+                                   uint32_t hidden, uint32_t ffn, uint32_t experts,
+                                   void* stream) {
+  FE2O3_FAULT("fe2o3_moe_ffn_top2_noalloc");
+  (void)top2_experts;
+  if (fe2o3_moe_ffn_workspace_bytes(tokens, hidden, ffn, experts) > kNoAllocScratchBytes)
+    return FE2O3_ERR_WORKSPACE;
+  void* ws = noalloc_scratch();
+  if (ws == nullptr) return (int32_t)hipErrorInvalidSymbol;
+  return ffn_top2(x, x_len, w_gate, w_gate_len, w_up, w_up_len, w_down, w_down_len, top2_len,
+                  expert_offsets, offsets_len, permutation, permutation_len, inverse, inverse_len,
+                  route_weights, weights_len, out, out_len, ws, kNoAllocScratchBytes, tokens,
+                  hidden, ffn, experts, false, stream);
 }
 
 int32_t fe2o3_moe_routing_check(const uint32_t* top2_experts, uint64_t top2_len,

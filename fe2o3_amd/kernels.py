@@ -183,6 +183,16 @@ def moe_ffn_top2(x, w_gate, w_up, w_down, routing: dict, out, workspace, tokens,
           stream=stream, sync=sync)
 
 
+def moe_ffn_top2_noalloc(x, w_gate, w_up, w_down, routing: dict, out, tokens, hidden, ffn,
+                         experts, stream=None, sync=True) -> None:
+    """fe2o3_moe_ffn_top2 without a workspace argument: the library's own
+    per-device scratch (FE2O3_MOE_NOALLOC_SCRATCH_BYTES), no allocation."""
+    _call("fe2o3_moe_ffn_top2_noalloc", *_ps(x), *_ps(w_gate), *_ps(w_up), *_ps(w_down),
+          *_ps(routing["top2"]), *_ps(routing["offsets"]), *_ps(routing["permutation"]),
+          *_ps(routing["inverse"]), *_ps(routing["weights"]), *_ps(out), tokens, hidden, ffn,
+          experts, stream=stream, sync=sync)
+
+
 def amax_f32(x: DeviceBuffer, amax: DeviceBuffer, stream=None, sync=True) -> None:
     _call("fe2o3_amax_f32", x.ptr, x.count, amax.ptr, stream=stream, sync=sync)
 

@@ -359,6 +359,30 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t *x, uint64_t x_len,
                            uint32_t hidden, uint32_t ffn, uint32_t experts,
                            void *stream);
 
+/* Allocation-free variant of fe2o3_moe_ffn_top2.  It has no counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as fe2o3_moe_ffn_top2 without the
+ * workspace: the scratch is a library-owned device array of 64 MiB per GPU
+ * (FE2O3_MOE_NOALLOC_SCRATCH_BYTES), held from library load to process end,
+ * so fe2o3_moe_ffn_workspace_bytes(tokens, hidden, ffn, experts) must not
+ * exceed it (else FE2O3_ERR_WORKSPACE; e.g. up to 481 tokens at hidden 4096,
+ * ffn 14336).  The call launches every kernel on `stream` and allocates or
+ * creates nothing (no memory, stream or event).  Every call on a GPU shares
+ * that GPU's scratch, so calls that overlap on one GPU (different streams,
+ * or host threads) race and must be serialized by the caller; no part of
+ * the scratch needs to start at zero (each call writes every row it reads). */
+#define FE2O3_MOE_NOALLOC_SCRATCH_BYTES (UINT64_C(64) << 20)
+int32_t fe2o3_moe_ffn_top2_noalloc(
+    const uint16_t *x, uint64_t x_len, const uint16_t *w_gate, uint64_t w_gate_len,
+    const uint16_t *w_up, uint64_t w_up_len, const uint16_t *w_down,
+    uint64_t w_down_len, const uint32_t *top2_experts, uint64_t top2_len,
+    const uint32_t *expert_offsets, uint64_t offsets_len,
+    const uint32_t *permutation, uint64_t permutation_len,
+    const uint32_t *inverse, uint64_t inverse_len, const float *route_weights,
+    uint64_t weights_len, uint16_t *out, uint64_t out_len, uint32_t tokens,
+    uint32_t hidden, uint32_t ffn, uint32_t experts, void *stream);
+
 /* ---- fp8 (OCP E4M3FN, per-tensor scale) ---------------------------------------------
  * Not in the reference (its only fp8 type is gfx942 FNUZ,
  * crates/fe2o3-device/src/fp8.rs:53-110, which gfx950's MFMA does not take):
