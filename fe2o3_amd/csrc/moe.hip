@@ -214,11 +214,43 @@ __global__ void __launch_bounds__(256) gather_kernel(const uint16_t* __restrict_
   for (uint32_t i = threadIdx.x; i < hidden / 8; i += blockDim.x) dst[i] = src[i];
 }
 
+// This workgroup's entry of the expert tile list (moe_tiles.hpp), computed
+// by each wave as expert_tile_lanes spells out: lane l loads expert
+// e_begin + l's row bounds (one memory round trip for all experts, where the
+// serial walk took two dependent scalar loads per expert, ~8% of a gate/up
+// tile), a wave scan sums the tile counts, a ballot finds the entry's
+// expert, and lane reads return its bounds as wave-uniform values.
 FE2O3_DEVICE bool expert_tile(const uint32_t* offsets, uint32_t e_begin, uint32_t e_end,
                               uint32_t routes, uint32_t n_blocks, uint32_t* e_out, uint32_t* row0,
                               uint32_t* rows, uint32_t* nb) {
-  return expert_tile_at(offsets, e_begin, e_end, routes, n_blocks, blockIdx.x, e_out, row0, rows,
-                        nb);
+  const uint32_t l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  uint32_t lo = 0, n = 0;
+  if (l < e_end - e_begin) expert_rows(offsets, e_begin + l, routes, &lo, &n);
+  uint32_t incl = (n + 255u) / 256u * n_blocks;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t v = (uint32_t)__shfl_up((int)incl, o, 64);
+    if (l >= (uint32_t)o) incl += v;
+  }
+  const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+  const uint32_t chunk = (total + 7u) / 8u;
+  const uint32_t slot = blockIdx.x >> 3;
+  if (slot >= chunk) return false;
+  const uint32_t x = (blockIdx.x & 7u) * chunk + slot;
+  if (x >= total) return false;
+  const int le = (int)__builtin_popcountll(__ballot(incl <= x));
+  const uint32_t lo_e = (uint32_t)__builtin_amdgcn_readlane((int)lo, le);
+  const uint32_t n_e = (uint32_t)__builtin_amdgcn_readlane((int)n, le);
+  const uint32_t incl_e = (uint32_t)__builtin_amdgcn_readlane((int)incl, le);
+  const uint32_t m_tiles = (n_e + 255u) / 256u;
+  const uint32_t xi = x - (incl_e - m_tiles * n_blocks);
+  const uint32_t mt = xi % m_tiles;
+  *e_out = e_begin + (uint32_t)le;
+  *nb = xi / m_tiles;
+  *row0 = lo_e + mt * 256u;
+  const uint32_t left = n_e - mt * 256u;
+  *rows = left < 256u ? left : 256u;
+  return true;
 }
 
 // silu(g) * u = g / (1 + e^-g) * u with the hardware exp2 and reciprocal

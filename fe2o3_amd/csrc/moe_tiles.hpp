@@ -67,6 +67,44 @@ FE2O3_HD bool expert_tile_at(const uint32_t* offsets, uint32_t e_begin, uint32_t
   return false;
 }
 
+// The same lookup in the form the kernels run it, one wave at a time: lane l
+// reads expert e_begin + l's bounds (one memory round trip for all experts),
+// the lanes' tile counts are prefix-summed, and the entry's expert is the
+// number of lanes whose inclusive sum is <= its list index (the sums do not
+// decrease).  This host form spells out the 64 lanes as loops; the device
+// form (moe.hip) uses a wave scan, a ballot and lane reads, step for step.
+// Experts: at most 64.
+FE2O3_HD bool expert_tile_lanes(const uint32_t* offsets, uint32_t e_begin, uint32_t e_end,
+                                uint32_t routes, uint32_t n_blocks, uint32_t block,
+                                uint32_t* e_out, uint32_t* row0, uint32_t* rows, uint32_t* nb) {
+  uint32_t lo[64], n[64], incl[64];
+  const uint32_t ne = e_end - e_begin;
+  uint32_t run = 0;
+  for (uint32_t l = 0; l < 64; ++l) {
+    lo[l] = n[l] = 0;
+    if (l < ne) expert_rows(offsets, e_begin + l, routes, &lo[l], &n[l]);
+    run += (n[l] + 255u) / 256u * n_blocks;
+    incl[l] = run;
+  }
+  const uint32_t total = incl[63];
+  const uint32_t chunk = (total + 7u) / 8u;
+  const uint32_t slot = block >> 3;
+  if (slot >= chunk) return false;
+  const uint32_t x = (block & 7u) * chunk + slot;
+  if (x >= total) return false;
+  uint32_t l = 0;
+  for (uint32_t i = 0; i < 64; ++i) l += incl[i] <= x ? 1u : 0u;
+  const uint32_t m_tiles = (n[l] + 255u) / 256u;
+  const uint32_t xi = x - (incl[l] - m_tiles * n_blocks);
+  const uint32_t mt = xi % m_tiles;
+  *e_out = e_begin + l;
+  *nb = xi / m_tiles;
+  *row0 = lo[l] + mt * 256u;
+  const uint32_t left = n[l] - mt * 256u;
+  *rows = left < 256u ? left : 256u;
+  return true;
+}
+
 // Grid sizes (workgroups, a multiple of 8) of the gate/up and down launches
 // for experts [e_begin, e_end): routes/256 rounded up plus one partial tile
 // per expert bounds the m-tiles of any consistent routing.

@@ -7,6 +7,8 @@
 //     an n-block in range.
 //  2. Consistent offsets (non-decreasing, total <= routes): over the grid,
 //     every tile of the list is run exactly once.
+//  3. The lane-parallel form the kernels run (expert_tile_lanes) gives every
+//     workgroup the same tile as the serial form.
 #include <stdint.h>
 #include <stdio.h>
 
@@ -52,9 +54,24 @@ int main() {
     for (uint64_t blk = 0; blk < grid; ++blk) {
       uint32_t e, row0, rows, nb;
       if (!fe2o3::expert_tile_at(off.data(), b, e_end, routes, n_blocks, (uint32_t)blk, &e, &row0,
-                                 &rows, &nb))
+                                 &rows, &nb)) {
+        uint32_t e2, r2, n2, b2;
+        if (fe2o3::expert_tile_lanes(off.data(), b, e_end, routes, n_blocks, (uint32_t)blk, &e2,
+                                     &r2, &n2, &b2)) {
+          if (failures < 10) printf("lanes form has an extra tile: iter %d\n", iter);
+          ++failures;
+        }
         continue;
+      }
       ++tiles_checked;
+      uint32_t e2, r2, n2, b2;
+      const bool hit2 = fe2o3::expert_tile_lanes(off.data(), b, e_end, routes, n_blocks,
+                                                 (uint32_t)blk, &e2, &r2, &n2, &b2);
+      if (!hit2 || e2 != e || r2 != row0 || n2 != rows || b2 != nb) {
+        if (failures < 10) printf("lanes form differs: iter %d block %llu\n", iter,
+                                  (unsigned long long)blk);
+        ++failures;
+      }
       if (e < b || e >= e_end || nb >= n_blocks || rows == 0 || rows > 256 ||
           (uint64_t)row0 + rows > routes) {
         if (failures < 10)
