@@ -47,6 +47,8 @@ struct Geo {
   static constexpr int kTileBytes = 256 * ROW_BYTES;         // one operand tile
   static constexpr int kInstPerWave = kTileBytes / 1024 / 4; // loads per wave per tile
   static constexpr int kK16 = ROW_BYTES / 2;                 // 16-bit k units per stage
+  // loads per wave and stage for an operand tile of `rows` rows
+  static constexpr int insts(int rows) { return rows * ROW_BYTES / 4096; }
 
   static FE2O3_DEVICE uint32_t swz(uint32_t r) {
     if (ROW_BYTES == 128) return (r ^ (r >> 2)) & 7u;
@@ -64,14 +66,16 @@ struct Geo {
 };
 
 
-// Source of one operand tile: for load slot j the base of its buffer
-// (wave-uniform) and this thread's byte offset of its chunk at k = 0; all
-// slots share one buffer extent.  Offsets and extent are 32-bit.
-template <int ROW_BYTES>
+// Source of one operand tile of N loads per wave: for load slot j the base
+// of its buffer (wave-uniform) and this thread's byte offset of its chunk
+// at k = 0; all slots share one buffer extent.  Offsets and extent are
+// 32-bit.  The B tile is always 256 rows; the A tile has the policy's
+// kARows rows (256, or fewer for short tiles).
+template <int ROW_BYTES, int N = Geo<ROW_BYTES>::kInstPerWave>
 struct Rows {
-  const void* base[Geo<ROW_BYTES>::kInstPerWave];
+  const void* base[N];
   uint32_t bytes;
-  uint32_t voff[Geo<ROW_BYTES>::kInstPerWave];
+  uint32_t voff[N];
 };
 
 FE2O3_DEVICE __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
@@ -89,14 +93,16 @@ FE2O3_DEVICE void b2l_b128(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, u
 // read per row; rows at or beyond valid_rows are clamped to the last valid
 // row (their products only reach outputs that are never stored).  The
 // caller guarantees ((valid_rows - 1) * ld + k16) * 2 < 2^31.
-template <int ROW_BYTES>
-FE2O3_DEVICE Rows<ROW_BYTES> dense_rows(const uint16_t* base, uint32_t ld, uint32_t valid_rows,
-                                        uint32_t k16) {
+template <int ROW_BYTES, int ROWS = 256>
+FE2O3_DEVICE Rows<ROW_BYTES, Geo<ROW_BYTES>::insts(ROWS)> dense_rows(const uint16_t* base,
+                                                                      uint32_t ld,
+                                                                      uint32_t valid_rows,
+                                                                      uint32_t k16) {
   using G = Geo<ROW_BYTES>;
-  Rows<ROW_BYTES> t;
+  Rows<ROW_BYTES, G::insts(ROWS)> t;
   t.bytes = ((valid_rows - 1u) * ld + k16) * 2u;
 #pragma unroll
-  for (int j = 0; j < G::kInstPerWave; ++j) {
+  for (int j = 0; j < G::insts(ROWS); ++j) {
     uint32_t row = G::inst_row(j);
     const uint32_t chunk = G::inst_chunk(row);
     if (row >= valid_rows) row = valid_rows - 1u;
@@ -108,8 +114,8 @@ FE2O3_DEVICE Rows<ROW_BYTES> dense_rows(const uint16_t* base, uint32_t ld, uint3
 
 // Loads j in [J0, J1) of one operand tile into the LDS tile at byte offset
 // `tile` of smem, k offset `kbytes` (wave-uniform).
-template <int ROW_BYTES, int J0, int J1>
-FE2O3_DEVICE void issue_part(const Rows<ROW_BYTES>& rows, uint32_t kbytes, uint8_t* smem,
+template <int ROW_BYTES, int J0, int J1, int N>
+FE2O3_DEVICE void issue_part(const Rows<ROW_BYTES, N>& rows, uint32_t kbytes, uint8_t* smem,
                              uint32_t tile, uint32_t wave) {
 #pragma unroll
   for (int j = J0; j < J1; ++j)
@@ -117,15 +123,16 @@ FE2O3_DEVICE void issue_part(const Rows<ROW_BYTES>& rows, uint32_t kbytes, uint8
              kbytes);
 }
 
-// Stage p's A tile at a(p); its B tile at b_region + b(p).  Fragment reads
-// add a(p) or b(p) (plus the row-block offset) as ds_read immediates; the
-// B region's base is folded into the per-lane B offsets, so every immediate
-// stays below 64 KiB.
-template <int ROW_BYTES, int STAGES>
+// Stage p's A tile (A_ROWS rows) at a(p); its B tile at b_region + b(p).
+// Fragment reads add a(p) or b(p) (plus the row-block offset) as ds_read
+// immediates; the B region's base is folded into the per-lane B offsets, so
+// every immediate stays below 64 KiB.
+template <int ROW_BYTES, int STAGES, int A_ROWS = 256>
 struct Lay {
   using G = Geo<ROW_BYTES>;
-  static constexpr uint32_t b_region = (uint32_t)STAGES * G::kTileBytes;
-  static constexpr uint32_t a(int p) { return (uint32_t)p * G::kTileBytes; }
+  static constexpr uint32_t a_tile = (uint32_t)A_ROWS * ROW_BYTES;
+  static constexpr uint32_t b_region = (uint32_t)STAGES * a_tile;
+  static constexpr uint32_t a(int p) { return (uint32_t)p * a_tile; }
   static constexpr uint32_t b(int p) { return (uint32_t)p * G::kTileBytes; }
   // largest row-block offset: 16-row block 7 (bf16) > 32-row block 3 (fp8)
   static_assert((STAGES - 1) * G::kTileBytes + 7 * 16 * ROW_BYTES < 65536,
@@ -148,17 +155,23 @@ constexpr int kWaitLgkm0 = waitcnt_imm(63, 0);
 // of the next substep, in the order the MFMAs first use them; and how the
 // first substep of the K loop writes (rather than adds to) the accumulators.
 
-struct Acc16 {
-  f32x4_t v[8][8];
+template <int RB>
+struct Acc16T {  // RB row blocks of 16 x 8 column blocks of 16
+  f32x4_t v[RB][8];
 };
+using Acc16 = Acc16T<8>;
 struct Acc32 {
   f32x16_t v[4][4];
 };
 
-// bf16: v_mfma_f32_16x16x32_bf16, 32 k per substep.  Lane l holds k
-// 8(l/16) .. +7 of row 16i + l%16 of the wave's 128 A rows (a[i]) and B rows
-// (b[j]); the swizzle of row 16i + r depends on i mod 4, hence four lane
-// offsets per operand and substep.  One read unit is one ds_read_b128.
+// bf16: v_mfma_f32_16x16x32_bf16, 32 k per substep.  Each wave owns RPW
+// output rows (RPW/16 row blocks) by 128 columns; the A tile holds 2 RPW
+// rows (256 for full tiles; 128, 64 or 32 for the short last tiles of the
+// MoE experts, which then cost the MFMAs and A loads of their rows only).
+// Lane l holds k 8(l/16) .. +7 of row 16i + l%16 of the wave's A rows (a[i])
+// and B rows (b[j]); the swizzle of a row depends on its index mod 32, hence
+// four lane offsets per operand and substep.  One read unit is one
+// ds_read_b128.
 //
 // The MFMAs are inline asm with the accumulator tied to the destination
 // ("+a").  Left to itself the compiler gives this 8x8 tile's MFMAs a
@@ -171,13 +184,16 @@ struct Acc32 {
 //     the epilogue's VALU reads of the accumulators;
 //   - fragment registers are only MFMA sources A and B, read at issue: the
 //     LDS reads that overwrite them need no wait states.
-template <int ROW_BYTES>
+template <int ROW_BYTES, int RPW = 128>
 struct Bf16Mma {
+  static_assert(RPW == 128 || RPW == 64 || RPW == 32 || RPW == 16, "rows per wave");
   using G = Geo<ROW_BYTES>;
-  using Acc = Acc16;
-  static constexpr int kSubsteps = ROW_BYTES / 64, kMfma = 64, kTn = 8, kReads = 16;
+  static constexpr int kRB = RPW / 16;
+  using Acc = Acc16T<kRB>;
+  static constexpr int kSubsteps = ROW_BYTES / 64, kMfma = kRB * 8, kTn = 8, kReads = kRB + 8;
+  static constexpr int kARows = 2 * RPW;
   struct Frags {
-    bf16x8_t a[8], b[8];
+    bf16x8_t a[kRB], b[8];
   };
   struct Lanes {
     uint32_t a[kSubsteps][4], b[kSubsteps][4];
@@ -192,8 +208,8 @@ struct Bf16Mma {
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
         const uint32_t c = 4u * s + g;
-        const uint32_t ra = wm * 128u + p * 16u + lr, rb = wn * 128u + p * 16u + lr;
-        l.a[s][p] = (wm * 128u + lr) * ROW_BYTES + ((c ^ G::swz(ra)) << 4);
+        const uint32_t ra = wm * RPW + p * 16u + lr, rb = wn * 128u + p * 16u + lr;
+        l.a[s][p] = (wm * RPW + lr) * ROW_BYTES + ((c ^ G::swz(ra)) << 4);
         l.b[s][p] = b_region + (wn * 128u + lr) * ROW_BYTES + ((c ^ G::swz(rb)) << 4);
       }
     return l;
@@ -231,7 +247,7 @@ struct Bf16Mma {
   static FE2O3_DEVICE void finish(Acc& acc) {
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < kRB; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) asm volatile("" : "+a"(acc.v[i][j]));
   }
@@ -248,6 +264,7 @@ struct Fp8Mma {
   using G = Geo<ROW_BYTES>;
   using Acc = Acc32;
   static constexpr int kSubsteps = ROW_BYTES / 64, kMfma = 16, kTn = 4, kReads = 8;
+  static constexpr int kARows = 256;
   struct Frags {
     i32x8_t a[4], b[4];
   };
@@ -336,17 +353,40 @@ struct Spread {
   }
 };
 
-// Copy C (0 .. 2*NJ-1: A slot C/2 for even C, B slot C/2 for odd C) of the
-// stage at k offset `kbytes` into LDS buffer `buf`.
-template <int ROW_BYTES, int STAGES, int C>
-FE2O3_DEVICE void copy_one(const Rows<ROW_BYTES>& ar, const Rows<ROW_BYTES>& br, uint32_t kbytes,
-                           uint8_t* smem, uint32_t wave, int buf) {
-  using L = Lay<ROW_BYTES, STAGES>;
-  constexpr int j = C >> 1;
-  const Rows<ROW_BYTES>& rows = (C & 1) ? br : ar;
-  const uint32_t tile = (C & 1) ? L::b_region + L::b(buf) : L::a(buf);
-  b2l_b128(rsrc(rows.base[j], rows.bytes), smem + tile + (4u * j + wave) * 1024u, rows.voff[j],
-           kbytes);
+// Order of a stage's NA A copies and NB B copies (NA <= NB): A copy i is
+// copy floor(i (NA + NB) / NA), the B copies fill the other positions in
+// slot order.  With NA = NB, A slot C/2 is copy C for even C and B slot C/2
+// copy C for odd C.
+template <int NA, int NB>
+struct CopyOrder {
+  static_assert(NA >= 1 && NA <= NB, "A copies spread among the B copies");
+  static constexpr int NC = NA + NB;
+  static constexpr bool is_a(int c) {
+    for (int i = 0; i < NA; ++i)
+      if (i * NC / NA == c) return true;
+    return false;
+  }
+  static constexpr int slot(int c) {
+    int n = 0;
+    for (int x = 0; x < c; ++x)
+      if (is_a(x) == is_a(c)) ++n;
+    return n;
+  }
+};
+
+// Copy C of the stage at k offset `kbytes` into LDS buffer `buf`.
+template <int ROW_BYTES, int STAGES, int A_ROWS, int C, int NA, int NB>
+FE2O3_DEVICE void copy_one(const Rows<ROW_BYTES, NA>& ar, const Rows<ROW_BYTES, NB>& br,
+                           uint32_t kbytes, uint8_t* smem, uint32_t wave, int buf) {
+  using L = Lay<ROW_BYTES, STAGES, A_ROWS>;
+  using O = CopyOrder<NA, NB>;
+  constexpr int j = O::slot(C);
+  if constexpr (O::is_a(C))
+    b2l_b128(rsrc(ar.base[j], ar.bytes), smem + L::a(buf) + (4u * j + wave) * 1024u, ar.voff[j],
+             kbytes);
+  else
+    b2l_b128(rsrc(br.base[j], br.bytes), smem + L::b_region + L::b(buf) + (4u * j + wave) * 1024u,
+             br.voff[j], kbytes);
 }
 
 // Substep S_ of a K step held in stage buffer P.  FIRST: the K loop's first
@@ -355,9 +395,12 @@ FE2O3_DEVICE void copy_one(const Rows<ROW_BYTES>& ar, const Rows<ROW_BYTES>& br,
 template <class M, int ROW_BYTES, int STAGES, int P, int S_, bool FIRST>
 struct Substep {
   using G = Geo<ROW_BYTES>;
-  using L = Lay<ROW_BYTES, STAGES>;
+  using L = Lay<ROW_BYTES, STAGES, M::kARows>;
   static constexpr int S = M::kSubsteps, MF = M::kMfma;
-  static constexpr int NC = 2 * G::kInstPerWave;  // copies per stage and wave
+  static constexpr int NA = G::insts(M::kARows), NB = G::kInstPerWave;
+  using RA_ = Rows<ROW_BYTES, NA>;
+  using RB_ = Rows<ROW_BYTES, NB>;
+  static constexpr int NC = NA + NB;              // copies per stage and wave
   static constexpr int kEarly = NC / 2;           // copies started at the barrier
   static constexpr int PN = (P + 1) % STAGES;     // buffer of the next step
   static constexpr int PL = (P + STAGES - 1) % STAGES;  // buffer of the late copies' stage
@@ -377,7 +420,7 @@ struct Substep {
   static constexpr int RS = LAST ? 0 : S_ + 1;
 
   template <int I>
-  static FE2O3_DEVICE void slot(const Rows<ROW_BYTES>& ar, const Rows<ROW_BYTES>& br,
+  static FE2O3_DEVICE void slot(const RA_& ar, const RB_& br,
                                 uint32_t k_next, uint32_t k_next2, uint8_t* smem, uint32_t wave,
                                 const typename M::Lanes& ln, typename M::Frags* f,
                                 typename M::Acc& acc) {
@@ -390,12 +433,13 @@ struct Substep {
       M::template mfma<FIRST && S_ == 0, I>(acc, f[FC]);
       if constexpr (LAST)  // early copies: stage t+STAGES into buffer P
         Spread<kEarly, kBarrierAt, MF>::template at<I>([&](auto n) {
-          copy_one<ROW_BYTES, STAGES, decltype(n)::value>(ar, br, k_next2, smem, wave, P);
+          copy_one<ROW_BYTES, STAGES, M::kARows, decltype(n)::value>(ar, br, k_next2, smem, wave,
+                                                                     P);
         });
       if constexpr (S_ == 0)  // late copies: the rest of stage t+STAGES-1
         Spread<NC - kEarly, 0, kLateTo>::template at<I>([&](auto n) {
-          copy_one<ROW_BYTES, STAGES, kEarly + decltype(n)::value>(ar, br, k_next, smem, wave,
-                                                                   PL);
+          copy_one<ROW_BYTES, STAGES, M::kARows, kEarly + decltype(n)::value>(ar, br, k_next,
+                                                                              smem, wave, PL);
         });
       Spread<M::kReads, kReadFrom, kReadTo>::template at<I>([&](auto n) {
         M::template read<RA, RB, RS, decltype(n)::value>(smem, ln, f[FN]);
@@ -404,7 +448,7 @@ struct Substep {
       slot<I + 1>(ar, br, k_next, k_next2, smem, wave, ln, f, acc);
     }
   }
-  static FE2O3_DEVICE void run(const Rows<ROW_BYTES>& ar, const Rows<ROW_BYTES>& br,
+  static FE2O3_DEVICE void run(const RA_& ar, const RB_& br,
                                uint32_t k_next, uint32_t k_next2, uint8_t* smem, uint32_t wave,
                                const typename M::Lanes& ln, typename M::Frags* f,
                                typename M::Acc& acc) {
@@ -425,7 +469,8 @@ struct Steps {
     return __builtin_amdgcn_readfirstlane((uint32_t)(st < steps ? st : steps - 1) *
                                           (G::kK16 * 2u));
   }
-  static FE2O3_DEVICE void run(const Rows<ROW_BYTES>& ar, const Rows<ROW_BYTES>& br, int kt,
+  using Sub0 = Substep<M, ROW_BYTES, STAGES, 0, 0, false>;
+  static FE2O3_DEVICE void run(const typename Sub0::RA_& ar, const typename Sub0::RB_& br, int kt,
                                int steps, uint8_t* smem, uint32_t wave,
                                const typename M::Lanes& ln, typename M::Frags* f,
                                typename M::Acc& acc) {
@@ -442,16 +487,17 @@ struct Steps {
 // K loop over k16 16-bit units per row (a multiple of Geo::kK16, at least one
 // stage); every accumulator is written (no zeroing beforehand).
 template <class M, int ROW_BYTES, int STAGES>
-FE2O3_DEVICE void mainloop(const Rows<ROW_BYTES>& ar, const Rows<ROW_BYTES>& br, uint32_t k16,
-                           uint8_t* smem, typename M::Acc& acc) {
+FE2O3_DEVICE void mainloop(const typename Substep<M, ROW_BYTES, STAGES, 0, 0, false>::RA_& ar,
+                           const typename Substep<M, ROW_BYTES, STAGES, 0, 0, false>::RB_& br,
+                           uint32_t k16, uint8_t* smem, typename M::Acc& acc) {
   using G = Geo<ROW_BYTES>;
-  using L = Lay<ROW_BYTES, STAGES>;
+  using L = Lay<ROW_BYTES, STAGES, M::kARows>;
   using Sub = Substep<M, ROW_BYTES, STAGES, 0, 0, false>;
   static_assert((ROW_BYTES == 128 && STAGES == 2) || (ROW_BYTES == 64 && STAGES == 4),
                 "two 64-k or four 32-k stages");
   static_assert(M::kSubsteps % 2 == 0 || STAGES % 2 == 0,
                 "fragment buffers alternate across the unrolled steps");
-  constexpr int NJ = G::kInstPerWave;
+  constexpr int NA = Sub::NA, NB = Sub::NB;
   const int steps = (int)(k16 / G::kK16);
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const typename M::Lanes ln = M::lanes(L::b_region);
@@ -461,12 +507,19 @@ FE2O3_DEVICE void mainloop(const Rows<ROW_BYTES>& ar, const Rows<ROW_BYTES>& br,
 #pragma unroll
   for (int st = 0; st + 1 < STAGES; ++st) {
     const uint32_t kb = st == 0 ? 0u : St::stage_k(st, steps);
-    issue_part<ROW_BYTES, 0, NJ>(ar, kb, smem, L::a(st), wave);
-    issue_part<ROW_BYTES, 0, NJ>(br, kb, smem, L::b_region + L::b(st), wave);
+    issue_part<ROW_BYTES, 0, NA>(ar, kb, smem, L::a(st), wave);
+    issue_part<ROW_BYTES, 0, NB>(br, kb, smem, L::b_region + L::b(st), wave);
   }
   const uint32_t kl = St::stage_k(STAGES - 1, steps);
-  issue_part<ROW_BYTES, 0, Sub::kEarly / 2>(ar, kl, smem, L::a(STAGES - 1), wave);
-  issue_part<ROW_BYTES, 0, Sub::kEarly / 2>(br, kl, smem, L::b_region + L::b(STAGES - 1), wave);
+  if constexpr (NA == NB) {
+    issue_part<ROW_BYTES, 0, Sub::kEarly / 2>(ar, kl, smem, L::a(STAGES - 1), wave);
+    issue_part<ROW_BYTES, 0, Sub::kEarly / 2>(br, kl, smem, L::b_region + L::b(STAGES - 1), wave);
+  } else {
+    Spread<Sub::kEarly, 0, 1>::template at<0>([&](auto n) {
+      copy_one<ROW_BYTES, STAGES, M::kARows, decltype(n)::value>(ar, br, kl, smem, wave,
+                                                                 STAGES - 1);
+    });
+  }
   // stage 0 landed
   __builtin_amdgcn_s_waitcnt(waitcnt_imm((STAGES - 2) * Sub::NC + Sub::kEarly, 0));
   __builtin_amdgcn_s_barrier();
@@ -502,9 +555,10 @@ FE2O3_DEVICE uint32_t lane_id() {
 }
 FE2O3_DEVICE uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
-// Acc16 (i, j, e): tile row wm*128 + 16i + lane%16, tile column
+// Acc16T (i, j, e): tile row wm*RPW + 16i + lane%16, tile column
 // wn*128 + 16j + 4(lane/16) + e.
-FE2O3_DEVICE uint32_t acc16_row0() { return (wave_id() >> 1) * 128u + (lane_id() & 15u); }
+template <int RPW = 128>
+FE2O3_DEVICE uint32_t acc16_row0() { return (wave_id() >> 1) * RPW + (lane_id() & 15u); }
 FE2O3_DEVICE uint32_t acc16_col0() { return (wave_id() & 1u) * 128u + 4u * (lane_id() >> 4); }
 
 // Acc32 (i, j, e): tile row wm*128 + 32i + lane%32, tile column

@@ -247,6 +247,52 @@ def test_moe_ffn_garbage_routing_stays_in_bounds(gpu, oracle):
         assert all(v.unchanged() for v in routing.values())
 
 
+@pytest.mark.parametrize("hidden,ffn", [(256, 384), (512, 256)])
+def test_moe_ffn_every_short_tile_path(gpu, oracle, hidden, ffn):
+    """A routing built by hand (every route admitted, slots in route order
+    per expert) whose expert row counts put last m-tiles of 1-32, 33-64,
+    65-128 and 129-256 rows, each on its own tile path (32, 64, 128 or 256 A
+    rows), beside full tiles of the same experts; every token's output
+    against the oracle."""
+    kern = _k()
+    counts = [5, 31, 32, 33, 64, 65, 128, 129, 200, 256, 257, 300, 289, 321, 384, 418]
+    experts = len(counts)
+    routes = sum(counts)
+    assert routes % 2 == 0
+    tokens = routes // 2
+    rng = np.random.default_rng(hidden + ffn)
+    top2 = np.repeat(np.arange(experts, dtype=np.uint32), counts)
+    rng.shuffle(top2)
+    order = np.argsort(top2, kind="stable")
+    perm = order.astype(np.uint32)
+    inv = np.empty(routes, np.uint32)
+    inv[order] = np.arange(routes, dtype=np.uint32)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.uint32)
+    w0 = rng.uniform(0.5, 1.0, tokens).astype(np.float32)
+    weights = np.stack([w0, np.float32(1.0) - w0], axis=1).ravel()
+    x = oracle.bf16_from_f32(rng.standard_normal(tokens * hidden)).reshape(tokens, hidden)
+    wsz = experts * ffn * hidden
+    wg, wu, wd = (oracle.bf16_from_f32(rng.standard_normal(wsz) * 0.05) for _ in range(3))
+    routing = {"top2": gpu.to_device(top2), "offsets": gpu.to_device(offsets),
+               "permutation": gpu.to_device(perm), "inverse": gpu.to_device(inv),
+               "weights": gpu.to_device(weights)}
+    ws = gpu.alloc(kern.moe_ffn_workspace_bytes(tokens, hidden, ffn, experts), np.uint8)
+    out = Guarded(gpu, np.full(tokens * hidden, 0x7FDE, np.uint16))
+    kern.moe_ffn_top2(gpu.to_device(x), gpu.to_device(wg), gpu.to_device(wu), gpu.to_device(wd),
+                      routing, out.body, ws, tokens, hidden, ffn, experts)
+    assert out.guards_intact()
+    got = bf16_to_f32(out.download()).reshape(tokens, hidden)
+    y = oracle.moe_ffn_routes(x, wg, wu, wd, hidden, ffn,
+                              np.arange(routes, dtype=np.uint32) // 2, top2)
+    want = np.zeros((tokens, hidden), np.float32)
+    for rank in range(2):
+        want = want + weights.reshape(tokens, 2)[:, rank][:, None] * y[rank::2]
+    assert rel_err(got, want) <= 1e-2
+    # every token within one bf16 rounding of its own reference row scale
+    scale = np.max(np.abs(want), axis=1, keepdims=True)
+    assert np.all(np.abs(got - want) <= 2.0 ** -7 * scale + 1e-6)
+
+
 def test_moe_ffn_small_with_drops(gpu, oracle):
     """Capacity below demand: dropped routes contribute nothing."""
     tokens, hidden, ffn, experts = 256, 256, 256, 8
