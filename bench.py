@@ -415,6 +415,65 @@ def sec_gemm_f32(ctx, stream, args):
                                  f"256^3 problem, {dt * 1e3:.1f} ms")}
 
 
+def sec_gemm_general(ctx, stream, args):
+    """tiled_gemm_general_v1 at 2048^3 with padded strides and alpha/beta
+    (C = 1.5 A B + 0.5 C, lda = ldb = ldc = 2056), both schedules."""
+    from fe2o3_amd import kernels
+    from oracle import oracle as orc
+    m = n = k = 2048
+    ld = 2056
+    alpha, beta = 1.5, 0.5
+    la, lb, lc = (m - 1) * ld + k, (k - 1) * ld + n, (m - 1) * ld + n
+    a, b = ctx.alloc(la, np.uint16), ctx.alloc(lb, np.uint16)
+    c0, c = ctx.alloc(lc, np.float32), ctx.alloc(lc, np.float32)
+    kernels.fill_normal_bf16(a, 7, 0xA, 1.0 / 32.0, stream=stream)
+    kernels.fill_normal_bf16(b, 7, 0xB, 1.0 / 32.0, stream=stream)
+    kernels.fill_normal_f32(c0, 7, 0xC, 1.0, stream=stream)
+    res = {"workload": "general bf16 GEMM 2048^3, strides 2056, alpha 1.5, beta 0.5, f32 C "
+                       "(tiled_gemm_general_v1)", "unit": "TFLOP/s"}
+    outs = {}
+    for sched, kern in (("reference", kernels.tiled_gemm_general_v1_gpu),
+                        ("vector_a", kernels.tiled_gemm_general_vector_a_v1_gpu)):
+        prep = kern.Kernel.load(ctx).prepare(a, b, c, m, n, k, ld, ld, ld, alpha, beta)
+        from fe2o3_amd import _lib
+        from fe2o3_amd.runtime import check
+
+        def step(prep=prep):  # C is read and written: restore it first (both timed alike)
+            check(_lib.lib().fe2o3_rt_memcpy_async(c.ptr, c0.ptr, c.nbytes, 3, stream.handle),
+                  "copy")
+            prep.launch_async(stream)
+        ms = _timed(ctx, stream, step, args)
+        outs[sched] = c.download()
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        res[sched] = {"ms": round(ms, 5), "value": round(tf, 2),
+                      "frac": round(tf / PEAK["bf16"], 4)}
+    res["kernel"] = "gemm_general_kernel<false> / <true>"
+    res["ms"] = res["vector_a"]["ms"]
+    res["value"] = res["vector_a"]["value"]
+    res["roofline"] = {"bound": "mfma", "peak": PEAK["bf16"], "frac": res["vector_a"]["frac"],
+                       "note": "ms includes a 34 MB device copy restoring C before each call"}
+    if not args.cpu_baseline:
+        return res
+    ha, hb, hc = a.download(), b.download(), c0.download()
+    r0, rows = 1000, 32
+    threads = _cpu_threads()
+    t0 = time.perf_counter()
+    rc, ref, _ = orc.general_reference_v1(rows, n, k, ld, ld, ld,
+                                          ha[r0 * ld:r0 * ld + (rows - 1) * ld + k], hb,
+                                          hc[r0 * ld:r0 * ld + (rows - 1) * ld + n], alpha, beta)
+    dt = time.perf_counter() - t0
+    got = np.stack([outs["reference"][(r0 + r) * ld:(r0 + r) * ld + n] for r in range(rows)])
+    same = outs["reference"].tobytes() == outs["vector_a"].tobytes()
+    res["parity"] = {"max_rel_err": _rel(got.ravel(), ref) if rc == 0 else None,
+                     "tolerance": 1e-5, "schedules_bit_identical": bool(same),
+                     "coverage": f"output rows {r0}..{r0 + rows - 1} (every column) against the "
+                                 "tiled CPU schedule; both schedules' whole outputs compared"}
+    res["cpu_baseline"] = _cpu(2.0 * rows * n * k / dt / 1e12, "TFLOP/s", 1,
+                               f"oracle/gemm.c fe2o3o_general_reference_v1 (tiled schedule, one "
+                               f"thread) on the {rows}-row parity block, {dt:.2f} s")
+    return res
+
+
 def sec_collectives(ctx, stream, args):
     """Wave64 collectives over 2^20 rows of 64 f32 with one mask per row:
     4 bytes in and 12 bytes out per element plus 8 bytes per row (HBM-bound)."""
@@ -481,6 +540,7 @@ SECONDARY = {
     "fp8_gemm": sec_fp8,
     "moe": sec_moe,
     "gemm_f32": sec_gemm_f32,
+    "gemm_general": sec_gemm_general,
     "collectives": sec_collectives,
     "routing_check": sec_routing_check,
 }
@@ -505,9 +565,11 @@ def calibrate_copy(ctx, stream, args):
 def _ok(par) -> bool:
     if par is None:
         return True
-    if "max_rel_err" in par and par.get("tolerance") == 1e-2:
-        if par["max_rel_err"] is None or not par["max_rel_err"] <= 1e-2:
+    if "max_rel_err" in par and par.get("tolerance") in (1e-2, 1e-5):
+        if par["max_rel_err"] is None or not par["max_rel_err"] <= par["tolerance"]:
             return False
+    if par.get("schedules_bit_identical") is False:
+        return False
     for key in ("bit_mismatches", "routing_mismatches", "policy_failures"):
         if key in par and par[key] != 0:
             return False

@@ -85,6 +85,8 @@ SIGNATURES = {
     "fe2o3_tiled_gemm_v1": (i32, [vp, u64, vp, u64, vp, u64, u32, u32, u32, vp]),
     "fe2o3_tiled_gemm_general_v1": (
         i32, [vp, u64, vp, u64, vp, u64, u32, u32, u32, u32, u32, u32, f32, f32, vp]),
+    "fe2o3_tiled_gemm_general_vector_a_v1": (
+        i32, [vp, u64, vp, u64, vp, u64, u32, u32, u32, u32, u32, u32, f32, f32, vp]),
     "fe2o3_scalar_gemm_v1": (i32, [vp, u64, vp, u64, vp, u64, u32, u32, u32, vp]),
     "fe2o3_gemm_bf16_nt": (i32, [vp, u64, vp, u64, vp, u64, u32, u32, u32, vp]),
     "fe2o3_row_softmax_v1": (i32, [vp, u64, vp, u64, vp]),

@@ -106,6 +106,13 @@ __global__ void __launch_bounds__(256) zero_fill_kernel(float* __restrict__ c, u
 constexpr int G_BM = 64, G_BN = 64, G_BK = 32;
 constexpr int G_LDK = G_BK + 8;  // padded LDS row (bf16 elements), 80 bytes
 
+// Two global-transfer schedules of the same kernel, as the reference has two
+// (crates/dialect-schedule/src/general_gemm.rs:13-38): VEC_A = false stages
+// every A and B element with a masked scalar load; VEC_A = true loads each
+// full, in-range, 8-byte-aligned group of 4 A elements with one 8-byte load
+// and falls back to masked scalar loads for the rest (tails, misaligned
+// rows); B stays scalar.  The staged tiles, hence the results, are the same.
+template <bool VEC_A>
 __global__ void __launch_bounds__(256) gemm_general_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, float* __restrict__ c,
     uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha,
@@ -129,9 +136,19 @@ __global__ void __launch_bounds__(256) gemm_general_kernel(
       const int r = t >> 2, d0 = (t & 3) * 8;
       const uint64_t gr = row0 + r;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint64_t gd = k0 + d0 + e;
-        a_lds[r * G_LDK + d0 + e] = (gr < m && gd < k) ? a[gr * lda + gd] : (uint16_t)0;
+      for (int v = 0; v < 2; ++v) {
+        const uint64_t gd0 = k0 + d0 + 4 * v;
+        const uint64_t idx = gr * lda + gd0;
+        if (VEC_A && gr < m && gd0 + 4 <= k && (((uintptr_t)(a + idx)) & 7u) == 0) {
+          *reinterpret_cast<uint2*>(a_lds + r * G_LDK + d0 + 4 * v) =
+              *reinterpret_cast<const uint2*>(a + idx);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint64_t gd = gd0 + e;
+            a_lds[r * G_LDK + d0 + 4 * v + e] = (gr < m && gd < k) ? a[gr * lda + gd] : (uint16_t)0;
+          }
+        }
       }
     }
     // B: thread t loads depth t/8, columns (t%8)*8 .. +7, stored transposed
@@ -262,7 +279,8 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_moe_expert_gemm_bf16_m16_n16_k16_v1", "tile16_bf16_kernel", (const void*)tile16_bf16_kernel, 64, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_v1", "tiled_v1_kernel", (const void*)tiled_v1_kernel, 64, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_v1", "zero_fill_kernel", (const void*)zero_fill_kernel, 256, 0}),
-    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_kernel", (const void*)gemm_general_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_kernel<false>", (const void*)gemm_general_kernel<false>, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_kernel<true>", (const void*)gemm_general_kernel<true>, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_scalar_gemm_v1", "scalar_gemm_kernel", (const void*)scalar_gemm_kernel, 256, 0})};
 
 }  // namespace
@@ -315,11 +333,14 @@ int32_t fe2o3_tiled_gemm_v1(const uint16_t* a, uint64_t a_len, const uint16_t* b
   return fe2o3_host::after_launch();
 }
 
-int32_t fe2o3_tiled_gemm_general_v1(const uint16_t* a, uint64_t a_len, const uint16_t* b,
-                                    uint64_t b_len, float* c, uint64_t c_len, uint32_t m,
-                                    uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb,
-                                    uint32_t ldc, float alpha, float beta, void* stream) {
-  FE2O3_FAULT("fe2o3_tiled_gemm_general_v1");
+}  // extern "C"
+
+namespace {
+
+template <bool VEC_A>
+int32_t general_gemm(const uint16_t* a, uint64_t a_len, const uint16_t* b, uint64_t b_len,
+                     float* c, uint64_t c_len, uint32_t m, uint32_t n, uint32_t k, uint32_t lda,
+                     uint32_t ldb, uint32_t ldc, float alpha, float beta, void* stream) {
   // examples/tiled_gemm_general_v1/src/kernel.rs:80-89
   if ((m != 0 && k != 0 && lda < k) || (k != 0 && n != 0 && ldb < n) ||
       (m != 0 && n != 0 && ldc < n))
@@ -333,9 +354,32 @@ int32_t fe2o3_tiled_gemm_general_v1(const uint16_t* a, uint64_t a_len, const uin
   if ((ea && !a) || (eb && !b) || !c) return FE2O3_ERR_NULL;
   dim3 grid((n + G_BN - 1) / G_BN, (m + G_BM - 1) / G_BM);
   if (grid.y > 65535u) return FE2O3_ERR_SHAPE;
-  gemm_general_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(a, b, c, m, n, k, lda, ldb, ldc,
-                                                             alpha, beta);
+  gemm_general_kernel<VEC_A><<<grid, 256, 0, (hipStream_t)stream>>>(a, b, c, m, n, k, lda, ldb,
+                                                                    ldc, alpha, beta);
   return fe2o3_host::after_launch();
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fe2o3_tiled_gemm_general_v1(const uint16_t* a, uint64_t a_len, const uint16_t* b,
+                                    uint64_t b_len, float* c, uint64_t c_len, uint32_t m,
+                                    uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb,
+                                    uint32_t ldc, float alpha, float beta, void* stream) {
+  FE2O3_FAULT("fe2o3_tiled_gemm_general_v1");
+  return general_gemm<false>(a, a_len, b, b_len, c, c_len, m, n, k, lda, ldb, ldc, alpha, beta,
+                             stream);
+}
+
+int32_t fe2o3_tiled_gemm_general_vector_a_v1(const uint16_t* a, uint64_t a_len,
+                                             const uint16_t* b, uint64_t b_len, float* c,
+                                             uint64_t c_len, uint32_t m, uint32_t n, uint32_t k,
+                                             uint32_t lda, uint32_t ldb, uint32_t ldc,
+                                             float alpha, float beta, void* stream) {
+  FE2O3_FAULT("fe2o3_tiled_gemm_general_vector_a_v1");
+  return general_gemm<true>(a, a_len, b, b_len, c, c_len, m, n, k, lda, ldb, ldc, alpha, beta,
+                            stream);
 }
 
 int32_t fe2o3_scalar_gemm_v1(const float* a, uint64_t a_len, const float* b, uint64_t b_len,

@@ -103,6 +103,13 @@ tiled_gemm_general_v1_gpu = _typed(
     "fe2o3_tiled_gemm_general_v1", [("a", U16, None), ("b", U16, None), ("c", F32, None)],
     [("m", u32), ("n", u32), ("k", u32), ("lda", u32), ("ldb", u32), ("ldc", u32),
      ("alpha", f32), ("beta", f32)])
+# the same kernel under the VectorizedAOnlyBf16GlobalTransferV1 schedule
+# (crates/dialect-schedule/src/general_gemm.rs:13-38)
+tiled_gemm_general_vector_a_v1_gpu = _typed(
+    "fe2o3_tiled_gemm_general_vector_a_v1",
+    [("a", U16, None), ("b", U16, None), ("c", F32, None)],
+    [("m", u32), ("n", u32), ("k", u32), ("lda", u32), ("ldb", u32), ("ldc", u32),
+     ("alpha", f32), ("beta", f32)])
 # examples/scalar_gemm_v1/src/kernel.rs:8
 scalar_gemm_v1_gpu = _typed(
     "fe2o3_scalar_gemm_v1", [("a", F32, None), ("b", F32, None), ("c", F32, None)],

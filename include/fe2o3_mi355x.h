@@ -204,6 +204,21 @@ int32_t fe2o3_tiled_gemm_general_v1(const uint16_t *a, uint64_t a_len,
                                     uint32_t ldb, uint32_t ldc, float alpha,
                                     float beta, void *stream);
 
+/* The same kernel contract and arguments under the reference's second
+ * schedule, VectorizedAOnlyBf16GlobalTransferV1
+ * (crates/dialect-schedule/src/general_gemm.rs:13-38; the hardware harness
+ * runs both schedules on the same seven profiles,
+ * examples/tiled_gemm_general_v1/hardware-harness/src/lib.rs:135-253): A is
+ * staged with one 8-byte load per full, in-range, 8-byte-aligned group of 4
+ * elements and masked scalar loads elsewhere; B stays scalar.  Results are
+ * bit-identical to fe2o3_tiled_gemm_general_v1. */
+int32_t fe2o3_tiled_gemm_general_vector_a_v1(const uint16_t *a, uint64_t a_len,
+                                             const uint16_t *b, uint64_t b_len,
+                                             float *c, uint64_t c_len, uint32_t m,
+                                             uint32_t n, uint32_t k, uint32_t lda,
+                                             uint32_t ldb, uint32_t ldc, float alpha,
+                                             float beta, void *stream);
+
 /* examples/scalar_gemm_v1/src/kernel.rs:8 scalar_gemm_v1(a: &[f32], b: &[f32],
  * c: DisjointSlice<f32>, m, n, k): row-major f32 C[m,n] = A[m,k] * B[k,n]
  * with the reference's per-output sequential, unfused recurrence

@@ -82,12 +82,19 @@ def test_moe_expert_tile_matches_slice1_semantics(gpu, oracle):
 
 # ---- tiled_gemm_general_v1 -------------------------------------------------------------
 
+GENERAL_SCHEDULES = {"reference": "tiled_gemm_general_v1_gpu",
+                     "vector-a": "tiled_gemm_general_vector_a_v1_gpu"}
+
+
+@pytest.mark.parametrize("schedule", list(GENERAL_SCHEDULES))
 @pytest.mark.parametrize("case", [c[0] for c in rv.GENERAL_CASES])
-def test_general_hardware_matrix_bit_exact(gpu, oracle, case):
+def test_general_hardware_matrix_bit_exact(gpu, oracle, case, schedule):
     """examples/tiled_gemm_general_v1/hardware-harness/src/lib.rs:139-253,
-    341-396, 1654-1700: poisoned bodies, patterned logical entries, output
-    bit-exact against the tiled CPU schedule, every non-logical C element
-    (stride padding) untouched, inputs unchanged, guards intact."""
+    341-396, 1654-1700: the seven profiles under each of the two schedules
+    (the reference's 14-case matrix): poisoned bodies, patterned logical
+    entries, output bit-exact against the tiled CPU schedule, every
+    non-logical C element (stride padding) untouched, inputs unchanged,
+    guards intact."""
     name, dims, strides, alpha, beta = next(c for c in rv.GENERAL_CASES if c[0] == case)
     m, n, k = dims
     lda, ldb, ldc = strides
@@ -98,7 +105,7 @@ def test_general_hardware_matrix_bit_exact(gpu, oracle, case):
     for r in range(m):
         expected[r * ldc:r * ldc + n] = out[r * n:(r + 1) * n]
     ga, gb, gc = Guarded(gpu, a), Guarded(gpu, b), Guarded(gpu, c)
-    _kernels().tiled_gemm_general_v1_gpu.Kernel.load(gpu).prepare(
+    getattr(_kernels(), GENERAL_SCHEDULES[schedule]).Kernel.load(gpu).prepare(
         ga.body, gb.body, gc.body, m, n, k, lda, ldb, ldc, alpha, beta).launch()
     got = gc.download()
     assert_same(got, expected, case)
@@ -113,7 +120,9 @@ def test_general_hardware_matrix_bit_exact(gpu, oracle, case):
 ])
 def test_general_random_within_tolerance(gpu, oracle, dims, strides, alpha, beta):
     """Random bf16 inputs: MFMA summation order differs from the sequential
-    recurrence; rel-err <= 1e-5 (fp32 outputs)."""
+    recurrence; rel-err <= 1e-5 (fp32 outputs).  The vectorized-A schedule
+    gives the same bits as the reference schedule (aligned and misaligned
+    A rows, tails)."""
     m, n, k = dims
     lda, ldb, ldc = strides
     rng = np.random.default_rng(m * 7919 + n * 31 + k)
@@ -130,6 +139,12 @@ def test_general_random_within_tolerance(gpu, oracle, dims, strides, alpha, beta
     rows = np.concatenate([got[r * ldc:r * ldc + n] for r in range(m)])
     assert rel_err(rows, out) <= 1e-5
     assert gc.guards_intact()
+    gv = Guarded(gpu, c)
+    _kernels().tiled_gemm_general_vector_a_v1_gpu.Kernel.load(gpu).prepare(
+        gpu.to_device(a), gpu.to_device(b), gv.body, m, n, k, lda, ldb, ldc, alpha,
+        beta).launch()
+    assert gv.guards_intact()
+    assert_same(gv.download(), got, "vector-a schedule vs reference schedule")
     # stride padding of C untouched
     for r in range(m - 1):
         assert got[r * ldc + n:(r + 1) * ldc].tobytes() == c[r * ldc + n:(r + 1) * ldc].tobytes()
