@@ -265,47 +265,52 @@ FE2O3_DEVICE float silu_mul(float g, float u) {
 
 constexpr int kRowBytes = 128, kStages = 2;  // 64 k per LDS stage, two stages
 constexpr int kSmem = kStages * 2 * gemm_pipe::Geo<kRowBytes>::kTileBytes;  // 128 KiB
-using Pipe = gemm_pipe::Geo<kRowBytes>;
 
-__global__ void __launch_bounds__(256, 1) gate_up_kernel(
-    const uint16_t* __restrict__ xc, const uint16_t* __restrict__ wg,
-    const uint16_t* __restrict__ wu, const uint32_t* __restrict__ offsets, uint32_t e_begin,
-    uint32_t e_end, uint32_t hidden, uint32_t ffn, uint32_t routes, uint16_t* __restrict__ hc) {
-  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  uint32_t e, row0, rows, nb;
-  if (!expert_tile(offsets, e_begin, e_end, routes, ffn / 128u, &e, &row0, &rows, &nb)) return;
+// One gate/up tile on the pipeline geometry G (ROW_BYTES of k per row and
+// stage, STAGES stages, RPW output rows per wave; the A tile holds 2 RPW
+// rows).  Full tiles run 256 rows on two 64-k stages.  An expert's short
+// last m-tile (at most 64 rows) runs 64 rows on four 32-k stages: its few
+// MFMAs per stage cannot hide the weight copies' latency, and three stages
+// of copies in flight can.  It keeps its place beside the same n-block's
+// full tiles in the work list, so it still shares their weights in L2.
+template <int ROW_BYTES, int STAGES, int RPW>
+FE2O3_DEVICE void gate_up_tile(const uint16_t* __restrict__ xc, const uint16_t* __restrict__ wg,
+                               const uint16_t* __restrict__ wu, uint32_t e, uint32_t row0,
+                               uint32_t rows, uint32_t nb, uint32_t hidden, uint32_t ffn,
+                               uint16_t* __restrict__ hc, uint8_t* smem) {
+  using G = gemm_pipe::Geo<ROW_BYTES>;
   const uint32_t f0 = nb * 128u;
-  const auto ar = gemm_pipe::dense_rows<kRowBytes>(xc + (uint64_t)row0 * hidden, hidden, rows,
-                                                   hidden);
+  const auto ar = gemm_pipe::dense_rows<ROW_BYTES, 2 * RPW>(xc + (uint64_t)row0 * hidden, hidden,
+                                                            rows, hidden);
   // B tile row r: 32-row block jb = r/32 belongs to wave column wn = jb/4;
   // within a wave column the blocks are gate f, up f, gate f+32, up f+32 for
   // f = f0 + 64*wn, so each lane's gate and up accumulators of one (row, f)
   // pair up in the epilogue.
   // The buffers are the expert's gate and up matrices.
-  gemm_pipe::Rows<kRowBytes> br;
+  gemm_pipe::Rows<ROW_BYTES> br;
   const uint64_t wbase = (uint64_t)e * ffn * hidden;
   br.bytes = ffn * hidden * 2u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
-  for (int j = 0; j < Pipe::kInstPerWave; ++j) {
-    const uint32_t row = Pipe::inst_row(j);
+  for (int j = 0; j < G::kInstPerWave; ++j) {
+    const uint32_t row = G::inst_row(j);
     // the load's rows lie in one 32-row block: gate or up is wave-uniform
-    const uint32_t jb = ((4u * j + wave) * Pipe::kRowsPerInst) >> 5, wn = jb >> 2, jj = jb & 3u;
+    const uint32_t jb = ((4u * j + wave) * G::kRowsPerInst) >> 5, wn = jb >> 2, jj = jb & 3u;
     const uint32_t f = f0 + wn * 64u + (jj >> 1) * 32u + (row & 31u);
     br.base[j] = ((jj & 1u) ? wu : wg) + wbase;
-    br.voff[j] = (f * hidden + Pipe::inst_chunk(row) * 8u) * 2u;
+    br.voff[j] = (f * hidden + G::inst_chunk(row) * 8u) * 2u;
   }
-  gemm_pipe::Acc16 acc;
-  gemm_pipe::mainloop<gemm_pipe::Bf16Mma<kRowBytes>, kRowBytes, kStages>(ar, br, hidden, smem,
-                                                                        acc);
+  using Mma = gemm_pipe::Bf16Mma<ROW_BYTES, RPW>;
+  typename Mma::Acc acc;
+  gemm_pipe::mainloop<Mma, ROW_BYTES, STAGES>(ar, br, hidden, smem, acc);
   // accumulator column j (16 B rows each) of wave column wn: j = 0,1 gate
   // f .. f+31, j = 2,3 up f .. f+31, j = 4,5 gate f+32 .., j = 6,7 up f+32 ..
   // (f = f0 + 64 wn); gate j pairs with up j + 2
-  const uint32_t r0 = gemm_pipe::acc16_row0();
+  const uint32_t r0 = gemm_pipe::acc16_row0<RPW>();
   const uint32_t c0 = gemm_pipe::acc16_col0();                // 128 wn + 4 (lane / 16)
   const uint32_t fl = f0 + ((c0 & 128u) >> 1) + (c0 & 127u);  // f0 + 64 wn + 4 (lane / 16)
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < Mma::kRB; ++i) {
     const uint32_t r = r0 + 16u * i;
     if (r >= rows) continue;
     uint16_t* out_row = hc + (uint64_t)(row0 + r) * ffn;
@@ -323,6 +328,49 @@ __global__ void __launch_bounds__(256, 1) gate_up_kernel(
   }
 }
 
+__global__ void __launch_bounds__(256, 1) gate_up_kernel(
+    const uint16_t* __restrict__ xc, const uint16_t* __restrict__ wg,
+    const uint16_t* __restrict__ wu, const uint32_t* __restrict__ offsets, uint32_t e_begin,
+    uint32_t e_end, uint32_t hidden, uint32_t ffn, uint32_t routes, uint16_t* __restrict__ hc) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  uint32_t e, row0, rows, nb;
+  if (!expert_tile(offsets, e_begin, e_end, routes, ffn / 128u, &e, &row0, &rows, &nb)) return;
+  if (rows > 64u)
+    gate_up_tile<128, 2, 128>(xc, wg, wu, e, row0, rows, nb, hidden, ffn, hc, smem);
+  else
+    gate_up_tile<64, 4, 32>(xc, wg, wu, e, row0, rows, nb, hidden, ffn, hc, smem);
+}
+
+// One down tile (split K: list entry nb = 2 * n-block + k-half; each half
+// writes its own fp32 partial, yc then yc + routes * hidden, which the
+// combine adds), on the geometry of gate_up_tile.
+template <int ROW_BYTES, int STAGES, int RPW>
+FE2O3_DEVICE void down_tile(const uint16_t* __restrict__ hc, const uint16_t* __restrict__ wd,
+                            uint32_t e, uint32_t row0, uint32_t rows, uint32_t nb,
+                            uint32_t hidden, uint32_t ffn, uint64_t routes,
+                            float* __restrict__ yc, uint8_t* smem) {
+  const uint32_t n0 = (nb >> 1) * 256u, kh = nb & 1u, k_half = ffn / 2u;
+  const auto ar = gemm_pipe::dense_rows<ROW_BYTES, 2 * RPW>(
+      hc + (uint64_t)row0 * ffn + kh * k_half, ffn, rows, k_half);
+  const auto br = gemm_pipe::dense_rows<ROW_BYTES>(
+      wd + (uint64_t)e * hidden * ffn + (uint64_t)n0 * ffn + kh * k_half, ffn, 256, k_half);
+  using Mma = gemm_pipe::Bf16Mma<ROW_BYTES, RPW>;
+  typename Mma::Acc acc;
+  gemm_pipe::mainloop<Mma, ROW_BYTES, STAGES>(ar, br, k_half, smem, acc);
+  float* part = yc + (uint64_t)kh * routes * hidden;
+  const uint32_t r0 = gemm_pipe::acc16_row0<RPW>(), c0 = gemm_pipe::acc16_col0();
+#pragma unroll
+  for (int i = 0; i < Mma::kRB; ++i) {
+    const uint32_t r = r0 + 16u * i;
+    if (r >= rows) continue;
+    float* out_row = part + (uint64_t)(row0 + r) * hidden + n0 + c0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *reinterpret_cast<f32x4_t*>(out_row + 16u * j) = acc.v[i][j];
+  }
+}
+
+// Split K in two: twice as many workgroups, each half as long, fill the last
+// wave of the grid better at this kernel's few hundred tiles.
 __global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict__ hc,
                                                       const uint16_t* __restrict__ wd,
                                                       const uint32_t* __restrict__ offsets,
@@ -330,32 +378,14 @@ __global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict
                                                       uint32_t hidden, uint32_t ffn,
                                                       uint64_t routes, float* __restrict__ yc) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  // Split K in two: list entry nb = 2 * n-block + k-half.  Each half writes
-  // its own fp32 partial (yc, then yc + routes * hidden); the combine adds
-  // them.  Twice as many workgroups, each half as long, fill the last wave of
-  // the grid better at this kernel's few hundred tiles.
   uint32_t e, row0, rows, nb;
   if (!expert_tile(offsets, e_begin, e_end, (uint32_t)routes, 2u * (hidden / 256u), &e, &row0,
                    &rows, &nb))
     return;
-  const uint32_t n0 = (nb >> 1) * 256u, kh = nb & 1u, k_half = ffn / 2u;
-  const auto ar = gemm_pipe::dense_rows<kRowBytes>(hc + (uint64_t)row0 * ffn + kh * k_half, ffn,
-                                                   rows, k_half);
-  const auto br = gemm_pipe::dense_rows<kRowBytes>(
-      wd + (uint64_t)e * hidden * ffn + (uint64_t)n0 * ffn + kh * k_half, ffn, 256, k_half);
-  gemm_pipe::Acc16 acc;
-  gemm_pipe::mainloop<gemm_pipe::Bf16Mma<kRowBytes>, kRowBytes, kStages>(ar, br, k_half, smem,
-                                                                        acc);
-  float* part = yc + (uint64_t)kh * routes * hidden;
-  const uint32_t r0 = gemm_pipe::acc16_row0(), c0 = gemm_pipe::acc16_col0();
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t r = r0 + 16u * i;
-    if (r >= rows) continue;
-    float* out_row = part + (uint64_t)(row0 + r) * hidden + n0 + c0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) *reinterpret_cast<f32x4_t*>(out_row + 16u * j) = acc.v[i][j];
-  }
+  if (rows > 64u)
+    down_tile<128, 2, 128>(hc, wd, e, row0, rows, nb, hidden, ffn, routes, yc, smem);
+  else
+    down_tile<64, 4, 32>(hc, wd, e, row0, rows, nb, hidden, ffn, routes, yc, smem);
 }
 
 __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ yc,
