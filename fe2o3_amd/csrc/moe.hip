@@ -6,13 +6,11 @@
 //      id (kernel.rs:25-33); route r = 2*token + rank; gating weights
 //      w0 = 1/(1+exp(l1-l0)), w1 = 1 - w0 (w0 in [0.5,1], so the pair sums to
 //      exactly 1 as examples/moe_expert_v1/src/pipeline.rs:137-148 requires).
-//   2. route_assign: one 128-thread workgroup; thread t owns a contiguous
-//      block of routes; per-expert counts per thread in LDS, a per-expert
-//      exclusive scan over threads, requested = totals, admitted =
-//      min(requested, capacity), offsets = exclusive scan of admitted with the
-//      terminal total; then each route gets rank = number of earlier routes
-//      (lower route id) of its expert, slot = offset + rank when
-//      rank < capacity (stable prefix), permutation[slot] = route,
+//   2. route_assign: one workgroup per 512 routes; requested = per-expert
+//      totals, admitted = min(requested, capacity), offsets = exclusive scan
+//      of admitted with the terminal total; each route gets rank = number of
+//      earlier routes (lower route id) of its expert, slot = offset + rank
+//      when rank < capacity (stable prefix), permutation[slot] = route,
 //      inverse[route] = slot, DROP sentinels elsewhere.  Integer work only:
 //      bit-identical to the reference's sort-based oracle.
 //
@@ -96,78 +94,133 @@ __global__ void __launch_bounds__(256) route_select_kernel(const T* __restrict__
   }
 }
 
-// A launch whose route_select rejected any token (an expert id out of
-// range in top2) is rejected as a whole: every output takes its sentinel --
-// top2, slots, permutation and inverse DROP, route weights +0, requested,
-// admitted and offsets 0 -- so no expert receives a route.
-__global__ void __launch_bounds__(ASSIGN_THREADS) route_assign_kernel(
+// Slot assignment, one workgroup per RA_ROUTES consecutive routes (one route
+// per thread).  Every workgroup first counts, per expert, the routes of the
+// whole top2 array and those before its own range, straight from top2 (a few
+// tens of KiB read from L2, so the workgroups need no scratch and no
+// communication); then each route's stable rank = routes of its expert
+// before the workgroup + those in earlier waves of the workgroup + those in
+// earlier lanes of its wave (per-expert wave ballots).  requested = totals,
+// admitted = min(requested, capacity), offsets = exclusive scan of admitted
+// with the terminal total; a route of rank < capacity gets slot
+// offsets[e] + rank, permutation[slot] = route, inverse[route] = slot; DROP
+// elsewhere.  Integer work only: bit-identical to the reference's sort-based
+// oracle for any number of workgroups.
+//
+// A launch whose route_select rejected any token (an expert id out of range
+// in top2) is rejected as a whole: every workgroup sees that entry, and
+// every output takes its sentinel -- top2, slots, permutation and inverse
+// DROP, route weights +0, requested, admitted and offsets 0 -- so no expert
+// receives a route.
+constexpr int RA_THREADS = 512, RA_WAVES = RA_THREADS / 64, RA_ROUTES = RA_THREADS;
+
+// For the 64 lanes' experts e (DROP = no route): calls fn(x, mask) once per
+// distinct expert x present, mask = the lanes holding x.
+template <class Fn>
+FE2O3_DEVICE void for_each_expert(uint32_t e, Fn&& fn) {
+  uint64_t left = __ballot(e != DROP);
+  while (left != 0ull) {
+    const int first = (int)__builtin_ctzll(left);
+    const uint32_t x = (uint32_t)__builtin_amdgcn_readlane((int)e, first);
+    const uint64_t mask = __ballot(e == x);
+    fn(x, mask);
+    left &= ~mask;
+  }
+}
+
+__global__ void __launch_bounds__(RA_THREADS) route_assign_kernel(
     uint32_t* __restrict__ top2, uint32_t routes, uint32_t experts, uint32_t capacity,
     uint32_t* __restrict__ requested, uint32_t* __restrict__ admitted,
     uint32_t* __restrict__ offsets, uint32_t* __restrict__ slots,
     uint32_t* __restrict__ permutation, uint32_t* __restrict__ inverse,
     float* __restrict__ weights) {
-  __shared__ uint32_t cnt[MAX_EXPERTS * ASSIGN_THREADS];
-  __shared__ uint32_t off_s[MAX_EXPERTS + 1];
-  const uint32_t t = threadIdx.x;
-  const uint32_t per = (routes + ASSIGN_THREADS - 1) / ASSIGN_THREADS;
-  const uint32_t r0 = t * per;
-  const uint32_t r1 = r0 + per < routes ? r0 + per : routes;
-  for (uint32_t e = 0; e < experts; ++e) cnt[e * ASSIGN_THREADS + t] = 0;
+  __shared__ uint32_t total[MAX_EXPERTS], before[MAX_EXPERTS], off_s[MAX_EXPERTS + 1];
+  __shared__ uint32_t wave_cnt[RA_WAVES][MAX_EXPERTS];
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+  const uint32_t start = blockIdx.x * (uint32_t)RA_ROUTES;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  if (t < experts) total[t] = before[t] = 0;
+  for (uint32_t i = t; i < RA_WAVES * MAX_EXPERTS; i += RA_THREADS) (&wave_cnt[0][0])[i] = 0;
+  __syncthreads();
+  // counts over all of top2, 64 routes per wave and chunk; the loads of
+  // eight chunks are issued together, then counted
+  constexpr int kBatch = 8;
   int rejected = 0;
-  for (uint32_t r = r0; r < r1; ++r) {
-    const uint32_t e = top2[r];
-    if (e < experts) cnt[e * ASSIGN_THREADS + t] += 1;
-    else rejected = 1;
+  for (uint32_t base0 = wave * 64u; base0 < routes; base0 += kBatch * RA_THREADS) {
+    uint32_t ev[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const uint32_t r = base0 + q * RA_THREADS + lane;
+      ev[q] = r < routes ? top2[r] : DROP;
+      rejected |= r < routes && ev[q] >= experts;
+      if (ev[q] >= experts) ev[q] = DROP;  // not an expert: counted nowhere
+    }
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const uint32_t base = base0 + q * RA_THREADS;
+      for_each_expert(ev[q], [&](uint32_t x, uint64_t mask) {
+        if (lane == 0) {
+          const uint32_t c = (uint32_t)__builtin_popcountll(mask);
+          atomicAdd(&total[x], c);
+          if (base < start) atomicAdd(&before[x], c);
+        }
+      });
+    }
   }
-  for (uint32_t r = t; r < routes; r += ASSIGN_THREADS) permutation[r] = DROP;
+  const uint32_t r = start + t;
   if (__syncthreads_or(rejected)) {
-    for (uint32_t r = t; r < routes; r += ASSIGN_THREADS) {
+    if (r < routes) {
       top2[r] = DROP;
       slots[r] = DROP;
       inverse[r] = DROP;
+      permutation[r] = DROP;
       if (weights != nullptr) weights[r] = 0.0f;
     }
-    if (t < experts) requested[t] = admitted[t] = offsets[t] = 0;
-    if (t == 0) offsets[experts] = 0;
+    if (blockIdx.x == 0) {
+      if (t < experts) requested[t] = admitted[t] = offsets[t] = 0;
+      if (t == 0) offsets[experts] = 0;
+    }
     return;
   }
-  if (t < experts) {  // exclusive scan of expert t's counts over threads
+  if (t == 0) {  // admitted counts and their exclusive scan (at most 64 experts)
     uint32_t run = 0;
-    for (uint32_t i = 0; i < ASSIGN_THREADS; ++i) {
-      const uint32_t c = cnt[t * ASSIGN_THREADS + i];
-      cnt[t * ASSIGN_THREADS + i] = run;
-      run += c;
+    for (uint32_t x = 0; x < experts; ++x) {
+      off_s[x] = run;
+      run += total[x] < capacity ? total[x] : capacity;
     }
-    requested[t] = run;
-    off_s[t] = run;  // temporarily the requested count
-  }
-  __syncthreads();
-  if (t == 0) {
-    uint32_t run = 0;
-    for (uint32_t e = 0; e < experts; ++e) {
-      const uint32_t adm = off_s[e] < capacity ? off_s[e] : capacity;
-      admitted[e] = adm;
-      offsets[e] = run;
-      off_s[e] = run;
-      run += adm;
-    }
-    offsets[experts] = run;
     off_s[experts] = run;
   }
+  // ranks within this wave, and this wave's count per expert
+  const uint32_t e = r < routes ? top2[r] : DROP;
+  uint32_t rank = 0;
+  for_each_expert(e, [&](uint32_t x, uint64_t mask) {
+    if (e == x) rank = (uint32_t)__builtin_popcountll(mask & lt);
+    if (lane == 0) wave_cnt[wave][x] = (uint32_t)__builtin_popcountll(mask);
+  });
   __syncthreads();
-  for (uint32_t r = r0; r < r1; ++r) {
-    const uint32_t e = top2[r];
-    const uint32_t rank = cnt[e * ASSIGN_THREADS + t]++;
-    if (rank < capacity) {
-      const uint32_t slot = off_s[e] + rank;
-      slots[r] = slot;
-      inverse[r] = slot;
-      permutation[slot] = r;
-    } else {
-      slots[r] = DROP;
-      inverse[r] = DROP;
+  if (blockIdx.x == 0) {
+    if (t < experts) {
+      requested[t] = total[t];
+      admitted[t] = total[t] < capacity ? total[t] : capacity;
+      offsets[t] = off_s[t];
     }
+    if (t == 0) offsets[experts] = off_s[experts];
   }
+  if (r >= routes) return;
+  rank += before[e];
+  for (uint32_t w = 0; w < wave; ++w) rank += wave_cnt[w][e];
+  if (rank < capacity) {
+    const uint32_t slot = off_s[e] + rank;
+    slots[r] = slot;
+    inverse[r] = slot;
+    permutation[slot] = r;
+  } else {
+    slots[r] = DROP;
+    inverse[r] = DROP;
+  }
+  // slots below the accepted total are each written by their route; the rest
+  // of the permutation holds the sentinel
+  if (r >= off_s[experts]) permutation[r] = DROP;
 }
 
 // examples/moe_expert_v1/src/kernel.rs:104-157: T=8, K=2, O=16.
@@ -471,7 +524,8 @@ int32_t route(const void* logits, uint64_t logits_len, uint32_t dtype, uint32_t*
       route_select_kernel<uint16_t><<<blocks, 256, 0, s>>>((const uint16_t*)logits, tokens,
                                                            experts, top2, weights, status);
   }
-  route_assign_kernel<<<1, ASSIGN_THREADS, 0, s>>>(top2, (uint32_t)routes, experts, capacity,
+  const unsigned assign_blocks = routes ? (unsigned)((routes + RA_ROUTES - 1) / RA_ROUTES) : 1u;
+  route_assign_kernel<<<assign_blocks, RA_THREADS, 0, s>>>(top2, (uint32_t)routes, experts, capacity,
                                                    requested, admitted, offsets, slots,
                                                    permutation, inverse, weights);
   return fe2o3_host::after_launch();
@@ -644,10 +698,10 @@ __global__ void __launch_bounds__(ASSIGN_THREADS) routing_check_kernel(
 // kernels behind each entry point (fe2o3_kernel_resources)
 const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1", "route_select_kernel<float>", (const void*)route_select_kernel<float>, 256, 0}),
-    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1", "route_assign_kernel", (const void*)route_assign_kernel, ASSIGN_THREADS, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1", "route_assign_kernel", (const void*)route_assign_kernel, RA_THREADS, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_select_kernel<float>", (const void*)route_select_kernel<float>, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_select_kernel<uint16_t>", (const void*)route_select_kernel<uint16_t>, 256, 0}),
-    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_assign_kernel", (const void*)route_assign_kernel, ASSIGN_THREADS, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_assign_kernel", (const void*)route_assign_kernel, RA_THREADS, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_expert_combine_f32_t8_k2_o16_v1", "combine_profile_kernel", (const void*)combine_profile_kernel, 128, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "gather_kernel", (const void*)gather_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "gate_up_kernel", (const void*)gate_up_kernel, 256, kSmem}),

@@ -110,6 +110,24 @@ def test_route_config5_bf16_logits_bit_exact(gpu, oracle, capacity):
     assert all(inv[perm[s]] == s for s in range(total))
 
 
+@pytest.mark.parametrize("tokens", [1, 255, 256, 257, 1000, 5000])
+@pytest.mark.parametrize("experts,capacity", [(2, 0xFFFFFFFF), (7, 100), (64, 3)])
+def test_route_workgroup_boundaries(gpu, oracle, tokens, experts, capacity):
+    """The slot assignment runs one workgroup per 512 routes: route counts
+    below, at and across workgroup boundaries, few and many experts, with
+    and without capacity drops; every output array bit-equal to the oracle
+    (logits rounded to multiples of 1/4, so ties are frequent)."""
+    rng = np.random.default_rng(tokens * 97 + experts)
+    logits = (np.round(rng.standard_normal(tokens * experts) * 4) / 4).astype(np.float32)
+    out = _route(gpu, gpu.to_device(logits), tokens, experts, capacity)
+    rc, ref = oracle.moe_top2_route(logits, tokens, experts, capacity)
+    assert rc == 0
+    names = dict(zip(["top2", "requested", "admitted", "offsets", "slots", "permutation",
+                      "inverse"], ROUTE_KEYS))
+    for mine, theirs in names.items():
+        assert_same(out[mine].download(), ref[theirs], mine)
+
+
 def test_route_f32_logits_many_experts(gpu, oracle):
     tokens, experts = 1000, 64
     rng = np.random.default_rng(3)
