@@ -51,6 +51,148 @@ class Fe2o3KernelResources(C.Structure):
     ]
 
 
+# ---- exact LDS GEMM lifecycle records (fe2o3_lds_gemm_slice1_*) ----------------------
+
+u8, c_char = C.c_uint8, C.c_char
+
+
+class Fe2o3Slice1ErrorV1(C.Structure):
+    _fields_ = [("kind", i32), ("index", i32), ("adapter_status", i32), ("reserved", i32),
+                ("expected", u64), ("actual", u64), ("field", c_char * 64)]
+
+
+class Fe2o3Slice1BufferContractV1(C.Structure):
+    _fields_ = [("role", u32), ("element", u32), ("elements", u64), ("bytes", u64),
+                ("length_identity", u8 * 32), ("ownership", u32), ("access", u32),
+                ("alias", u32), ("reserved", u32)]
+
+
+class Fe2o3Slice1ContractV1(C.Structure):
+    _fields_ = [("profile", u32), ("code_object_version", u32), ("target", c_char * 32),
+                ("identity", u8 * 32), ("grid", u32 * 3), ("workgroup", u32 * 3),
+                ("wavefront_size", u32), ("explicit_kernarg_bytes", u32),
+                ("complete_kernarg_bytes", u32), ("kernarg_alignment", u32),
+                ("static_lds_bytes", u32), ("lds_allocations", u32),
+                ("lds_bytes_per_allocation", u32), ("lds_alignment", u32),
+                ("buffers", Fe2o3Slice1BufferContractV1 * 3)]
+
+
+class Fe2o3Slice1InspectionV1(C.Structure):
+    _fields_ = [("byte_len", u64), ("code_object_version", u32), ("e_flags", u32),
+                ("target", c_char * 64), ("kd_group_segment_bytes", u32),
+                ("kd_private_segment_bytes", u32), ("kd_kernarg_bytes", u32),
+                ("kd_wavefront_size", u32), ("md_kernarg_bytes", u32),
+                ("md_kernarg_alignment", u32), ("md_group_segment_bytes", u32),
+                ("md_private_segment_bytes", u32), ("md_wavefront_size", u32),
+                ("md_max_flat_workgroup_size", u32), ("explicit_args", u32),
+                ("explicit_bytes", u32), ("implicit_offset", u32), ("implicit_bytes", u32),
+                ("sgpr_spills", u32), ("vgpr_spills", u32), ("uses_dynamic_stack", u32),
+                ("reserved", u32)]
+
+
+class Fe2o3Slice1ArtifactV1(C.Structure):
+    _fields_ = [("finalizer_identity", u8 * 32), ("build_digest", u8 * 32),
+                ("import_identity", u8 * 32), ("profile_identity", u8 * 32),
+                ("contract", Fe2o3Slice1ContractV1), ("inspection", Fe2o3Slice1InspectionV1)]
+
+
+class Fe2o3Slice1JoinFactsV1(C.Structure):
+    _fields_ = [("import_matches", u8), ("profile_matches", u8), ("contract_matches", u8),
+                ("finalized_output_matches", u8), ("inspection_matches", u8),
+                ("host_profile_identity_matches", u8), ("reserved", u8 * 2),
+                ("contract", Fe2o3Slice1ContractV1), ("host_target", c_char * 32),
+                ("host_profile", u32), ("host_grid", u32 * 3), ("host_workgroup", u32 * 3),
+                ("host_static_lds", u32), ("host_dynamic_lds", u32),
+                ("host_explicit_kernarg", u32), ("host_complete_kernarg", u32),
+                ("host_kernarg_alignment", u32), ("host_length_identities", (u8 * 32) * 3)]
+
+
+class Fe2o3Slice1GeometryV1(C.Structure):
+    _fields_ = [("grid", u32 * 3), ("workgroup", u32 * 3), ("dynamic_lds_bytes", u32)]
+
+
+class Fe2o3Slice1EnvironmentV1(C.Structure):
+    _fields_ = [("runtime_instance", u8 * 16), ("physical_target", c_char * 64),
+                ("hip_ordinal", i32), ("physical_uuid", u8 * 16), ("agent_target", c_char * 64),
+                ("agent_handle", u64), ("agent_runtime_instance", u8 * 16),
+                ("agent_physical_uuid", u8 * 16)]
+
+
+class Fe2o3Slice1LoadV1(C.Structure):
+    _fields_ = [("digest", u8 * 32), ("byte_len", u64), ("runtime_instance", u8 * 16),
+                ("agent_handle", u64), ("executable_object", u8 * 16)]
+
+
+class Fe2o3Slice1ResolutionV1(C.Structure):
+    _fields_ = [("executable_object", u8 * 16), ("kernel_object", u8 * 16),
+                ("symbol", c_char * 64), ("kernarg_segment_bytes", u64),
+                ("kernarg_alignment", u64)]
+
+
+class Fe2o3Slice1ResourcesV1(C.Structure):
+    _fields_ = [("executable_object", u8 * 16), ("kernel_object", u8 * 16),
+                ("group_segment_bytes", u32), ("private_segment_bytes", u32)]
+
+
+class Fe2o3Slice1ImplicitV1(C.Structure):
+    _fields_ = [("executable_object", u8 * 16), ("kernel_object", u8 * 16),
+                ("geometry", Fe2o3Slice1GeometryV1), ("explicit_bytes", u64),
+                ("implicit_offset", u64), ("implicit_bytes", u64), ("completed", u32),
+                ("reserved", u32)]
+
+
+class Fe2o3Slice1DispatchV1(C.Structure):
+    _fields_ = [("dispatch_identity", u8 * 16), ("executable_object", u8 * 16),
+                ("kernel_object", u8 * 16), ("geometry", Fe2o3Slice1GeometryV1),
+                ("completed", u32)]
+
+
+class Fe2o3Slice1UnloadV1(C.Structure):
+    _fields_ = [("executable_object", u8 * 16), ("runtime_instance", u8 * 16),
+                ("agent_handle", u64), ("released", u32), ("reserved", u32)]
+
+
+pu64 = C.POINTER(u64)
+SLICE1_CONTEXT_FN = C.CFUNCTYPE(i32, vp, C.POINTER(u8 * 16))
+SLICE1_ENVIRONMENT_FN = C.CFUNCTYPE(i32, vp, C.POINTER(Fe2o3Slice1EnvironmentV1))
+SLICE1_LOAD_FN = C.CFUNCTYPE(i32, vp, C.POINTER(u8), u64, C.POINTER(u8 * 32), pu64,
+                             C.POINTER(Fe2o3Slice1LoadV1))
+SLICE1_RESOLVE_FN = C.CFUNCTYPE(i32, vp, u64, C.c_char_p, pu64, C.POINTER(Fe2o3Slice1ResolutionV1))
+SLICE1_RESOURCES_FN = C.CFUNCTYPE(i32, vp, u64, u64, C.POINTER(Fe2o3Slice1ResourcesV1))
+SLICE1_IMPLICIT_FN = C.CFUNCTYPE(i32, vp, u64, u64, C.POINTER(Fe2o3Slice1GeometryV1), u64, u64, u64,
+                                 C.POINTER(u8), u64, C.POINTER(Fe2o3Slice1ImplicitV1))
+SLICE1_LAUNCH_FN = C.CFUNCTYPE(i32, vp, u64, u64, C.POINTER(Fe2o3Slice1GeometryV1), C.POINTER(u8),
+                               u64, C.POINTER(Fe2o3Slice1DispatchV1))
+SLICE1_DROP_KERNEL_FN = C.CFUNCTYPE(None, vp, u64)
+SLICE1_UNLOAD_FN = C.CFUNCTYPE(i32, vp, u64, C.POINTER(Fe2o3Slice1UnloadV1))
+SLICE1_DROP_ADAPTER_FN = C.CFUNCTYPE(None, vp)
+SLICE1_RELEASE_FN = C.CFUNCTYPE(None, vp)
+
+
+class Fe2o3Slice1AdapterV1(C.Structure):
+    _fields_ = [("self", vp), ("context_identity", SLICE1_CONTEXT_FN),
+                ("observe_environment", SLICE1_ENVIRONMENT_FN),
+                ("load_executable", SLICE1_LOAD_FN), ("resolve_kernel", SLICE1_RESOLVE_FN),
+                ("observe_resources", SLICE1_RESOURCES_FN),
+                ("initialize_implicit_kernarg", SLICE1_IMPLICIT_FN),
+                ("launch_and_wait", SLICE1_LAUNCH_FN), ("drop_kernel", SLICE1_DROP_KERNEL_FN),
+                ("unload_executable", SLICE1_UNLOAD_FN), ("drop_adapter", SLICE1_DROP_ADAPTER_FN)]
+
+
+class Fe2o3Slice1ReceiptV1(C.Structure):
+    _fields_ = [("finalizer_identity", u8 * 32), ("import_identity", u8 * 32),
+                ("profile_identity", u8 * 32), ("executable_object", u8 * 16),
+                ("kernel_object", u8 * 16), ("dispatch_identity", u8 * 16),
+                ("unload_identity", u8 * 32)]
+
+
+class Fe2o3Slice1ObservationV1(C.Structure):
+    _fields_ = [("state", i32), ("leases_retained", u32), ("holds_executable", u32),
+                ("holds_kernel", u32), ("environment", Fe2o3Slice1EnvironmentV1),
+                ("load", Fe2o3Slice1LoadV1), ("resolution", Fe2o3Slice1ResolutionV1),
+                ("resources", Fe2o3Slice1ResourcesV1), ("dispatch_identity", u8 * 16),
+                ("last_error", Fe2o3Slice1ErrorV1)]
+
 # name -> (restype, argtypes).  Order and meaning follow the header.
 SIGNATURES = {
     "fe2o3_status_string": (C.c_char_p, [i32]),
@@ -124,6 +266,22 @@ SIGNATURES = {
         i32, [vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, u64, vp]),
     "fe2o3_lds_reduce_i32_v1": (i32, [vp, u64, vp, u64, vp]),
     "fe2o3_scoped_atomic_add_u32_v1": (i32, [vp, u64, vp, u64, vp, vp]),
+    "fe2o3_sha256_v1": (i32, [vp, u64, C.POINTER(u8 * 32)]),
+    "fe2o3_lds_gemm_slice1_artifact_v1": (i32, [C.POINTER(Fe2o3Slice1ArtifactV1)]),
+    "fe2o3_lds_gemm_slice1_join_facts_v1": (i32, [C.POINTER(Fe2o3Slice1JoinFactsV1)]),
+    "fe2o3_lds_gemm_slice1_validate_join_v1": (
+        i32, [C.POINTER(Fe2o3Slice1JoinFactsV1), C.POINTER(Fe2o3Slice1ErrorV1)]),
+    "fe2o3_lds_gemm_slice1_join_v1": (
+        i32, [vp, u64, vp, u64, vp, u64, i32, SLICE1_RELEASE_FN, vp, pvp,
+              C.POINTER(Fe2o3Slice1ErrorV1)]),
+    "fe2o3_lds_gemm_slice1_hip_adapter_v1": (i32, [i32, C.POINTER(Fe2o3Slice1AdapterV1)]),
+    "fe2o3_lds_gemm_slice1_context_identity_v1": (i32, [i32, C.POINTER(u8 * 16)]),
+    "fe2o3_lds_gemm_slice1_load_v1": (
+        i32, [vp, C.POINTER(Fe2o3Slice1AdapterV1), C.POINTER(Fe2o3Slice1ErrorV1)]),
+    "fe2o3_lds_gemm_slice1_dispatch_and_wait_v1": (i32, [vp, C.POINTER(Fe2o3Slice1ErrorV1)]),
+    "fe2o3_lds_gemm_slice1_unload_v1": (i32, [vp, C.POINTER(Fe2o3Slice1ReceiptV1)]),
+    "fe2o3_lds_gemm_slice1_release_v1": (None, [vp]),
+    "fe2o3_lds_gemm_slice1_observe_v1": (i32, [vp, C.POINTER(Fe2o3Slice1ObservationV1)]),
 }
 
 

@@ -106,6 +106,10 @@ const char* fe2o3_status_string(int32_t status) {
     case FE2O3_ERR_M_TAIL: return "M is not a multiple of the 16-row tile";
     case FE2O3_ERR_N_TAIL: return "N is not a multiple of the 16-column tile";
     case FE2O3_ERR_K_TAIL: return "K is not a multiple of the 16-deep reduction tile";
+    case FE2O3_ERR_JOIN: return "code object and host request do not reconcile";
+    case FE2O3_ERR_LOAD: return "lifecycle load rejected";
+    case FE2O3_ERR_DISPATCH: return "lifecycle dispatch rejected";
+    case FE2O3_ERR_STATE: return "lifecycle call out of order";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);

@@ -482,6 +482,317 @@ typedef struct Fe2o3KernelResources {
 int32_t fe2o3_kernel_resources(const char *entry, uint32_t index, Fe2o3KernelResources *out,
                                uint32_t *count);
 
+/* ---- typed lifecycle of the exact LDS GEMM code object -----------------------------------
+ *
+ * crates/fe2o3-host/src/generated_lds_gemm_lifecycle.rs: a one-shot,
+ * linear lifecycle over one code object of the exact 16x16x16 LDS GEMM
+ * profile: join (:276) -> load (:298) -> dispatch_and_wait (:391) ->
+ * unload (:522).  The code object is the library's own gfx950 build of
+ * tiled_gemm_lds_v1 (code object v6, xnack-), embedded in the library; it
+ * is never exposed.  Its kernarg ABI is the reference's: 48 explicit bytes
+ * ({u64 address, u64 elements} for A, B and C), then a 256-byte implicit
+ * suffix initialized for the launch geometry, 304 bytes in all, 8-byte
+ * aligned in the descriptor and 16-byte aligned for the dispatch.
+ *
+ * The lifecycle is an opaque handle whose state only moves forward:
+ *   JOINED --load--> LOADED --dispatch_and_wait--> COMPLETED --unload--> (receipt, freed)
+ * A failed load or dispatch performs every cleanup the reached state needs
+ * (kernel dropped, then one terminal unload, then the A/B/C leases and the
+ * adapter released) and leaves the handle FAILED.  Calling a transition in
+ * another state returns FE2O3_ERR_STATE and changes nothing.
+ * fe2o3_lds_gemm_slice1_release_v1 frees a handle in any state, unloading
+ * first when it holds a loaded executable (the reference's Drop).  An
+ * unload that the adapter reports as failed, or whose observation does not
+ * match the load, aborts the process (generated_lds_gemm_lifecycle.rs:
+ * 779-806): the executable's state is then unknown.
+ *
+ * Runtime access goes through an adapter: a table of callbacks
+ * (ReviewedExactLdsGemmRuntimeAdapterV1, :101-121, and the HSA lifecycle
+ * adapter it extends).  fe2o3_lds_gemm_slice1_hip_adapter_v1 returns the
+ * library's HIP adapter (module load from memory, function resolution,
+ * resource query, module launch with an explicit kernarg buffer, stream
+ * synchronize, module unload).  A caller may supply its own table, e.g.
+ * to observe or fault-inject the lifecycle without a GPU.  Adapter
+ * callbacks return 0 on success, anything else on failure; the lifecycle
+ * validates every observation they return against what it asked for.
+ */
+#define FE2O3_ERR_JOIN (-27)     /* code object / host request reconciliation failed */
+#define FE2O3_ERR_LOAD (-28)     /* environment, load, resolution or resources rejected */
+#define FE2O3_ERR_DISPATCH (-29) /* implicit kernarg or dispatch rejected                */
+#define FE2O3_ERR_STATE (-30)    /* lifecycle call out of order                         */
+
+#define FE2O3_SLICE1_EXPLICIT_KERNARG_BYTES 48u
+#define FE2O3_SLICE1_IMPLICIT_KERNARG_BYTES 256u
+#define FE2O3_SLICE1_COMPLETE_KERNARG_BYTES 304u
+#define FE2O3_SLICE1_CONTRACT_KERNARG_ALIGNMENT 8u
+#define FE2O3_SLICE1_HSA_KERNARG_ALIGNMENT 16u
+#define FE2O3_SLICE1_STATIC_LDS_BYTES 1024u
+
+/* lifecycle states */
+enum {
+  FE2O3_SLICE1_JOINED = 1,
+  FE2O3_SLICE1_LOADED = 2,
+  FE2O3_SLICE1_COMPLETED = 3,
+  FE2O3_SLICE1_FAILED = 4
+};
+
+/* error kinds: ExactLdsGemmSlice1JoinErrorV1 (:126-135), the host-request
+ * preparation errors of crates/fe2o3-host/src/generated_lds_gemm.rs:676-720,
+ * ExactLdsGemmSlice1LoadErrorV1 (:167-177) and
+ * ExactLdsGemmSlice1DispatchErrorV1 (:216-223). */
+enum {
+  FE2O3_SLICE1_E_NONE = 0,
+  FE2O3_SLICE1_E_IMPORT_IDENTITY = 1,
+  FE2O3_SLICE1_E_PROFILE_IDENTITY = 2,
+  FE2O3_SLICE1_E_CONTRACT = 3,
+  FE2O3_SLICE1_E_FINALIZED_OUTPUT = 4,  /* field: which code-object fact drifted */
+  FE2O3_SLICE1_E_CONTRACT_FIELD = 5,
+  FE2O3_SLICE1_E_BUFFER_CONTRACT = 6,   /* index: buffer                          */
+  FE2O3_SLICE1_E_HOST_LENGTH_IDENTITY = 7,
+  FE2O3_SLICE1_E_HOST_FIELD = 8,
+  FE2O3_SLICE1_E_HOST_LENGTH = 9,       /* index: role, expected, actual          */
+  FE2O3_SLICE1_E_HOST_NULL = 10,
+  FE2O3_SLICE1_E_HOST_ALIGNMENT = 11,   /* expected: required bytes               */
+  FE2O3_SLICE1_E_HOST_OUTPUT_OVERLAP = 12, /* index: the input C overlaps         */
+  FE2O3_SLICE1_E_HOST_ADDRESS_OVERFLOW = 13,
+  FE2O3_SLICE1_E_CONTEXT_IDENTITY = 20,
+  FE2O3_SLICE1_E_ENVIRONMENT_ADAPTER = 21,
+  FE2O3_SLICE1_E_ENVIRONMENT = 22,
+  FE2O3_SLICE1_E_LOAD_ADAPTER = 23,
+  FE2O3_SLICE1_E_LOAD_OBSERVATION = 24,
+  FE2O3_SLICE1_E_KERNEL_ADAPTER = 25,
+  FE2O3_SLICE1_E_KERNEL_OBSERVATION = 26,
+  FE2O3_SLICE1_E_RESOURCE_ADAPTER = 27,
+  FE2O3_SLICE1_E_RESOURCE_OBSERVATION = 28,
+  FE2O3_SLICE1_E_IMPLICIT_ADAPTER = 40,
+  FE2O3_SLICE1_E_IMPLICIT_OBSERVATION = 41,
+  FE2O3_SLICE1_E_EXPLICIT_KERNARG_MUTATION = 42,
+  FE2O3_SLICE1_E_DISPATCH_ADAPTER = 43,
+  FE2O3_SLICE1_E_DISPATCH_OBSERVATION = 44
+};
+
+typedef struct Fe2o3Slice1ErrorV1 {
+  int32_t kind;           /* FE2O3_SLICE1_E_*                                 */
+  int32_t index;          /* buffer / role index where the kind names one, else -1 */
+  int32_t adapter_status; /* what the failing adapter callback returned, else 0 */
+  int32_t reserved;
+  uint64_t expected, actual;
+  char field[64];         /* the drifted field, as the reference names it, or "" */
+} Fe2o3Slice1ErrorV1;
+
+/* roles 1 = A, 2 = B, 3 = C; element 1 = bf16 bits in u16, 2 = f32;
+ * ownership 0 = shared borrow, 1 = unique borrow; access 0 = read-only,
+ * 1 = read-write; alias 0 = shared read-only, 1 = exclusive. */
+typedef struct Fe2o3Slice1BufferContractV1 {
+  uint32_t role, element;
+  uint64_t elements, bytes;
+  uint8_t length_identity[32];
+  uint32_t ownership, access, alias, reserved;
+} Fe2o3Slice1BufferContractV1;
+
+/* ExactLdsGemmContractV1 (crates/fe2o3-hsaco-finalize/src/
+ * lds_gemm_profile_registry.rs:606-670) for the gfx950 code object. */
+typedef struct Fe2o3Slice1ContractV1 {
+  uint32_t profile;  /* 1 = Slice1M16N16K16 */
+  uint32_t code_object_version;
+  char target[32];
+  uint8_t identity[32];
+  uint32_t grid[3], workgroup[3];
+  uint32_t wavefront_size;
+  uint32_t explicit_kernarg_bytes, complete_kernarg_bytes, kernarg_alignment;
+  uint32_t static_lds_bytes, lds_allocations, lds_bytes_per_allocation, lds_alignment;
+  Fe2o3Slice1BufferContractV1 buffers[3];
+} Fe2o3Slice1ContractV1;
+
+/* What the embedded code object itself says: ELF header, kernel descriptor
+ * (tiled_gemm_lds_v1.kd) and the AMDGPU metadata note. */
+typedef struct Fe2o3Slice1InspectionV1 {
+  uint64_t byte_len;
+  uint32_t code_object_version; /* from EI_ABIVERSION                              */
+  uint32_t e_flags;
+  char target[64];              /* metadata amdhsa.target, without the triple      */
+  uint32_t kd_group_segment_bytes, kd_private_segment_bytes, kd_kernarg_bytes, kd_wavefront_size;
+  uint32_t md_kernarg_bytes, md_kernarg_alignment, md_group_segment_bytes,
+      md_private_segment_bytes;
+  uint32_t md_wavefront_size, md_max_flat_workgroup_size;
+  uint32_t explicit_args, explicit_bytes; /* by-value arguments and their extent   */
+  uint32_t implicit_offset, implicit_bytes; /* first hidden argument, suffix bytes */
+  uint32_t sgpr_spills, vgpr_spills, uses_dynamic_stack, reserved;
+} Fe2o3Slice1InspectionV1;
+
+/* The finalized artifact: identities, contract and inspection.  The
+ * finalizer identity is the SHA-256 of the code-object bytes computed now;
+ * build_digest is the SHA-256 recorded when the library was built. */
+typedef struct Fe2o3Slice1ArtifactV1 {
+  uint8_t finalizer_identity[32];
+  uint8_t build_digest[32];
+  uint8_t import_identity[32];
+  uint8_t profile_identity[32];
+  Fe2o3Slice1ContractV1 contract;
+  Fe2o3Slice1InspectionV1 inspection;
+} Fe2o3Slice1ArtifactV1;
+
+/* JoinFactsV1 (:985-1034): everything join reconciles, as booleans for the
+ * identity comparisons plus the contract and host-request fields.
+ * inspection_matches: the code object's own ELF/descriptor/metadata facts
+ * agree with the contract (checked with finalized_output_matches). */
+typedef struct Fe2o3Slice1JoinFactsV1 {
+  uint8_t import_matches, profile_matches, contract_matches, finalized_output_matches;
+  uint8_t inspection_matches, host_profile_identity_matches, reserved[2];
+  Fe2o3Slice1ContractV1 contract;
+  char host_target[32];
+  uint32_t host_profile;
+  uint32_t host_grid[3], host_workgroup[3];
+  uint32_t host_static_lds, host_dynamic_lds;
+  uint32_t host_explicit_kernarg, host_complete_kernarg, host_kernarg_alignment;
+  uint8_t host_length_identities[3][32];
+} Fe2o3Slice1JoinFactsV1;
+
+typedef struct Fe2o3Slice1GeometryV1 {
+  uint32_t grid[3], workgroup[3], dynamic_lds_bytes;
+} Fe2o3Slice1GeometryV1;
+
+/* Observations (crates/fe2o3-host/src/hsa_executable_lifecycle.rs types of
+ * the same names).  Object identities are 16 opaque bytes. */
+typedef struct Fe2o3Slice1EnvironmentV1 {
+  uint8_t runtime_instance[16];
+  char physical_target[64];
+  int32_t hip_ordinal;
+  uint8_t physical_uuid[16];
+  char agent_target[64];
+  uint64_t agent_handle;
+  uint8_t agent_runtime_instance[16];
+  uint8_t agent_physical_uuid[16];
+} Fe2o3Slice1EnvironmentV1;
+
+typedef struct Fe2o3Slice1LoadV1 {
+  uint8_t digest[32];
+  uint64_t byte_len;
+  uint8_t runtime_instance[16];
+  uint64_t agent_handle;
+  uint8_t executable_object[16];
+} Fe2o3Slice1LoadV1;
+
+typedef struct Fe2o3Slice1ResolutionV1 {
+  uint8_t executable_object[16], kernel_object[16];
+  char symbol[64];
+  uint64_t kernarg_segment_bytes, kernarg_alignment;
+} Fe2o3Slice1ResolutionV1;
+
+typedef struct Fe2o3Slice1ResourcesV1 {
+  uint8_t executable_object[16], kernel_object[16];
+  uint32_t group_segment_bytes, private_segment_bytes;
+} Fe2o3Slice1ResourcesV1;
+
+typedef struct Fe2o3Slice1ImplicitV1 {
+  uint8_t executable_object[16], kernel_object[16];
+  Fe2o3Slice1GeometryV1 geometry;
+  uint64_t explicit_bytes, implicit_offset, implicit_bytes;
+  uint32_t completed, reserved;
+} Fe2o3Slice1ImplicitV1;
+
+typedef struct Fe2o3Slice1DispatchV1 {
+  uint8_t dispatch_identity[16];
+  uint8_t executable_object[16], kernel_object[16];
+  Fe2o3Slice1GeometryV1 geometry;
+  uint32_t completed;
+} Fe2o3Slice1DispatchV1;
+
+typedef struct Fe2o3Slice1UnloadV1 {
+  uint8_t executable_object[16];
+  uint8_t runtime_instance[16];
+  uint64_t agent_handle;
+  uint32_t released, reserved;
+} Fe2o3Slice1UnloadV1;
+
+/* The runtime adapter.  `self` is passed back to every callback.  The
+ * lifecycle takes the table over at load and calls drop_adapter exactly
+ * once when it is done with it (also when load fails).  Handles
+ * (`executable`, `kernel`) are the adapter's own opaque values. */
+typedef struct Fe2o3Slice1AdapterV1 {
+  void *self;
+  int32_t (*context_identity)(void *self, uint8_t identity[16]);
+  int32_t (*observe_environment)(void *self, Fe2o3Slice1EnvironmentV1 *out);
+  int32_t (*load_executable)(void *self, const uint8_t *bytes, uint64_t byte_len,
+                             const uint8_t digest[32], uint64_t *executable,
+                             Fe2o3Slice1LoadV1 *out);
+  int32_t (*resolve_kernel)(void *self, uint64_t executable, const char *symbol,
+                            uint64_t *kernel, Fe2o3Slice1ResolutionV1 *out);
+  int32_t (*observe_resources)(void *self, uint64_t executable, uint64_t kernel,
+                               Fe2o3Slice1ResourcesV1 *out);
+  int32_t (*initialize_implicit_kernarg)(void *self, uint64_t executable, uint64_t kernel,
+                                         const Fe2o3Slice1GeometryV1 *geometry,
+                                         uint64_t explicit_bytes, uint64_t implicit_offset,
+                                         uint64_t implicit_bytes, uint8_t *kernarg,
+                                         uint64_t kernarg_bytes, Fe2o3Slice1ImplicitV1 *out);
+  int32_t (*launch_and_wait)(void *self, uint64_t executable, uint64_t kernel,
+                             const Fe2o3Slice1GeometryV1 *geometry, uint8_t *kernarg,
+                             uint64_t kernarg_bytes, Fe2o3Slice1DispatchV1 *out);
+  void (*drop_kernel)(void *self, uint64_t kernel);
+  int32_t (*unload_executable)(void *self, uint64_t executable, Fe2o3Slice1UnloadV1 *out);
+  void (*drop_adapter)(void *self);
+} Fe2o3Slice1AdapterV1;
+
+/* Terminal receipt (UnloadedExactLdsGemmSlice1V1, :569-607). */
+typedef struct Fe2o3Slice1ReceiptV1 {
+  uint8_t finalizer_identity[32], import_identity[32], profile_identity[32];
+  uint8_t executable_object[16], kernel_object[16], dispatch_identity[16];
+  uint8_t unload_identity[32];
+} Fe2o3Slice1ReceiptV1;
+
+/* Descriptive view of a live handle. */
+typedef struct Fe2o3Slice1ObservationV1 {
+  int32_t state;
+  uint32_t leases_retained; /* the handle still refers to A, B and C */
+  uint32_t holds_executable, holds_kernel;
+  Fe2o3Slice1EnvironmentV1 environment;
+  Fe2o3Slice1LoadV1 load;
+  Fe2o3Slice1ResolutionV1 resolution;
+  Fe2o3Slice1ResourcesV1 resources;
+  uint8_t dispatch_identity[16];
+  Fe2o3Slice1ErrorV1 last_error;
+} Fe2o3Slice1ObservationV1;
+
+typedef struct Fe2o3Slice1Lifecycle Fe2o3Slice1Lifecycle;
+
+/* The embedded artifact's identities, contract and inspection. */
+int32_t fe2o3_lds_gemm_slice1_artifact_v1(Fe2o3Slice1ArtifactV1 *out);
+/* JoinFactsV1::from_exact for the embedded artifact and the canonical host
+ * request, and validate_join over any facts (:1036-1094, :1168-1218): the first
+ * mismatch in the reference's order, as FE2O3_ERR_JOIN plus *error. */
+int32_t fe2o3_lds_gemm_slice1_join_facts_v1(Fe2o3Slice1JoinFactsV1 *out);
+int32_t fe2o3_lds_gemm_slice1_validate_join_v1(const Fe2o3Slice1JoinFactsV1 *facts,
+                                               Fe2o3Slice1ErrorV1 *error);
+/* Prepare the host request (A, B: 256 bf16 values, 2-byte aligned; C: 256
+ * f32, 4-byte aligned and disjoint from A and B; generated_lds_gemm.rs:
+ * 559-670) and join it to the embedded artifact.  `release_leases`, if
+ * given, is called with `user` exactly once, when the handle stops
+ * referring to A, B and C (at completion, failure or release).  `device`
+ * is the HIP ordinal the buffers belong to; load checks the adapter's
+ * context identity against it. */
+int32_t fe2o3_lds_gemm_slice1_join_v1(const uint16_t *a, uint64_t a_len, const uint16_t *b,
+                                      uint64_t b_len, float *c, uint64_t c_len, int32_t device,
+                                      void (*release_leases)(void *user), void *user,
+                                      Fe2o3Slice1Lifecycle **out, Fe2o3Slice1ErrorV1 *error);
+/* The library's HIP adapter bound to `device` (context identity: the
+ * ordinal and this process). */
+int32_t fe2o3_lds_gemm_slice1_hip_adapter_v1(int32_t device, Fe2o3Slice1AdapterV1 *out);
+/* The context identity a handle joined for `device` expects. */
+int32_t fe2o3_lds_gemm_slice1_context_identity_v1(int32_t device, uint8_t identity[16]);
+int32_t fe2o3_lds_gemm_slice1_load_v1(Fe2o3Slice1Lifecycle *lifecycle,
+                                      const Fe2o3Slice1AdapterV1 *adapter,
+                                      Fe2o3Slice1ErrorV1 *error);
+int32_t fe2o3_lds_gemm_slice1_dispatch_and_wait_v1(Fe2o3Slice1Lifecycle *lifecycle,
+                                                   Fe2o3Slice1ErrorV1 *error);
+/* COMPLETED only: terminal unload, receipt, handle freed. */
+int32_t fe2o3_lds_gemm_slice1_unload_v1(Fe2o3Slice1Lifecycle *lifecycle,
+                                        Fe2o3Slice1ReceiptV1 *receipt);
+void fe2o3_lds_gemm_slice1_release_v1(Fe2o3Slice1Lifecycle *lifecycle);
+int32_t fe2o3_lds_gemm_slice1_observe_v1(const Fe2o3Slice1Lifecycle *lifecycle,
+                                         Fe2o3Slice1ObservationV1 *out);
+/* SHA-256 (FIPS 180-4), the digest every identity above is built from. */
+int32_t fe2o3_sha256_v1(const void *data, uint64_t len, uint8_t digest[32]);
+
 /* ---- collectives and workgroup synchronization ----------------------------------------- */
 
 /* examples/wave64_collectives_v1/src/kernel.rs:18-67 (wave64_collectives_v1).

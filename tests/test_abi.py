@@ -99,10 +99,13 @@ def test_kernel_resource_record_and_registry_without_gpu():
         count = ctypes.c_uint32(12345)
         assert L.fe2o3_kernel_resources(entry.encode(), 10**6, None, ctypes.byref(count)) == -2
         assert count.value == n, entry
-    # every declared kernel entry point (not the runtime seam) registers a kernel
-    kernel_entries = [n for n in _declared() if not n.startswith(("fe2o3_rt_", "fe2o3Hip"))
+    # every declared kernel entry point (not the runtime seam, and not the
+    # code-object lifecycle, whose kernel lives in its own loaded module)
+    # registers a kernel
+    kernel_entries = [n for n in _declared()
+                      if not n.startswith(("fe2o3_rt_", "fe2o3Hip", "fe2o3_lds_gemm_slice1_"))
                       and n not in ("fe2o3_status_string", "fe2o3_kernel_resources",
-                                    "fe2o3_moe_ffn_workspace_bytes")]
+                                    "fe2o3_moe_ffn_workspace_bytes", "fe2o3_sha256_v1")]
     for entry in kernel_entries:
         count = ctypes.c_uint32(0)
         L.fe2o3_kernel_resources(entry.encode(), 10**6, None, ctypes.byref(count))
@@ -163,3 +166,41 @@ def test_tiled_gemm_v1_plan_without_gpu():
     # K = 0 with tails in M or N still rejects; K = 0 itself is a host fill
     assert L.fe2o3_tiled_gemm_v1(None, 0, None, 0, None, 17 * 16, 17, 16, 0, None) == -24
     assert b"16-row tile" in L.fe2o3_status_string(-24)
+
+
+SLICE1_RECORDS = ["Fe2o3Slice1ErrorV1", "Fe2o3Slice1BufferContractV1", "Fe2o3Slice1ContractV1",
+                  "Fe2o3Slice1InspectionV1", "Fe2o3Slice1ArtifactV1", "Fe2o3Slice1JoinFactsV1",
+                  "Fe2o3Slice1GeometryV1", "Fe2o3Slice1EnvironmentV1", "Fe2o3Slice1LoadV1",
+                  "Fe2o3Slice1ResolutionV1", "Fe2o3Slice1ResourcesV1", "Fe2o3Slice1ImplicitV1",
+                  "Fe2o3Slice1DispatchV1", "Fe2o3Slice1UnloadV1", "Fe2o3Slice1AdapterV1",
+                  "Fe2o3Slice1ReceiptV1", "Fe2o3Slice1ObservationV1"]
+
+
+def test_lifecycle_record_layouts_match_the_header(tmp_path):
+    """Every lifecycle record's size, alignment and field offsets as the C
+    compiler lays them out from include/fe2o3_mi355x.h equal the ctypes
+    mirror's."""
+    import shutil
+    import subprocess
+    from fe2o3_amd import _lib
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "fe2o3_mi355x.h"',
+             "int main(void) {"]
+    expect = []
+    for name in SLICE1_RECORDS:
+        rec = getattr(_lib, name)
+        lines.append(f'printf("%zu %zu\\n", sizeof({name}), _Alignof({name}));')
+        expect.append(f"{C.sizeof(rec)} {C.alignment(rec)}")
+        for field, _ in rec._fields_:
+            lines.append(f'printf("%zu\\n", offsetof({name}, {field}));')
+            expect.append(str(getattr(rec, field).offset))
+    lines += ["return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-std=c11", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                   check=True)
+    got = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    assert got[:-1] == expect
