@@ -189,7 +189,10 @@ def sec_flash(ctx, stream, causal, args):
                        f"D128 bf16 (config 3{'b' if causal else 'a'})",
            "kernel": f"flash_fwd_kernel<{str(bool(causal)).lower()}>", "ms": ms,
            "value": round(tf, 2), "unit": "TFLOP/s",
-           "roofline": {"bound": "mfma", "peak": PEAK["bf16"], "frac": round(tf / PEAK["bf16"], 4)}}
+           "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK["bf16"],
+                        "unit": "TFLOP/s", "frac": round(tf / PEAK["bf16"], 4),
+                        "traffic": _traffic_from_profiles(
+                            f"flash_fwd_b8_h32_s4096_d128_{'causal' if causal else 'noncausal'}")}}
     if not args.cpu_baseline:
         return res
     # parity: 8 query rows in every one of the 256 (batch, head) pairs, one
@@ -285,7 +288,9 @@ def sec_fp8(ctx, stream, args):
     res = {"workload": "fp8 e4m3 GEMM 8192^3, per-tensor scales, bf16 out (config 4)",
            "kernel": "gemm_fp8_kernel<false>", "ms": ms, "value": round(tf, 2), "unit": "TFLOP/s",
            "quantize_ms_both_operands": round(quant_ms, 4),
-           "roofline": {"bound": "mfma", "peak": PEAK["fp8"], "frac": round(tf / PEAK["fp8"], 4)}}
+           "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK["fp8"],
+                        "unit": "TFLOP/s", "frac": round(tf / PEAK["fp8"], 4),
+                        "traffic": _traffic_from_profiles("gemm_fp8_8192")}}
     if not args.cpu_baseline:
         return res
     # parity: one whole 128-row block (every column) and 4096 random outputs
@@ -341,7 +346,10 @@ def sec_moe(ctx, stream, args):
                        "router + gather + gate/up SiLU + down + combine (config 5)",
            "kernel": "gate_up_kernel + down_kernel", "ms": ms, "value": round(tf, 2),
            "unit": "TFLOP/s",
-           "roofline": {"bound": "mfma", "peak": PEAK["bf16"], "frac": round(tf / PEAK["bf16"], 4)}}
+           "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK["bf16"],
+                        "unit": "TFLOP/s", "frac": round(tf / PEAK["bf16"], 4),
+                        "traffic": _traffic_from_profiles("moe_top2_t4096_h4096_e8_f14336"),
+                        "traffic_scope": "one layer, all kernels"}}
     if not args.cpu_baseline:
         return res
     # parity: every routing array of all 4096 tokens bit for bit; the FFN

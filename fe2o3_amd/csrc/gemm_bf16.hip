@@ -97,13 +97,21 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_nt_256_kernel(const uint16_t
     gemm_pipe::store_bf16(acc, c_tile, n);
 }
 
+// K = 0: C is all +0 (an empty sum).  A grid-stride fill kernel rather than
+// a memset node, so a caller may capture the launch in a HIP graph.
+__global__ void __launch_bounds__(256) zero_fill_bf16_kernel(uint16_t* __restrict__ c, uint64_t n) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) c[i] = 0;
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // kernels behind each entry point (fe2o3_kernel_resources)
 const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel", (const void*)gemm_bf16_nt_256_kernel<false>, 256, kFastSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel<staged>", (const void*)gemm_bf16_nt_256_kernel<true>, 256, kFastSmem}),
-    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_generic_kernel", (const void*)gemm_bf16_nt_generic_kernel, 256, 0})};
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_generic_kernel", (const void*)gemm_bf16_nt_generic_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "zero_fill_bf16_kernel", (const void*)zero_fill_bf16_kernel, 256, 0})};
 
 }  // namespace
 
@@ -115,7 +123,12 @@ extern "C" int32_t fe2o3_gemm_bf16_nt(const uint16_t* a, uint64_t a_len, const u
     return FE2O3_ERR_LENGTH;
   if (c_len == 0) return FE2O3_OK;
   if ((a_len && !a) || (b_len && !b) || !c) return FE2O3_ERR_NULL;
-  if (k == 0) return (int32_t)hipMemsetAsync(c, 0, c_len * 2, (hipStream_t)stream);
+  if (k == 0) {
+    const uint64_t blocks = (c_len + 255) / 256;
+    zero_fill_bf16_kernel<<<(unsigned)(blocks < 4096u ? blocks : 4096u), 256, 0,
+                            (hipStream_t)stream>>>(c, c_len);
+    return fe2o3_host::after_launch();
+  }
   // fast path: whole tiles, whole stages, 16-byte rows, and a 256-row panel
   // (512 * k bytes) inside the 32-bit range of its buffer resource
   const bool fast = m % 256 == 0 && n % 256 == 0 && k % gemm_pipe::Geo<kRowBytes>::kK16 == 0 &&

@@ -305,6 +305,17 @@ def test_gemm_bf16_nt_config2_4096(gpu, oracle):
     _nt_case(gpu, oracle, m, n, k, seed=1)
 
 
+@pytest.mark.parametrize("m,n", [(256, 512), (3, 7)])
+def test_gemm_bf16_nt_k0_writes_positive_zero(gpu, m, n):
+    """K = 0: every output is +0 (the empty sum), the guards untouched."""
+    a = gpu.alloc(0, np.uint16)
+    b = gpu.alloc(0, np.uint16)
+    c = Guarded(gpu, np.full(m * n, 0xFFFF, np.uint16))
+    _kernels().gemm_bf16_nt_gpu.Kernel.load(gpu).prepare(a, b, c.body, m, n, 0).launch()
+    assert c.guards_intact()
+    assert c.download().tolist() == [0] * (m * n)
+
+
 def test_gemm_bf16_nt_rejects_bad_lengths(gpu):
     from fe2o3_amd.runtime import Fe2o3Error
     a = gpu.alloc(256 * 64, np.uint16)
