@@ -10,7 +10,12 @@
 //
 // The GEMM reuses the 256x256 tile machinery of the bf16 GEMM: one LDS stage
 // is 128 bytes of k per row, i.e. 128 fp8 values, and each substep of 64 k
-// issues v_mfma_scale_f32_32x32x64_f8f6f4 (5.0 PFLOP/s dense peak).
+// issues v_mfma_scale_f32_32x32x64_f8f6f4 (5.0 PFLOP/s dense peak).  Any M
+// and N run on it (edge tiles store only their valid rows and columns);
+// K not a multiple of 128, or unaligned operands, take a bounds-checked
+// 64x64-tile kernel that widens E4M3 to bf16 exactly while staging and
+// multiplies on bf16 MFMAs (the products are exact either way); K = 0
+// writes +0.
 #include "common.hpp"
 #include "gemm_core.hpp"
 #include "gemm_pipe.hpp"
@@ -76,7 +81,10 @@ constexpr int kFp8Smem = kFp8Stages * 2 * gemm_pipe::Geo<kFp8RowBytes>::kTileByt
 
 // STAGED: C leaves through LDS in whole rows with nontemporal stores
 // (gemm_pipe::store_bf16_staged), for operands that stream from HBM.
-template <bool STAGED>
+// EDGE: M or N is not a multiple of 256 (or C is not 16-byte aligned): the
+// grid covers ceil(M/256) x ceil(N/256) tiles, operand rows past M (N) repeat
+// the last valid row, and each tile stores only its valid rows and columns.
+template <bool STAGED, bool EDGE>
 __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restrict__ a,
                                                           const uint8_t* __restrict__ b,
                                                           const float* __restrict__ scale_a,
@@ -84,13 +92,17 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
                                                           uint16_t* __restrict__ c, uint32_t m,
                                                           uint32_t n, uint32_t k) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const uint32_t tiles_m = EDGE ? (m + 255u) / 256u : m / 256u;
+  const uint32_t tiles_n = EDGE ? (n + 255u) / 256u : n / 256u;
   uint32_t tm, tn;
-  gemm_core::xcd_tile_order(blockIdx.x, m / 256, n / 256, &tm, &tn);
+  gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  const uint32_t rows_a = EDGE ? min(256u, m - tm * 256u) : 256u;
+  const uint32_t rows_b = EDGE ? min(256u, n - tn * 256u) : 256u;
   const uint32_t k16 = k / 2;  // rows addressed in 16-bit units
   const uint16_t* a16 = reinterpret_cast<const uint16_t*>(a + (uint64_t)tm * 256 * k);
   const uint16_t* b16 = reinterpret_cast<const uint16_t*>(b + (uint64_t)tn * 256 * k);
-  const auto ar = gemm_pipe::dense_rows<kFp8RowBytes>(a16, k16, 256, k16);
-  const auto br = gemm_pipe::dense_rows<kFp8RowBytes>(b16, k16, 256, k16);
+  const auto ar = gemm_pipe::dense_rows<kFp8RowBytes>(a16, k16, rows_a, k16);
+  const auto br = gemm_pipe::dense_rows<kFp8RowBytes>(b16, k16, rows_b, k16);
   gemm_pipe::Acc32 acc;
   gemm_pipe::mainloop<gemm_pipe::Fp8Mma<kFp8RowBytes>, kFp8RowBytes, kFp8Stages>(ar, br, k16,
                                                                                  smem, acc);
@@ -102,10 +114,76 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc.v[i][j][e] *= sab;
   uint16_t* c_tile = c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256;
-  if constexpr (STAGED)
+  if constexpr (EDGE)
+    gemm_pipe::store_bf16_edge(acc, c_tile, n, rows_a, rows_b);
+  else if constexpr (STAGED)
     gemm_pipe::store_bf16_staged(acc, smem, c_tile, n);
   else
     gemm_pipe::store_bf16(acc, c_tile, n);
+}
+
+// ---- any shape ---------------------------------------------------------------------------
+// 64x64 output tiles, 32 k per step; each operand element is widened to bf16
+// (exact) on its way to LDS, zero outside m x k / n x k, and four waves (2x2,
+// 32x32 each) multiply with v_mfma_f32_16x16x32_bf16.  The scale product is
+// applied to the fp32 sums, as on the fast path.
+constexpr int G8_BM = 64, G8_BN = 64, G8_BK = 32, G8_LDK = G8_BK + 8;
+
+__global__ void __launch_bounds__(256) gemm_fp8_generic_kernel(
+    const uint8_t* __restrict__ a, const uint8_t* __restrict__ b, const float* __restrict__ scale_a,
+    const float* __restrict__ scale_b, uint16_t* __restrict__ c, uint32_t m, uint32_t n,
+    uint32_t k) {
+  __shared__ __attribute__((aligned(16))) uint16_t a_lds[G8_BM * G8_LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t b_lds[G8_BN * G8_LDK];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const uint64_t row0 = (uint64_t)blockIdx.y * G8_BM, col0 = (uint64_t)blockIdx.x * G8_BN;
+  f32x4_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (uint64_t k0 = 0; k0 < k; k0 += G8_BK) {
+    const int r = t >> 2, d0 = (t & 3) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint64_t gd = k0 + d0 + e;
+      const uint64_t ga = row0 + r, gb = col0 + r;
+      a_lds[r * G8_LDK + d0 + e] = (ga < m && gd < k) ? bf16_bits_from_e4m3(a[ga * k + gd]) : 0;
+      b_lds[r * G8_LDK + d0 + e] = (gb < n && gd < k) ? bf16_bits_from_e4m3(b[gb * k + gd]) : 0;
+    }
+    __syncthreads();
+    const int rc = lane & 15, chunk = lane >> 4;
+    bf16x8_t af[2], bf[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      af[i] = *reinterpret_cast<const bf16x8_t*>(a_lds + (wm * 32 + i * 16 + rc) * G8_LDK + chunk * 8);
+      bf[i] = *reinterpret_cast<const bf16x8_t*>(b_lds + (wn * 32 + i * 16 + rc) * G8_LDK + chunk * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    __syncthreads();
+  }
+  const float sab = scale_a[0] * scale_b[0];
+  const int col_in = lane & 15, row_in = (lane >> 4) * 4;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint64_t gr = row0 + wm * 32 + i * 16 + row_in + e;
+        const uint64_t gc = col0 + wn * 32 + j * 16 + col_in;
+        if (gr < m && gc < n) c[gr * n + gc] = bf16_bits_from_f32(acc[i][j][e] * sab);
+      }
+}
+
+__global__ void __launch_bounds__(256) zero_fill_bf16_kernel(uint16_t* __restrict__ c, uint64_t n) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) c[i] = 0;
 }
 
 unsigned grid_for(uint64_t n) {
@@ -120,8 +198,11 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_amax_f32", "amax_kernel", (const void*)amax_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_fp8_scale_from_amax", "scale_kernel", (const void*)scale_kernel, 1, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_quantize_e4m3", "quantize_kernel", (const void*)quantize_kernel, 256, 0}),
-    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel", (const void*)gemm_fp8_kernel<false>, 256, kFp8Smem}),
-    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel<staged>", (const void*)gemm_fp8_kernel<true>, 256, kFp8Smem})};
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel", (const void*)gemm_fp8_kernel<false, false>, 256, kFp8Smem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel<staged>", (const void*)gemm_fp8_kernel<true, false>, 256, kFp8Smem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel<edge>", (const void*)gemm_fp8_kernel<false, true>, 256, kFp8Smem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_generic_kernel", (const void*)gemm_fp8_generic_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "zero_fill_bf16_kernel", (const void*)zero_fill_bf16_kernel, 256, 0})};
 
 }  // namespace
 
@@ -163,22 +244,40 @@ int32_t fe2o3_gemm_fp8_nt(const uint8_t* a, uint64_t a_len, const uint8_t* b, ui
   if (a_len != (uint64_t)m * k || b_len != (uint64_t)n * k || c_len != (uint64_t)m * n)
     return FE2O3_ERR_LENGTH;
   if (c_len == 0) return FE2O3_OK;
-  if (m % 256 != 0 || n % 256 != 0 || k % 128 != 0 || k == 0) return FE2O3_ERR_SHAPE;
-  // a 256-row fp8 panel (256 * k bytes) within its buffer resource's 32-bit range
-  if (256ull * k >= (1ull << 31)) return FE2O3_ERR_SHAPE;
-  if (!a || !b || !c || !scale_a || !scale_b) return FE2O3_ERR_NULL;
-  if ((((uintptr_t)a | (uintptr_t)b | (uintptr_t)c) & 15u) != 0) return FE2O3_ERR_ALIGNMENT;
+  if ((a_len && !a) || (b_len && !b) || !c || !scale_a || !scale_b) return FE2O3_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  if (k == 0) {  // the empty sum: +0 (a fill kernel, so the launch can be captured)
+    const uint64_t blocks = (c_len + 255) / 256;
+    zero_fill_bf16_kernel<<<(unsigned)(blocks < 4096u ? blocks : 4096u), 256, 0, s>>>(c, c_len);
+    return fe2o3_host::after_launch();
+  }
+  // fast path: whole 128-k stages, 16-byte operand rows, and a 256-row fp8
+  // panel (256 * k bytes) within its buffer resource's 32-bit range
+  const bool fast = k % 128 == 0 && 256ull * k < (1ull << 31) &&
+                    (((uintptr_t)a | (uintptr_t)b) & 15u) == 0;
+  if (!fast) {
+    const dim3 grid((n + G8_BN - 1) / G8_BN, (m + G8_BM - 1) / G8_BM);
+    if (grid.y > 65535u) return FE2O3_ERR_SHAPE;
+    gemm_fp8_generic_kernel<<<grid, 256, 0, s>>>(a, b, scale_a, scale_b, c, m, n, k);
+    return fe2o3_host::after_launch();
+  }
   static const int32_t lds_rc = fe2o3_host::set_dynamic_lds(
-      {(const void*)gemm_fp8_kernel<false>, (const void*)gemm_fp8_kernel<true>}, kFp8Smem);
+      {(const void*)gemm_fp8_kernel<false, false>, (const void*)gemm_fp8_kernel<true, false>,
+       (const void*)gemm_fp8_kernel<false, true>},
+      kFp8Smem);
   if (lds_rc != FE2O3_OK) return lds_rc;
-  const uint64_t tiles = (uint64_t)(m / 256) * (n / 256);
+  const bool whole = m % 256 == 0 && n % 256 == 0 && ((uintptr_t)c & 15u) == 0;
+  const uint64_t tiles = (uint64_t)((m + 255) / 256) * ((n + 255) / 256);
   if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
-  if (gemm_core::staged_epilogue(((uint64_t)m + n) * k))
-    gemm_fp8_kernel<true><<<(unsigned)tiles, 256, kFp8Smem, (hipStream_t)stream>>>(
-        a, b, scale_a, scale_b, c, m, n, k);
+  if (!whole)
+    gemm_fp8_kernel<false, true><<<(unsigned)tiles, 256, kFp8Smem, s>>>(a, b, scale_a, scale_b,
+                                                                         c, m, n, k);
+  else if (gemm_core::staged_epilogue(((uint64_t)m + n) * k))
+    gemm_fp8_kernel<true, false><<<(unsigned)tiles, 256, kFp8Smem, s>>>(a, b, scale_a, scale_b,
+                                                                         c, m, n, k);
   else
-    gemm_fp8_kernel<false><<<(unsigned)tiles, 256, kFp8Smem, (hipStream_t)stream>>>(
-        a, b, scale_a, scale_b, c, m, n, k);
+    gemm_fp8_kernel<false, false><<<(unsigned)tiles, 256, kFp8Smem, s>>>(a, b, scale_a, scale_b,
+                                                                          c, m, n, k);
   return fe2o3_host::after_launch();
 }
 

@@ -48,4 +48,20 @@ FE2O3_HD uint8_t e4m3_from_bits(uint32_t bits) {
   return (uint8_t)(sign | code);
 }
 
+// E4M3FN -> bf16 bits, exact: every E4M3 value has at most 4 significant
+// bits and an exponent in [-9, 8], which bf16 holds exactly.  NaN
+// (S.1111.111) becomes a quiet bf16 NaN of the same sign; subnormals m*2^-9
+// are normalized.
+FE2O3_HD uint16_t bf16_bits_from_e4m3(uint8_t q) {
+  const uint32_t sign = ((uint32_t)q & 0x80u) << 8;
+  const uint32_t e = ((uint32_t)q >> 3) & 15u, m = (uint32_t)q & 7u;
+  if (e == 15u && m == 7u) return (uint16_t)(sign | 0x7fc0u);
+  if (e != 0u) return (uint16_t)(sign | ((e + 120u) << 7) | (m << 4));
+  if (m == 0u) return (uint16_t)sign;
+  // m * 2^-9 with the leading one of m at bit p (0..2): 2^(p-9) * 1.f
+  const uint32_t p = m >= 4u ? 2u : (m >= 2u ? 1u : 0u);
+  const uint32_t frac = (m << (3u - p)) & 7u;
+  return (uint16_t)(sign | ((p + 118u) << 7) | (frac << 4));
+}
+
 }  // namespace fe2o3

@@ -2,10 +2,11 @@
 // A[m,k] (row-major) * B^T with B stored [n,k] (k contiguous, i.e. the
 // BASELINE's column-major B), fp32 accumulation, RNE bf16 output.
 //
-// Fast path (m, n multiples of 256, k a multiple of 64 below 2^22, 16-byte
-// aligned): the 256x256 pipelined MFMA tile of gemm_pipe.hpp with 64 k per
-// LDS stage and two stages, workgroups ordered XCD-aware (gemm_core.hpp).
-// Any other shape uses a bounds-checked 64x64-tile MFMA kernel.
+// Fast path (k a multiple of 64 below 2^22, A and B 16-byte aligned): the
+// 256x256 pipelined MFMA tile of gemm_pipe.hpp with 64 k per LDS stage and
+// two stages, workgroups ordered XCD-aware (gemm_core.hpp); m or n not a
+// multiple of 256 (or an unaligned C) runs its edge form.  Any other shape
+// uses a bounds-checked 64x64-tile MFMA kernel.
 #include "common.hpp"
 #include "gemm_core.hpp"
 #include "gemm_pipe.hpp"
@@ -76,22 +77,31 @@ constexpr int kFastSmem = kStages * 2 * gemm_pipe::Geo<kRowBytes>::kTileBytes;  
 
 // STAGED: C leaves through LDS in whole rows with nontemporal stores
 // (gemm_pipe::store_bf16_staged), for operands that stream from HBM.
-template <bool STAGED>
+// EDGE: M or N is not a multiple of 256; the grid covers ceil(M/256) x
+// ceil(N/256) tiles, operand rows past M (N) repeat the last valid row
+// (their products reach only outputs that are not stored), and each tile
+// stores only its valid rows and columns, element by element.
+template <bool STAGED, bool EDGE>
 __global__ void __launch_bounds__(256, 1) gemm_bf16_nt_256_kernel(const uint16_t* __restrict__ a,
                                                                    const uint16_t* __restrict__ b,
                                                                    uint16_t* __restrict__ c,
                                                                    uint32_t m, uint32_t n,
                                                                    uint32_t k) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  const uint32_t tiles_m = m / 256, tiles_n = n / 256;
+  const uint32_t tiles_m = EDGE ? (m + 255u) / 256u : m / 256u;
+  const uint32_t tiles_n = EDGE ? (n + 255u) / 256u : n / 256u;
   uint32_t tm, tn;
   gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
-  const auto ar = gemm_pipe::dense_rows<kRowBytes>(a + (uint64_t)tm * 256 * k, k, 256, k);
-  const auto br = gemm_pipe::dense_rows<kRowBytes>(b + (uint64_t)tn * 256 * k, k, 256, k);
+  const uint32_t rows_a = EDGE ? min(256u, m - tm * 256u) : 256u;
+  const uint32_t rows_b = EDGE ? min(256u, n - tn * 256u) : 256u;
+  const auto ar = gemm_pipe::dense_rows<kRowBytes>(a + (uint64_t)tm * 256 * k, k, rows_a, k);
+  const auto br = gemm_pipe::dense_rows<kRowBytes>(b + (uint64_t)tn * 256 * k, k, rows_b, k);
   gemm_pipe::Acc16 acc;
   gemm_pipe::mainloop<gemm_pipe::Bf16Mma<kRowBytes>, kRowBytes, kStages>(ar, br, k, smem, acc);
   uint16_t* c_tile = c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256;
-  if constexpr (STAGED)
+  if constexpr (EDGE)
+    gemm_pipe::store_bf16_edge(acc, c_tile, n, rows_a, rows_b);
+  else if constexpr (STAGED)
     gemm_pipe::store_bf16_staged(acc, smem, c_tile, n);
   else
     gemm_pipe::store_bf16(acc, c_tile, n);
@@ -108,8 +118,9 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // kernels behind each entry point (fe2o3_kernel_resources)
 const fe2o3_host::KernelRegistrar kRegistered[] = {
-    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel", (const void*)gemm_bf16_nt_256_kernel<false>, 256, kFastSmem}),
-    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel<staged>", (const void*)gemm_bf16_nt_256_kernel<true>, 256, kFastSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel", (const void*)gemm_bf16_nt_256_kernel<false, false>, 256, kFastSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel<staged>", (const void*)gemm_bf16_nt_256_kernel<true, false>, 256, kFastSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel<edge>", (const void*)gemm_bf16_nt_256_kernel<false, true>, 256, kFastSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_generic_kernel", (const void*)gemm_bf16_nt_generic_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "zero_fill_bf16_kernel", (const void*)zero_fill_bf16_kernel, 256, 0})};
 
@@ -129,23 +140,29 @@ extern "C" int32_t fe2o3_gemm_bf16_nt(const uint16_t* a, uint64_t a_len, const u
                             (hipStream_t)stream>>>(c, c_len);
     return fe2o3_host::after_launch();
   }
-  // fast path: whole tiles, whole stages, 16-byte rows, and a 256-row panel
-  // (512 * k bytes) inside the 32-bit range of its buffer resource
-  const bool fast = m % 256 == 0 && n % 256 == 0 && k % gemm_pipe::Geo<kRowBytes>::kK16 == 0 &&
-                    512ull * k < (1ull << 31) && aligned16(a) && aligned16(b) && aligned16(c);
+  // fast path: whole stages, 16-byte operand rows, and a 256-row panel
+  // (512 * k bytes) inside the 32-bit range of its buffer resource; whole
+  // tiles with a 16-byte aligned C take the plain tile, any other M and N
+  // the edge tile
+  const bool fast = k % gemm_pipe::Geo<kRowBytes>::kK16 == 0 && 512ull * k < (1ull << 31) &&
+                    aligned16(a) && aligned16(b);
   if (fast) {
     static const int32_t lds_rc = fe2o3_host::set_dynamic_lds(
-        {(const void*)gemm_bf16_nt_256_kernel<false>, (const void*)gemm_bf16_nt_256_kernel<true>},
+        {(const void*)gemm_bf16_nt_256_kernel<false, false>,
+         (const void*)gemm_bf16_nt_256_kernel<true, false>,
+         (const void*)gemm_bf16_nt_256_kernel<false, true>},
         kFastSmem);
     if (lds_rc != FE2O3_OK) return lds_rc;
-    const uint64_t tiles = (uint64_t)(m / 256) * (n / 256);
+    const bool whole = m % 256 == 0 && n % 256 == 0 && aligned16(c);
+    const uint64_t tiles = (uint64_t)((m + 255) / 256) * ((n + 255) / 256);
     if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
-    if (gemm_core::staged_epilogue(((uint64_t)m + n) * k * 2u))
-      gemm_bf16_nt_256_kernel<true><<<(unsigned)tiles, 256, kFastSmem, (hipStream_t)stream>>>(
-          a, b, c, m, n, k);
+    hipStream_t s = (hipStream_t)stream;
+    if (!whole)
+      gemm_bf16_nt_256_kernel<false, true><<<(unsigned)tiles, 256, kFastSmem, s>>>(a, b, c, m, n, k);
+    else if (gemm_core::staged_epilogue(((uint64_t)m + n) * k * 2u))
+      gemm_bf16_nt_256_kernel<true, false><<<(unsigned)tiles, 256, kFastSmem, s>>>(a, b, c, m, n, k);
     else
-      gemm_bf16_nt_256_kernel<false><<<(unsigned)tiles, 256, kFastSmem, (hipStream_t)stream>>>(
-          a, b, c, m, n, k);
+      gemm_bf16_nt_256_kernel<false, false><<<(unsigned)tiles, 256, kFastSmem, s>>>(a, b, c, m, n, k);
     return fe2o3_host::after_launch();
   }
   dim3 grid((n + N_BN - 1) / N_BN, (m + N_BM - 1) / N_BM);

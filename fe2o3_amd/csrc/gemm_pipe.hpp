@@ -579,6 +579,47 @@ FE2O3_DEVICE void store_bf16(const Acc16& acc, uint16_t* c_tile, uint64_t ldc) {
     }
 }
 
+// Edge tiles (the last tile row or column of a C whose M or N is not a
+// multiple of 256): only tile rows < rows_valid and columns < cols_valid are
+// written, one 2-byte store per element, so C rows need no alignment.  The
+// values are those store_bf16 writes.
+FE2O3_DEVICE void store_bf16_edge(const Acc16& acc, uint16_t* c_tile, uint64_t ldc,
+                                  uint32_t rows_valid, uint32_t cols_valid) {
+  const uint32_t row0 = acc16_row0(), col0 = acc16_col0();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t r = row0 + 16u * i;
+    if (r >= rows_valid) continue;
+    uint16_t* out = c_tile + (uint64_t)r * ldc;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t c = col0 + 16u * j + e;
+        if (c < cols_valid) out[c] = bf16_bits_from_f32(acc.v[i][j][e]);
+      }
+  }
+}
+
+FE2O3_DEVICE void store_bf16_edge(const Acc32& acc, uint16_t* c_tile, uint64_t ldc,
+                                  uint32_t rows_valid, uint32_t cols_valid) {
+  const uint32_t row0 = acc32_row0();
+  const uint32_t col0 = (wave_id() & 1u) * 128u + 4u * (lane_id() >> 5);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t r = row0 + 32u * i;
+    if (r >= rows_valid) continue;
+    uint16_t* out = c_tile + (uint64_t)r * ldc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const uint32_t c = col0 + 32u * j + 8u * (e / 4) + (e % 4);
+        if (c < cols_valid) out[c] = bf16_bits_from_f32(acc.v[i][j][e]);
+      }
+  }
+}
+
 // Staged stores. Straight from the accumulators, one store instruction writes
 // 32 bytes into each of 16 (Acc16) or 32 (Acc32) rows, parts of cache
 // lines. Here each wave first writes its 128x128 block as bf16 into its own

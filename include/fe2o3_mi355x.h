@@ -233,8 +233,11 @@ int32_t fe2o3_scalar_gemm_v1(const float *a, uint64_t a_len, const float *b,
  * tiled_gemm_general_v1 to the MI355X shape: C[m,n] (bf16, row-major) =
  * A[m,k] (bf16, row-major) * B^T where B is stored column-major, i.e. as
  * [n,k] with k contiguous; fp32 accumulation, RNE bf16 output.  Exact
- * lengths m*k, n*k, m*n.  Any m, n, k; the MFMA fast path needs m, n
- * multiples of 256, k a multiple of 64 and 16-byte aligned pointers. */
+ * lengths m*k, n*k, m*n.  Any m, n, k.  The pipelined 256x256 MFMA tile
+ * runs whenever k is a multiple of 64 (k*512 < 2^31) and A and B are 16-byte
+ * aligned: whole tiles when m and n are multiples of 256 and C is 16-byte
+ * aligned, edge tiles (element-wise masked stores) otherwise.  Other shapes
+ * take a bounds-checked 64x64-tile kernel; k = 0 writes +0. */
 int32_t fe2o3_gemm_bf16_nt(const uint16_t *a, uint64_t a_len,
                            const uint16_t *b, uint64_t b_len, uint16_t *c,
                            uint64_t c_len, uint32_t m, uint32_t n, uint32_t k,
@@ -412,8 +415,12 @@ int32_t fe2o3_fp8_scale_from_amax(const float *amax, float *scale, void *stream)
 int32_t fe2o3_quantize_e4m3(const float *x, uint64_t x_len, const float *scale,
                             uint8_t *q, uint64_t q_len, void *stream);
 /* C[m,n] bf16 = (scale_a[0]*scale_b[0]) * (A_q[m,k] . B_q[n,k]^T), fp32
- * accumulation; A row-major, B stored [n,k] (k contiguous).  m, n multiples
- * of 256, k a multiple of 128. */
+ * accumulation; A row-major, B stored [n,k] (k contiguous).  Any m, n, k.
+ * The pipelined fp8 MFMA tile runs whenever k is a multiple of 128
+ * (k*256 < 2^31) and A and B are 16-byte aligned (edge tiles for m or n not
+ * a multiple of 256 or an unaligned C); otherwise a bounds-checked kernel
+ * widens E4M3 to bf16 exactly and multiplies on bf16 MFMAs.  k = 0 writes
+ * +0.  The products of two E4M3 values are exact in fp32 on both paths. */
 int32_t fe2o3_gemm_fp8_nt(const uint8_t *a, uint64_t a_len, const uint8_t *b,
                           uint64_t b_len, const float *scale_a,
                           const float *scale_b, uint16_t *c, uint64_t c_len,

@@ -7,6 +7,7 @@
 #include "../fe2o3_amd/csrc/fp8_codec.hpp"
 
 extern "C" unsigned char fe2o3o_fp8e4m3_from_f32(float value);
+extern "C" float fe2o3o_fp8e4m3_to_f32(unsigned char bits);
 
 int main() {
   unsigned long long mismatches = 0;
@@ -24,6 +25,18 @@ int main() {
       if (first_bad < 0) first_bad = i;
     }
   }
-  printf("mismatches %llu first %lld\n", mismatches, first_bad);
-  return mismatches == 0 ? 0 : 1;
+  // the decoder the generic fp8 GEMM stages with: all 256 codes, exact
+  unsigned decode_bad = 0;
+  for (unsigned q = 0; q < 256; ++q) {
+    const unsigned int bits = (unsigned int)fe2o3::bf16_bits_from_e4m3((unsigned char)q) << 16;
+    float got;
+    memcpy(&got, &bits, 4);
+    const float want = fe2o3o_fp8e4m3_to_f32((unsigned char)q);
+    unsigned int want_bits;
+    memcpy(&want_bits, &want, 4);
+    const bool both_nan = got != got && want != want && (bits >> 31) == (want_bits >> 31);
+    if (!both_nan && bits != want_bits) ++decode_bad;
+  }
+  printf("mismatches %llu first %lld decode_mismatches %u\n", mismatches, first_bad, decode_bad);
+  return mismatches == 0 && decode_bad == 0 ? 0 : 1;
 }

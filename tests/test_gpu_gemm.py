@@ -281,6 +281,33 @@ def test_gemm_bf16_nt_fast_path(gpu, oracle, m, n, k):
     _nt_case(gpu, oracle, m, n, k, seed=1)
 
 
+# M or N not a multiple of 256 with whole 64-k stages: edge tiles of the
+# pipelined kernel (clamped operand rows, element-wise masked stores)
+@pytest.mark.parametrize("m,n,k", [(300, 520, 512), (257, 255, 128), (1, 1000, 64),
+                                   (1000, 264, 1024), (4000, 4000, 256)])
+def test_gemm_bf16_nt_edge_tiles(gpu, oracle, m, n, k):
+    rows = None if m * n <= 1_100_000 else [0, 255, 256, 1999, 3839, 3840, 3999]
+    _nt_case(gpu, oracle, m, n, k, seed=6, rows=rows)
+
+
+def test_gemm_bf16_nt_whole_tiles_unaligned_c(gpu, oracle):
+    """Whole tiles but C at an odd element offset: the edge form, 2-byte
+    stores; every output against the oracle and the neighbours untouched."""
+    m, n, k = 256, 512, 192
+    kern = _kernels()
+    da, db = gpu.alloc(m * k, np.uint16), gpu.alloc(n * k, np.uint16)
+    kern.fill_normal_bf16(da, 8, 0xA, 1.0 / np.sqrt(k))
+    kern.fill_normal_bf16(db, 8, 0xB, 1.0 / np.sqrt(k))
+    c = Guarded(gpu, np.full(m * n + 1, 0x7FDE, np.uint16))
+    body = c.full.view(65, m * n)  # one element past the guard: 2-byte aligned only
+    kern.gemm_bf16_nt_gpu.Kernel.load(gpu).prepare(da, db, body, m, n, k).launch()
+    full = c.full.download()
+    assert c.guards_intact() and full[64] == 0x7FDE
+    got = bf16_to_f32(full[65:65 + m * n]).reshape(m, n)
+    ref = oracle.gemm_bf16_nt_rows(m, n, k, da.download(), db.download(), 0, m).reshape(m, n)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-3 * np.max(np.abs(ref)))
+
+
 def test_gemm_bf16_nt_more_tiles_than_cus(gpu, oracle):
     """264 output tiles (more than one per CU): sampled rows of every tile
     row against the oracle."""

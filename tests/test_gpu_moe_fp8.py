@@ -455,6 +455,24 @@ def test_gemm_fp8_all_outputs(gpu, oracle, m, n, k):
     assert _fp8_case(gpu, oracle, m, n, k, (rr.ravel(), cc.ravel())) <= 1e-2
 
 
+# any M, N: edge tiles on the fast path (K a multiple of 128), the generic
+# bounds-checked kernel otherwise (E4M3 widened exactly to bf16)
+@pytest.mark.parametrize("m,n,k", [(300, 520, 256), (1, 257, 128), (257, 256, 384),
+                                   (100, 70, 96), (33, 65, 200), (256, 256, 160), (5, 3, 1)])
+def test_gemm_fp8_any_shape(gpu, oracle, m, n, k):
+    rr, cc = np.meshgrid(np.arange(m), np.arange(n), indexing="ij")
+    assert _fp8_case(gpu, oracle, m, n, k, (rr.ravel(), cc.ravel())) <= 1e-2
+
+
+def test_gemm_fp8_k0_writes_positive_zero(gpu):
+    kern = _k()
+    one = gpu.to_device(np.array([1.0], np.float32))
+    empty = gpu.alloc(0, np.uint8)
+    c = Guarded(gpu, np.full(7 * 9, 0xFFFF, np.uint16))
+    kern.gemm_fp8_nt(empty, empty, one, one, c.body, 7, 9, 0)
+    assert c.guards_intact() and c.download().tolist() == [0] * 63
+
+
 def test_gemm_fp8_config4_sampled(gpu, oracle):
     """8192^3 e4m3 with amax/448 per-tensor scales; one
     whole 128-row block (rows 4096..4223, all 8192 columns: 1M outputs at
