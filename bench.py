@@ -425,14 +425,22 @@ def sec_gemm_f32(ctx, stream, args):
 
 def sec_gemm_general(ctx, stream, args):
     """tiled_gemm_general_v1 at 2048^3 with padded strides and alpha/beta
-    (C = 1.5 A B + 0.5 C, lda = ldb = ldc = 2056), both schedules."""
-    from fe2o3_amd import kernels
+    (C = 1.5 A B + 0.5 C, lda = ldb = ldc = 2056): the pipelined 256x256
+    tile (the shape qualifies), and both staged schedules on the same data
+    with A two bytes past a 16-byte boundary (which the tile does not take).
+    Each launch reads and rewrites C (C converges to 3 A B); it is restored
+    before the parity call."""
+    from fe2o3_amd import _lib, kernels
+    from fe2o3_amd.runtime import check
     from oracle import oracle as orc
     m = n = k = 2048
     ld = 2056
     alpha, beta = 1.5, 0.5
     la, lb, lc = (m - 1) * ld + k, (k - 1) * ld + n, (m - 1) * ld + n
-    a, b = ctx.alloc(la, np.uint16), ctx.alloc(lb, np.uint16)
+    a = ctx.alloc(la, np.uint16)
+    a_buf = ctx.alloc(la + 8, np.uint16)
+    a_off = a_buf.view(1, la)
+    b = ctx.alloc(lb, np.uint16)
     c0, c = ctx.alloc(lc, np.float32), ctx.alloc(lc, np.float32)
     kernels.fill_normal_bf16(a, 7, 0xA, 1.0 / 32.0, stream=stream)
     kernels.fill_normal_bf16(b, 7, 0xB, 1.0 / 32.0, stream=stream)
@@ -440,42 +448,45 @@ def sec_gemm_general(ctx, stream, args):
     res = {"workload": "general bf16 GEMM 2048^3, strides 2056, alpha 1.5, beta 0.5, f32 C "
                        "(tiled_gemm_general_v1)", "unit": "TFLOP/s"}
     outs = {}
-    for sched, kern in (("reference", kernels.tiled_gemm_general_v1_gpu),
-                        ("vector_a", kernels.tiled_gemm_general_vector_a_v1_gpu)):
-        prep = kern.Kernel.load(ctx).prepare(a, b, c, m, n, k, ld, ld, ld, alpha, beta)
-        from fe2o3_amd import _lib
-        from fe2o3_amd.runtime import check
-
-        def step(prep=prep):  # C is read and written: restore it first (both timed alike)
-            check(_lib.lib().fe2o3_rt_memcpy_async(c.ptr, c0.ptr, c.nbytes, 3, stream.handle),
+    runs = (("pipelined", kernels.tiled_gemm_general_v1_gpu, a),
+            ("reference", kernels.tiled_gemm_general_v1_gpu, None),
+            ("vector_a", kernels.tiled_gemm_general_vector_a_v1_gpu, None))
+    for name, kern, a_in in runs:
+        if a_in is None:  # A's data moved to the 2-byte offset: the staged kernels
+            check(_lib.lib().fe2o3_rt_memcpy_async(a_off.ptr, a.ptr, a.nbytes, 3, stream.handle),
                   "copy")
-            prep.launch_async(stream)
-        ms = _timed(ctx, stream, step, args)
-        outs[sched] = c.download()
+            a_in = a_off
+        prep = kern.Kernel.load(ctx).prepare(a_in, b, c, m, n, k, ld, ld, ld, alpha, beta)
+        check(_lib.lib().fe2o3_rt_memcpy_async(c.ptr, c0.ptr, c.nbytes, 3, stream.handle), "copy")
+        ms = _timed(ctx, stream, lambda: prep.launch_async(stream), args)
+        check(_lib.lib().fe2o3_rt_memcpy_async(c.ptr, c0.ptr, c.nbytes, 3, stream.handle), "copy")
+        prep.launch(stream)
+        outs[name] = c.download()
         tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        res[sched] = {"ms": round(ms, 5), "value": round(tf, 2),
-                      "frac": round(tf / PEAK["bf16"], 4)}
-    res["kernel"] = "gemm_general_kernel<false> / <true>"
-    res["ms"] = res["vector_a"]["ms"]
-    res["value"] = res["vector_a"]["value"]
-    res["roofline"] = {"bound": "mfma", "peak": PEAK["bf16"], "frac": res["vector_a"]["frac"],
-                       "note": "ms includes a 34 MB device copy restoring C before each call"}
+        res[name] = {"ms": round(ms, 5), "value": round(tf, 2),
+                     "frac": round(tf / PEAK["bf16"], 4)}
+    res["kernel"] = ("gemm_general_pipe_kernel (pipelined); gemm_general_kernel<false> / <true> "
+                     "(staged schedules)")
+    res["ms"] = res["pipelined"]["ms"]
+    res["value"] = res["pipelined"]["value"]
+    res["roofline"] = {"bound": "mfma", "achieved": res["value"], "peak": PEAK["bf16"],
+                       "unit": "TFLOP/s", "frac": res["pipelined"]["frac"],
+                       "note": "64 tiles of 256x256 on 256 CUs at this shape"}
     if not args.cpu_baseline:
         return res
     ha, hb, hc = a.download(), b.download(), c0.download()
     r0, rows = 1000, 32
-    threads = _cpu_threads()
     t0 = time.perf_counter()
     rc, ref, _ = orc.general_reference_v1(rows, n, k, ld, ld, ld,
                                           ha[r0 * ld:r0 * ld + (rows - 1) * ld + k], hb,
                                           hc[r0 * ld:r0 * ld + (rows - 1) * ld + n], alpha, beta)
     dt = time.perf_counter() - t0
-    got = np.stack([outs["reference"][(r0 + r) * ld:(r0 + r) * ld + n] for r in range(rows)])
-    same = outs["reference"].tobytes() == outs["vector_a"].tobytes()
+    got = np.stack([outs["pipelined"][(r0 + r) * ld:(r0 + r) * ld + n] for r in range(rows)])
+    same = all(outs[x].tobytes() == outs["pipelined"].tobytes() for x in ("reference", "vector_a"))
     res["parity"] = {"max_rel_err": _rel(got.ravel(), ref) if rc == 0 else None,
-                     "tolerance": 1e-5, "schedules_bit_identical": bool(same),
+                     "tolerance": 1e-5, "paths_bit_identical": bool(same),
                      "coverage": f"output rows {r0}..{r0 + rows - 1} (every column) against the "
-                                 "tiled CPU schedule; both schedules' whole outputs compared"}
+                                 "tiled CPU schedule; the three paths' whole outputs compared"}
     res["cpu_baseline"] = _cpu(2.0 * rows * n * k / dt / 1e12, "TFLOP/s", 1,
                                f"oracle/gemm.c fe2o3o_general_reference_v1 (tiled schedule, one "
                                f"thread) on the {rows}-row parity block, {dt:.2f} s")
@@ -576,7 +587,7 @@ def _ok(par) -> bool:
     if "max_rel_err" in par and par.get("tolerance") in (1e-2, 1e-5):
         if par["max_rel_err"] is None or not par["max_rel_err"] <= par["tolerance"]:
             return False
-    if par.get("schedules_bit_identical") is False:
+    if par.get("schedules_bit_identical") is False or par.get("paths_bit_identical") is False:
         return False
     for key in ("bit_mismatches", "routing_mismatches", "policy_failures"):
         if key in par and par[key] != 0:

@@ -25,6 +25,7 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // LDS pointer type expected by the global->LDS builtin.
 typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
 
 namespace fe2o3 {
 

@@ -109,8 +109,6 @@ constexpr int STAGE_BYTES = 2 * TILE_BYTES; // K tile then V tile
 constexpr int SMEM_BYTES = 2 * STAGE_BYTES; // 64 KiB: two stages
 constexpr float RESCALE_SLACK = 8.0f;       // log2 units: p may reach 2^8 before a rescale
 
-typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
-
 // Both tiles are [64 keys][128 d] bf16 rows of 256 B holding 16 chunks of
 // 16 B.  K chunk c of row r sits at c ^ (r & 15): the S^T operand reads (32
 // consecutive rows, one chunk) are conflict-free.  V chunk c of row r sits at

@@ -70,12 +70,16 @@ struct Geo {
 // of its buffer (wave-uniform) and this thread's byte offset of its chunk
 // at k = 0; all slots share one buffer extent.  Offsets and extent are
 // 32-bit.  The B tile is always 256 rows; the A tile has the policy's
-// kARows rows (256, or fewer for short tiles).
-template <int ROW_BYTES, int N = Geo<ROW_BYTES>::kInstPerWave>
+// kARows rows (256, or fewer for short tiles).  KN: the operand is stored
+// [k][n] (rows of n, kn_rows) and a stage's k offset `kbytes` (the byte
+// offset along a k-contiguous row) becomes kbytes * kmul bytes down the rows.
+template <int ROW_BYTES, int N = Geo<ROW_BYTES>::kInstPerWave, bool KN = false>
 struct Rows {
   const void* base[N];
   uint32_t bytes;
   uint32_t voff[N];
+  uint32_t kmul;
+  FE2O3_DEVICE uint32_t soff(uint32_t kbytes) const { return KN ? kbytes * kmul : kbytes; }
 };
 
 FE2O3_DEVICE __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
@@ -114,13 +118,45 @@ FE2O3_DEVICE Rows<ROW_BYTES, Geo<ROW_BYTES>::insts(ROWS)> dense_rows(const uint1
 
 // Loads j in [J0, J1) of one operand tile into the LDS tile at byte offset
 // `tile` of smem, k offset `kbytes` (wave-uniform).
-template <int ROW_BYTES, int J0, int J1, int N>
-FE2O3_DEVICE void issue_part(const Rows<ROW_BYTES, N>& rows, uint32_t kbytes, uint8_t* smem,
+template <int ROW_BYTES, int J0, int J1, int N, bool KN>
+FE2O3_DEVICE void issue_part(const Rows<ROW_BYTES, N, KN>& rows, uint32_t kbytes, uint8_t* smem,
                              uint32_t tile, uint32_t wave) {
 #pragma unroll
   for (int j = J0; j < J1; ++j)
     b2l_b128(rsrc(rows.base[j], rows.bytes), smem + tile + (4u * j + wave) * 1024u, rows.voff[j],
-             kbytes);
+             rows.soff(kbytes));
+}
+
+// B stored [k][n] (row-major, ldb elements apart), 256 columns from `base`:
+// one stage is 64 k-rows of 512 bytes.  Load j of wave w moves k-rows
+// 2(4j + w) and 2(4j + w) + 1; lane l fills LDS chunk position l % 32 of
+// k-row 2(4j + w) + l / 32 with global chunk (l % 32) ^ kn_swz(row), i.e.
+// columns 8c .. 8c + 7 of chunk c are stored at chunk position c ^
+// kn_swz(row).  Columns at or past valid_cols read the last valid chunk
+// (their products reach only outputs that are never stored).  The caller
+// guarantees ((k16 - 1) * ld + 256) * 2 < 2^31 and 16-byte aligned rows.
+FE2O3_DEVICE uint32_t kn_swz(uint32_t krow) {
+  // twice a 4-bit row code: the 16 rows one transposing fragment read
+  // touches (8g + q, g, q < 4) get 16 different codes, so its 64 lanes'
+  // 8-byte pieces fill 32 distinct 16-byte positions of the 512-byte rows
+  return 2u * ((krow & 3u) | (((krow >> 3) & 3u) << 2));
+}
+FE2O3_DEVICE Rows<128, 8, true> kn_rows(const uint16_t* base, uint32_t ld, uint32_t valid_cols,
+                                        uint32_t k16) {
+  Rows<128, 8, true> t;
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  const uint32_t last_chunk = (valid_cols - 1u) / 8u;
+  t.bytes = ((k16 - 1u) * ld + valid_cols) * 2u;  // reads past C's columns return 0
+  t.kmul = ld;  // a stage of 64 k (128 bytes along a k row) is 64 rows of ld elements
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t krow = 2u * (4u * j + w) + lane / 32u;
+    uint32_t chunk = (lane % 32u) ^ kn_swz(krow);
+    if (chunk > last_chunk) chunk = last_chunk;
+    t.base[j] = base;
+    t.voff[j] = (krow * ld + chunk * 8u) * 2u;
+  }
+  return t;
 }
 
 // Stage p's A tile (A_ROWS rows) at a(p); its B tile at b_region + b(p).
@@ -192,6 +228,7 @@ struct Bf16Mma {
   using Acc = Acc16T<kRB>;
   static constexpr int kSubsteps = ROW_BYTES / 64, kMfma = kRB * 8, kTn = 8, kReads = kRB + 8;
   static constexpr int kARows = 2 * RPW;
+  static constexpr bool kBKN = false;
   struct Frags {
     bf16x8_t a[kRB], b[8];
   };
@@ -253,6 +290,78 @@ struct Bf16Mma {
   }
 };
 
+// bf16 with B stored [k][n] (kn_rows): the A side is Bf16Mma<128>'s; a B
+// fragment (k 8(l/16) .. +7 of column 16j + l%16) is read from the row-major
+// LDS tile with two ds_read_b64_tr_b16.  Within each 16-lane group the
+// instruction hands lane i element M[4e + i/4][i%4] (e = 0..3) of the 16 x 4
+// block whose row r is the 4 bf16 at lane r's address; lane i of group G
+// addresses k-row kb + i/4, columns c0 + 4(i%4) (kb = 32s + 8G, c0 the
+// fragment's first column), so it receives B[kb + e][c0 + i]: four k of its
+// column, and the second read (k-rows + 4, 2048 bytes on) the next four.  The
+// per-lane byte offsets of the eight fragments differ by more than a
+// constant (kn_swz mixes the column bits), so each substep keeps eight.
+struct Bf16MmaKN {
+  using A = Bf16Mma<128, 128>;
+  using Acc = A::Acc;
+  static constexpr int kRB = A::kRB, kSubsteps = A::kSubsteps, kMfma = A::kMfma, kTn = A::kTn;
+  static constexpr int kReads = A::kReads;
+  static constexpr int kARows = A::kARows;
+  static constexpr bool kBKN = true;
+  using Frags = A::Frags;
+  struct Lanes {
+    uint32_t a[kSubsteps][4], b[kSubsteps][8];
+  };
+  static FE2O3_DEVICE Lanes lanes(uint32_t b_region) {
+    const typename A::Lanes la = A::lanes(b_region);
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t wn = wave & 1u, g = lane >> 4, i = lane & 15u;
+    Lanes l;
+#pragma unroll
+    for (int s = 0; s < kSubsteps; ++s) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) l.a[s][p] = la.a[s][p];
+      const uint32_t krow = 32u * s + 8u * g + (i >> 2);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t chunk = wn * 16u + 2u * j + ((i & 3u) >> 1);
+        l.b[s][j] = b_region + krow * 512u + ((chunk ^ kn_swz(krow)) << 4) + (i & 1u) * 8u;
+      }
+    }
+    return l;
+  }
+  template <uint32_t A_TILE, uint32_t B_TILE, int S, int R>
+  static FE2O3_DEVICE void read(const uint8_t* smem, const Lanes& l, Frags& f) {
+    static_assert(R >= 0 && R < kReads, "read unit");
+    if constexpr (R == 0) {
+      f.a[0] = *reinterpret_cast<const bf16x8_t*>(smem + l.a[S][0] + A_TILE);
+    } else if constexpr (R <= 8) {
+      constexpr int j = R - 1;
+      // inline asm: as a builtin the transposing read is taken to alias the
+      // global->LDS copies in flight and gets a vmcnt(0) before it, which
+      // drains the copy pipeline every substep.  It does not alias them
+      // (copies fill the other stage), and its result is waited for with the
+      // A read a0 issued before it: the compiler's lgkmcnt wait for a0 at
+      // the next substep's first MFMA leaves only the later A reads a1..a7
+      // outstanding, and LDS reads complete in order.
+      const lds_bf16x4_t* p = (const lds_bf16x4_t*)(smem + l.b[S][j]);
+      bf16x4_t lo, hi;
+      asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
+                   : "=v"(lo), "=v"(hi)
+                   : "v"(p), "i"(B_TILE), "i"(B_TILE + 2048u));
+      f.b[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
+      constexpr int ii = R - 8;
+      f.a[ii] = *reinterpret_cast<const bf16x8_t*>(smem + l.a[S][ii & 3] +
+                                                   (A_TILE + ii * 16u * 128u));
+    }
+  }
+  template <bool FIRST, int I>
+  static FE2O3_DEVICE void mfma(Acc& acc, const Frags& f) {
+    A::template mfma<FIRST, I>(acc, f);
+  }
+  static FE2O3_DEVICE void finish(Acc& acc) { A::finish(acc); }
+};
+
 // OCP fp8 e4m3: v_mfma_scale_f32_32x32x64_f8f6f4 with both formats e4m3
 // (cbsz = blgp = 0) and unit E8M0 block scales (127 = 2^0), 64 k per
 // substep.  Lane l holds k 32(l/32) .. +31 (chunks 4s + 2(l/32) and the next)
@@ -265,6 +374,7 @@ struct Fp8Mma {
   using Acc = Acc32;
   static constexpr int kSubsteps = ROW_BYTES / 64, kMfma = 16, kTn = 4, kReads = 8;
   static constexpr int kARows = 256;
+  static constexpr bool kBKN = false;
   struct Frags {
     i32x8_t a[4], b[4];
   };
@@ -375,8 +485,8 @@ struct CopyOrder {
 };
 
 // Copy C of the stage at k offset `kbytes` into LDS buffer `buf`.
-template <int ROW_BYTES, int STAGES, int A_ROWS, int C, int NA, int NB>
-FE2O3_DEVICE void copy_one(const Rows<ROW_BYTES, NA>& ar, const Rows<ROW_BYTES, NB>& br,
+template <int ROW_BYTES, int STAGES, int A_ROWS, int C, int NA, int NB, bool BKN>
+FE2O3_DEVICE void copy_one(const Rows<ROW_BYTES, NA>& ar, const Rows<ROW_BYTES, NB, BKN>& br,
                            uint32_t kbytes, uint8_t* smem, uint32_t wave, int buf) {
   using L = Lay<ROW_BYTES, STAGES, A_ROWS>;
   using O = CopyOrder<NA, NB>;
@@ -386,7 +496,7 @@ FE2O3_DEVICE void copy_one(const Rows<ROW_BYTES, NA>& ar, const Rows<ROW_BYTES, 
              kbytes);
   else
     b2l_b128(rsrc(br.base[j], br.bytes), smem + L::b_region + L::b(buf) + (4u * j + wave) * 1024u,
-             br.voff[j], kbytes);
+             br.voff[j], br.soff(kbytes));
 }
 
 // Substep S_ of a K step held in stage buffer P.  FIRST: the K loop's first
@@ -399,7 +509,7 @@ struct Substep {
   static constexpr int S = M::kSubsteps, MF = M::kMfma;
   static constexpr int NA = G::insts(M::kARows), NB = G::kInstPerWave;
   using RA_ = Rows<ROW_BYTES, NA>;
-  using RB_ = Rows<ROW_BYTES, NB>;
+  using RB_ = Rows<ROW_BYTES, NB, M::kBKN>;
   static constexpr int NC = NA + NB;              // copies per stage and wave
   static constexpr int kEarly = NC / 2;           // copies started at the barrier
   static constexpr int PN = (P + 1) % STAGES;     // buffer of the next step

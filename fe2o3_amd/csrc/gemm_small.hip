@@ -10,6 +10,8 @@
 //     recurrence, LDS-tiled and register-blocked (4x4 outputs per thread),
 //     bit-identical to the scalar oracle.
 #include "common.hpp"
+#include "gemm_core.hpp"
+#include "gemm_pipe.hpp"
 #include "internal.hpp"
 
 namespace {
@@ -337,6 +339,97 @@ int32_t fe2o3_tiled_gemm_v1(const uint16_t* a, uint64_t a_len, const uint16_t* b
 
 namespace {
 
+// ---- general GEMM on the pipelined tile ----------------------------------------------
+// The same contract on the 256x256 MFMA tile of gemm_pipe.hpp: A's rows
+// (lda apart) are k-contiguous as the tile wants; B is stored [k][n], so its
+// 64-k stages arrive as 64 rows of 256 columns and the MFMA fragments are
+// read with the transposing LDS read (gemm_pipe::Bf16MmaKN).  Rows past m
+// and columns past n repeat the last valid ones and are not stored.  Each
+// accumulator receives the same 16x16x32 MFMAs over the same k slices in the
+// same order as in gemm_general_kernel, so both give the same bits.  The
+// epilogue is that kernel's: alpha * sum and beta * C rounded separately,
+// then added.
+constexpr int kGpRowBytes = 128, kGpStages = 2;
+constexpr int kGpSmem = kGpStages * 2 * gemm_pipe::Geo<kGpRowBytes>::kTileBytes;  // 128 KiB
+
+__global__ void __launch_bounds__(256, 1) gemm_general_pipe_kernel(
+    const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, float* __restrict__ c,
+    uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha,
+    float beta) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const uint32_t tiles_m = (m + 255u) / 256u, tiles_n = (n + 255u) / 256u;
+  uint32_t tm, tn;
+  gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  const uint32_t rows = min(256u, m - tm * 256u), cols = min(256u, n - tn * 256u);
+  const auto ar = gemm_pipe::dense_rows<kGpRowBytes>(a + (uint64_t)tm * 256u * lda, lda, rows, k);
+  const auto br = gemm_pipe::kn_rows(b + (uint64_t)tn * 256u, ldb, cols, k);
+  gemm_pipe::Acc16 acc;
+  gemm_pipe::mainloop<gemm_pipe::Bf16MmaKN, kGpRowBytes, kGpStages>(ar, br, k, smem, acc);
+  // Per 16-row block: every C load of the lane first (one wait), then the
+  // products and stores.  Whole 256-column tiles of a 16-byte aligned C with
+  // ldc % 4 == 0 move 4 columns per access; otherwise element by element,
+  // the loads of columns past n clamped to the last valid one (not stored).
+  {
+#pragma clang fp contract(off)
+    const uint32_t row0 = gemm_pipe::acc16_row0(), col0 = gemm_pipe::acc16_col0();
+    float* c_tile = c + (uint64_t)tm * 256u * ldc + (uint64_t)tn * 256u;
+    const bool vec = cols == 256u && ldc % 4u == 0u && ((uintptr_t)c & 15u) == 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t r = row0 + 16u * i;
+      if (r >= rows) continue;
+      float* out = c_tile + (uint64_t)r * ldc;
+      if (vec) {
+        f32x4_t cv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) cv[j] = *reinterpret_cast<const f32x4_t*>(out + col0 + 16u * j);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          f32x4_t y;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float product = alpha * acc.v[i][j][e];
+            const float initial = beta * cv[j][e];
+            y[e] = product + initial;
+          }
+          *reinterpret_cast<f32x4_t*>(out + col0 + 16u * j) = y;
+        }
+      } else {
+        float cv[8][4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) cv[j][e] = out[min(col0 + 16u * j + e, cols - 1u)];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t col = col0 + 16u * j + e;
+            if (col < cols) {
+              const float product = alpha * acc.v[i][j][e];
+              const float initial = beta * cv[j][e];
+              out[col] = product + initial;
+            }
+          }
+      }
+    }
+  }
+}
+
+const fe2o3_host::KernelRegistrar kRegisteredPipe[] = {
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe_kernel", (const void*)gemm_general_pipe_kernel, 256, kGpSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe_kernel", (const void*)gemm_general_pipe_kernel, 256, kGpSmem})};
+
+// Host: whether the pipelined tile takes this general GEMM: whole 64-k
+// stages, 16-byte aligned rows of A and B, and both operands' panels within
+// a buffer resource's 32-bit range.
+bool general_pipe_ok(const uint16_t* a, const uint16_t* b, uint32_t k, uint32_t lda,
+                     uint32_t ldb) {
+  return k != 0 && k % 64 == 0 && lda % 8 == 0 && ldb % 8 == 0 &&
+         (((uintptr_t)a | (uintptr_t)b) & 15u) == 0 && (255ull * lda + k) * 2 < (1ull << 31) &&
+         ((uint64_t)(k - 1) * ldb + 256) * 2 < (1ull << 31);
+}
+
 template <bool VEC_A>
 int32_t general_gemm(const uint16_t* a, uint64_t a_len, const uint16_t* b, uint64_t b_len,
                      float* c, uint64_t c_len, uint32_t m, uint32_t n, uint32_t k, uint32_t lda,
@@ -352,6 +445,16 @@ int32_t general_gemm(const uint16_t* a, uint64_t a_len, const uint16_t* b, uint6
   if (a_len < ea || b_len < eb || c_len < ec) return FE2O3_ERR_LENGTH;
   if (m == 0 || n == 0) return FE2O3_OK;  // empty output: no dispatch
   if ((ea && !a) || (eb && !b) || !c) return FE2O3_ERR_NULL;
+  if (general_pipe_ok(a, b, k, lda, ldb)) {
+    static const int32_t lds_rc =
+        fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe_kernel}, kGpSmem);
+    if (lds_rc != FE2O3_OK) return lds_rc;
+    const uint64_t tiles = (uint64_t)((m + 255) / 256) * ((n + 255) / 256);
+    if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
+    gemm_general_pipe_kernel<<<(unsigned)tiles, 256, kGpSmem, (hipStream_t)stream>>>(
+        a, b, c, m, n, k, lda, ldb, ldc, alpha, beta);
+    return fe2o3_host::after_launch();
+  }
   dim3 grid((n + G_BN - 1) / G_BN, (m + G_BM - 1) / G_BM);
   if (grid.y > 65535u) return FE2O3_ERR_SHAPE;
   gemm_general_kernel<VEC_A><<<grid, 256, 0, (hipStream_t)stream>>>(a, b, c, m, n, k, lda, ldb,

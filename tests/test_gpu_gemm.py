@@ -150,6 +150,50 @@ def test_general_random_within_tolerance(gpu, oracle, dims, strides, alpha, beta
         assert got[r * ldc + n:(r + 1) * ldc].tobytes() == c[r * ldc + n:(r + 1) * ldc].tobytes()
 
 
+@pytest.mark.parametrize("dims,strides,alpha,beta", [
+    ((300, 520, 512), (520, 528, 530), 1.5, 0.5),
+    ((256, 256, 64), (64, 256, 256), 1.0, 0.0),
+    ((1000, 264, 1024), (1032, 264, 270), -0.75, 2.0),
+    ((17, 1000, 128), (136, 1003, 1003), 1.0, 1.0),
+    ((64, 300, 64), (64, 304, 301), 0.5, -1.0),  # last column chunk reads B's padding
+])
+def test_general_pipelined_tile_matches_staged_kernel(gpu, oracle, dims, strides, alpha, beta):
+    """Shapes the pipelined 256x256 tile takes (whole 64-k stages, 16-byte
+    aligned A and B rows) against the same data through the 64x64 staged
+    kernel (A moved to a 2-byte offset, which the tile does not take): the
+    same bits, also with NaN and infinity in A's and B's stride padding; C's
+    padding untouched; rel-err <= 1e-5 against the tiled CPU schedule."""
+    m, n, k = dims
+    lda, ldb, ldc = strides
+    rng = np.random.default_rng(m + n + k)
+    la, lb, lc = (m - 1) * lda + k, (k - 1) * ldb + n, (m - 1) * ldc + n
+    a = oracle.bf16_from_f32(rng.standard_normal(la).astype(np.float32))
+    b = oracle.bf16_from_f32(rng.standard_normal(lb).astype(np.float32))
+    for r in range(m - 1):  # A's padding: NaN and infinity payloads
+        a[r * lda + k:(r + 1) * lda] = np.where(np.arange(lda - k) % 2, 0x7F80, 0x7FC1)
+    for r in range(k - 1):
+        b[r * ldb + n:(r + 1) * ldb] = 0xFF80
+    c = rng.standard_normal(lc).astype(np.float32)
+    kern = _kernels().tiled_gemm_general_v1_gpu.Kernel.load(gpu)
+    gc = Guarded(gpu, c)
+    kern.prepare(gpu.to_device(a), gpu.to_device(b), gc.body, m, n, k, lda, ldb, ldc, alpha,
+                 beta).launch()
+    assert gc.guards_intact()
+    # the same A two bytes past a 16-byte boundary: the staged kernel
+    a_off = Guarded(gpu, np.concatenate([np.zeros(1, np.uint16), a]))
+    gs = Guarded(gpu, c)
+    kern.prepare(a_off.full.view(65, la), gpu.to_device(b), gs.body, m, n, k, lda, ldb, ldc,
+                 alpha, beta).launch()
+    got = gc.download()
+    assert_same(got, gs.download(), "pipelined tile vs staged kernel")
+    for r in range(m - 1):
+        assert got[r * ldc + n:(r + 1) * ldc].tobytes() == c[r * ldc + n:(r + 1) * ldc].tobytes()
+    rows = np.concatenate([got[r * ldc:r * ldc + n] for r in range(m)])
+    rc, out, _ = oracle.general_reference_v1(m, n, k, lda, ldb, ldc, a, b, c, alpha, beta)
+    assert rc == 0
+    assert rel_err(rows, out) <= 1e-5
+
+
 def test_general_rejects_small_stride_and_short_slice(gpu):
     from fe2o3_amd.runtime import Fe2o3Error
     a = gpu.to_device(np.zeros(64, np.uint16))
