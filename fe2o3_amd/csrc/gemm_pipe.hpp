@@ -342,7 +342,8 @@ struct Bf16MmaKN {
       // (copies fill the other stage), and its result is waited for with the
       // A read a0 issued before it: the compiler's lgkmcnt wait for a0 at
       // the next substep's first MFMA leaves only the later A reads a1..a7
-      // outstanding, and LDS reads complete in order.
+      // outstanding, and LDS reads complete in order.  The compiled kernel is
+      // replayed against that rule by tests/test_isa_lds_waits.py.
       const lds_bf16x4_t* p = (const lds_bf16x4_t*)(smem + l.b[S][j]);
       bf16x4_t lo, hi;
       asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"

@@ -1,0 +1,80 @@
+"""The pipelined general GEMM issues its transposing LDS reads as inline asm
+(gemm_pipe::Bf16MmaKN::read), which the compiler does not see as loads: it
+relies on the compiler's own s_waitcnt lgkmcnt for the A read issued before
+them.  This CPU test compiles gemm_small.hip for gfx950 to assembly and
+replays gemm_general_pipe_kernel's instruction stream with in-order LDS
+completion: no instruction may read a VGPR that an LDS read has not yet
+delivered (no s_waitcnt lgkmcnt covering it).  Scalar loads share the
+counter; the replay ignores them, which only keeps more LDS reads pending
+than the hardware would, so the check stays conservative.  The check is
+shown to fire on the same stream with its lgkmcnt waits removed."""
+from __future__ import annotations
+
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "fe2o3_amd", "csrc")
+
+
+def _regs(tok):
+    m = re.match(r"([va])\[(\d+):(\d+)\]", tok)
+    if m:
+        return {(m.group(1), r) for r in range(int(m.group(2)), int(m.group(3)) + 1)}
+    m = re.match(r"([va])(\d+)$", tok)
+    return {(m.group(1), int(m.group(2)))} if m else set()
+
+
+def _violations(lines):
+    pending, bad = [], 0
+    for line in lines:
+        if not line or line.startswith(".") or line.endswith(":"):
+            continue
+        op = line.split()[0]
+        args = [a.strip() for a in line[len(op):].split(",")]
+        if op == "s_waitcnt":
+            m = re.search(r"lgkmcnt\((\d+)\)", line)
+            if m:
+                keep = int(m.group(1))
+                pending = pending[len(pending) - keep:] if 0 < keep < len(pending) else (
+                    [] if keep == 0 else pending)
+            continue
+        srcs = set()
+        for a in args[1:]:
+            srcs |= _regs(a)
+        live = set().union(*pending) if pending else set()
+        if srcs & live and not op.startswith("ds_"):
+            bad += 1
+        if op.startswith("ds_read"):
+            pending.append(_regs(args[0]))
+        elif op.startswith("ds_"):
+            pending.append(set())
+    return bad
+
+
+def test_general_pipe_kernel_lds_reads_are_waited_for(tmp_path):
+    hipcc = "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc) or shutil.which("python3") is None:
+        pytest.skip("hipcc not available")
+    out = tmp_path / "gemm_small.s"
+    subprocess.run([hipcc, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang",
+                    "-target-feature", "-Xclang", "-packed-fp32-ops", "-munsafe-fp-atomics",
+                    "--cuda-device-only", "-S", "-I" + os.path.join(CSRC, "_build"),
+                    os.path.join(CSRC, "gemm_small.hip"), "-o", str(out)],
+                   check=True, capture_output=True)
+    text = out.read_text()
+    m = re.search(r"^(_Z\S*gemm_general_pipe_kernel\S*):\s*;.*?\n(.*?)\n\s*s_endpgm", text,
+                  re.S | re.M)
+    assert m, "kernel not found in the assembly"
+    body = [l.split(";")[0].strip() for l in m.group(2).split("\n")]
+    assert sum("ds_read_b64_tr_b16" in l for l in body) >= 64
+    assert _violations(body) == 0
+    # the check fires when the waits are gone
+    stripped = [re.sub(r"lgkmcnt\(\d+\)", "", l) if l.startswith("s_waitcnt") else l
+                for l in body]
+    stripped = [l for l in stripped if l.strip() != "s_waitcnt"]
+    assert _violations(stripped) > 100
