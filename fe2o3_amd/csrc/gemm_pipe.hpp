@@ -202,8 +202,8 @@ struct Acc32 {
 
 // bf16: v_mfma_f32_16x16x32_bf16, 32 k per substep.  Each wave owns RPW
 // output rows (RPW/16 row blocks) by 128 columns; the A tile holds 2 RPW
-// rows (256 for full tiles; 128, 64 or 32 for the short last tiles of the
-// MoE experts, which then cost the MFMAs and A loads of their rows only).
+// rows (256 for full tiles; any multiple of 32 for the MoE experts' tiles,
+// which then cost the MFMAs and A loads of their rows only).
 // Lane l holds k 8(l/16) .. +7 of row 16i + l%16 of the wave's A rows (a[i])
 // and B rows (b[j]); the swizzle of a row depends on its index mod 32, hence
 // four lane offsets per operand and substep.  One read unit is one
@@ -222,7 +222,7 @@ struct Acc32 {
 //     LDS reads that overwrite them need no wait states.
 template <int ROW_BYTES, int RPW = 128>
 struct Bf16Mma {
-  static_assert(RPW == 128 || RPW == 64 || RPW == 32 || RPW == 16, "rows per wave");
+  static_assert(RPW % 16 == 0 && RPW >= 16 && RPW <= 128, "rows per wave");
   using G = Geo<ROW_BYTES>;
   static constexpr int kRB = RPW / 16;
   using Acc = Acc16T<kRB>;

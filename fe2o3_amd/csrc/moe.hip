@@ -297,12 +297,9 @@ FE2O3_DEVICE bool expert_tile(const uint32_t* offsets, uint32_t e_begin, uint32_
   const uint32_t incl_e = (uint32_t)__builtin_amdgcn_readlane((int)incl, le);
   const uint32_t m_tiles = (n_e + 255u) / 256u;
   const uint32_t xi = x - (incl_e - m_tiles * n_blocks);
-  const uint32_t mt = xi % m_tiles;
   *e_out = e_begin + (uint32_t)le;
   *nb = xi / m_tiles;
-  *row0 = lo_e + mt * 256u;
-  const uint32_t left = n_e - mt * 256u;
-  *rows = left < 256u ? left : 256u;
+  m_tile(lo_e, n_e, m_tiles, xi % m_tiles, row0, rows);
   return true;
 }
 
@@ -319,13 +316,28 @@ FE2O3_DEVICE float silu_mul(float g, float u) {
 constexpr int kRowBytes = 128, kStages = 2;  // 64 k per LDS stage, two stages
 constexpr int kSmem = kStages * 2 * gemm_pipe::Geo<kRowBytes>::kTileBytes;  // 128 KiB
 
+// The form a tile of `rows` rows runs on: fn(RPW) with RPW output rows per
+// wave, the A tile holding 2 RPW rows = `rows` rounded up to 32, on two 64-k
+// stages; fn(0) for a tile of at most 64 rows (an expert of at most 64 rows,
+// as the tile list deals rows out), which runs 64 rows on four 32-k stages:
+// its few MFMAs per stage cannot hide the weight copies' latency, and three
+// stages of copies in flight can.  The MFMAs and A copies of a tile are
+// those of its own rows; the B copies are the whole n-block's.
+template <class Fn>
+FE2O3_DEVICE void by_tile_rows(uint32_t rows, Fn&& fn) {
+  using std::integral_constant;
+  if (rows > 224u) fn(integral_constant<int, 128>{});
+  else if (rows > 192u) fn(integral_constant<int, 112>{});
+  else if (rows > 160u) fn(integral_constant<int, 96>{});
+  else if (rows > 128u) fn(integral_constant<int, 80>{});
+  else if (rows > 96u) fn(integral_constant<int, 64>{});
+  else if (rows > 64u) fn(integral_constant<int, 48>{});
+  else fn(integral_constant<int, 0>{});
+}
+
 // One gate/up tile on the pipeline geometry G (ROW_BYTES of k per row and
 // stage, STAGES stages, RPW output rows per wave; the A tile holds 2 RPW
-// rows).  Full tiles run 256 rows on two 64-k stages.  An expert's short
-// last m-tile (at most 64 rows) runs 64 rows on four 32-k stages: its few
-// MFMAs per stage cannot hide the weight copies' latency, and three stages
-// of copies in flight can.  It keeps its place beside the same n-block's
-// full tiles in the work list, so it still shares their weights in L2.
+// rows; the form by_tile_rows picks).
 template <int ROW_BYTES, int STAGES, int RPW>
 FE2O3_DEVICE void gate_up_tile(const uint16_t* __restrict__ xc, const uint16_t* __restrict__ wg,
                                const uint16_t* __restrict__ wu, uint32_t e, uint32_t row0,
@@ -388,10 +400,13 @@ __global__ void __launch_bounds__(256, 1) gate_up_kernel(
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   uint32_t e, row0, rows, nb;
   if (!expert_tile(offsets, e_begin, e_end, routes, ffn / 128u, &e, &row0, &rows, &nb)) return;
-  if (rows > 64u)
-    gate_up_tile<128, 2, 128>(xc, wg, wu, e, row0, rows, nb, hidden, ffn, hc, smem);
-  else
-    gate_up_tile<64, 4, 32>(xc, wg, wu, e, row0, rows, nb, hidden, ffn, hc, smem);
+  by_tile_rows(rows, [&](auto rpw) {
+    constexpr int R = decltype(rpw)::value;
+    if constexpr (R == 0)
+      gate_up_tile<64, 4, 32>(xc, wg, wu, e, row0, rows, nb, hidden, ffn, hc, smem);
+    else
+      gate_up_tile<128, 2, R>(xc, wg, wu, e, row0, rows, nb, hidden, ffn, hc, smem);
+  });
 }
 
 // One down tile (split K: list entry nb = 2 * n-block + k-half; each half
@@ -435,10 +450,13 @@ __global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict
   if (!expert_tile(offsets, e_begin, e_end, (uint32_t)routes, 2u * (hidden / 256u), &e, &row0,
                    &rows, &nb))
     return;
-  if (rows > 64u)
-    down_tile<128, 2, 128>(hc, wd, e, row0, rows, nb, hidden, ffn, routes, yc, smem);
-  else
-    down_tile<64, 4, 32>(hc, wd, e, row0, rows, nb, hidden, ffn, routes, yc, smem);
+  by_tile_rows(rows, [&](auto rpw) {
+    constexpr int R = decltype(rpw)::value;
+    if constexpr (R == 0)
+      down_tile<64, 4, 32>(hc, wd, e, row0, rows, nb, hidden, ffn, routes, yc, smem);
+    else
+      down_tile<128, 2, R>(hc, wd, e, row0, rows, nb, hidden, ffn, routes, yc, smem);
+  });
 }
 
 __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ yc,

@@ -1,8 +1,12 @@
 // moe_tiles.hpp -- the work list of the MoE expert GEMMs.
 //
 // The tiles of experts [e_begin, e_end) form one list: expert-major, then
-// n-block, then the expert's 256-row m-tiles, so consecutive entries share a
-// weight block and runs of entries share the expert's rows.  Workgroup id i
+// n-block, then the expert's m-tiles, so consecutive entries share a weight
+// block and runs of entries share the expert's rows.  An expert of n rows
+// has ceil(n / 256) m-tiles, over which its ceil(n / 32) 32-row blocks are
+// dealt out evenly (m_tile): 1033 rows are tiles of 224, 224, 224, 192 and
+// 169 rows rather than four of 256 and a remainder of 9, and every tile runs
+// on an A tile of its own size rounded up to 32 rows.  Workgroup id i
 // runs on XCD i % 8; XCD x takes the x-th contiguous eighth of the list in
 // order, so the workgroups that share a weight block run at the same time
 // behind one L2.  The grid is sized for the most m-tiles routing can produce;
@@ -35,6 +39,22 @@ FE2O3_HD void expert_rows(const uint32_t* offsets, uint32_t e, uint32_t routes, 
   *n = b > a ? b - a : 0u;
 }
 
+// Rows of m-tile mt (< m_tiles = ceil(n / 256)) of an expert whose n >= 1
+// rows start at lo: the first ceil(n/32) % m_tiles tiles take one 32-row
+// block more than the others.  Every tile has 1..256 rows (at most
+// ceil(ceil(n/32) / m_tiles) <= 8 blocks, and the last starts below n), and
+// the tiles cover [lo, lo + n) in order, each row once.
+FE2O3_HD void m_tile(uint32_t lo, uint32_t n, uint32_t m_tiles, uint32_t mt, uint32_t* row0,
+                     uint32_t* rows) {
+  const uint32_t blocks = (n + 31u) / 32u;
+  const uint32_t q = blocks / m_tiles, r = blocks % m_tiles;
+  const uint32_t off = 32u * (mt * q + (mt < r ? mt : r));
+  const uint32_t cap = 32u * (q + (mt < r ? 1u : 0u));
+  const uint32_t left = n - off;
+  *row0 = lo + off;
+  *rows = left < cap ? left : cap;
+}
+
 // Entry of workgroup `block` in the list: expert, first row, row count
 // (1..256) and n-block; false when the workgroup has no entry.
 FE2O3_HD bool expert_tile_at(const uint32_t* offsets, uint32_t e_begin, uint32_t e_end,
@@ -54,12 +74,9 @@ FE2O3_HD bool expert_tile_at(const uint32_t* offsets, uint32_t e_begin, uint32_t
     expert_rows(offsets, e, routes, &lo, &n);
     const uint32_t m_tiles = (n + 255u) / 256u;
     if (x < m_tiles * n_blocks) {
-      const uint32_t mt = x % m_tiles;
       *e_out = e;
       *nb = x / m_tiles;
-      *row0 = lo + mt * 256u;
-      const uint32_t left = n - mt * 256u;
-      *rows = left < 256u ? left : 256u;
+      m_tile(lo, n, m_tiles, x % m_tiles, row0, rows);
       return true;
     }
     x -= m_tiles * n_blocks;
@@ -96,12 +113,9 @@ FE2O3_HD bool expert_tile_lanes(const uint32_t* offsets, uint32_t e_begin, uint3
   for (uint32_t i = 0; i < 64; ++i) l += incl[i] <= x ? 1u : 0u;
   const uint32_t m_tiles = (n[l] + 255u) / 256u;
   const uint32_t xi = x - (incl[l] - m_tiles * n_blocks);
-  const uint32_t mt = xi % m_tiles;
   *e_out = e_begin + l;
   *nb = xi / m_tiles;
-  *row0 = lo[l] + mt * 256u;
-  const uint32_t left = n[l] - mt * 256u;
-  *rows = left < 256u ? left : 256u;
+  m_tile(lo[l], n[l], m_tiles, xi % m_tiles, row0, rows);
   return true;
 }
 

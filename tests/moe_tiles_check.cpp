@@ -9,9 +9,15 @@
 //     every tile of the list is run exactly once.
 //  3. The lane-parallel form the kernels run (expert_tile_lanes) gives every
 //     workgroup the same tile as the serial form.
+//  4. Consistent offsets: for every (expert, n-block) the tiles cover the
+//     expert's rows exactly once, in ceil(n / 256) tiles whose row counts
+//     differ by less than 64, each above 96 rows when there are two or more
+//     (no short remainder tile).
 #include <stdint.h>
 #include <stdio.h>
 
+#include <algorithm>
+#include <map>
 #include <set>
 #include <tuple>
 #include <vector>
@@ -50,6 +56,7 @@ int main() {
     const uint32_t e_end = b + 1 + rnd() % (experts - b);
     const uint64_t grid = fe2o3::expert_grid(routes, e_end - b, n_blocks);
     std::set<std::tuple<uint32_t, uint32_t, uint32_t>> seen;
+    std::map<std::pair<uint32_t, uint32_t>, std::vector<std::pair<uint32_t, uint32_t>>> spans;
     bool dup = false;
     for (uint64_t blk = 0; blk < grid; ++blk) {
       uint32_t e, row0, rows, nb;
@@ -80,6 +87,7 @@ int main() {
         ++failures;
       }
       if (!seen.insert(std::make_tuple(e, row0, nb)).second) dup = true;
+      spans[{e, nb}].push_back({row0, rows});
     }
     if (mode >= 2) {
       uint64_t want = 0;
@@ -89,6 +97,30 @@ int main() {
           printf("coverage: iter %d got %zu tiles want %llu dup %d\n", iter, seen.size(),
                  (unsigned long long)want, (int)dup);
         ++failures;
+      }
+      for (uint32_t e = b; e < e_end; ++e) {
+        const uint32_t n = off[e + 1] - off[e], m_tiles = (n + 255u) / 256u;
+        for (uint32_t nb = 0; nb < n_blocks && n > 0; ++nb) {
+          auto it = spans.find({e, nb});
+          bool ok = it != spans.end() && it->second.size() == m_tiles;
+          if (ok) {
+            auto v = it->second;
+            std::sort(v.begin(), v.end());
+            uint32_t at = off[e], lo_rows = 256, hi_rows = 0;
+            for (auto& t : v) {
+              ok = ok && t.first == at;
+              at += t.second;
+              lo_rows = std::min(lo_rows, t.second);
+              hi_rows = std::max(hi_rows, t.second);
+            }
+            ok = ok && at == off[e + 1] && hi_rows - lo_rows < 64 &&
+                 (m_tiles < 2 || lo_rows > 96);
+          }
+          if (!ok) {
+            if (failures < 10) printf("rows: iter %d expert %u n-block %u n %u\n", iter, e, nb, n);
+            ++failures;
+          }
+        }
       }
     }
   }

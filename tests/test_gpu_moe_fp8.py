@@ -268,9 +268,10 @@ def test_moe_ffn_garbage_routing_stays_in_bounds(gpu, oracle):
 @pytest.mark.parametrize("hidden,ffn", [(256, 384), (512, 256)])
 def test_moe_ffn_every_short_tile_path(gpu, oracle, hidden, ffn):
     """A routing built by hand (every route admitted, slots in route order
-    per expert) whose expert row counts put last m-tiles of 1-32, 33-64,
-    65-128 and 129-256 rows, each on its own tile path (32, 64, 128 or 256 A
-    rows), beside full tiles of the same experts; every token's output
+    per expert) whose expert row counts put tiles on every A-tile form: the
+    short form (at most 64 rows: 5, 31, 32, 33, 64) and A tiles of 96 (65),
+    128 (128, and the 97-row second tile of 257), 160 (129, 289, 300), 192
+    (321, 384), 224 (200, 418) and 256 rows (256); every token's output
     against the oracle."""
     kern = _k()
     counts = [5, 31, 32, 33, 64, 65, 128, 129, 200, 256, 257, 300, 289, 321, 384, 418]
@@ -320,28 +321,30 @@ def test_moe_ffn_small_with_drops(gpu, oracle):
 
 
 def _tail_tokens(offsets, permutation):
-    """Tokens routed to rows of each expert's short last m-tile (at most 64
-    rows) and to the last rows of its full m-tiles, plus its first row."""
+    """Tokens routed to the rows on both sides of every boundary between
+    m-tiles of 256 rows, plus each expert's first and last rows.  An expert
+    of 257-300 rows, which once ran as a full tile and a remainder of at most
+    44 rows, runs as two tiles of 160 and 97-140 rows; the picked rows
+    include the last rows of both."""
     rows = set()
-    tails = mains = 0
+    split = 0
     for e in range(len(offsets) - 1):
         lo, hi = int(offsets[e]), int(offsets[e + 1])
-        full, rem = divmod(hi - lo, 256)
-        if 0 < rem <= 64:
-            tails += 1
-            rows.update(range(lo + full * 256, hi))
-        if full:
-            mains += 1
-            rows.update(range(lo + full * 256 - 8, lo + full * 256))
-        rows.add(lo)
-    assert tails >= 2 and mains >= 2, (tails, mains)
+        if hi - lo > 256:
+            split += 1
+            rows.update(range(lo + 248, hi))
+            rows.update(range(lo + 120, lo + 168))  # around the balanced boundary
+        rows.update(range(lo, min(hi, lo + 4)))
+        rows.update(range(max(lo, hi - 4), hi))
+    assert split >= 2, split
     return sorted({int(permutation[r]) >> 1 for r in rows if r < int(offsets[-1])})
 
 
 def test_moe_ffn_short_last_tiles(gpu, oracle):
-    """Experts of 256-300 rows: one full m-tile plus a last m-tile of at most
-    64 rows; every token routed into such a row is checked, with the last
-    rows of each full tile."""
+    """Experts of 256-300 rows, dealt out as two tiles of 32-row blocks
+    (160 and 97-140 rows): every token routed into the rows around the
+    tile boundary and the 256-row mark is checked, with each expert's first
+    and last rows."""
     tokens, hidden, ffn, experts = 1100, 512, 1024, 8
     worst, _ = _ffn_case(gpu, oracle, tokens, hidden, ffn, experts, 0xFFFFFFFF, _tail_tokens)
     assert worst <= 1e-2, worst

@@ -239,9 +239,13 @@ class Leases:
 
 
 def _buffers():
-    a = np.zeros(256, np.uint16)
-    b = np.zeros(256, np.uint16)
-    c = np.zeros(256, np.float32)
+    # one arena, regions 16 KiB apart: the overlap cases below cannot reach
+    # a region other than the one they name, wherever the allocator puts it
+    arena = np.zeros(3 * 16384, np.uint8)
+    base = -arena.ctypes.data % 256
+    a = arena[base:base + 512].view(np.uint16)
+    b = arena[base + 16384:base + 16384 + 512].view(np.uint16)
+    c = arena[base + 32768 - 256:base + 32768 - 256 + 1024].view(np.float32)
     return a, b, c
 
 
