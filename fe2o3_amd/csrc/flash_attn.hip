@@ -121,7 +121,10 @@ FE2O3_DEVICE uint32_t swz_k(uint32_t r) { return r & 15u; }
 FE2O3_DEVICE uint32_t swz_v(uint32_t r) { return ((r & 3u) << 1) ^ ((r & 3u) << 2); }
 
 // K and V of one head are read through buffer resources (base = the head,
-// range = its seq * 256 bytes).  One tile is 16 loads of 1 KiB (4 rows of
+// range = its seq * 256 bytes).  A partial last key tile (seq not a multiple
+// of 64) has rows past seq: the range check returns zero for them, and the
+// LDS-direct load writes those zeros into the tile, so the masked keys'
+// P = 0 meets V = 0 there, never a stale value of another tile or launch.  One tile is 16 loads of 1 KiB (4 rows of
 // 256 B), wave w issuing loads j = 0 .. 16/WAVES - 1 of rows
 // 4 (WAVES j + w) .. +3.  The chunk swizzles depend on the row mod 16 only,
 // and 4 WAVES is a multiple of 16, so a thread's byte offset within the tile
@@ -191,7 +194,7 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
   // head the causal order is heaviest tile (most key tiles) first.
   // With `paired`, a workgroup runs two query tiles of one head, r then
   // nq-1-r, so every causal workgroup does the same nq+1 key tiles.
-  const uint32_t nq = seq / BQ;
+  const uint32_t nq = (seq + BQ - 1u) / BQ;  // the last tile may be partial
   const uint32_t per_head = paired ? nq / 2u : nq;
   uint32_t bh, rank;
   if (heads % 8u == 0u) {
@@ -216,12 +219,14 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
                              : (CAUSAL ? nq - 1u - rank : rank);
   const uint32_t q_row0 = qt * BQ + w * 32u;  // first query row of this wave
   const uint32_t my_q = q_row0 + lr;
+  // rows past seq (a partial last tile) compute on row seq-1 and store nothing
+  const uint32_t q_load = my_q < seq ? my_q : seq - 1u;
 
   // Q fragments (second MFMA operand): lane holds row my_q, d = 16*ds + 8*g .. +7
   bf16x8_t qf[8];
 #pragma unroll
   for (int ds = 0; ds < 8; ++ds)
-    qf[ds] = *reinterpret_cast<const bf16x8_t*>(qh + (uint64_t)my_q * D + ds * 16 + g * 8);
+    qf[ds] = *reinterpret_cast<const bf16x8_t*>(qh + (uint64_t)q_load * D + ds * 16 + g * 8);
 
   f32x16_t acc[4];
 #pragma unroll
@@ -231,7 +236,8 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
   float m_ref = -INFINITY;  // exp reference, log2 domain (>= running max - slack)
   float l_run = 0.0f;       // this lane's partial row sum of exp2(s*c - m_ref)
 
-  const uint32_t n_kv = CAUSAL ? (qt + 1u) * (BQ / BKV) : seq / BKV;
+  const uint32_t kv_tiles = (seq + BKV - 1u) / BKV;
+  const uint32_t n_kv = CAUSAL ? min((qt + 1u) * (BQ / BKV), kv_tiles) : kv_tiles;
   issue_tile(ksrc, k_off, 0u, smem, wave);
   issue_tile(vsrc, v_off, 0u, smem + TILE_BYTES, wave);
   wait_vmcnt0();
@@ -274,6 +280,17 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
                       nxt + (is_v ? TILE_BYTES : 0), wave, jj);
           }
         }
+      }
+      // keys past seq (the partial last tile; causal rows below seq mask
+      // them as future keys)
+      if (!CAUSAL && key0 + (uint32_t)BKV > seq) {
+        // key = key0 + 4g + c(kb, e) is past seq when c >= lim
+        const int lim = (int)(seq - key0) - 4 * (int)g;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (kb * 32 + 8 * (e >> 2) + (e & 3) >= lim) s[kb][e] = -INFINITY;
       }
       // mask the diagonal tile
       if (CAUSAL && key0 + 63u > q_row0) {
@@ -343,6 +360,7 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
   const float l_tot = l_run + swap_half(l_run);
   const float inv = 1.0f / l_tot;
   uint16_t* oh = o + head + (uint64_t)my_q * D;
+  if (my_q < seq) {
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -353,7 +371,8 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
       packed[1] = pack_bf16x2(acc[db][4 * qd + 2] * inv, acc[db][4 * qd + 3] * inv);
       *reinterpret_cast<u32x2_t*>(oh + d) = packed;
     }
-  if (lse != nullptr && g == 0) {
+  }
+  if (lse != nullptr && g == 0 && my_q < seq) {
     // natural-log statistic: max(s)*scale + ln(sum) = (m_ref + log2(sum)) * ln 2
     lse[(uint64_t)bh * seq + my_q] = (m_ref + __log2f(l_tot)) * 0.69314718055994531f;
   }
@@ -397,7 +416,7 @@ int32_t fe2o3_flash_attention_fwd(const uint16_t* q, uint64_t q_len, const uint1
   if (q_len != n || k_len != n || v_len != n || o_len != n) return FE2O3_ERR_LENGTH;
   if (lse != nullptr && lse_len != bh * seq) return FE2O3_ERR_LENGTH;
   if (n == 0) return FE2O3_OK;
-  if (seq % BQ != 0 || bh > 0xffffffffu) return FE2O3_ERR_SHAPE;
+  if (bh > 0xffffffffu) return FE2O3_ERR_SHAPE;
   // K/V of one head are addressed through a 32-bit buffer range
   if ((uint64_t)seq * D * 2 > 0x7fffffffu) return FE2O3_ERR_SHAPE;
   if (!q || !k || !v || !o) return FE2O3_ERR_NULL;
@@ -411,8 +430,9 @@ int32_t fe2o3_flash_attention_fwd(const uint16_t* q, uint64_t q_len, const uint1
   // one linear workgroup id per (query tile, batch*head); see the kernel
   // causal: pairs of query tiles per workgroup (every workgroup the same
   // work) when the tile count is even; non-causal tiles are equal already
-  const uint32_t paired = causal && (seq / BQ) % 2u == 0u ? 1u : 0u;
-  const uint64_t wgs = (uint64_t)(seq / BQ) / (paired ? 2u : 1u) * bh;
+  const uint32_t nq = (seq + BQ - 1u) / BQ;  // query tiles per head, the last maybe partial
+  const uint32_t paired = causal && nq % 2u == 0u ? 1u : 0u;
+  const uint64_t wgs = (uint64_t)nq / (paired ? 2u : 1u) * bh;
   if (wgs > 0x7fffffffu) return FE2O3_ERR_SHAPE;
   const dim3 grid((unsigned)wgs);
   if (causal)

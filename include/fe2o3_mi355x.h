@@ -275,8 +275,9 @@ int32_t fe2o3_flash_attention_causal_f32_b1_h1_n8_d16_v1(
  * [batch, heads, seq, head_dim] (head_dim contiguous), O = softmax(scale *
  * Q K^T [+ causal mask]) V with fp32 online max/sum; lse (may be NULL)
  * receives the fp32 natural-log row statistic max + ln(sum) per
- * [batch, heads, seq].  head_dim must be 128; seq a multiple of 128 for the
- * MFMA path (other seq values are rejected with FE2O3_ERR_SHAPE). */
+ * [batch, heads, seq].  head_dim must be 128 (FE2O3_ERR_SHAPE otherwise);
+ * any seq >= 1 with seq * 256 < 2^31 (the last 128-row query tile and
+ * 64-key tile of a head may be partial); scale positive and finite. */
 int32_t fe2o3_flash_attention_fwd(const uint16_t *q, uint64_t q_len,
                                   const uint16_t *k, uint64_t k_len,
                                   const uint16_t *v, uint64_t v_len,

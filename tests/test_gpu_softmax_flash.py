@@ -263,13 +263,84 @@ def test_flash_noncausal_key_permutation_invariance(gpu):
 
 
 def test_flash_rejects_bad_shapes(gpu):
+    """head_dim other than 128 and a scale that is not positive and finite
+    are refused before any launch, the output untouched."""
     from fe2o3_amd.runtime import Fe2o3Error
     a = gpu.alloc(100 * 64, np.uint16)
     K = _k().flash_attention_fwd_gpu.Kernel.load(gpu)
     with pytest.raises(Fe2o3Error) as e:
         K.prepare(a, a, a, a, None, 1, 1, 100, 64, 0, 0.125).launch()
     assert e.value.status == -3
-    b = gpu.alloc(100 * 128, np.uint16)
-    with pytest.raises(Fe2o3Error) as e:
-        K.prepare(b, b, b, b, None, 1, 1, 100, 128, 0, 0.125).launch()
-    assert e.value.status == -3
+    b = gpu.to_device(np.zeros(100 * 128, np.uint16))
+    o = Guarded(gpu, np.full(100 * 128, 0x7FDE, np.uint16))
+    for bad in (0.0, -0.125, float("inf"), float("nan")):
+        with pytest.raises(Fe2o3Error) as e:
+            K.prepare(b, b, b, o.body, None, 1, 1, 100, 128, 0, bad).launch()
+        assert e.value.status == -3
+    assert o.unchanged()
+
+
+def _guarded_qkv(gpu, b, h, s, seed):
+    """Q, K, V ~ N(0,1) bf16 in guard-banded buffers (bf16 NaN guards): a
+    read past a head's seq rows of the last (batch, head) would meet NaN."""
+    rng = np.random.default_rng(seed)
+    n = b * h * s * 128
+    host = [(rng.standard_normal(n).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+            for _ in range(3)]
+    return host, [Guarded(gpu, t) for t in host]
+
+
+@pytest.mark.parametrize("causal", [False, True])
+# partial last query tiles (seq % 128) and key tiles (seq % 64), one key
+# tile only (1, 37, 64), odd and even query-tile counts (causal pairing)
+@pytest.mark.parametrize("b,h,s", [(1, 1, 1), (1, 2, 37), (1, 1, 64), (2, 1, 100), (1, 1, 129),
+                                   (1, 2, 200), (1, 1, 1000)])
+def test_flash_any_seq_all_rows(gpu, oracle, b, h, s, causal):
+    """seq not a multiple of 128: every row and its LSE against the f64
+    oracle; outputs past seq untouched (guards), inputs unchanged."""
+    host, (gq, gk, gv) = _guarded_qkv(gpu, b, h, s, seed=s + 7 * b + h)
+    n = b * h * s * 128
+    scale = 1.0 / np.sqrt(128.0)
+    o = Guarded(gpu, np.full(n, 0x7FDE, np.uint16))
+    l = Guarded(gpu, np.full(b * h * s, np.nan, np.float32))
+    _k().flash_attention_fwd_gpu.Kernel.load(gpu).prepare(
+        gq.body, gk.body, gv.body, o.body, l.body, b, h, s, 128, 1 if causal else 0,
+        scale).launch()
+    assert o.guards_intact() and l.guards_intact()
+    assert gq.unchanged() and gk.unchanged() and gv.unchanged()
+    bh = np.repeat(np.arange(b * h, dtype=np.uint32), s)
+    rows = np.tile(np.arange(s, dtype=np.uint32), b * h)
+    rc, ref, ref_lse = oracle.flash_attention_rows_bf16(*host, s, 128, causal, scale, bh, rows)
+    assert rc == 0
+    got = bf16_to_f32(o.download()).reshape(-1, 128)
+    assert np.all(np.isfinite(got))
+    assert rel_err(got, ref) <= 1e-2
+    assert rel_err(l.download(), ref_lse) <= 1e-5  # fp32 output: the 1e-5 bar
+
+
+def test_flash_partial_key_tile_ignores_stale_lds(gpu, oracle):
+    """The rows of a partial key tile past seq are read as zero, not left
+    as they were: a launch whose V is all NaN (seq 64, 512 heads, every CU
+    busy) leaves NaN rows in LDS, and a following launch at seq 37 still
+    matches the oracle with finite outputs."""
+    kern = _k().flash_attention_fwd_gpu.Kernel.load(gpu)
+    heads, s0 = 512, 64
+    n0 = heads * s0 * 128
+    q0 = gpu.to_device(np.full(n0, 0x3F80, np.uint16))  # 1.0
+    v0 = gpu.to_device(np.full(n0, 0x7FC0, np.uint16))  # NaN
+    o0 = gpu.alloc(n0, np.uint16)
+    kern.prepare(q0, q0, v0, o0, None, 1, heads, s0, 128, 0, 0.125).launch()
+    for causal in (False, True):
+        b, h, s = 1, 64, 37
+        host, (gq, gk, gv) = _guarded_qkv(gpu, b, h, s, seed=11)
+        n = b * h * s * 128
+        o = Guarded(gpu, np.full(n, 0x7FDE, np.uint16))
+        kern.prepare(gq.body, gk.body, gv.body, o.body, None, b, h, s, 128, int(causal),
+                     0.125).launch()
+        got = bf16_to_f32(o.download()).reshape(-1, 128)
+        assert np.all(np.isfinite(got)) and o.guards_intact()
+        bh = np.repeat(np.arange(b * h, dtype=np.uint32), s)
+        rows = np.tile(np.arange(s, dtype=np.uint32), b * h)
+        rc, ref, _ = oracle.flash_attention_rows_bf16(*host, s, 128, causal, 0.125, bh, rows)
+        assert rc == 0
+        assert rel_err(got, ref) <= 1e-2
