@@ -202,8 +202,10 @@ struct Acc32 {
 
 // bf16: v_mfma_f32_16x16x32_bf16, 32 k per substep.  Each wave owns RPW
 // output rows (RPW/16 row blocks) by 128 columns; the A tile holds 2 RPW
-// rows (256 for full tiles; any multiple of 32 for the MoE experts' tiles,
-// which then cost the MFMAs and A loads of their rows only).
+// rows (256 for full tiles; any multiple of 32 up to 288 for the MoE
+// experts' tiles, which then cost the MFMAs and A loads of their rows
+// only).  Row blocks 0-7 accumulate in AGPRs (all 256 of them); a ninth
+// (RPW = 144) in 32 VGPRs.
 // Lane l holds k 8(l/16) .. +7 of row 16i + l%16 of the wave's A rows (a[i])
 // and B rows (b[j]); the swizzle of a row depends on its index mod 32, hence
 // four lane offsets per operand and substep.  One read unit is one
@@ -219,10 +221,13 @@ struct Acc32 {
 //   - finish() puts explicit wait states (s_nop) between the last MFMA and
 //     the epilogue's VALU reads of the accumulators;
 //   - fragment registers are only MFMA sources A and B, read at issue: the
-//     LDS reads that overwrite them need no wait states.
+//     LDS reads that overwrite them need no wait states;
+//   - accumulators, AGPR or VGPR, are touched by nothing but these MFMAs
+//     between the first substep and finish() (tests/test_isa_mfma_acc.py
+//     checks the compiled MoE kernels for it).
 template <int ROW_BYTES, int RPW = 128>
 struct Bf16Mma {
-  static_assert(RPW % 16 == 0 && RPW >= 16 && RPW <= 128, "rows per wave");
+  static_assert(RPW % 16 == 0 && RPW >= 16 && RPW <= 144, "rows per wave");
   using G = Geo<ROW_BYTES>;
   static constexpr int kRB = RPW / 16;
   using Acc = Acc16T<kRB>;
@@ -270,12 +275,18 @@ struct Bf16Mma {
   template <bool FIRST, int I>
   static FE2O3_DEVICE void mfma(Acc& acc, const Frags& f) {
     constexpr int i = I / kTn, j = I % kTn;
-    if constexpr (FIRST)
+    if constexpr (FIRST && i < 8)
       asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0"
                    : "=a"(acc.v[i][j]) : "v"(f.b[j]), "v"(f.a[i]));
-    else
+    else if constexpr (FIRST)
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0"
+                   : "=v"(acc.v[i][j]) : "v"(f.b[j]), "v"(f.a[i]));
+    else if constexpr (i < 8)
       asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
                    : "+a"(acc.v[i][j]) : "v"(f.b[j]), "v"(f.a[i]));
+    else
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                   : "+v"(acc.v[i][j]) : "v"(f.b[j]), "v"(f.a[i]));
   }
   // wait states between the last MFMA's accumulator write and the VALU reads
   // that follow (an 8-pass MFMA needs at most 18); every accumulator then
@@ -286,7 +297,10 @@ struct Bf16Mma {
 #pragma unroll
     for (int i = 0; i < kRB; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) asm volatile("" : "+a"(acc.v[i][j]));
+      for (int j = 0; j < 8; ++j) {
+        if (i < 8) asm volatile("" : "+a"(acc.v[i][j]));
+        else asm volatile("" : "+v"(acc.v[i][j]));
+      }
   }
 };
 
@@ -464,13 +478,13 @@ struct Spread {
   }
 };
 
-// Order of a stage's NA A copies and NB B copies (NA <= NB): A copy i is
-// copy floor(i (NA + NB) / NA), the B copies fill the other positions in
-// slot order.  With NA = NB, A slot C/2 is copy C for even C and B slot C/2
+// Order of a stage's NA A copies and NB B copies: A copy i is copy
+// floor(i (NA + NB) / NA) (distinct for i < NA), the B copies fill the
+// other positions in slot order.  With NA = NB, A slot C/2 is copy C for even C and B slot C/2
 // copy C for odd C.
 template <int NA, int NB>
 struct CopyOrder {
-  static_assert(NA >= 1 && NA <= NB, "A copies spread among the B copies");
+  static_assert(NA >= 1 && NB >= 1, "copies of both operands");
   static constexpr int NC = NA + NB;
   static constexpr bool is_a(int c) {
     for (int i = 0; i < NA; ++i)

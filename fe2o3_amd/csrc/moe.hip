@@ -279,7 +279,7 @@ FE2O3_DEVICE bool expert_tile(const uint32_t* offsets, uint32_t e_begin, uint32_
   const uint32_t l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
   uint32_t lo = 0, n = 0;
   if (l < e_end - e_begin) expert_rows(offsets, e_begin + l, routes, &lo, &n);
-  uint32_t incl = (n + 255u) / 256u * n_blocks;
+  uint32_t incl = expert_m_tiles(n) * n_blocks;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     const uint32_t v = (uint32_t)__shfl_up((int)incl, o, 64);
@@ -295,7 +295,7 @@ FE2O3_DEVICE bool expert_tile(const uint32_t* offsets, uint32_t e_begin, uint32_
   const uint32_t lo_e = (uint32_t)__builtin_amdgcn_readlane((int)lo, le);
   const uint32_t n_e = (uint32_t)__builtin_amdgcn_readlane((int)n, le);
   const uint32_t incl_e = (uint32_t)__builtin_amdgcn_readlane((int)incl, le);
-  const uint32_t m_tiles = (n_e + 255u) / 256u;
+  const uint32_t m_tiles = expert_m_tiles(n_e);
   const uint32_t xi = x - (incl_e - m_tiles * n_blocks);
   *e_out = e_begin + (uint32_t)le;
   *nb = xi / m_tiles;
@@ -314,19 +314,23 @@ FE2O3_DEVICE float silu_mul(float g, float u) {
 }
 
 constexpr int kRowBytes = 128, kStages = 2;  // 64 k per LDS stage, two stages
-constexpr int kSmem = kStages * 2 * gemm_pipe::Geo<kRowBytes>::kTileBytes;  // 128 KiB
+// two stages of a 288-row A tile and a 256-row B tile: 136 KiB
+constexpr int kSmem = kStages * (int)(kMaxTileRows + 256u) * kRowBytes;
 
 // The form a tile of `rows` rows runs on: fn(RPW) with RPW output rows per
 // wave, the A tile holding 2 RPW rows = `rows` rounded up to 32, on two 64-k
-// stages; fn(0) for a tile of at most 64 rows (an expert of at most 64 rows,
-// as the tile list deals rows out), which runs 64 rows on four 32-k stages:
+// stages (the 288-row form keeps its ninth row block's accumulators in
+// VGPRs: an expert of up to 1152 rows takes four tiles, not five); fn(0)
+// for a tile of at most 64 rows (an expert of at most 64 rows, as the tile
+// list deals rows out), which runs 64 rows on four 32-k stages:
 // its few MFMAs per stage cannot hide the weight copies' latency, and three
 // stages of copies in flight can.  The MFMAs and A copies of a tile are
 // those of its own rows; the B copies are the whole n-block's.
 template <class Fn>
 FE2O3_DEVICE void by_tile_rows(uint32_t rows, Fn&& fn) {
   using std::integral_constant;
-  if (rows > 224u) fn(integral_constant<int, 128>{});
+  if (rows > 256u) fn(integral_constant<int, 144>{});
+  else if (rows > 224u) fn(integral_constant<int, 128>{});
   else if (rows > 192u) fn(integral_constant<int, 112>{});
   else if (rows > 160u) fn(integral_constant<int, 96>{});
   else if (rows > 128u) fn(integral_constant<int, 80>{});
@@ -842,9 +846,9 @@ int32_t ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate, uint
       permutation_len != routes || inverse_len != routes || weights_len != routes ||
       out_len != (uint64_t)tokens * hidden)
     return FE2O3_ERR_LENGTH;
-  // 256-row operand panels and one expert's gate/up matrix must fit the
-  // 32-bit range of a buffer resource
-  if (512ull * ffn >= (1ull << 31) || 512ull * hidden >= (1ull << 31) ||
+  // operand panels of up to 288 rows and one expert's gate/up matrix must
+  // fit the 32-bit range of a buffer resource
+  if (2ull * kMaxTileRows * ffn >= (1ull << 31) || 2ull * kMaxTileRows * hidden >= (1ull << 31) ||
       2ull * ffn * hidden >= (1ull << 31))
     return FE2O3_ERR_SHAPE;
   if (tokens == 0) return FE2O3_OK;
@@ -860,7 +864,7 @@ int32_t ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate, uint
       {(const void*)gate_up_kernel, (const void*)down_kernel}, kSmem);
   if (lds_rc != FE2O3_OK) return lds_rc;
   hipStream_t s = (hipStream_t)stream;
-  // the most m-tiles any routing yields for experts [b, e): routes/256
+  // the most m-tiles any routing yields for experts [b, e): routes/288
   // rounded up, plus one partial tile per expert
   auto grids = [&](uint32_t n_experts, uint64_t* gu, uint64_t* dn) {
     *gu = expert_grid(routes, n_experts, ffn / 128u);

@@ -3,10 +3,10 @@
 // The tiles of experts [e_begin, e_end) form one list: expert-major, then
 // n-block, then the expert's m-tiles, so consecutive entries share a weight
 // block and runs of entries share the expert's rows.  An expert of n rows
-// has ceil(n / 256) m-tiles, over which its ceil(n / 32) 32-row blocks are
-// dealt out evenly (m_tile): 1033 rows are tiles of 224, 224, 224, 192 and
-// 169 rows rather than four of 256 and a remainder of 9, and every tile runs
-// on an A tile of its own size rounded up to 32 rows.  Workgroup id i
+// has ceil(n / 288) m-tiles (kMaxTileRows), over which its ceil(n / 32)
+// 32-row blocks are dealt out evenly (m_tile): 1033 rows are tiles of 288,
+// 256, 256 and 233 rows rather than four of 256 and a remainder of 9, and
+// every tile runs on an A tile of its own size rounded up to 32 rows.  Workgroup id i
 // runs on XCD i % 8; XCD x takes the x-th contiguous eighth of the list in
 // order, so the workgroups that share a weight block run at the same time
 // behind one L2.  The grid is sized for the most m-tiles routing can produce;
@@ -31,6 +31,8 @@
 
 namespace fe2o3 {
 
+constexpr uint32_t kMaxTileRows = 288;  // rows of the largest expert tile
+
 FE2O3_HD void expert_rows(const uint32_t* offsets, uint32_t e, uint32_t routes, uint32_t* lo,
                           uint32_t* n) {
   const uint32_t a = offsets[e] < routes ? offsets[e] : routes;
@@ -39,10 +41,13 @@ FE2O3_HD void expert_rows(const uint32_t* offsets, uint32_t e, uint32_t routes, 
   *n = b > a ? b - a : 0u;
 }
 
-// Rows of m-tile mt (< m_tiles = ceil(n / 256)) of an expert whose n >= 1
-// rows start at lo: the first ceil(n/32) % m_tiles tiles take one 32-row
-// block more than the others.  Every tile has 1..256 rows (at most
-// ceil(ceil(n/32) / m_tiles) <= 8 blocks, and the last starts below n), and
+// m-tiles of an expert of n rows
+FE2O3_HD uint32_t expert_m_tiles(uint32_t n) { return (n + kMaxTileRows - 1u) / kMaxTileRows; }
+
+// Rows of m-tile mt (< m_tiles = expert_m_tiles(n)) of an expert whose
+// n >= 1 rows start at lo: the first ceil(n/32) % m_tiles tiles take one
+// 32-row block more than the others.  Every tile has 1..288 rows (at most
+// ceil(ceil(n/32) / m_tiles) <= 9 blocks, and the last starts below n), and
 // the tiles cover [lo, lo + n) in order, each row once.
 FE2O3_HD void m_tile(uint32_t lo, uint32_t n, uint32_t m_tiles, uint32_t mt, uint32_t* row0,
                      uint32_t* rows) {
@@ -56,14 +61,14 @@ FE2O3_HD void m_tile(uint32_t lo, uint32_t n, uint32_t m_tiles, uint32_t mt, uin
 }
 
 // Entry of workgroup `block` in the list: expert, first row, row count
-// (1..256) and n-block; false when the workgroup has no entry.
+// (1..288) and n-block; false when the workgroup has no entry.
 FE2O3_HD bool expert_tile_at(const uint32_t* offsets, uint32_t e_begin, uint32_t e_end,
                              uint32_t routes, uint32_t n_blocks, uint32_t block, uint32_t* e_out,
                              uint32_t* row0, uint32_t* rows, uint32_t* nb) {
   uint32_t total = 0, lo, n;
   for (uint32_t e = e_begin; e < e_end; ++e) {
     expert_rows(offsets, e, routes, &lo, &n);
-    total += (n + 255u) / 256u * n_blocks;
+    total += expert_m_tiles(n) * n_blocks;
   }
   const uint32_t chunk = (total + 7u) / 8u;
   const uint32_t slot = block >> 3;
@@ -72,7 +77,7 @@ FE2O3_HD bool expert_tile_at(const uint32_t* offsets, uint32_t e_begin, uint32_t
   if (x >= total) return false;
   for (uint32_t e = e_begin; e < e_end; ++e) {
     expert_rows(offsets, e, routes, &lo, &n);
-    const uint32_t m_tiles = (n + 255u) / 256u;
+    const uint32_t m_tiles = expert_m_tiles(n);
     if (x < m_tiles * n_blocks) {
       *e_out = e;
       *nb = x / m_tiles;
@@ -100,7 +105,7 @@ FE2O3_HD bool expert_tile_lanes(const uint32_t* offsets, uint32_t e_begin, uint3
   for (uint32_t l = 0; l < 64; ++l) {
     lo[l] = n[l] = 0;
     if (l < ne) expert_rows(offsets, e_begin + l, routes, &lo[l], &n[l]);
-    run += (n[l] + 255u) / 256u * n_blocks;
+    run += expert_m_tiles(n[l]) * n_blocks;
     incl[l] = run;
   }
   const uint32_t total = incl[63];
@@ -111,7 +116,7 @@ FE2O3_HD bool expert_tile_lanes(const uint32_t* offsets, uint32_t e_begin, uint3
   if (x >= total) return false;
   uint32_t l = 0;
   for (uint32_t i = 0; i < 64; ++i) l += incl[i] <= x ? 1u : 0u;
-  const uint32_t m_tiles = (n[l] + 255u) / 256u;
+  const uint32_t m_tiles = expert_m_tiles(n[l]);
   const uint32_t xi = x - (incl[l] - m_tiles * n_blocks);
   *e_out = e_begin + l;
   *nb = xi / m_tiles;
@@ -120,10 +125,10 @@ FE2O3_HD bool expert_tile_lanes(const uint32_t* offsets, uint32_t e_begin, uint3
 }
 
 // Grid sizes (workgroups, a multiple of 8) of the gate/up and down launches
-// for experts [e_begin, e_end): routes/256 rounded up plus one partial tile
+// for experts [e_begin, e_end): routes/288 rounded up plus one partial tile
 // per expert bounds the m-tiles of any consistent routing.
 FE2O3_HD uint64_t expert_grid(uint64_t routes, uint32_t n_experts, uint32_t n_blocks) {
-  const uint64_t m_tiles = (routes + 255u) / 256u + n_experts;
+  const uint64_t m_tiles = (routes + kMaxTileRows - 1u) / kMaxTileRows + n_experts;
   return (m_tiles * n_blocks + 7u) / 8u * 8u;
 }
 

@@ -3,14 +3,14 @@
 // Test infrastructure: built and run by tests/test_moe_tiles.py.
 //  1. Arbitrary offsets (random words, values beyond the routes, decreasing
 //     runs): every workgroup of the launch grid gets a tile inside the
-//     workspace rows [0, routes), of 1..256 rows, of an expert in range and
+//     workspace rows [0, routes), of 1..288 rows, of an expert in range and
 //     an n-block in range.
 //  2. Consistent offsets (non-decreasing, total <= routes): over the grid,
 //     every tile of the list is run exactly once.
 //  3. The lane-parallel form the kernels run (expert_tile_lanes) gives every
 //     workgroup the same tile as the serial form.
 //  4. Consistent offsets: for every (expert, n-block) the tiles cover the
-//     expert's rows exactly once, in ceil(n / 256) tiles whose row counts
+//     expert's rows exactly once, in ceil(n / 288) tiles whose row counts
 //     differ by less than 64, each above 96 rows when there are two or more
 //     (no short remainder tile).
 #include <stdint.h>
@@ -79,7 +79,7 @@ int main() {
                                   (unsigned long long)blk);
         ++failures;
       }
-      if (e < b || e >= e_end || nb >= n_blocks || rows == 0 || rows > 256 ||
+      if (e < b || e >= e_end || nb >= n_blocks || rows == 0 || rows > 288 ||
           (uint64_t)row0 + rows > routes) {
         if (failures < 10)
           printf("bounds: iter %d block %llu e %u row0 %u rows %u nb %u routes %u\n", iter,
@@ -91,7 +91,7 @@ int main() {
     }
     if (mode >= 2) {
       uint64_t want = 0;
-      for (uint32_t e = b; e < e_end; ++e) want += (off[e + 1] - off[e] + 255u) / 256u * n_blocks;
+      for (uint32_t e = b; e < e_end; ++e) want += (off[e + 1] - off[e] + 287u) / 288u * n_blocks;
       if (dup || seen.size() != want) {
         if (failures < 10)
           printf("coverage: iter %d got %zu tiles want %llu dup %d\n", iter, seen.size(),
@@ -99,14 +99,14 @@ int main() {
         ++failures;
       }
       for (uint32_t e = b; e < e_end; ++e) {
-        const uint32_t n = off[e + 1] - off[e], m_tiles = (n + 255u) / 256u;
+        const uint32_t n = off[e + 1] - off[e], m_tiles = (n + 287u) / 288u;
         for (uint32_t nb = 0; nb < n_blocks && n > 0; ++nb) {
           auto it = spans.find({e, nb});
           bool ok = it != spans.end() && it->second.size() == m_tiles;
           if (ok) {
             auto v = it->second;
             std::sort(v.begin(), v.end());
-            uint32_t at = off[e], lo_rows = 256, hi_rows = 0;
+            uint32_t at = off[e], lo_rows = 288, hi_rows = 0;
             for (auto& t : v) {
               ok = ok && t.first == at;
               at += t.second;

@@ -270,9 +270,10 @@ def test_moe_ffn_every_short_tile_path(gpu, oracle, hidden, ffn):
     """A routing built by hand (every route admitted, slots in route order
     per expert) whose expert row counts put tiles on every A-tile form: the
     short form (at most 64 rows: 5, 31, 32, 33, 64) and A tiles of 96 (65),
-    128 (128, and the 97-row second tile of 257), 160 (129, 289, 300), 192
-    (321, 384), 224 (200, 418) and 256 rows (256); every token's output
-    against the oracle."""
+    128 (128), 160 (129, both tiles of 289 and of 300, the second of 321),
+    192 (the first of 321, both of 384), 224 (200, both of 418), 256 (256)
+    and 288 rows (257, whose ninth row block accumulates in VGPRs); every
+    token's output against the oracle."""
     kern = _k()
     counts = [5, 31, 32, 33, 64, 65, 128, 129, 200, 256, 257, 300, 289, 321, 384, 418]
     experts = len(counts)
@@ -321,11 +322,12 @@ def test_moe_ffn_small_with_drops(gpu, oracle):
 
 
 def _tail_tokens(offsets, permutation):
-    """Tokens routed to the rows on both sides of every boundary between
-    m-tiles of 256 rows, plus each expert's first and last rows.  An expert
-    of 257-300 rows, which once ran as a full tile and a remainder of at most
-    44 rows, runs as two tiles of 160 and 97-140 rows; the picked rows
-    include the last rows of both."""
+    """Tokens routed to the rows around the 256-row mark and around row 160
+    of every expert over 256 rows, plus each expert's first and last rows.
+    An expert of 257-300 rows, which once ran as a full tile and a remainder
+    of at most 44 rows, runs as one 288-row tile (up to 288 rows) or as two
+    tiles of 160 and 129-140 rows; the picked rows include the last rows of
+    each."""
     rows = set()
     split = 0
     for e in range(len(offsets) - 1):
@@ -341,10 +343,10 @@ def _tail_tokens(offsets, permutation):
 
 
 def test_moe_ffn_short_last_tiles(gpu, oracle):
-    """Experts of 256-300 rows, dealt out as two tiles of 32-row blocks
-    (160 and 97-140 rows): every token routed into the rows around the
-    tile boundary and the 256-row mark is checked, with each expert's first
-    and last rows."""
+    """Experts of about 275 rows (one 288-row tile, or two of 160 and
+    129-140 rows past 288): every token routed into the rows around the
+    256-row mark and the two-tile boundary is checked, with each expert's
+    first and last rows."""
     tokens, hidden, ffn, experts = 1100, 512, 1024, 8
     worst, _ = _ffn_case(gpu, oracle, tokens, hidden, ffn, experts, 0xFFFFFFFF, _tail_tokens)
     assert worst <= 1e-2, worst
