@@ -27,6 +27,7 @@
 // Expert row ranges come from the device-resident offsets, so the whole
 // layer runs without a host round trip: the grouped GEMM grids are sized
 // for the worst case and workgroups beyond the last expert tile exit.
+#include <atomic>
 #include <mutex>
 
 #include "common.hpp"
@@ -413,15 +414,15 @@ __global__ void __launch_bounds__(256, 1) gate_up_kernel(
   });
 }
 
-// One down tile (split K: list entry nb = 2 * n-block + k-half; each half
-// writes its own fp32 partial, yc then yc + routes * hidden, which the
-// combine adds), on the geometry of gate_up_tile.
+// One down tile, on the geometry of gate_up_tile.  K is split in `kparts`
+// (1 or 2) parts: list entry nb = kparts * n-block + part, and part p writes
+// its own fp32 partial at yc + p * routes * hidden, which the combine adds.
 template <int ROW_BYTES, int STAGES, int RPW>
 FE2O3_DEVICE void down_tile(const uint16_t* __restrict__ hc, const uint16_t* __restrict__ wd,
                             uint32_t e, uint32_t row0, uint32_t rows, uint32_t nb,
-                            uint32_t hidden, uint32_t ffn, uint64_t routes,
+                            uint32_t hidden, uint32_t ffn, uint64_t routes, uint32_t kparts,
                             float* __restrict__ yc, uint8_t* smem) {
-  const uint32_t n0 = (nb >> 1) * 256u, kh = nb & 1u, k_half = ffn / 2u;
+  const uint32_t n0 = nb / kparts * 256u, kh = nb % kparts, k_half = ffn / kparts;
   const auto ar = gemm_pipe::dense_rows<ROW_BYTES, 2 * RPW>(
       hc + (uint64_t)row0 * ffn + kh * k_half, ffn, rows, k_half);
   const auto br = gemm_pipe::dense_rows<ROW_BYTES>(
@@ -441,25 +442,26 @@ FE2O3_DEVICE void down_tile(const uint16_t* __restrict__ hc, const uint16_t* __r
   }
 }
 
-// Split K in two: twice as many workgroups, each half as long, fill the last
-// wave of the grid better at this kernel's few hundred tiles.
+// kparts = 2 (split K: twice as many workgroups, each half as long) when
+// that fills the grid's last round of tiles better (down_k_parts).
 __global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict__ hc,
                                                       const uint16_t* __restrict__ wd,
                                                       const uint32_t* __restrict__ offsets,
                                                       uint32_t e_begin, uint32_t e_end,
                                                       uint32_t hidden, uint32_t ffn,
-                                                      uint64_t routes, float* __restrict__ yc) {
+                                                      uint64_t routes, uint32_t kparts,
+                                                      float* __restrict__ yc) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   uint32_t e, row0, rows, nb;
-  if (!expert_tile(offsets, e_begin, e_end, (uint32_t)routes, 2u * (hidden / 256u), &e, &row0,
+  if (!expert_tile(offsets, e_begin, e_end, (uint32_t)routes, kparts * (hidden / 256u), &e, &row0,
                    &rows, &nb))
     return;
   by_tile_rows(rows, [&](auto rpw) {
     constexpr int R = decltype(rpw)::value;
     if constexpr (R == 0)
-      down_tile<64, 4, 32>(hc, wd, e, row0, rows, nb, hidden, ffn, routes, yc, smem);
+      down_tile<64, 4, 32>(hc, wd, e, row0, rows, nb, hidden, ffn, routes, kparts, yc, smem);
     else
-      down_tile<128, 2, R>(hc, wd, e, row0, rows, nb, hidden, ffn, routes, yc, smem);
+      down_tile<128, 2, R>(hc, wd, e, row0, rows, nb, hidden, ffn, routes, kparts, yc, smem);
   });
 }
 
@@ -467,7 +469,8 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
                                                       const uint32_t* __restrict__ inverse,
                                                       const float* __restrict__ weights,
                                                       uint32_t tokens, uint32_t hidden,
-                                                      uint64_t routes, uint16_t* __restrict__ out) {
+                                                      uint64_t routes, uint32_t kparts,
+                                                      uint16_t* __restrict__ out) {
 #pragma clang fp contract(off)
   const uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 4 outputs each
   const uint64_t per_token = hidden / 4u;
@@ -481,11 +484,13 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
     if (slot >= routes) continue;  // DROP, or not a slot
     const float w = weights[route];
     const f32x4_t y0 = *reinterpret_cast<const f32x4_t*>(yc + (uint64_t)slot * hidden + h);
-    const f32x4_t y1 = *reinterpret_cast<const f32x4_t*>(yc + routes * hidden +
-                                                         (uint64_t)slot * hidden + h);
+    f32x4_t y1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (kparts == 2u)
+      y1 = *reinterpret_cast<const f32x4_t*>(yc + routes * hidden + (uint64_t)slot * hidden + h);
 #pragma unroll
     for (int z = 0; z < 4; ++z) {
-      const float y = y0[z] + y1[z];  // the two k-halves of the down projection
+      // the down projection, or the sum of its two k-part partials
+      const float y = kparts == 2u ? y0[z] + y1[z] : y0[z];
       const float wv = w * y;
       acc[z] = acc[z] + wv;
     }
@@ -510,7 +515,7 @@ Workspace carve(void* base, uint32_t tokens, uint32_t hidden, uint32_t ffn) {
   Workspace w;
   uint8_t* p = (uint8_t*)base;
   const uint64_t xb = align256(routes * hidden * 2), hb = align256(routes * ffn * 2),
-                 yb = align256(2 * routes * hidden * 4);  // two k-half partials
+                 yb = align256(2 * routes * hidden * 4);  // up to two k-part partials
   w.xc = (uint16_t*)p;
   w.hc = (uint16_t*)(p + xb);
   w.yc = (float*)(p + xb + hb);
@@ -823,6 +828,42 @@ uint64_t fe2o3_moe_ffn_workspace_bytes(uint32_t tokens, uint32_t hidden, uint32_
 
 namespace {
 
+// Compute units of the current device, cached per device (256 on MI355X;
+// 256 also if the query fails: the value only steers down_k_parts).
+uint32_t device_cus() {
+  static constexpr int kMaxDevices = 64;
+  static std::atomic<uint32_t> cus[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256u;
+  uint32_t c = cus[dev].load(std::memory_order_relaxed);
+  if (c == 0u) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        v <= 0)
+      v = 256;
+    c = (uint32_t)v;
+    cus[dev].store(c, std::memory_order_relaxed);
+  }
+  return c;
+}
+
+// K parts of the down GEMM: 2 (two half-K tiles per output tile, two fp32
+// partials) only when that fills the grid's rounds of `cus` tiles better
+// than whole-K tiles, each of which counts two half-K rounds.  The m-tile
+// count is that of an even routing (experts x expert_m_tiles(routes /
+// experts)); routing is device data, and the choice only affects speed.
+// Measured in one process (whole K against split K; balanced routings of n
+// rows per expert, 8 experts, hidden 4096, FFN 14336): n = 100 +21%,
+// 270 +18%, 600 +4% (split kept), n = 300 -1.6%, 1040 -4.1%, 1100 -4.1%,
+// 1150 -3.4%, config 5 -3.9% (whole K chosen).
+uint32_t down_k_parts(uint64_t routes, uint32_t experts, uint32_t hidden, uint32_t cus) {
+  const uint64_t per = (routes + experts - 1u) / experts;
+  const uint64_t m = (uint64_t)experts * expert_m_tiles((uint32_t)per);
+  const uint64_t t1 = m * (hidden / 256u);  // whole-K tiles
+  const uint64_t rounds1 = (t1 + cus - 1u) / cus, rounds2 = (2u * t1 + cus - 1u) / cus;
+  return 2u * rounds1 <= rounds2 ? 1u : 2u;
+}
+
 // The expert FFN behind both C-ABI entry points.  `split_streams` runs the
 // second half of the experts on the per-device side stream (created on
 // first use); without it every kernel runs on the caller's stream and the
@@ -866,9 +907,10 @@ int32_t ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate, uint
   hipStream_t s = (hipStream_t)stream;
   // the most m-tiles any routing yields for experts [b, e): routes/288
   // rounded up, plus one partial tile per expert
+  const uint32_t kparts = down_k_parts(routes, experts, hidden, device_cus());
   auto grids = [&](uint32_t n_experts, uint64_t* gu, uint64_t* dn) {
     *gu = expert_grid(routes, n_experts, ffn / 128u);
-    *dn = expert_grid(routes, n_experts, 2u * (hidden / 256u));
+    *dn = expert_grid(routes, n_experts, kparts * (hidden / 256u));
     return *gu <= 0x7fffffffu && *dn <= 0x7fffffffu;
   };
   auto experts_ffn = [&](uint32_t b, uint32_t e, hipStream_t st) {
@@ -877,7 +919,7 @@ int32_t ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate, uint
     gate_up_kernel<<<(unsigned)gu, 256, kSmem, st>>>(ws.xc, w_gate, w_up, expert_offsets, b, e,
                                                      hidden, ffn, (uint32_t)routes, ws.hc);
     down_kernel<<<(unsigned)dn, 256, kSmem, st>>>(ws.hc, w_down, expert_offsets, b, e, hidden,
-                                                  ffn, routes, ws.yc);
+                                                  ffn, routes, kparts, ws.yc);
   };
   uint64_t gu_all, dn_all;
   if (!grids(experts, &gu_all, &dn_all)) return FE2O3_ERR_SHAPE;
@@ -903,7 +945,8 @@ int32_t ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate, uint
   }
   const uint64_t threads = (uint64_t)tokens * (hidden / 4u);
   combine_kernel<<<(unsigned)((threads + 255u) / 256u), 256, 0, s>>>(ws.yc, inverse, route_weights,
-                                                                    tokens, hidden, routes, out);
+                                                                    tokens, hidden, routes, kparts,
+                                                                    out);
   return fe2o3_host::after_launch();
 }
 

@@ -321,6 +321,18 @@ def test_moe_ffn_small_with_drops(gpu, oracle):
     assert worst <= 1e-2, worst
 
 
+def test_moe_ffn_whole_k_down(gpu, oracle):
+    """1200 tokens, hidden 4096, 8 experts: an even routing would give 16
+    m-tiles of 16 n-blocks, exactly one round of 256 down tiles over K
+    whole, which the entry point then prefers to two rounds of half-K tiles
+    (the smaller FFN tests run split K); the first and last 8 slots of every
+    expert against the oracle."""
+    tokens, hidden, ffn, experts = 1200, 4096, 512, 8
+    worst, _ = _ffn_case(gpu, oracle, tokens, hidden, ffn, experts, 0xFFFFFFFF,
+                         _per_expert_tokens(8))
+    assert worst <= 1e-2, worst
+
+
 def _tail_tokens(offsets, permutation):
     """Tokens routed to the rows around the 256-row mark and around row 160
     of every expert over 256 rows, plus each expert's first and last rows.
