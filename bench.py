@@ -425,9 +425,11 @@ def sec_gemm_f32(ctx, stream, args):
 
 def sec_gemm_general(ctx, stream, args):
     """tiled_gemm_general_v1 at 2048^3 with padded strides and alpha/beta
-    (C = 1.5 A B + 0.5 C, lda = ldb = ldc = 2056): the pipelined 256x256
-    tile (the shape qualifies), and both staged schedules on the same data
-    with A two bytes past a 16-byte boundary (which the tile does not take).
+    (C = 1.5 A B + 0.5 C, lda = ldb = ldc = 2056): the pipelined tile (the
+    shape qualifies; its 64 tiles of 256x256 would leave most CUs idle, so
+    it runs 256 tiles of 128x128), and both staged schedules on the same
+    data with A two bytes past a 16-byte boundary (which the tiles do not
+    take).
     Each launch reads and rewrites C (C converges to 3 A B); it is restored
     before the parity call."""
     from fe2o3_amd import _lib, kernels
@@ -465,7 +467,8 @@ def sec_gemm_general(ctx, stream, args):
         tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         res[name] = {"ms": round(ms, 5), "value": round(tf, 2),
                      "frac": round(tf / PEAK["bf16"], 4)}
-    res["kernel"] = ("gemm_general_pipe_kernel (pipelined); gemm_general_kernel<false> / <true> "
+    res["kernel"] = ("gemm_general_pipe128_kernel<3> (pipelined, 128x128 tiles at this size); "
+                     "gemm_general_kernel<false> / <true> "
                      "(staged schedules)")
     res["ms"] = res["pipelined"]["ms"]
     res["value"] = res["pipelined"]["value"]

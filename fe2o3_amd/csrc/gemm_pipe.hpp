@@ -159,19 +159,20 @@ FE2O3_DEVICE Rows<128, 8, true> kn_rows(const uint16_t* base, uint32_t ld, uint3
   return t;
 }
 
-// Stage p's A tile (A_ROWS rows) at a(p); its B tile at b_region + b(p).
-// Fragment reads add a(p) or b(p) (plus the row-block offset) as ds_read
-// immediates; the B region's base is folded into the per-lane B offsets, so
-// every immediate stays below 64 KiB.
-template <int ROW_BYTES, int STAGES, int A_ROWS = 256>
+// Stage p's A tile (A_ROWS rows) at a(p); its B tile (B_TILE bytes: 256
+// rows, or a policy's smaller tile) at b_region + b(p).  Fragment reads add
+// a(p) or b(p) (plus the row-block offset) as ds_read immediates; the B
+// region's base is folded into the per-lane B offsets, so every immediate
+// stays below 64 KiB.
+template <int ROW_BYTES, int STAGES, int A_ROWS = 256, int B_TILE = 256 * ROW_BYTES>
 struct Lay {
   using G = Geo<ROW_BYTES>;
   static constexpr uint32_t a_tile = (uint32_t)A_ROWS * ROW_BYTES;
   static constexpr uint32_t b_region = (uint32_t)STAGES * a_tile;
   static constexpr uint32_t a(int p) { return (uint32_t)p * a_tile; }
-  static constexpr uint32_t b(int p) { return (uint32_t)p * G::kTileBytes; }
+  static constexpr uint32_t b(int p) { return (uint32_t)p * (uint32_t)B_TILE; }
   // largest row-block offset: 16-row block 7 (bf16) > 32-row block 3 (fp8)
-  static_assert((STAGES - 1) * G::kTileBytes + 7 * 16 * ROW_BYTES < 65536,
+  static_assert((STAGES - 1) * B_TILE + 7 * 16 * ROW_BYTES < 65536,
                 "fragment read offsets fit the ds_read immediate");
 };
 
@@ -184,6 +185,37 @@ constexpr int kWaitVm0Lgkm0 = waitcnt_imm(0, 0);
 constexpr int kWaitVm0 = waitcnt_imm(0, 15);
 constexpr int kWaitLgkm0 = waitcnt_imm(63, 0);
 
+// B stored [k][n] for 128-column tiles (Bf16MmaKN64): one stage is 64 k-rows
+// of 256 bytes.  Load j of wave w moves k-rows 4(4j + w) .. +3; lane l fills
+// LDS chunk position l % 16 of k-row 4(4j + w) + l / 16 with global chunk
+// (l % 16) ^ kn_swz16(row).  Columns at or past valid_cols read the last
+// valid chunk (their products reach only outputs that are never stored).
+// The caller guarantees ((k16 - 1) * ld + 128) * 2 < 2^31 and 16-byte
+// aligned rows.
+FE2O3_DEVICE uint32_t kn_swz16(uint32_t krow) {
+  // twice a 3-bit row code: the 8 rows a half wave of one transposing read
+  // touches (8g + q, g < 2, q < 4) get 8 different codes, so its 32 lanes'
+  // 8-byte pieces fill 16 distinct 16-byte positions of the 256-byte rows
+  return 2u * ((krow & 3u) | (((krow >> 3) & 1u) << 2));
+}
+FE2O3_DEVICE Rows<128, 4, true> kn_rows128(const uint16_t* base, uint32_t ld, uint32_t valid_cols,
+                                           uint32_t k16) {
+  Rows<128, 4, true> t;
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  const uint32_t last_chunk = (valid_cols - 1u) / 8u;
+  t.bytes = ((k16 - 1u) * ld + valid_cols) * 2u;  // reads past C's columns return 0
+  t.kmul = ld;  // a stage of 64 k (128 bytes along a k row) is 64 rows of ld elements
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t krow = 4u * (4u * j + w) + lane / 16u;
+    uint32_t chunk = (lane % 16u) ^ kn_swz16(krow);
+    if (chunk > last_chunk) chunk = last_chunk;
+    t.base[j] = base;
+    t.voff[j] = (krow * ld + chunk * 8u) * 2u;
+  }
+  return t;
+}
+
 // ---- instruction policies --------------------------------------------------------------------
 //
 // A policy fixes, per substep (a k slice of one stage): kMfma MFMAs, issued
@@ -191,9 +223,9 @@ constexpr int kWaitLgkm0 = waitcnt_imm(63, 0);
 // of the next substep, in the order the MFMAs first use them; and how the
 // first substep of the K loop writes (rather than adds to) the accumulators.
 
-template <int RB>
-struct Acc16T {  // RB row blocks of 16 x 8 column blocks of 16
-  f32x4_t v[RB][8];
+template <int RB, int CB = 8>
+struct Acc16T {  // RB row blocks of 16 x CB column blocks of 16
+  f32x4_t v[RB][CB];
 };
 using Acc16 = Acc16T<8>;
 struct Acc32 {
@@ -234,6 +266,7 @@ struct Bf16Mma {
   static constexpr int kSubsteps = ROW_BYTES / 64, kMfma = kRB * 8, kTn = 8, kReads = kRB + 8;
   static constexpr int kARows = 2 * RPW;
   static constexpr bool kBKN = false;
+  static constexpr int kBTileBytes = G::kTileBytes;
   struct Frags {
     bf16x8_t a[kRB], b[8];
   };
@@ -321,6 +354,7 @@ struct Bf16MmaKN {
   static constexpr int kReads = A::kReads;
   static constexpr int kARows = A::kARows;
   static constexpr bool kBKN = true;
+  static constexpr int kBTileBytes = A::kBTileBytes;
   using Frags = A::Frags;
   struct Lanes {
     uint32_t a[kSubsteps][4], b[kSubsteps][8];
@@ -377,6 +411,84 @@ struct Bf16MmaKN {
   static FE2O3_DEVICE void finish(Acc& acc) { A::finish(acc); }
 };
 
+// bf16 with B stored [k][n], 128 x 128 tiles: for GEMMs whose 256 x 256
+// tiles would leave most CUs idle (a quarter of the output per tile, four
+// times the tiles).  Each wave owns 64 rows by 64 columns (4 x 4 MFMA
+// tiles, accumulators in 64 AGPRs); the A tile holds 128 rows (the A side
+// of Bf16Mma<128, 64>), the B tile 64 k-rows of 128 columns (kn_rows128).
+// B fragments are read as in Bf16MmaKN, from 256-byte rows (the second read
+// of a fragment 4 k-rows, 1024 bytes, on).
+struct Bf16MmaKN64 {
+  using A = Bf16Mma<128, 64>;
+  static constexpr int kRB = 4, kTn = 4, kSubsteps = A::kSubsteps, kMfma = 16, kReads = 8;
+  static constexpr int kARows = A::kARows;  // 128
+  static constexpr bool kBKN = true;
+  static constexpr int kBTileBytes = 64 * 256;
+  using Acc = Acc16T<4, 4>;
+  struct Frags {
+    bf16x8_t a[4], b[4];
+  };
+  struct Lanes {
+    uint32_t a[kSubsteps][4], b[kSubsteps][4];
+  };
+  static FE2O3_DEVICE Lanes lanes(uint32_t b_region) {
+    const typename A::Lanes la = A::lanes(b_region);
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t wn = wave & 1u, g = lane >> 4, i = lane & 15u;
+    Lanes l;
+#pragma unroll
+    for (int s = 0; s < kSubsteps; ++s) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) l.a[s][p] = la.a[s][p];
+      const uint32_t krow = 32u * s + 8u * g + (i >> 2);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t chunk = wn * 8u + 2u * j + ((i & 3u) >> 1);
+        l.b[s][j] = b_region + krow * 256u + ((chunk ^ kn_swz16(krow)) << 4) + (i & 1u) * 8u;
+      }
+    }
+    return l;
+  }
+  // read unit R of substep S: a0, b0 .. b3, a1 .. a3 (the order and the
+  // inline-asm transposing reads of Bf16MmaKN, for the same reason)
+  template <uint32_t A_TILE, uint32_t B_TILE, int S, int R>
+  static FE2O3_DEVICE void read(const uint8_t* smem, const Lanes& l, Frags& f) {
+    static_assert(R >= 0 && R < kReads, "read unit");
+    if constexpr (R == 0) {
+      f.a[0] = *reinterpret_cast<const bf16x8_t*>(smem + l.a[S][0] + A_TILE);
+    } else if constexpr (R <= 4) {
+      constexpr int j = R - 1;
+      const lds_bf16x4_t* p = (const lds_bf16x4_t*)(smem + l.b[S][j]);
+      bf16x4_t lo, hi;
+      asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
+                   : "=v"(lo), "=v"(hi)
+                   : "v"(p), "i"(B_TILE), "i"(B_TILE + 1024u));
+      f.b[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
+      constexpr int ii = R - 4;
+      f.a[ii] = *reinterpret_cast<const bf16x8_t*>(smem + l.a[S][ii & 3] +
+                                                   (A_TILE + ii * 16u * 128u));
+    }
+  }
+  template <bool FIRST, int I>
+  static FE2O3_DEVICE void mfma(Acc& acc, const Frags& f) {
+    constexpr int i = I / kTn, j = I % kTn;
+    if constexpr (FIRST)
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0"
+                   : "=a"(acc.v[i][j]) : "v"(f.b[j]), "v"(f.a[i]));
+    else
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                   : "+a"(acc.v[i][j]) : "v"(f.b[j]), "v"(f.a[i]));
+  }
+  static FE2O3_DEVICE void finish(Acc& acc) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc.v[i][j]));
+  }
+};
+
 // OCP fp8 e4m3: v_mfma_scale_f32_32x32x64_f8f6f4 with both formats e4m3
 // (cbsz = blgp = 0) and unit E8M0 block scales (127 = 2^0), 64 k per
 // substep.  Lane l holds k 32(l/32) .. +31 (chunks 4s + 2(l/32) and the next)
@@ -390,6 +502,7 @@ struct Fp8Mma {
   static constexpr int kSubsteps = ROW_BYTES / 64, kMfma = 16, kTn = 4, kReads = 8;
   static constexpr int kARows = 256;
   static constexpr bool kBKN = false;
+  static constexpr int kBTileBytes = G::kTileBytes;
   struct Frags {
     i32x8_t a[4], b[4];
   };
@@ -503,7 +616,7 @@ struct CopyOrder {
 template <int ROW_BYTES, int STAGES, int A_ROWS, int C, int NA, int NB, bool BKN>
 FE2O3_DEVICE void copy_one(const Rows<ROW_BYTES, NA>& ar, const Rows<ROW_BYTES, NB, BKN>& br,
                            uint32_t kbytes, uint8_t* smem, uint32_t wave, int buf) {
-  using L = Lay<ROW_BYTES, STAGES, A_ROWS>;
+  using L = Lay<ROW_BYTES, STAGES, A_ROWS, NB * 4096>;  // NB 1-KiB loads per wave
   using O = CopyOrder<NA, NB>;
   constexpr int j = O::slot(C);
   if constexpr (O::is_a(C))
@@ -520,9 +633,9 @@ FE2O3_DEVICE void copy_one(const Rows<ROW_BYTES, NA>& ar, const Rows<ROW_BYTES, 
 template <class M, int ROW_BYTES, int STAGES, int P, int S_, bool FIRST>
 struct Substep {
   using G = Geo<ROW_BYTES>;
-  using L = Lay<ROW_BYTES, STAGES, M::kARows>;
+  using L = Lay<ROW_BYTES, STAGES, M::kARows, M::kBTileBytes>;
   static constexpr int S = M::kSubsteps, MF = M::kMfma;
-  static constexpr int NA = G::insts(M::kARows), NB = G::kInstPerWave;
+  static constexpr int NA = G::insts(M::kARows), NB = M::kBTileBytes / 4096;
   using RA_ = Rows<ROW_BYTES, NA>;
   using RB_ = Rows<ROW_BYTES, NB, M::kBKN>;
   static constexpr int NC = NA + NB;              // copies per stage and wave
@@ -616,10 +729,11 @@ FE2O3_DEVICE void mainloop(const typename Substep<M, ROW_BYTES, STAGES, 0, 0, fa
                            const typename Substep<M, ROW_BYTES, STAGES, 0, 0, false>::RB_& br,
                            uint32_t k16, uint8_t* smem, typename M::Acc& acc) {
   using G = Geo<ROW_BYTES>;
-  using L = Lay<ROW_BYTES, STAGES, M::kARows>;
+  using L = Lay<ROW_BYTES, STAGES, M::kARows, M::kBTileBytes>;
   using Sub = Substep<M, ROW_BYTES, STAGES, 0, 0, false>;
-  static_assert((ROW_BYTES == 128 && STAGES == 2) || (ROW_BYTES == 64 && STAGES == 4),
-                "two 64-k or four 32-k stages");
+  static_assert((ROW_BYTES == 128 && (STAGES == 2 || STAGES == 3)) ||
+                    (ROW_BYTES == 64 && STAGES == 4),
+                "two or three 64-k stages, or four 32-k stages");
   static_assert(M::kSubsteps % 2 == 0 || STAGES % 2 == 0,
                 "fragment buffers alternate across the unrolled steps");
   constexpr int NA = Sub::NA, NB = Sub::NB;
@@ -652,7 +766,13 @@ FE2O3_DEVICE void mainloop(const typename Substep<M, ROW_BYTES, STAGES, 0, 0, fa
   Spread<M::kReads, 0, 1>::template at<0>([&](auto n) {
     M::template read<L::a(0), L::b(0), 0, decltype(n)::value>(smem, ln, f[0]);
   });
-  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  // every first fragment landed.  The wait is inline asm between scheduling
+  // barriers: a policy's inline-asm reads are invisible to the compiler's
+  // wait tracking, which may otherwise move reads past a builtin wait or
+  // drop the wait as redundant (seen with three 128 x 128 stages).
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
   int kt = 0;
   if (steps >= STAGES) {
     Steps<M, ROW_BYTES, STAGES, 0, false, true>::run(ar, br, 0, steps, smem, wave, ln, f, acc);
@@ -681,10 +801,11 @@ FE2O3_DEVICE uint32_t lane_id() {
 FE2O3_DEVICE uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // Acc16T (i, j, e): tile row wm*RPW + 16i + lane%16, tile column
-// wn*128 + 16j + 4(lane/16) + e.
+// wn*CPW + 16j + 4(lane/16) + e (CPW = 128, or 64 for Bf16MmaKN64).
 template <int RPW = 128>
 FE2O3_DEVICE uint32_t acc16_row0() { return (wave_id() >> 1) * RPW + (lane_id() & 15u); }
-FE2O3_DEVICE uint32_t acc16_col0() { return (wave_id() & 1u) * 128u + 4u * (lane_id() >> 4); }
+template <int CPW = 128>  // columns per wave
+FE2O3_DEVICE uint32_t acc16_col0() { return (wave_id() & 1u) * CPW + 4u * (lane_id() >> 4); }
 
 // Acc32 (i, j, e): tile row wm*128 + 32i + lane%32, tile column
 // wn*128 + 32j + 8(e/4) + 4(lane/32) + e%4.

@@ -352,6 +352,60 @@ namespace {
 constexpr int kGpRowBytes = 128, kGpStages = 2;
 constexpr int kGpSmem = kGpStages * 2 * gemm_pipe::Geo<kGpRowBytes>::kTileBytes;  // 128 KiB
 
+// C = alpha * acc + beta * C over one tile of TM x TN outputs (rows x cols
+// valid), accumulators Acc16T<RB, CB> of waves holding RPW rows by CPW
+// columns.  Per 16-row block: every C load of the lane first (one wait),
+// then the products and stores.  Whole-width tiles of a 16-byte aligned C
+// with ldc % 4 == 0 move 4 columns per access; otherwise element by element,
+// the loads of columns past n clamped to the last valid one (not stored).
+template <int TN, int RPW, int CPW, class Acc>
+FE2O3_DEVICE void general_epilogue(const Acc& acc, float* c_tile, uint32_t rows, uint32_t cols,
+                                   uint32_t ldc, bool c_aligned, float alpha, float beta) {
+#pragma clang fp contract(off)
+  constexpr int RB = RPW / 16, CB = CPW / 16;
+  const uint32_t row0 = gemm_pipe::acc16_row0<RPW>(), col0 = gemm_pipe::acc16_col0<CPW>();
+  const bool vec = cols == (uint32_t)TN && ldc % 4u == 0u && c_aligned;
+#pragma unroll
+  for (int i = 0; i < RB; ++i) {
+    const uint32_t r = row0 + 16u * i;
+    if (r >= rows) continue;
+    float* out = c_tile + (uint64_t)r * ldc;
+    if (vec) {
+      f32x4_t cv[CB];
+#pragma unroll
+      for (int j = 0; j < CB; ++j) cv[j] = *reinterpret_cast<const f32x4_t*>(out + col0 + 16u * j);
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        f32x4_t y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float product = alpha * acc.v[i][j][e];
+          const float initial = beta * cv[j][e];
+          y[e] = product + initial;
+        }
+        *reinterpret_cast<f32x4_t*>(out + col0 + 16u * j) = y;
+      }
+    } else {
+      float cv[CB][4];
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cv[j][e] = out[min(col0 + 16u * j + e, cols - 1u)];
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t col = col0 + 16u * j + e;
+          if (col < cols) {
+            const float product = alpha * acc.v[i][j][e];
+            const float initial = beta * cv[j][e];
+            out[col] = product + initial;
+          }
+        }
+    }
+  }
+}
+
 __global__ void __launch_bounds__(256, 1) gemm_general_pipe_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, float* __restrict__ c,
     uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha,
@@ -365,60 +419,51 @@ __global__ void __launch_bounds__(256, 1) gemm_general_pipe_kernel(
   const auto br = gemm_pipe::kn_rows(b + (uint64_t)tn * 256u, ldb, cols, k);
   gemm_pipe::Acc16 acc;
   gemm_pipe::mainloop<gemm_pipe::Bf16MmaKN, kGpRowBytes, kGpStages>(ar, br, k, smem, acc);
-  // Per 16-row block: every C load of the lane first (one wait), then the
-  // products and stores.  Whole 256-column tiles of a 16-byte aligned C with
-  // ldc % 4 == 0 move 4 columns per access; otherwise element by element,
-  // the loads of columns past n clamped to the last valid one (not stored).
-  {
-#pragma clang fp contract(off)
-    const uint32_t row0 = gemm_pipe::acc16_row0(), col0 = gemm_pipe::acc16_col0();
-    float* c_tile = c + (uint64_t)tm * 256u * ldc + (uint64_t)tn * 256u;
-    const bool vec = cols == 256u && ldc % 4u == 0u && ((uintptr_t)c & 15u) == 0u;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t r = row0 + 16u * i;
-      if (r >= rows) continue;
-      float* out = c_tile + (uint64_t)r * ldc;
-      if (vec) {
-        f32x4_t cv[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) cv[j] = *reinterpret_cast<const f32x4_t*>(out + col0 + 16u * j);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          f32x4_t y;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float product = alpha * acc.v[i][j][e];
-            const float initial = beta * cv[j][e];
-            y[e] = product + initial;
-          }
-          *reinterpret_cast<f32x4_t*>(out + col0 + 16u * j) = y;
-        }
-      } else {
-        float cv[8][4];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) cv[j][e] = out[min(col0 + 16u * j + e, cols - 1u)];
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t col = col0 + 16u * j + e;
-            if (col < cols) {
-              const float product = alpha * acc.v[i][j][e];
-              const float initial = beta * cv[j][e];
-              out[col] = product + initial;
-            }
-          }
-      }
-    }
-  }
+  general_epilogue<256, 128, 128>(acc, c + (uint64_t)tm * 256u * ldc + (uint64_t)tn * 256u, rows,
+                                  cols, ldc, ((uintptr_t)c & 15u) == 0u, alpha, beta);
+}
+
+// The same GEMM on 128 x 128 tiles (Bf16MmaKN64), for problems whose
+// 256 x 256 tiles would not fill the CUs: two stages (64 KiB of LDS, two
+// workgroups per CU) when there are more tiles than CUs, else three (96 KiB,
+// one workgroup per CU, copies two stages ahead: +24% at 2048^3, -5% at
+// 4096 x 2048 x 2048 where two workgroups per CU pay more).  The k order of
+// every output's MFMAs is that of the 256 x 256 tile, so C is bit-identical
+// to it.
+template <int STAGES>
+constexpr int kGp64Smem =
+    STAGES * (128 * kGpRowBytes + gemm_pipe::Bf16MmaKN64::kBTileBytes);
+template <int STAGES>
+__global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_general_pipe128_kernel(
+    const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, float* __restrict__ c,
+    uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha,
+    float beta) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const uint32_t tiles_m = (m + 127u) / 128u, tiles_n = (n + 127u) / 128u;
+  uint32_t tm, tn;
+  gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  const uint32_t rows = min(128u, m - tm * 128u), cols = min(128u, n - tn * 128u);
+  const auto ar =
+      gemm_pipe::dense_rows<kGpRowBytes, 128>(a + (uint64_t)tm * 128u * lda, lda, rows, k);
+  const auto br = gemm_pipe::kn_rows128(b + (uint64_t)tn * 128u, ldb, cols, k);
+  gemm_pipe::Bf16MmaKN64::Acc acc;
+  gemm_pipe::mainloop<gemm_pipe::Bf16MmaKN64, kGpRowBytes, STAGES>(ar, br, k, smem, acc);
+  general_epilogue<128, 64, 64>(acc, c + (uint64_t)tm * 128u * ldc + (uint64_t)tn * 128u, rows,
+                                cols, ldc, ((uintptr_t)c & 15u) == 0u, alpha, beta);
 }
 
 const fe2o3_host::KernelRegistrar kRegisteredPipe[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe_kernel", (const void*)gemm_general_pipe_kernel, 256, kGpSmem}),
-    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe_kernel", (const void*)gemm_general_pipe_kernel, 256, kGpSmem})};
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe128_kernel<2>", (const void*)gemm_general_pipe128_kernel<2>, 256, kGp64Smem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe128_kernel<3>", (const void*)gemm_general_pipe128_kernel<3>, 256, kGp64Smem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe_kernel", (const void*)gemm_general_pipe_kernel, 256, kGpSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<2>", (const void*)gemm_general_pipe128_kernel<2>, 256, kGp64Smem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<3>", (const void*)gemm_general_pipe128_kernel<3>, 256, kGp64Smem<3>})};
+
+// At most this many 256 x 256 tiles (half of MI355X's 256 CUs), the GEMM
+// runs on 128 x 128 tiles instead, three-stage up to 2 kSmallGrid of them
+// (one per CU).
+constexpr uint64_t kSmallGrid = 128;
 
 // Host: whether the pipelined tile takes this general GEMM: whole 64-k
 // stages, 16-byte aligned rows of A and B, and both operands' panels within
@@ -449,8 +494,26 @@ int32_t general_gemm(const uint16_t* a, uint64_t a_len, const uint16_t* b, uint6
     static const int32_t lds_rc =
         fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe_kernel}, kGpSmem);
     if (lds_rc != FE2O3_OK) return lds_rc;
+    static const int32_t lds128_rc =
+        fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe128_kernel<2>}, kGp64Smem<2>);
+    static const int32_t lds128s3_rc =
+        fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe128_kernel<3>}, kGp64Smem<3>);
+    if (lds128_rc != FE2O3_OK) return lds128_rc;
+    if (lds128s3_rc != FE2O3_OK) return lds128s3_rc;
     const uint64_t tiles = (uint64_t)((m + 255) / 256) * ((n + 255) / 256);
     if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
+    if (tiles <= kSmallGrid) {  // 256 x 256 tiles would leave most CUs idle
+      const uint64_t tiles128 = (uint64_t)((m + 127) / 128) * ((n + 127) / 128);
+      if (tiles128 > kSmallGrid * 2)
+        gemm_general_pipe128_kernel<2><<<(unsigned)tiles128, 256, kGp64Smem<2>,
+                                         (hipStream_t)stream>>>(a, b, c, m, n, k, lda, ldb, ldc,
+                                                                alpha, beta);
+      else
+        gemm_general_pipe128_kernel<3><<<(unsigned)tiles128, 256, kGp64Smem<3>,
+                                         (hipStream_t)stream>>>(a, b, c, m, n, k, lda, ldb, ldc,
+                                                                alpha, beta);
+      return fe2o3_host::after_launch();
+    }
     gemm_general_pipe_kernel<<<(unsigned)tiles, 256, kGpSmem, (hipStream_t)stream>>>(
         a, b, c, m, n, k, lda, ldb, ldc, alpha, beta);
     return fe2o3_host::after_launch();

@@ -156,13 +156,15 @@ def test_general_random_within_tolerance(gpu, oracle, dims, strides, alpha, beta
     ((1000, 264, 1024), (1032, 264, 270), -0.75, 2.0),
     ((17, 1000, 128), (136, 1003, 1003), 1.0, 1.0),
     ((64, 300, 64), (64, 304, 301), 0.5, -1.0),  # last column chunk reads B's padding
+    ((3000, 2900, 128), (136, 2904, 2910), 1.25, -0.5),  # 144 tiles of 256: the 256x256 tile
 ])
 def test_general_pipelined_tile_matches_staged_kernel(gpu, oracle, dims, strides, alpha, beta):
-    """Shapes the pipelined 256x256 tile takes (whole 64-k stages, 16-byte
-    aligned A and B rows) against the same data through the 64x64 staged
-    kernel (A moved to a 2-byte offset, which the tile does not take): the
-    same bits, also with NaN and infinity in A's and B's stride padding; C's
-    padding untouched; rel-err <= 1e-5 against the tiled CPU schedule."""
+    """Shapes the pipelined tiles take (whole 64-k stages, 16-byte aligned A
+    and B rows; 128x128 tiles up to 128 tiles of 256x256, the 256x256 tile
+    beyond) against the same data through the 64x64 staged kernel (A moved
+    to a 2-byte offset, which the tiles do not take): the same bits, also
+    with NaN and infinity in A's and B's stride padding; C's padding
+    untouched; rel-err <= 1e-5 against the tiled CPU schedule."""
     m, n, k = dims
     lda, ldb, ldc = strides
     rng = np.random.default_rng(m + n + k)

@@ -1,8 +1,9 @@
 """The pipelined general GEMM issues its transposing LDS reads as inline asm
-(gemm_pipe::Bf16MmaKN::read), which the compiler does not see as loads: it
+(gemm_pipe::Bf16MmaKN::read, Bf16MmaKN64::read), which the compiler does not see as loads: it
 relies on the compiler's own s_waitcnt lgkmcnt for the A read issued before
 them.  This CPU test compiles gemm_small.hip for gfx950 to assembly and
-replays gemm_general_pipe_kernel's instruction stream with in-order LDS
+replays the instruction streams of gemm_general_pipe_kernel (256x256
+tiles) and gemm_general_pipe128_kernel<2>, <3> (128x128) with in-order LDS
 completion: no instruction may read a VGPR that an LDS read has not yet
 delivered (no s_waitcnt lgkmcnt covering it).  Scalar loads share the
 counter; the replay ignores them, which only keeps more LDS reads pending
@@ -67,14 +68,17 @@ def test_general_pipe_kernel_lds_reads_are_waited_for(tmp_path):
                     os.path.join(CSRC, "gemm_small.hip"), "-o", str(out)],
                    check=True, capture_output=True)
     text = out.read_text()
-    m = re.search(r"^(_Z\S*gemm_general_pipe_kernel\S*):\s*;.*?\n(.*?)\n\s*s_endpgm", text,
-                  re.S | re.M)
-    assert m, "kernel not found in the assembly"
-    body = [l.split(";")[0].strip() for l in m.group(2).split("\n")]
-    assert sum("ds_read_b64_tr_b16" in l for l in body) >= 64
-    assert _violations(body) == 0
-    # the check fires when the waits are gone
-    stripped = [re.sub(r"lgkmcnt\(\d+\)", "", l) if l.startswith("s_waitcnt") else l
-                for l in body]
-    stripped = [l for l in stripped if l.strip() != "s_waitcnt"]
-    assert _violations(stripped) > 100
+    found = 0
+    for m in re.finditer(r"^(_Z\S*gemm_general_pipe\S*kernel\S*):\s*;.*?\n(.*?)\n\s*s_endpgm",
+                         text, re.S | re.M):
+        name = m.group(1)
+        found += 1
+        body = [l.split(";")[0].strip() for l in m.group(2).split("\n")]
+        assert sum("ds_read_b64_tr_b16" in l for l in body) >= 64, name
+        assert _violations(body) == 0, name
+        # the check fires when the waits are gone
+        stripped = [re.sub(r"lgkmcnt\(\d+\)", "", l) if l.startswith("s_waitcnt") else l
+                    for l in body]
+        stripped = [l for l in stripped if l.strip() != "s_waitcnt"]
+        assert _violations(stripped) > 50, name
+    assert found == 3  # 256x256, and 128x128 on two and three stages
