@@ -107,6 +107,37 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_nt_256_kernel(const uint16_t
     gemm_pipe::store_bf16(acc, c_tile, n);
 }
 
+// The small-grid form: 128 x 128 tiles (Bf16Mma64) for GEMMs whose 256 x 256
+// tiles would leave most CUs idle; three 64-k stages (96 KiB) while the
+// tiles fit one per CU, else two (64 KiB, two workgroups per CU).  Every
+// output gets the MFMAs of the 256 x 256 tile in the same k order, so C is
+// bit-identical to it.  WHOLE: M and N multiples of 128 and C 16-byte
+// aligned; otherwise rows past M (N) repeat the last valid row and only
+// valid elements are stored.
+template <int STAGES>
+constexpr int kSmallSmem = STAGES * (128 * kRowBytes + gemm_pipe::Bf16Mma64::kBTileBytes);
+template <int STAGES, bool WHOLE>
+__global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_bf16_nt_128_kernel(
+    const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint16_t* __restrict__ c,
+    uint32_t m, uint32_t n, uint32_t k) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const uint32_t tiles_m = (m + 127u) / 128u, tiles_n = (n + 127u) / 128u;
+  uint32_t tm, tn;
+  gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  const uint32_t rows_a = WHOLE ? 128u : min(128u, m - tm * 128u);
+  const uint32_t rows_b = WHOLE ? 128u : min(128u, n - tn * 128u);
+  const auto ar = gemm_pipe::dense_rows<kRowBytes, 128>(a + (uint64_t)tm * 128 * k, k, rows_a, k);
+  const auto br = gemm_pipe::dense_rows<kRowBytes, 128>(b + (uint64_t)tn * 128 * k, k, rows_b, k);
+  gemm_pipe::Bf16Mma64::Acc acc;
+  gemm_pipe::mainloop<gemm_pipe::Bf16Mma64, kRowBytes, STAGES>(ar, br, k, smem, acc);
+  gemm_pipe::store_bf16_128<WHOLE>(acc, c + (uint64_t)tm * 128 * n + (uint64_t)tn * 128, n,
+                                   rows_a, rows_b);
+}
+
+// At most this many 256 x 256 tiles (half of MI355X's 256 CUs), the GEMM
+// runs on 128 x 128 tiles.
+constexpr uint64_t kSmallGrid = 128;
+
 // K = 0: C is all +0 (an empty sum).  A grid-stride fill kernel rather than
 // a memset node, so a caller may capture the launch in a HIP graph.
 __global__ void __launch_bounds__(256) zero_fill_bf16_kernel(uint16_t* __restrict__ c, uint64_t n) {
@@ -121,6 +152,10 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel", (const void*)gemm_bf16_nt_256_kernel<false, false>, 256, kFastSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel<staged>", (const void*)gemm_bf16_nt_256_kernel<true, false>, 256, kFastSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel<edge>", (const void*)gemm_bf16_nt_256_kernel<false, true>, 256, kFastSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<2>", (const void*)gemm_bf16_nt_128_kernel<2, true>, 256, kSmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<2, edge>", (const void*)gemm_bf16_nt_128_kernel<2, false>, 256, kSmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<3>", (const void*)gemm_bf16_nt_128_kernel<3, true>, 256, kSmallSmem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<3, edge>", (const void*)gemm_bf16_nt_128_kernel<3, false>, 256, kSmallSmem<3>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_generic_kernel", (const void*)gemm_bf16_nt_generic_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "zero_fill_bf16_kernel", (const void*)zero_fill_bf16_kernel, 256, 0})};
 
@@ -157,6 +192,32 @@ extern "C" int32_t fe2o3_gemm_bf16_nt(const uint16_t* a, uint64_t a_len, const u
     const uint64_t tiles = (uint64_t)((m + 255) / 256) * ((n + 255) / 256);
     if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
     hipStream_t s = (hipStream_t)stream;
+    if (tiles <= kSmallGrid) {  // 256 x 256 tiles would leave most CUs idle
+      static const int32_t small2_rc = fe2o3_host::set_dynamic_lds(
+          {(const void*)gemm_bf16_nt_128_kernel<2, true>,
+           (const void*)gemm_bf16_nt_128_kernel<2, false>},
+          kSmallSmem<2>);
+      static const int32_t small3_rc = fe2o3_host::set_dynamic_lds(
+          {(const void*)gemm_bf16_nt_128_kernel<3, true>,
+           (const void*)gemm_bf16_nt_128_kernel<3, false>},
+          kSmallSmem<3>);
+      if (small2_rc != FE2O3_OK) return small2_rc;
+      if (small3_rc != FE2O3_OK) return small3_rc;
+      const uint64_t t128 = (uint64_t)((m + 127) / 128) * ((n + 127) / 128);
+      const bool whole128 = m % 128 == 0 && n % 128 == 0 && aligned16(c);
+      const unsigned g = (unsigned)t128;
+      if (t128 > 2 * kSmallGrid) {
+        if (whole128)
+          gemm_bf16_nt_128_kernel<2, true><<<g, 256, kSmallSmem<2>, s>>>(a, b, c, m, n, k);
+        else
+          gemm_bf16_nt_128_kernel<2, false><<<g, 256, kSmallSmem<2>, s>>>(a, b, c, m, n, k);
+      } else if (whole128) {
+        gemm_bf16_nt_128_kernel<3, true><<<g, 256, kSmallSmem<3>, s>>>(a, b, c, m, n, k);
+      } else {
+        gemm_bf16_nt_128_kernel<3, false><<<g, 256, kSmallSmem<3>, s>>>(a, b, c, m, n, k);
+      }
+      return fe2o3_host::after_launch();
+    }
     if (!whole)
       gemm_bf16_nt_256_kernel<false, true><<<(unsigned)tiles, 256, kFastSmem, s>>>(a, b, c, m, n, k);
     else if (gemm_core::staged_epilogue(((uint64_t)m + n) * k * 2u))

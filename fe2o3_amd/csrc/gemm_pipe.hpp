@@ -411,6 +411,73 @@ struct Bf16MmaKN {
   static FE2O3_DEVICE void finish(Acc& acc) { A::finish(acc); }
 };
 
+// bf16, both operands k-contiguous (dense_rows), 128 x 128 tiles: the small
+// grid form of Bf16Mma.  Each wave owns 64 rows by 64 columns (4 x 4 MFMA
+// tiles, 64 AGPRs); A and B tiles of 128 rows.  All reads are ds_read_b128,
+// in Bf16Mma's order (a0, b0 .. b3, a1 .. a3).
+struct Bf16Mma64 {
+  using A = Bf16Mma<128, 64>;
+  using G = Geo<128>;
+  static constexpr int kRB = 4, kTn = 4, kSubsteps = A::kSubsteps, kMfma = 16, kReads = 8;
+  static constexpr int kARows = A::kARows;  // 128
+  static constexpr bool kBKN = false;
+  static constexpr int kBTileBytes = 128 * 128;
+  using Acc = Acc16T<4, 4>;
+  struct Frags {
+    bf16x8_t a[4], b[4];
+  };
+  struct Lanes {
+    uint32_t a[kSubsteps][4], b[kSubsteps][4];
+  };
+  static FE2O3_DEVICE Lanes lanes(uint32_t b_region) {
+    const typename A::Lanes la = A::lanes(b_region);
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t wn = wave & 1u, lr = lane & 15u, g = lane >> 4;
+    Lanes l;
+#pragma unroll
+    for (int s = 0; s < kSubsteps; ++s)
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t c = 4u * s + g, rb = wn * 64u + p * 16u + lr;
+        l.a[s][p] = la.a[s][p];
+        l.b[s][p] = b_region + (wn * 64u + lr) * 128u + ((c ^ G::swz(rb)) << 4);
+      }
+    return l;
+  }
+  template <uint32_t A_TILE, uint32_t B_TILE, int S, int R>
+  static FE2O3_DEVICE void read(const uint8_t* smem, const Lanes& l, Frags& f) {
+    static_assert(R >= 0 && R < kReads, "read unit");
+    if constexpr (R == 0) {
+      f.a[0] = *reinterpret_cast<const bf16x8_t*>(smem + l.a[S][0] + A_TILE);
+    } else if constexpr (R <= 4) {
+      constexpr int j = R - 1;
+      f.b[j] = *reinterpret_cast<const bf16x8_t*>(smem + l.b[S][j & 3] +
+                                                  (B_TILE + j * 16u * 128u));
+    } else {
+      constexpr int i = R - 4;
+      f.a[i] = *reinterpret_cast<const bf16x8_t*>(smem + l.a[S][i & 3] +
+                                                  (A_TILE + i * 16u * 128u));
+    }
+  }
+  template <bool FIRST, int I>
+  static FE2O3_DEVICE void mfma(Acc& acc, const Frags& f) {
+    constexpr int i = I / kTn, j = I % kTn;
+    if constexpr (FIRST)
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0"
+                   : "=a"(acc.v[i][j]) : "v"(f.b[j]), "v"(f.a[i]));
+    else
+      asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                   : "+a"(acc.v[i][j]) : "v"(f.b[j]), "v"(f.a[i]));
+  }
+  static FE2O3_DEVICE void finish(Acc& acc) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc.v[i][j]));
+  }
+};
+
 // bf16 with B stored [k][n], 128 x 128 tiles: for GEMMs whose 256 x 256
 // tiles would leave most CUs idle (a quarter of the output per tile, four
 // times the tiles).  Each wave owns 64 rows by 64 columns (4 x 4 MFMA
@@ -844,6 +911,36 @@ FE2O3_DEVICE void store_bf16_edge(const Acc16& acc, uint16_t* c_tile, uint64_t l
         const uint32_t c = col0 + 16u * j + e;
         if (c < cols_valid) out[c] = bf16_bits_from_f32(acc.v[i][j][e]);
       }
+  }
+}
+
+// A 128 x 128 tile of Acc16T<4, 4> (waves of 64 x 64): whole tiles of a
+// 16-byte aligned C (WHOLE) as 8-byte pieces; otherwise only rows <
+// rows_valid and columns < cols_valid, one 2-byte store per element.
+template <bool WHOLE>
+FE2O3_DEVICE void store_bf16_128(const Acc16T<4, 4>& acc, uint16_t* c_tile, uint64_t ldc,
+                                 uint32_t rows_valid, uint32_t cols_valid) {
+  const uint32_t row0 = acc16_row0<64>(), col0 = acc16_col0<64>();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t r = row0 + 16u * i;
+    if (!WHOLE && r >= rows_valid) continue;
+    uint16_t* out = c_tile + (uint64_t)r * ldc;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (WHOLE) {
+        u32x2_t packed;
+        packed[0] = pack_bf16x2(acc.v[i][j][0], acc.v[i][j][1]);
+        packed[1] = pack_bf16x2(acc.v[i][j][2], acc.v[i][j][3]);
+        *reinterpret_cast<u32x2_t*>(out + col0 + 16u * j) = packed;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t c = col0 + 16u * j + e;
+          if (c < cols_valid) out[c] = bf16_bits_from_f32(acc.v[i][j][e]);
+        }
+      }
+    }
   }
 }
 

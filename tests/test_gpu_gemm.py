@@ -319,10 +319,12 @@ def test_gemm_bf16_nt_generic_shapes(gpu, oracle, m, n, k):
 
 
 # K steps of 64: k = 64 is the first step alone (tail only), 128 the first
-# two-step group alone, 192 and 320 whole groups plus a one-step tail
+# two-step group alone, 192 and 320 whole groups plus a one-step tail.  Up to
+# 128 tiles of 256x256 the GEMM runs on 128x128 tiles: three-stage up to 256
+# of them, two-stage beyond (4096 x 2048: 512 small tiles).
 @pytest.mark.parametrize("m,n,k", [(256, 256, 64), (256, 256, 128), (256, 512, 256),
                                    (512, 768, 1024), (1024, 256, 4096), (256, 256, 320),
-                                   (512, 256, 192)])
+                                   (512, 256, 192), (4096, 2048, 128)])
 def test_gemm_bf16_nt_fast_path(gpu, oracle, m, n, k):
     _nt_case(gpu, oracle, m, n, k, seed=1)
 
@@ -330,10 +332,30 @@ def test_gemm_bf16_nt_fast_path(gpu, oracle, m, n, k):
 # M or N not a multiple of 256 with whole 64-k stages: edge tiles of the
 # pipelined kernel (clamped operand rows, element-wise masked stores)
 @pytest.mark.parametrize("m,n,k", [(300, 520, 512), (257, 255, 128), (1, 1000, 64),
-                                   (1000, 264, 1024), (4000, 4000, 256)])
+                                   (1000, 264, 1024), (4000, 4000, 256), (4000, 2000, 128)])
 def test_gemm_bf16_nt_edge_tiles(gpu, oracle, m, n, k):
     rows = None if m * n <= 1_100_000 else [0, 255, 256, 1999, 3839, 3840, 3999]
     _nt_case(gpu, oracle, m, n, k, seed=6, rows=rows)
+
+
+def test_gemm_bf16_nt_small_grid_matches_large_tiles(gpu):
+    """The same 2048 rows of A against the same B: at M = 2048 (64 tiles of
+    256x256, so 128x128 tiles run) and inside M = 4352 (136 tiles, the
+    256x256 tile), on whole and on edge shapes.  Every output gets the same
+    MFMAs in the same k order on both tiles: the rows are bit-identical."""
+    kern = _kernels()
+    for n, k in ((2048, 512), (2000, 320)):
+        big = 4352
+        da = gpu.alloc(big * k, np.uint16)
+        db = gpu.alloc(n * k, np.uint16)
+        kern.fill_normal_bf16(da, 12, 0xA, 1.0 / np.sqrt(k))
+        kern.fill_normal_bf16(db, 12, 0xB, 1.0 / np.sqrt(k))
+        K = kern.gemm_bf16_nt_gpu.Kernel.load(gpu)
+        c_big = gpu.alloc(big * n, np.uint16)
+        K.prepare(da, db, c_big, big, n, k).launch()
+        c_small = gpu.alloc(2048 * n, np.uint16)
+        K.prepare(da.view(0, 2048 * k), db, c_small, 2048, n, k).launch()
+        assert_same(c_small.download(), c_big.download()[:2048 * n], f"n={n} k={k}")
 
 
 def test_gemm_bf16_nt_whole_tiles_unaligned_c(gpu, oracle):
