@@ -122,6 +122,49 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
     gemm_pipe::store_bf16(acc, c_tile, n);
 }
 
+// The small-grid form: 128 x 128 tiles (Fp8Mma64) for GEMMs whose 256 x 256
+// tiles would leave most CUs idle; three 128-k stages (96 KiB) while the
+// tiles fit one per CU, else two (64 KiB, two workgroups per CU).  Every
+// output gets the MFMAs of the 256 x 256 tile in the same k order, and the
+// same scaling, so C is bit-identical to it.  WHOLE: M and N multiples of
+// 128 and C 16-byte aligned; otherwise rows past M (N) repeat the last valid
+// row and only valid elements are stored.
+template <int STAGES>
+constexpr int kFp8SmallSmem = STAGES * 2 * 128 * kFp8RowBytes;
+template <int STAGES, bool WHOLE>
+__global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_fp8_128_kernel(
+    const uint8_t* __restrict__ a, const uint8_t* __restrict__ b, const float* __restrict__ scale_a,
+    const float* __restrict__ scale_b, uint16_t* __restrict__ c, uint32_t m, uint32_t n,
+    uint32_t k) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const uint32_t tiles_m = (m + 127u) / 128u, tiles_n = (n + 127u) / 128u;
+  uint32_t tm, tn;
+  gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  const uint32_t rows_a = WHOLE ? 128u : min(128u, m - tm * 128u);
+  const uint32_t rows_b = WHOLE ? 128u : min(128u, n - tn * 128u);
+  const uint32_t k16 = k / 2;  // rows addressed in 16-bit units
+  const uint16_t* a16 = reinterpret_cast<const uint16_t*>(a + (uint64_t)tm * 128 * k);
+  const uint16_t* b16 = reinterpret_cast<const uint16_t*>(b + (uint64_t)tn * 128 * k);
+  const auto ar = gemm_pipe::dense_rows<kFp8RowBytes, 128>(a16, k16, rows_a, k16);
+  const auto br = gemm_pipe::dense_rows<kFp8RowBytes, 128>(b16, k16, rows_b, k16);
+  typename gemm_pipe::Fp8Mma64<kFp8RowBytes>::Acc acc;
+  gemm_pipe::mainloop<gemm_pipe::Fp8Mma64<kFp8RowBytes>, kFp8RowBytes, STAGES>(ar, br, k16,
+                                                                               smem, acc);
+  const float sab = scale_a[0] * scale_b[0];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc.v[i][j][e] *= sab;
+  gemm_pipe::store_bf16_fp8_128<WHOLE>(acc, c + (uint64_t)tm * 128 * n + (uint64_t)tn * 128, n,
+                                       rows_a, rows_b);
+}
+
+// At most this many 256 x 256 tiles (half of MI355X's 256 CUs), the GEMM
+// runs on 128 x 128 tiles.
+constexpr uint64_t kFp8SmallGrid = 128;
+
 // ---- any shape ---------------------------------------------------------------------------
 // 64x64 output tiles, 32 k per step; each operand element is widened to bf16
 // (exact) on its way to LDS, zero outside m x k / n x k, and four waves (2x2,
@@ -201,6 +244,10 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel", (const void*)gemm_fp8_kernel<false, false>, 256, kFp8Smem}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel<staged>", (const void*)gemm_fp8_kernel<true, false>, 256, kFp8Smem}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel<edge>", (const void*)gemm_fp8_kernel<false, true>, 256, kFp8Smem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<2>", (const void*)gemm_fp8_128_kernel<2, true>, 256, kFp8SmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<2, edge>", (const void*)gemm_fp8_128_kernel<2, false>, 256, kFp8SmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<3>", (const void*)gemm_fp8_128_kernel<3, true>, 256, kFp8SmallSmem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<3, edge>", (const void*)gemm_fp8_128_kernel<3, false>, 256, kFp8SmallSmem<3>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_generic_kernel", (const void*)gemm_fp8_generic_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "zero_fill_bf16_kernel", (const void*)zero_fill_bf16_kernel, 256, 0})};
 
@@ -269,6 +316,34 @@ int32_t fe2o3_gemm_fp8_nt(const uint8_t* a, uint64_t a_len, const uint8_t* b, ui
   const bool whole = m % 256 == 0 && n % 256 == 0 && ((uintptr_t)c & 15u) == 0;
   const uint64_t tiles = (uint64_t)((m + 255) / 256) * ((n + 255) / 256);
   if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
+  if (tiles <= kFp8SmallGrid) {  // 256 x 256 tiles would leave most CUs idle
+    static const int32_t small2_rc = fe2o3_host::set_dynamic_lds(
+        {(const void*)gemm_fp8_128_kernel<2, true>, (const void*)gemm_fp8_128_kernel<2, false>},
+        kFp8SmallSmem<2>);
+    static const int32_t small3_rc = fe2o3_host::set_dynamic_lds(
+        {(const void*)gemm_fp8_128_kernel<3, true>, (const void*)gemm_fp8_128_kernel<3, false>},
+        kFp8SmallSmem<3>);
+    if (small2_rc != FE2O3_OK) return small2_rc;
+    if (small3_rc != FE2O3_OK) return small3_rc;
+    const uint64_t t128 = (uint64_t)((m + 127) / 128) * ((n + 127) / 128);
+    const bool whole128 = m % 128 == 0 && n % 128 == 0 && ((uintptr_t)c & 15u) == 0;
+    const unsigned g = (unsigned)t128;
+    if (t128 > 2 * kFp8SmallGrid) {
+      if (whole128)
+        gemm_fp8_128_kernel<2, true><<<g, 256, kFp8SmallSmem<2>, s>>>(a, b, scale_a, scale_b, c,
+                                                                      m, n, k);
+      else
+        gemm_fp8_128_kernel<2, false><<<g, 256, kFp8SmallSmem<2>, s>>>(a, b, scale_a, scale_b, c,
+                                                                       m, n, k);
+    } else if (whole128) {
+      gemm_fp8_128_kernel<3, true><<<g, 256, kFp8SmallSmem<3>, s>>>(a, b, scale_a, scale_b, c, m,
+                                                                    n, k);
+    } else {
+      gemm_fp8_128_kernel<3, false><<<g, 256, kFp8SmallSmem<3>, s>>>(a, b, scale_a, scale_b, c,
+                                                                     m, n, k);
+    }
+    return fe2o3_host::after_launch();
+  }
   if (!whole)
     gemm_fp8_kernel<false, true><<<(unsigned)tiles, 256, kFp8Smem, s>>>(a, b, scale_a, scale_b,
                                                                          c, m, n, k);

@@ -228,9 +228,11 @@ struct Acc16T {  // RB row blocks of 16 x CB column blocks of 16
   f32x4_t v[RB][CB];
 };
 using Acc16 = Acc16T<8>;
-struct Acc32 {
-  f32x16_t v[4][4];
+template <int RB, int CB>
+struct Acc32T {  // RB row blocks of 32 x CB column blocks of 32
+  f32x16_t v[RB][CB];
 };
+using Acc32 = Acc32T<4, 4>;
 
 // bf16: v_mfma_f32_16x16x32_bf16, 32 k per substep.  Each wave owns RPW
 // output rows (RPW/16 row blocks) by 128 columns; the A tile holds 2 RPW
@@ -625,6 +627,64 @@ struct Fp8Mma {
   static FE2O3_DEVICE void finish(Acc&) {}
 };
 
+// OCP fp8 e4m3, 128 x 128 tiles: the small-grid form of Fp8Mma.  Each wave
+// owns 64 rows by 64 columns (2 x 2 MFMA tiles); A and B tiles of 128 rows.
+template <int ROW_BYTES>
+struct Fp8Mma64 {
+  using G = Geo<ROW_BYTES>;
+  using Acc = Acc32T<2, 2>;
+  static constexpr int kSubsteps = ROW_BYTES / 64, kMfma = 4, kTn = 2, kReads = 4;
+  static constexpr int kARows = 128;
+  static constexpr bool kBKN = false;
+  static constexpr int kBTileBytes = 128 * ROW_BYTES;
+  struct Frags {
+    i32x8_t a[2], b[2];
+  };
+  struct Lanes {
+    uint32_t a[kSubsteps][2][2], b[kSubsteps][2][2];  // [substep][row parity][chunk]
+  };
+  static FE2O3_DEVICE Lanes lanes(uint32_t b_region) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t wm = wave >> 1, wn = wave & 1u;
+    const uint32_t lr = lane & 31u, g = lane >> 5;
+    Lanes l;
+#pragma unroll
+    for (int s = 0; s < kSubsteps; ++s)
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t c = 4u * s + 2u * g + h;
+          const uint32_t ra = wm * 64u + p * 32u + lr, rb = wn * 64u + p * 32u + lr;
+          l.a[s][p][h] = (wm * 64u + lr) * ROW_BYTES + ((c ^ G::swz(ra)) << 4);
+          l.b[s][p][h] = b_region + (wn * 64u + lr) * ROW_BYTES + ((c ^ G::swz(rb)) << 4);
+        }
+    return l;
+  }
+  // read unit R of substep S: a0, b0, b1, a1
+  template <uint32_t A_TILE, uint32_t B_TILE, int S, int R>
+  static FE2O3_DEVICE void read(const uint8_t* smem, const Lanes& l, Frags& f) {
+    static_assert(R >= 0 && R < kReads, "read unit");
+    constexpr uint32_t kRow = 32u * ROW_BYTES;
+    if constexpr (R == 0) {
+      f.a[0] = Fp8Mma<ROW_BYTES>::frag(smem, l.a[S][0], A_TILE);
+    } else if constexpr (R <= 2) {
+      constexpr int j = R - 1;
+      f.b[j] = Fp8Mma<ROW_BYTES>::frag(smem, l.b[S][j], B_TILE + j * kRow);
+    } else {
+      f.a[1] = Fp8Mma<ROW_BYTES>::frag(smem, l.a[S][1], A_TILE + kRow);
+    }
+  }
+  template <bool FIRST, int I>
+  static FE2O3_DEVICE void mfma(Acc& acc, const Frags& f) {
+    constexpr int i = I / kTn, j = I % kTn;
+    const f32x16_t c = FIRST ? f32x16_t{} : acc.v[i][j];
+    acc.v[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[j], f.a[i], c, 0, 0, 0,
+                                                                  127, 0, 127);
+  }
+  static FE2O3_DEVICE void finish(Acc&) {}
+};
+
 // ---- the pipeline ----------------------------------------------------------------------------
 //
 // Two stages (ROW_BYTES 128: 64 bf16 or 128 fp8 of k) in two LDS buffers; a K step is one
@@ -874,9 +934,10 @@ FE2O3_DEVICE uint32_t acc16_row0() { return (wave_id() >> 1) * RPW + (lane_id() 
 template <int CPW = 128>  // columns per wave
 FE2O3_DEVICE uint32_t acc16_col0() { return (wave_id() & 1u) * CPW + 4u * (lane_id() >> 4); }
 
-// Acc32 (i, j, e): tile row wm*128 + 32i + lane%32, tile column
-// wn*128 + 32j + 8(e/4) + 4(lane/32) + e%4.
-FE2O3_DEVICE uint32_t acc32_row0() { return (wave_id() >> 1) * 128u + (lane_id() & 31u); }
+// Acc32T (i, j, e): tile row wm*RPW + 32i + lane%32, tile column
+// wn*RPW + 32j + 8(e/4) + 4(lane/32) + e%4 (RPW = 128, or 64 for Fp8Mma64).
+template <int RPW = 128>
+FE2O3_DEVICE uint32_t acc32_row0() { return (wave_id() >> 1) * RPW + (lane_id() & 31u); }
 
 FE2O3_DEVICE void store_bf16(const Acc16& acc, uint16_t* c_tile, uint64_t ldc) {
   const uint32_t row0 = acc16_row0(), col0 = acc16_col0();
@@ -1056,5 +1117,54 @@ FE2O3_DEVICE void store_bf16(const Acc32& acc, uint16_t* c_tile, uint64_t ldc) {
       }
 }
 
+
+// A 128 x 128 tile of Acc32T<2, 2> (waves of 64 x 64): whole tiles of a
+// 16-byte aligned C (WHOLE) with store_bf16(Acc32)'s lane-half exchange,
+// 16 bytes per lane; otherwise only rows < rows_valid and columns <
+// cols_valid, one 2-byte store per element.
+template <bool WHOLE>
+FE2O3_DEVICE void store_bf16_fp8_128(const Acc32T<2, 2>& acc, uint16_t* c_tile, uint64_t ldc,
+                                     uint32_t rows_valid, uint32_t cols_valid) {
+  const uint32_t row0 = acc32_row0<64>();
+  if constexpr (WHOLE) {
+    const uint32_t col0 = (wave_id() & 1u) * 64u + 8u * (lane_id() >> 5);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int qe = 2 * p, qo = 2 * p + 1;
+          const uint32_t y0 = pack_bf16x2(acc.v[i][j][4 * qe + 0], acc.v[i][j][4 * qe + 1]);
+          const uint32_t y1 = pack_bf16x2(acc.v[i][j][4 * qe + 2], acc.v[i][j][4 * qe + 3]);
+          const uint32_t x0 = pack_bf16x2(acc.v[i][j][4 * qo + 0], acc.v[i][j][4 * qo + 1]);
+          const uint32_t x1 = pack_bf16x2(acc.v[i][j][4 * qo + 2], acc.v[i][j][4 * qo + 3]);
+          const auto s0 = __builtin_amdgcn_permlane32_swap(y0, x0, false, false);
+          const auto s1 = __builtin_amdgcn_permlane32_swap(y1, x1, false, false);
+          u32x4_t packed;
+          packed[0] = s0[0];
+          packed[1] = s1[0];
+          packed[2] = s0[1];
+          packed[3] = s1[1];
+          *reinterpret_cast<u32x4_t*>(c_tile + (uint64_t)(row0 + 32u * i) * ldc + col0 +
+                                      32u * j + 16u * p) = packed;
+        }
+  } else {
+    const uint32_t col0 = (wave_id() & 1u) * 64u + 4u * (lane_id() >> 5);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t r = row0 + 32u * i;
+      if (r >= rows_valid) continue;
+      uint16_t* out = c_tile + (uint64_t)r * ldc;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const uint32_t c = col0 + 32u * j + 8u * (e / 4) + (e % 4);
+          if (c < cols_valid) out[c] = bf16_bits_from_f32(acc.v[i][j][e]);
+        }
+    }
+  }
+}
 
 }  // namespace gemm_pipe

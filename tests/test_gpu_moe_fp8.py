@@ -481,6 +481,41 @@ def test_gemm_fp8_any_shape(gpu, oracle, m, n, k):
     assert _fp8_case(gpu, oracle, m, n, k, (rr.ravel(), cc.ravel())) <= 1e-2
 
 
+@pytest.mark.parametrize("m,n,k", [(4096, 2048, 128), (4000, 2000, 256)])
+def test_gemm_fp8_small_grid_two_stage(gpu, oracle, m, n, k):
+    """128 tiles of 256x256 (512 small tiles: the two-stage 128x128 form),
+    whole and edge: sampled outputs of every tile row against the oracle."""
+    rng = np.random.default_rng(m + n + k)
+    rows = np.concatenate([np.arange(0, m, 128), rng.integers(0, m, 4000)])
+    cols = rng.integers(0, n, rows.size)
+    assert _fp8_case(gpu, oracle, m, n, k, (rows, cols)) <= 1e-2
+
+
+def test_gemm_fp8_small_grid_matches_large_tiles(gpu):
+    """The same 2048 rows of A against the same B: at M = 2048 (64 tiles of
+    256x256, so 128x128 tiles run) and inside M = 4352 (136 tiles, the
+    256x256 tile), on whole and edge shapes: every output gets the same MFMAs
+    in the same k order and the same scale, so the rows are bit-identical."""
+    kern = _k()
+    for n, k in ((2048, 512), (2000, 384)):
+        big = 4352
+        a32 = gpu.alloc(big * k, np.float32)
+        b32 = gpu.alloc(n * k, np.float32)
+        kern.fill_normal_f32(a32, 9, 0xA, 1.0)
+        kern.fill_normal_f32(b32, 9, 0xB, 1.0)
+        sa, sb, am = gpu.alloc(1, np.float32), gpu.alloc(1, np.float32), gpu.alloc(1, np.float32)
+        aq, bq = gpu.alloc(big * k, np.uint8), gpu.alloc(n * k, np.uint8)
+        for src, s_, q in ((a32, sa, aq), (b32, sb, bq)):
+            kern.amax_f32(src, am)
+            kern.fp8_scale_from_amax(am, s_)
+            kern.quantize_e4m3(src, s_, q)
+        c_big = gpu.alloc(big * n, np.uint16)
+        kern.gemm_fp8_nt(aq, bq, sa, sb, c_big, big, n, k)
+        c_small = gpu.alloc(2048 * n, np.uint16)
+        kern.gemm_fp8_nt(aq.view(0, 2048 * k), bq, sa, sb, c_small, 2048, n, k)
+        assert_same(c_small.download(), c_big.download()[:2048 * n], f"n={n} k={k}")
+
+
 def test_gemm_fp8_k0_writes_positive_zero(gpu):
     kern = _k()
     one = gpu.to_device(np.array([1.0], np.float32))
