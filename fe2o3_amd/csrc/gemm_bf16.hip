@@ -116,14 +116,21 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_nt_256_kernel(const uint16_t
 // valid elements are stored.
 template <int STAGES>
 constexpr int kSmallSmem = STAGES * (128 * kRowBytes + gemm_pipe::Bf16Mma64::kBTileBytes);
-template <int STAGES, bool WHOLE>
+//
+// TAIL: the last, partial round of a 256 x 256 grid (tiles first_big .. end
+// of gemm_core::xcd_tile_order's list), each as four 128 x 128 quarters
+// (gemm_core::tail_quarter).
+template <int STAGES, bool WHOLE, bool TAIL = false>
 __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_bf16_nt_128_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint16_t* __restrict__ c,
-    uint32_t m, uint32_t n, uint32_t k) {
+    uint32_t m, uint32_t n, uint32_t k, uint32_t first_big = 0) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  const uint32_t tiles_m = (m + 127u) / 128u, tiles_n = (n + 127u) / 128u;
   uint32_t tm, tn;
-  gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  if constexpr (TAIL) {
+    if (!gemm_core::tail_quarter(blockIdx.x, first_big, m, n, &tm, &tn)) return;
+  } else {
+    gemm_core::xcd_tile_order(blockIdx.x, (m + 127u) / 128u, (n + 127u) / 128u, &tm, &tn);
+  }
   const uint32_t rows_a = WHOLE ? 128u : min(128u, m - tm * 128u);
   const uint32_t rows_b = WHOLE ? 128u : min(128u, n - tn * 128u);
   const auto ar = gemm_pipe::dense_rows<kRowBytes, 128>(a + (uint64_t)tm * 128 * k, k, rows_a, k);
@@ -134,8 +141,10 @@ __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_bf16_nt_128_ker
                                    rows_a, rows_b);
 }
 
-// At most this many 256 x 256 tiles (half of MI355X's 256 CUs), the GEMM
-// runs on 128 x 128 tiles.
+// MI355X's CUs, and at most this many 256 x 256 tiles (half of them) the
+// GEMM runs on 128 x 128 tiles (or, for the last of several rounds, its
+// tiles run as 128 x 128 quarters).
+constexpr uint64_t kCUs = 256;
 constexpr uint64_t kSmallGrid = 128;
 
 // K = 0: C is all +0 (an empty sum).  A grid-stride fill kernel rather than
@@ -156,6 +165,10 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<2, edge>", (const void*)gemm_bf16_nt_128_kernel<2, false>, 256, kSmallSmem<2>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<3>", (const void*)gemm_bf16_nt_128_kernel<3, true>, 256, kSmallSmem<3>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<3, edge>", (const void*)gemm_bf16_nt_128_kernel<3, false>, 256, kSmallSmem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<2, tail>", (const void*)gemm_bf16_nt_128_kernel<2, true, true>, 256, kSmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<2, edge, tail>", (const void*)gemm_bf16_nt_128_kernel<2, false, true>, 256, kSmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<3, tail>", (const void*)gemm_bf16_nt_128_kernel<3, true, true>, 256, kSmallSmem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<3, edge, tail>", (const void*)gemm_bf16_nt_128_kernel<3, false, true>, 256, kSmallSmem<3>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_generic_kernel", (const void*)gemm_bf16_nt_generic_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "zero_fill_bf16_kernel", (const void*)zero_fill_bf16_kernel, 256, 0})};
 
@@ -218,12 +231,42 @@ extern "C" int32_t fe2o3_gemm_bf16_nt(const uint16_t* a, uint64_t a_len, const u
       }
       return fe2o3_host::after_launch();
     }
+    // A last round of at most kSmallGrid tiles (half the CUs or fewer) runs
+    // as 128 x 128 quarters on all CUs after the full rounds.
+    const uint64_t full = tiles / kCUs * kCUs, rest = tiles - full;
+    const bool tail = full > 0 && rest > 0 && rest <= kSmallGrid;
+    const unsigned big = (unsigned)(tail ? full : tiles);
     if (!whole)
-      gemm_bf16_nt_256_kernel<false, true><<<(unsigned)tiles, 256, kFastSmem, s>>>(a, b, c, m, n, k);
+      gemm_bf16_nt_256_kernel<false, true><<<big, 256, kFastSmem, s>>>(a, b, c, m, n, k);
     else if (gemm_core::staged_epilogue(((uint64_t)m + n) * k * 2u))
-      gemm_bf16_nt_256_kernel<true, false><<<(unsigned)tiles, 256, kFastSmem, s>>>(a, b, c, m, n, k);
+      gemm_bf16_nt_256_kernel<true, false><<<big, 256, kFastSmem, s>>>(a, b, c, m, n, k);
     else
-      gemm_bf16_nt_256_kernel<false, false><<<(unsigned)tiles, 256, kFastSmem, s>>>(a, b, c, m, n, k);
+      gemm_bf16_nt_256_kernel<false, false><<<big, 256, kFastSmem, s>>>(a, b, c, m, n, k);
+    if (tail) {
+      static const int32_t tail2_rc = fe2o3_host::set_dynamic_lds(
+          {(const void*)gemm_bf16_nt_128_kernel<2, true, true>,
+           (const void*)gemm_bf16_nt_128_kernel<2, false, true>},
+          kSmallSmem<2>);
+      static const int32_t tail3_rc = fe2o3_host::set_dynamic_lds(
+          {(const void*)gemm_bf16_nt_128_kernel<3, true, true>,
+           (const void*)gemm_bf16_nt_128_kernel<3, false, true>},
+          kSmallSmem<3>);
+      if (tail2_rc != FE2O3_OK) return tail2_rc;
+      if (tail3_rc != FE2O3_OK) return tail3_rc;
+      const bool whole128 = m % 128 == 0 && n % 128 == 0 && aligned16(c);
+      const unsigned g = (unsigned)((rest + 7) / 8 * 32);  // 4 quarters, 8 per XCD row
+      const uint32_t first = (uint32_t)full;
+      if (4 * rest > kCUs) {  // more quarters than CUs: two-stage, two per CU
+        if (whole128)
+          gemm_bf16_nt_128_kernel<2, true, true><<<g, 256, kSmallSmem<2>, s>>>(a, b, c, m, n, k, first);
+        else
+          gemm_bf16_nt_128_kernel<2, false, true><<<g, 256, kSmallSmem<2>, s>>>(a, b, c, m, n, k, first);
+      } else if (whole128) {
+        gemm_bf16_nt_128_kernel<3, true, true><<<g, 256, kSmallSmem<3>, s>>>(a, b, c, m, n, k, first);
+      } else {
+        gemm_bf16_nt_128_kernel<3, false, true><<<g, 256, kSmallSmem<3>, s>>>(a, b, c, m, n, k, first);
+      }
+    }
     return fe2o3_host::after_launch();
   }
   dim3 grid((n + N_BN - 1) / N_BN, (m + N_BM - 1) / N_BM);

@@ -26,6 +26,24 @@ FE2O3_DEVICE void xcd_tile_order(uint32_t pid, uint32_t tiles_m, uint32_t tiles_
   *tn = r / size_m;
 }
 
+// The tail form of a 256 x 256 grid: workgroup 8(4j + q) + x of a launch
+// over the tiles first_big .. end of xcd_tile_order's list takes quarter q
+// (128 x 128) of tile first_big + 8j + x, so a tile's quarters run on the
+// XCD (x) its neighbours in the list ran on.  False when the tile is past
+// the grid or the quarter past an edge tile's rows or columns.
+FE2O3_DEVICE bool tail_quarter(uint32_t wg, uint32_t first_big, uint32_t m, uint32_t n,
+                               uint32_t* tm, uint32_t* tn) {
+  const uint32_t x = wg & 7u, q = wg >> 3;
+  const uint32_t big = first_big + 8u * (q >> 2) + x;
+  const uint32_t big_m = (m + 255u) / 256u, big_n = (n + 255u) / 256u;
+  if (big >= big_m * big_n) return false;
+  uint32_t btm, btn;
+  xcd_tile_order(big, big_m, big_n, &btm, &btn);
+  *tm = 2u * btm + ((q & 3u) >> 1);
+  *tn = 2u * btn + (q & 1u);
+  return *tm * 128u < m && *tn * 128u < n;
+}
+
 // Host: whether a 256x256-tile launch whose operands (A and B together) take
 // `operand_bytes` stores C through LDS (gemm_pipe::store_bf16_staged).  C
 // written straight from the accumulators lands in the caches in part-lines;

@@ -433,15 +433,21 @@ __global__ void __launch_bounds__(256, 1) gemm_general_pipe_kernel(
 template <int STAGES>
 constexpr int kGp64Smem =
     STAGES * (128 * kGpRowBytes + gemm_pipe::Bf16MmaKN64::kBTileBytes);
-template <int STAGES>
+// TAIL: the last, partial round of a 256 x 256 grid (tiles first_big .. end
+// of gemm_core::xcd_tile_order's list), each as four 128 x 128 quarters
+// (gemm_core::tail_quarter).
+template <int STAGES, bool TAIL = false>
 __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_general_pipe128_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, float* __restrict__ c,
     uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha,
-    float beta) {
+    float beta, uint32_t first_big = 0) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  const uint32_t tiles_m = (m + 127u) / 128u, tiles_n = (n + 127u) / 128u;
   uint32_t tm, tn;
-  gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  if constexpr (TAIL) {
+    if (!gemm_core::tail_quarter(blockIdx.x, first_big, m, n, &tm, &tn)) return;
+  } else {
+    gemm_core::xcd_tile_order(blockIdx.x, (m + 127u) / 128u, (n + 127u) / 128u, &tm, &tn);
+  }
   const uint32_t rows = min(128u, m - tm * 128u), cols = min(128u, n - tn * 128u);
   const auto ar =
       gemm_pipe::dense_rows<kGpRowBytes, 128>(a + (uint64_t)tm * 128u * lda, lda, rows, k);
@@ -456,13 +462,19 @@ const fe2o3_host::KernelRegistrar kRegisteredPipe[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe_kernel", (const void*)gemm_general_pipe_kernel, 256, kGpSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe128_kernel<2>", (const void*)gemm_general_pipe128_kernel<2>, 256, kGp64Smem<2>}),
     fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe128_kernel<3>", (const void*)gemm_general_pipe128_kernel<3>, 256, kGp64Smem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe128_kernel<2, tail>", (const void*)gemm_general_pipe128_kernel<2, true>, 256, kGp64Smem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe128_kernel<3, tail>", (const void*)gemm_general_pipe128_kernel<3, true>, 256, kGp64Smem<3>}),
     fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe_kernel", (const void*)gemm_general_pipe_kernel, 256, kGpSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<2>", (const void*)gemm_general_pipe128_kernel<2>, 256, kGp64Smem<2>}),
-    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<3>", (const void*)gemm_general_pipe128_kernel<3>, 256, kGp64Smem<3>})};
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<3>", (const void*)gemm_general_pipe128_kernel<3>, 256, kGp64Smem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<2, tail>", (const void*)gemm_general_pipe128_kernel<2, true>, 256, kGp64Smem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<3, tail>", (const void*)gemm_general_pipe128_kernel<3, true>, 256, kGp64Smem<3>})};
 
-// At most this many 256 x 256 tiles (half of MI355X's 256 CUs), the GEMM
+// MI355X's CUs; at most kSmallGrid 256 x 256 tiles (half of them), the GEMM
 // runs on 128 x 128 tiles instead, three-stage up to 2 kSmallGrid of them
-// (one per CU).
+// (one per CU), and a last round of at most kSmallGrid tiles after full
+// rounds runs as 128 x 128 quarters.
+constexpr uint64_t kCUs = 256;
 constexpr uint64_t kSmallGrid = 128;
 
 // Host: whether the pipelined tile takes this general GEMM: whole 64-k
@@ -514,8 +526,28 @@ int32_t general_gemm(const uint16_t* a, uint64_t a_len, const uint16_t* b, uint6
                                                                 alpha, beta);
       return fe2o3_host::after_launch();
     }
-    gemm_general_pipe_kernel<<<(unsigned)tiles, 256, kGpSmem, (hipStream_t)stream>>>(
+    // a last round of at most kSmallGrid tiles runs as 128 x 128 quarters
+    // on all CUs after the full rounds
+    const uint64_t full = tiles / kCUs * kCUs, rest = tiles - full;
+    const bool tail = full > 0 && rest > 0 && rest <= kSmallGrid;
+    hipStream_t s = (hipStream_t)stream;
+    gemm_general_pipe_kernel<<<(unsigned)(tail ? full : tiles), 256, kGpSmem, s>>>(
         a, b, c, m, n, k, lda, ldb, ldc, alpha, beta);
+    if (tail) {
+      static const int32_t tail2_rc = fe2o3_host::set_dynamic_lds(
+          {(const void*)gemm_general_pipe128_kernel<2, true>}, kGp64Smem<2>);
+      static const int32_t tail3_rc = fe2o3_host::set_dynamic_lds(
+          {(const void*)gemm_general_pipe128_kernel<3, true>}, kGp64Smem<3>);
+      if (tail2_rc != FE2O3_OK) return tail2_rc;
+      if (tail3_rc != FE2O3_OK) return tail3_rc;
+      const unsigned g = (unsigned)((rest + 7) / 8 * 32);  // 4 quarters, 8 per XCD row
+      if (4 * rest > kCUs)  // more quarters than CUs: two-stage, two per CU
+        gemm_general_pipe128_kernel<2, true><<<g, 256, kGp64Smem<2>, s>>>(
+            a, b, c, m, n, k, lda, ldb, ldc, alpha, beta, (uint32_t)full);
+      else
+        gemm_general_pipe128_kernel<3, true><<<g, 256, kGp64Smem<3>, s>>>(
+            a, b, c, m, n, k, lda, ldb, ldc, alpha, beta, (uint32_t)full);
+    }
     return fe2o3_host::after_launch();
   }
   dim3 grid((n + G_BN - 1) / G_BN, (m + G_BM - 1) / G_BM);

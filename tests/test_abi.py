@@ -94,8 +94,8 @@ def test_kernel_resource_record_and_registry_without_gpu():
     for name, off in offsets.items():
         assert getattr(R, name).offset == off
     L = _lib.lib()
-    expected = {"fe2o3_gemm_bf16_nt": 9, "fe2o3_flash_attention_fwd": 2, "fe2o3_moe_ffn_top2": 4,
-                "fe2o3_gemm_fp8_nt": 9, "fe2o3_row_softmax": 13, "fe2o3_moe_routing_check": 1,
+    expected = {"fe2o3_gemm_bf16_nt": 13, "fe2o3_flash_attention_fwd": 2, "fe2o3_moe_ffn_top2": 4,
+                "fe2o3_gemm_fp8_nt": 13, "fe2o3_row_softmax": 13, "fe2o3_moe_routing_check": 1,
                 "fe2o3_wave64_collectives_v1": 1, "no_such_entry": 0}
     for entry, n in expected.items():
         count = ctypes.c_uint32(12345)

@@ -196,6 +196,35 @@ def test_general_pipelined_tile_matches_staged_kernel(gpu, oracle, dims, strides
     assert rel_err(rows, out) <= 1e-5
 
 
+@pytest.mark.parametrize("m,n,k", [(6144, 6144, 128), (6000, 6100, 192)])
+def test_general_tail_round_matches_row_blocks(gpu, m, n, k):
+    """576 tiles of 256x256 (the last 64 as 128x128 quarters after two full
+    rounds), alpha/beta with a nonzero C: the same C computed as row blocks
+    of 2048 (no tail) is bit-identical."""
+    kern = _kernels()
+    lda, ldb, ldc = k + 8, (n + 15) // 8 * 8, n + 4  # A and B rows 16-byte aligned
+    da = gpu.alloc((m - 1) * lda + k, np.uint16)
+    db = gpu.alloc((k - 1) * ldb + n, np.uint16)
+    kern.fill_normal_bf16(da, 14, 0xA, 1.0)
+    kern.fill_normal_bf16(db, 14, 0xB, 1.0)
+    c0 = np.random.default_rng(m).standard_normal((m - 1) * ldc + n).astype(np.float32)
+    K = kern.tiled_gemm_general_v1_gpu.Kernel.load(gpu)
+    gc = Guarded(gpu, c0)
+    K.prepare(da, db, gc.body, m, n, k, lda, ldb, ldc, 1.25, 0.5).launch()
+    assert gc.guards_intact()
+    whole = gc.download()
+    for r0 in range(0, m, 2048):
+        rows = min(2048, m - r0)
+        span = (rows - 1) * ldc + n
+        part = gpu.to_device(c0[r0 * ldc:r0 * ldc + span])
+        K.prepare(da.view(r0 * lda, (rows - 1) * lda + k), db, part, rows, n, k, lda, ldb, ldc,
+                  1.25, 0.5).launch()
+        got = part.download()
+        for r in range(rows):
+            assert got[r * ldc:r * ldc + n].tobytes() == \
+                whole[(r0 + r) * ldc:(r0 + r) * ldc + n].tobytes(), (r0, r)
+
+
 def test_general_rejects_small_stride_and_short_slice(gpu):
     from fe2o3_amd.runtime import Fe2o3Error
     a = gpu.to_device(np.zeros(64, np.uint16))
@@ -356,6 +385,29 @@ def test_gemm_bf16_nt_small_grid_matches_large_tiles(gpu):
         c_small = gpu.alloc(2048 * n, np.uint16)
         K.prepare(da.view(0, 2048 * k), db, c_small, 2048, n, k).launch()
         assert_same(c_small.download(), c_big.download()[:2048 * n], f"n={n} k={k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(6144, 6144, 256), (6000, 6100, 192), (4096, 14336, 128)])
+def test_gemm_bf16_nt_tail_round_matches_row_blocks(gpu, m, n, k):
+    """576 (or 896) tiles of 256x256: the full rounds on the 256x256 tile and
+    the last 64 (128) tiles as 128x128 quarters.  The same C computed as row
+    blocks of 2048 (at most 200 tiles each, no tail) is bit-identical; the
+    guards around C are untouched."""
+    kern = _kernels()
+    da = gpu.alloc(m * k, np.uint16)
+    db = gpu.alloc(n * k, np.uint16)
+    kern.fill_normal_bf16(da, 13, 0xA, 1.0 / np.sqrt(k))
+    kern.fill_normal_bf16(db, 13, 0xB, 1.0 / np.sqrt(k))
+    K = kern.gemm_bf16_nt_gpu.Kernel.load(gpu)
+    c = Guarded(gpu, np.full(m * n, 0x7FDE, np.uint16))
+    K.prepare(da, db, c.body, m, n, k).launch()
+    assert c.guards_intact()
+    whole = c.download()
+    for r0 in range(0, m, 2048):
+        rows = min(2048, m - r0)
+        part = gpu.alloc(rows * n, np.uint16)
+        K.prepare(da.view(r0 * k, rows * k), db, part, rows, n, k).launch()
+        assert_same(part.download(), whole[r0 * n:(r0 + rows) * n], f"rows {r0}..{r0 + rows}")
 
 
 def test_gemm_bf16_nt_whole_tiles_unaligned_c(gpu, oracle):
