@@ -269,6 +269,7 @@ struct Bf16Mma {
   static constexpr int kARows = 2 * RPW;
   static constexpr bool kBKN = false;
   static constexpr int kBTileBytes = G::kTileBytes;
+  static constexpr int kLateSlots = kMfma;  // late copies spread over a whole substep 0
   struct Frags {
     bf16x8_t a[kRB], b[8];
   };
@@ -357,6 +358,7 @@ struct Bf16MmaKN {
   static constexpr int kARows = A::kARows;
   static constexpr bool kBKN = true;
   static constexpr int kBTileBytes = A::kBTileBytes;
+  static constexpr int kLateSlots = kMfma;
   using Frags = A::Frags;
   struct Lanes {
     uint32_t a[kSubsteps][4], b[kSubsteps][8];
@@ -424,6 +426,7 @@ struct Bf16Mma64 {
   static constexpr int kARows = A::kARows;  // 128
   static constexpr bool kBKN = false;
   static constexpr int kBTileBytes = 128 * 128;
+  static constexpr int kLateSlots = kMfma;
   using Acc = Acc16T<4, 4>;
   struct Frags {
     bf16x8_t a[4], b[4];
@@ -493,6 +496,7 @@ struct Bf16MmaKN64 {
   static constexpr int kARows = A::kARows;  // 128
   static constexpr bool kBKN = true;
   static constexpr int kBTileBytes = 64 * 256;
+  static constexpr int kLateSlots = kMfma;
   using Acc = Acc16T<4, 4>;
   struct Frags {
     bf16x8_t a[4], b[4];
@@ -572,6 +576,10 @@ struct Fp8Mma {
   static constexpr int kARows = 256;
   static constexpr bool kBKN = false;
   static constexpr int kBTileBytes = G::kTileBytes;
+  // late copies over the first 3/4 of substep 0: they land earlier before
+  // the barrier's wait (8192^3: 318 -> 310 us; the bf16 tile is 1% slower
+  // with it, so it keeps the whole substep)
+  static constexpr int kLateSlots = 3 * kMfma / 4;
   struct Frags {
     i32x8_t a[4], b[4];
   };
@@ -637,6 +645,7 @@ struct Fp8Mma64 {
   static constexpr int kARows = 128;
   static constexpr bool kBKN = false;
   static constexpr int kBTileBytes = 128 * ROW_BYTES;
+  static constexpr int kLateSlots = kMfma;
   struct Frags {
     i32x8_t a[2], b[2];
   };
@@ -695,7 +704,8 @@ struct Fp8Mma64 {
 //   every substep but the last: the next substep's fragment reads over
 //     [M/8, 7M/8);
 //   substep 0: the second half of stage t+1's copies (A and B alternating)
-//     into the other buffer over [0, M);
+//     into the other buffer over [0, L), L = the policy's kLateSlots (M, or
+//     3M/4 for fp8);
 //   last substep: MFMAs up to M/2; wait for stage t+1's copies and cross the
 //     barrier; then stage t+1's first fragment reads over [M/2, M), and the
 //     first half of stage t+2's copies into buffer P over [M/2, M).
@@ -774,7 +784,7 @@ struct Substep {
   // late copies: all of substep 0, or its first half when it is also the
   // last substep (every late copy precedes the barrier, every early one
   // follows it, which keeps the wait counts exact)
-  static constexpr int kLateTo = LAST ? kBarrierAt : MF;
+  static constexpr int kLateTo = LAST ? kBarrierAt : M::kLateSlots;
   // fragment buffers alternate by substep over the whole K loop
   static constexpr int FC = (P * S + S_) & 1, FN = FC ^ 1;
   static constexpr int kReadFrom = LAST ? MF / 2 : MF / 8;
