@@ -387,7 +387,10 @@ def test_gemm_bf16_nt_small_grid_matches_large_tiles(gpu):
         assert_same(c_small.download(), c_big.download()[:2048 * n], f"n={n} k={k}")
 
 
-@pytest.mark.parametrize("m,n,k", [(6144, 6144, 256), (6000, 6100, 192), (4096, 14336, 128)])
+# 6144 x 6144 x 8192: operands of 192 MiB, so the full rounds store C through
+# LDS (the staged epilogue) while the tail quarters store it directly
+@pytest.mark.parametrize("m,n,k", [(6144, 6144, 256), (6000, 6100, 192), (4096, 14336, 128),
+                                   (6144, 6144, 8192)])
 def test_gemm_bf16_nt_tail_round_matches_row_blocks(gpu, m, n, k):
     """576 (or 896) tiles of 256x256: the full rounds on the 256x256 tile and
     the last 64 (128) tiles as 128x128 quarters.  The same C computed as row
