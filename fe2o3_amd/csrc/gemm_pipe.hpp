@@ -398,8 +398,10 @@ struct Bf16MmaKN {
       // replayed against that rule by tests/test_isa_lds_waits.py.
       const lds_bf16x4_t* p = (const lds_bf16x4_t*)(smem + l.b[S][j]);
       bf16x4_t lo, hi;
+      // early-clobber outputs: the second read takes its address from p
+      // after the first is in flight, so lo must not be given p's register
       asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
-                   : "=v"(lo), "=v"(hi)
+                   : "=&v"(lo), "=&v"(hi)
                    : "v"(p), "i"(B_TILE), "i"(B_TILE + 2048u));
       f.b[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     } else {
@@ -533,8 +535,9 @@ struct Bf16MmaKN64 {
       constexpr int j = R - 1;
       const lds_bf16x4_t* p = (const lds_bf16x4_t*)(smem + l.b[S][j]);
       bf16x4_t lo, hi;
+      // early-clobber outputs, as in Bf16MmaKN::read
       asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\tds_read_b64_tr_b16 %1, %2 offset:%4"
-                   : "=v"(lo), "=v"(hi)
+                   : "=&v"(lo), "=&v"(hi)
                    : "v"(p), "i"(B_TILE), "i"(B_TILE + 1024u));
       f.b[j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     } else {

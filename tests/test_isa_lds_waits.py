@@ -5,8 +5,11 @@ them.  This CPU test compiles gemm_small.hip for gfx950 to assembly and
 replays the instruction streams of gemm_general_pipe_kernel (256x256
 tiles) and gemm_general_pipe128_kernel<2>, <3> (128x128, whole grids and
 tail rounds) with in-order LDS
-completion: no instruction may read a VGPR that an LDS read has not yet
-delivered (no s_waitcnt lgkmcnt covering it).  Scalar loads share the
+completion: no instruction -- an LDS read's address included -- may read a
+VGPR that an LDS read has not yet delivered (no s_waitcnt lgkmcnt covering
+it).  The two reads of one inline-asm pair are the case the compiler cannot
+see: without early-clobber outputs it may give the first read's destination
+the register that holds the second read's address.  Scalar loads share the
 counter; the replay ignores them, which only keeps more LDS reads pending
 than the hardware would, so the check stays conservative.  The check is
 shown to fire on the same stream with its lgkmcnt waits removed."""
@@ -45,11 +48,16 @@ def _violations(lines):
                 pending = pending[len(pending) - keep:] if 0 < keep < len(pending) else (
                     [] if keep == 0 else pending)
             continue
+        # sources: every operand after the destination; a DS write or atomic
+        # without return reads all of its operands (the address first).  An
+        # LDS read may name its own destination as its address (it reads the
+        # address at issue), but not a destination of an earlier read still
+        # in flight
         srcs = set()
-        for a in args[1:]:
-            srcs |= _regs(a)
+        for a in (args if op.startswith("ds_write") else args[1:]):
+            srcs |= _regs(a.split()[0] if a else a)
         live = set().union(*pending) if pending else set()
-        if srcs & live and not op.startswith("ds_"):
+        if srcs & live:
             bad += 1
         if op.startswith("ds_read"):
             pending.append(_regs(args[0]))
