@@ -30,6 +30,9 @@
 //      XOR-permuted per row against bank conflicts.  The next tile's loads
 //      are spread one per two S^T MFMAs rather than issued as a burst
 //      (+3%).
+//    * Both MFMA runs alternate accumulators (S^T: the two key blocks; PV:
+//      the four d blocks), and each LDS operand is read two MFMAs ahead of
+//      its MFMA (+3% over the scheduler's read-just-before-use).
 //    * Causal: a workgroup runs query tiles r and nq-1-r of one head in
 //      turn, so every workgroup does nq+1 key tiles; a wave skips the
 //      MFMAs of key tiles that lie entirely above its rows and masks the
@@ -145,6 +148,12 @@ FE2O3_DEVICE uint32_t tile_voffset() {
 }
 
 constexpr int kLoadsPerTile = 16 / WAVES;  // 1 KiB loads per wave and tile
+// LDS operand fragments are read this many MFMAs ahead of their MFMA (2, 4
+// and 6 run within 1% of each other; reading each just before its MFMA, the
+// scheduler's own choice, ran 3% slower)
+constexpr int kAhead = 2;
+// __builtin_amdgcn_sched_group_barrier instruction classes
+constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
 static_assert(16 % (2 * kLoadsPerTile) == 0, "a tile's copies spread evenly over 16 MFMAs");
 
 FE2O3_DEVICE void copy_load(__amdgpu_buffer_rsrc_t src, uint32_t voff, uint32_t tile_byte,
@@ -258,28 +267,40 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
       issue_tile(vsrc, v_off, nt, nxt + TILE_BYTES, wave);
     }
     if (active) {
-      // S^T = K Q^T : two 32-key blocks
+      // S^T = K Q^T : two 32-key blocks.  MFMA i (0..15) is key block kb = i%2
+      // at d slice ds = i/2, so consecutive MFMAs feed the two accumulators
+      // in turn (each accumulator still sums its d slices in order).  Each K
+      // fragment is read kAhead MFMAs before its MFMA, and the group
+      // barriers keep that order (read, MFMA, copy) against the
+      // scheduler, which otherwise reads each fragment just before its use
+      // and waits for it there.  The next tile's copies go one per two
+      // MFMAs (K loads, then V).
       f32x16_t s[2];
+      constexpr int kCopyEvery = 16 / (2 * kLoadsPerTile);
+      auto kread = [&](int i) {
+        const uint32_t krow = (uint32_t)(i & 1) * 32u + lr;
+        const uint32_t c = 2u * (uint32_t)(i >> 1) + g;
+        return *reinterpret_cast<const bf16x8_t*>(cur + krow * 256u + ((c ^ swz_k(krow)) << 4));
+      };
+      bf16x8_t kf[16];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const uint32_t krow = kb * 32u + lr;
+      for (int i = 0; i < kAhead; ++i) kf[i] = kread(i);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kAhead, 0);
 #pragma unroll
-        for (int ds = 0; ds < 8; ++ds) {
-          const uint32_t c = 2u * ds + g;
-          const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(
-              cur + krow * 256u + ((c ^ swz_k(krow)) << 4));
-          s[kb] = ds == 0 ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[0], f32x16_t{}, 0, 0, 0)
-                          : __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ds], s[kb], 0, 0, 0);
-          // the next tile's copies, spread over these 16 MFMAs (K loads, then V)
-          constexpr int kCopyEvery = 16 / (2 * kLoadsPerTile);
-          const int slot = kb * 8 + ds;
-          if (slot % kCopyEvery == 0) {
-            const int n = slot / kCopyEvery, jj = n % kLoadsPerTile;
-            const bool is_v = n >= kLoadsPerTile;
-            copy_load(is_v ? vsrc : ksrc, is_v ? v_off : k_off, nt,
-                      nxt + (is_v ? TILE_BYTES : 0), wave, jj);
-          }
+      for (int i = 0; i < 16; ++i) {
+        const int ds = i >> 1, kb = i & 1;
+        if (i + kAhead < 16) kf[i + kAhead] = kread(i + kAhead);
+        s[kb] = ds == 0 ? __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[i], qf[0], f32x16_t{}, 0, 0, 0)
+                        : __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[i], qf[ds], s[kb], 0, 0, 0);
+        if (i % kCopyEvery == 0) {
+          const int n = i / kCopyEvery, jj = n % kLoadsPerTile;
+          const bool is_v = n >= kLoadsPerTile;
+          copy_load(is_v ? vsrc : ksrc, is_v ? v_off : k_off, nt,
+                    nxt + (is_v ? TILE_BYTES : 0), wave, jj);
         }
+        if (i + kAhead < 16) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        if (i % kCopyEvery == 0) __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
       }
       // keys past seq (the partial last tile; causal rows below seq mask
       // them as future keys)
@@ -342,14 +363,25 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
       // not raising it).
       const uint8_t* vt = cur + TILE_BYTES;
       __builtin_amdgcn_s_setprio(1);
+      // MFMA i (0..15) is d block db = i%4 of key half (kb = i/8, h = (i/4)%2):
+      // consecutive MFMAs update different accumulators, each accumulator
+      // still sums its key halves in order.  The V^T operand (two
+      // transposing reads) is read kAhead MFMAs ahead, as the K fragments.
+      auto vread = [&](int i) {
+        return read_vt(vt, (uint32_t)(i & 3), (uint32_t)(i >> 3), (uint32_t)((i >> 2) & 1));
+      };
+      bf16x8_t vf[16];
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+      for (int i = 0; i < kAhead; ++i) vf[i] = vread(i);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kAhead, 1);
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-            acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(read_vt(vt, db, kb, h), pf[kb][h],
-                                                              acc[db], 0, 0, 0);
+      for (int i = 0; i < 16; ++i) {
+        if (i + kAhead < 16) vf[i + kAhead] = vread(i + kAhead);
+        const int db = i & 3, kb = i >> 3, h = (i >> 2) & 1;
+        acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[i], pf[kb][h], acc[db], 0, 0, 0);
+        if (i + kAhead < 16) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 1);
+      }
       __builtin_amdgcn_s_setprio(0);
     }
     wait_vmcnt0();
