@@ -359,8 +359,8 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
       // O^T += V^T P^T.  Each SIMD runs one wave of each of two workgroups; a
       // wave raises its issue priority while it issues these MFMAs, so the
       // matrix core is fed first and the other wave's softmax fills the gaps
-      // (measured: +1% over raising it for the S^T MFMAs as well, +2% over
-      // not raising it).
+      // (measured: +3.6% over not raising it, and about as much over raising
+      // it for the S^T MFMAs as well or instead).
       const uint8_t* vt = cur + TILE_BYTES;
       __builtin_amdgcn_s_setprio(1);
       // MFMA i (0..15) is d block db = i%4 of key half (kb = i/8, h = (i/4)%2):
