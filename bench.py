@@ -531,6 +531,41 @@ def sec_collectives(ctx, stream, args):
                        "coverage": "256 rows spread over all rows, all three outputs"}}
 
 
+def sec_fp8_fnuz(ctx, stream, args):
+    """gfx942 FNUZ E4M3 narrowing (Fp8E4M3Fnuz::from_f32 over an array) of
+    2^28 f32: 4 bytes in and 1 byte out per element (HBM-bound)."""
+    from fe2o3_amd import kernels
+    from oracle import oracle as orc
+    n = 1 << 28
+    x = ctx.alloc(n, np.float32)
+    q = ctx.alloc(n, np.uint8)
+    kernels.fill_normal_f32(x, 7, 0xF0A2, 40.0, stream=stream)
+    ms = _timed(ctx, stream, lambda: kernels.fp8_fnuz_from_f32(
+        x, q, kernels.FNUZ_E4M3, stream=stream, sync=False), args)
+    gbs = n * 5 / (ms * 1e-3) / 1e9
+    res = {"workload": "gfx942 FNUZ E4M3 narrowing of 2^28 f32 (fp8.rs from_f32 over an array)",
+           "kernel": "fnuz_from_f32_kernel<e4m3>", "ms": ms, "value": round(gbs, 1),
+           "unit": "GB/s",
+           "roofline": {"bound": "hbm", "peak": PEAK["hbm_gbs"],
+                        "frac": round(gbs / PEAK["hbm_gbs"], 4)}}
+    if not args.cpu_baseline:
+        return res
+    # parity: 16 blocks of 2^20 elements spread over the array
+    per = 1 << 20
+    starts = [i * (n // 16) + (i * 7919) % (n // 16 - per) for i in range(16)]
+    hx = np.concatenate([x.view(s0, per).download() for s0 in starts])
+    hq = np.concatenate([q.view(s0, per).download() for s0 in starts])
+    t0 = time.perf_counter()
+    ref = orc.fnuz_from_f32(hx, orc.FNUZ_E4M3)
+    dt = time.perf_counter() - t0
+    return {**res,
+            "parity": {"bit_mismatches": int(np.count_nonzero(hq != ref)), "tolerance": "bit-exact",
+                       "coverage": f"{hx.size} elements (16 blocks of 2^20 spread over the 2^28)"},
+            "cpu_baseline": _cpu(hx.size * 5 / dt / 1e9, "GB/s", 1,
+                                 f"oracle/fp8.c fe2o3o_fnuz_from_f32_array (scalar) on the "
+                                 f"{hx.size} parity elements, {dt:.2f} s")}
+
+
 def sec_routing_check(ctx, stream, args):
     """Routing-output consistency check of config 5's router output (4096
     tokens, 8 experts, unbounded capacity): one workgroup, latency-bound."""
@@ -564,6 +599,7 @@ SECONDARY = {
     "gemm_f32": sec_gemm_f32,
     "gemm_general": sec_gemm_general,
     "collectives": sec_collectives,
+    "fp8_fnuz": sec_fp8_fnuz,
     "routing_check": sec_routing_check,
 }
 

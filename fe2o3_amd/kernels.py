@@ -214,6 +214,26 @@ def quantize_e4m3(x: DeviceBuffer, scale: DeviceBuffer, q: DeviceBuffer, stream=
           sync=sync)
 
 
+# gfx942 FNUZ fp8 formats (FE2O3_FP8_FNUZ_E4M3 / _E5M2)
+FNUZ_E4M3, FNUZ_E5M2 = 0, 1
+
+
+def fp8_fnuz_from_f32(x: DeviceBuffer, q: DeviceBuffer, fmt: int, stream=None,
+                      sync=True) -> None:
+    """q = Fp8E4M3Fnuz / Fp8E5M2Fnuz::from_f32(x) elementwise
+    (crates/fe2o3-device/src/fp8.rs:85-95, 193-203)."""
+    _call("fe2o3_fp8_fnuz_from_f32", x.ptr, x.count, q.ptr, q.count, fmt, stream=stream,
+          sync=sync)
+
+
+def fp8_fnuz_to_f32(q: DeviceBuffer, x: DeviceBuffer, fmt: int, stream=None,
+                    sync=True) -> None:
+    """x = Fp8E4M3Fnuz / Fp8E5M2Fnuz::to_f32(q) elementwise
+    (crates/fe2o3-device/src/fp8.rs:92-95, 200-203)."""
+    _call("fe2o3_fp8_fnuz_to_f32", q.ptr, q.count, x.ptr, x.count, fmt, stream=stream,
+          sync=sync)
+
+
 def gemm_fp8_nt(a, b, scale_a, scale_b, c, m, n, k, stream=None, sync=True) -> None:
     _call("fe2o3_gemm_fp8_nt", a.ptr, a.count, b.ptr, b.count, scale_a.ptr, scale_b.ptr,
           c.ptr, c.count, m, n, k, stream=stream, sync=sync)

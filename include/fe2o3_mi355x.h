@@ -402,6 +402,29 @@ int32_t fe2o3_moe_ffn_top2_noalloc(
     uint64_t weights_len, uint16_t *out, uint64_t out_len, uint32_t tokens,
     uint32_t hidden, uint32_t ffn, uint32_t experts, void *stream);
 
+/* ---- gfx942 FNUZ fp8 values ----------------------------------------------------------
+ * crates/fe2o3-device/src/fp8.rs:85-95 and :193-203 (Fp8E4M3Fnuz / Fp8E5M2Fnuz
+ * ::from_f32 and ::to_f32; bodies f32_to_fnuz / fnuz_to_f32, :296-381), over
+ * whole device arrays.  FNUZ: one unsigned zero 0x00, sole NaN 0x80, no
+ * infinities.  E4M3 FNUZ: bias 8, finite range +-240; E5M2 FNUZ: bias 16,
+ * +-57344.  The reference's packed Fp8*Fnuzx4 (fp8.rs:272-294, 435-518; lane i in bits
+ * 8i..8i+7) is the little-endian 32-bit view of four consecutive codes. */
+#define FE2O3_FP8_FNUZ_E4M3 0
+#define FE2O3_FP8_FNUZ_E5M2 1
+
+/* q[i] = from_f32(x[i]): round to nearest, ties to even; a magnitude above
+ * the largest finite value saturates to it; NaN and +-inf give 0x80;
+ * whatever rounds to zero (negative zero included) gives 0x00.  Any
+ * alignment (16-byte accesses when x and q are both 16-byte aligned).
+ * FE2O3_ERR_SHAPE for another format, FE2O3_ERR_LENGTH when the lengths
+ * differ; n = 0 launches nothing. */
+int32_t fe2o3_fp8_fnuz_from_f32(const float *x, uint64_t x_len, uint8_t *q,
+                                uint64_t q_len, int32_t format, void *stream);
+/* x[i] = to_f32(q[i]), exact; 0x80 gives the f32 bits 0xffc00000 (the
+ * negative quiet NaN gfx942 widens it to).  Errors as above. */
+int32_t fe2o3_fp8_fnuz_to_f32(const uint8_t *q, uint64_t q_len, float *x,
+                              uint64_t x_len, int32_t format, void *stream);
+
 /* ---- fp8 (OCP E4M3FN, per-tensor scale) ---------------------------------------------
  * Not in the reference (its only fp8 type is gfx942 FNUZ,
  * crates/fe2o3-device/src/fp8.rs:53-110, which gfx950's MFMA does not take):

@@ -241,6 +241,10 @@ void fe2o3o_moe_ffn_routes(const uint16_t *x, const uint16_t *w_gate,
 /* ---- OCP FP8 E4M3FN ------------------------------------------------------ */
 uint8_t fe2o3o_fp8e4m3_from_f32(float value);
 float fe2o3o_fp8e4m3_to_f32(uint8_t bits);
+/* gfx942 FNUZ fp8 (format 0 = E4M3, 1 = E5M2): crates/fe2o3-device/src/fp8.rs:296-381 */
+uint8_t fe2o3o_fnuz_from_f32_bits(uint32_t bits, int32_t format);
+uint32_t fe2o3o_fnuz_to_f32_bits(uint8_t q, int32_t format);
+void fe2o3o_fnuz_from_f32_array(const float *x, uint64_t n, int32_t format, uint8_t *q);
 float fe2o3o_amax_f32(const float *x, uint64_t n, int32_t threads);
 void fe2o3o_quantize_e4m3(const float *x, uint64_t n, float scale,
                           uint8_t *out, int32_t threads);

@@ -143,3 +143,88 @@ void fe2o3o_gemm_fp8_nt_rows(uint32_t n, uint32_t k, const uint8_t *a, const uin
     free(arow);
   }
 }
+
+/* ---- gfx942 FNUZ fp8 (Fp8E4M3Fnuz, Fp8E5M2Fnuz) ----------------------------
+ * Restates crates/fe2o3-device/src/fp8.rs:296-381 (f32_to_fnuz, fnuz_to_f32,
+ * round_shift_right_ties_even) with the format constants of
+ * Fp8E4M3Fnuz::from_f32 / to_f32 (:85-95: 3 fraction bits, bias 8, largest
+ * finite 240 = 0x43700000) and Fp8E5M2Fnuz (:193-203: 2 bits, bias 16,
+ * 57344 = 0x47600000).  FNUZ: one unsigned zero 0x00, sole NaN 0x80 (widened
+ * to the f32 bits 0xffc00000), no infinities; narrowing rounds to nearest,
+ * ties to even, saturates finite overflow to +-max, sends NaN and +-inf to
+ * 0x80 and everything that rounds to zero (negative zero included) to 0x00.
+ * format: 0 = E4M3 FNUZ, 1 = E5M2 FNUZ. */
+static void fnuz_format(int32_t format, int *mbits, int *bias, uint32_t *max_bits) {
+  if (format == 0) {
+    *mbits = 3; *bias = 8; *max_bits = 0x43700000u;
+  } else {
+    *mbits = 2; *bias = 16; *max_bits = 0x47600000u;
+  }
+}
+
+/* x / 2^s rounded to nearest, ties to even; x < 2^25 here, so every
+ * s >= 64 gives 0. */
+static uint64_t shr_rne(uint64_t x, unsigned s) {
+  if (s == 0) return x;
+  if (s >= 64) return 0; /* x < 2^25: at most 2^-39 of a unit, rounds to 0 */
+  uint64_t q = x >> s, r = x & ((1ull << s) - 1ull), half = 1ull << (s - 1);
+  return (r > half || (r == half && (q & 1ull))) ? q + 1ull : q;
+}
+
+uint8_t fe2o3o_fnuz_from_f32_bits(uint32_t bits, int32_t format) {
+  int mb, bias;
+  uint32_t maxb;
+  fnuz_format(format, &mb, &bias, &maxb);
+  const uint32_t mag = bits & 0x7fffffffu;
+  const uint8_t sign = (uint8_t)((bits >> 24) & 0x80u);
+  if (mag >= 0x7f800000u) return 0x80; /* NaN, +-inf */
+  if (mag == 0) return 0;
+  if (mag > maxb) return (uint8_t)(sign | 0x7f);
+  /* mag = sig * 2^(e - 23); an f32 subnormal (e = -127) is far below every
+   * FNUZ quantum and rounds to zero below whichever value sig takes */
+  const int e = (int)(mag >> 23) - 127;
+  const uint64_t sig = (uint64_t)((mag & 0x7fffffu) | 0x800000u);
+  const int emin = 1 - bias; /* exponent of the smallest normal */
+  uint32_t code;
+  if (e < emin) {
+    /* units of the subnormal quantum 2^(emin - mb): sig * 2^(e - 23 - emin + mb) */
+    const int s = 23 + emin - mb - e;
+    code = (uint32_t)shr_rne(sig, (unsigned)s); /* 2^mb (smallest normal) at most */
+    if (code == 0) return 0;
+  } else {
+    uint64_t m = shr_rne(sig, (unsigned)(23 - mb)); /* in [2^mb, 2^(mb+1)] */
+    int ef = e + bias;
+    if (m == (1ull << (mb + 1))) {
+      m >>= 1;
+      ef += 1;
+    }
+    code = ((uint32_t)ef << mb) | (uint32_t)(m & ((1u << mb) - 1u));
+  }
+  return (uint8_t)(sign | code);
+}
+
+uint32_t fe2o3o_fnuz_to_f32_bits(uint8_t q, int32_t format) {
+  int mb, bias;
+  uint32_t maxb;
+  fnuz_format(format, &mb, &bias, &maxb);
+  if (q == 0x80) return 0xffc00000u;
+  if (q == 0) return 0;
+  /* value = (-1)^s * frac * 2^(emin - mb) (exponent field 0), else
+   * (2^mb + frac) * 2^(ef - bias - mb); built as a double, exact, then
+   * narrowed (every FNUZ value is an f32 value) */
+  const int ef = (q & 0x7f) >> mb, frac = q & ((1 << mb) - 1);
+  double v = ef == 0 ? ldexp((double)frac, 1 - bias - mb)
+                     : ldexp((double)((1 << mb) + frac), ef - bias - mb);
+  float f = (float)((q & 0x80) ? -v : v);
+  uint32_t out;
+  memcpy(&out, &f, 4);
+  return out;
+}
+
+void fe2o3o_fnuz_from_f32_array(const float *x, uint64_t n, int32_t format, uint8_t *q) {
+  for (uint64_t i = 0; i < n; ++i) {
+    uint32_t b;
+    memcpy(&b, &x[i], 4);
+    q[i] = fe2o3o_fnuz_from_f32_bits(b, format);
+  }
+}

@@ -119,6 +119,9 @@ def _declare(L):
                                          i32]),
         "fe2o3o_fp8e4m3_from_f32": (C.c_uint8, [f32]),
         "fe2o3o_fp8e4m3_to_f32": (f32, [C.c_uint8]),
+        "fe2o3o_fnuz_from_f32_bits": (C.c_uint8, [u32, i32]),
+        "fe2o3o_fnuz_to_f32_bits": (u32, [C.c_uint8, i32]),
+        "fe2o3o_fnuz_from_f32_array": (None, [f32p, u64, i32, u8p]),
         "fe2o3o_amax_f32": (f32, [f32p, u64, i32]),
         "fe2o3o_quantize_e4m3": (None, [f32p, u64, f32, u8p, i32]),
         "fe2o3o_gemm_fp8_points": (None, [u32, u8p, u8p, u64, f32, f32p, u16p, i32]),
@@ -479,6 +482,30 @@ def fp8_from_f32(x: float) -> int:
 
 def fp8_to_f32(b: int) -> float:
     return lib().fe2o3o_fp8e4m3_to_f32(b)
+
+
+# gfx942 FNUZ fp8: format 0 = E4M3 FNUZ, 1 = E5M2 FNUZ
+FNUZ_E4M3, FNUZ_E5M2 = 0, 1
+
+
+def fnuz_from_f32_bits(bits: int, fmt: int) -> int:
+    return lib().fe2o3o_fnuz_from_f32_bits(bits, fmt)
+
+
+def fnuz_to_f32_bits(q: int, fmt: int) -> int:
+    return lib().fe2o3o_fnuz_to_f32_bits(q, fmt)
+
+
+def fnuz_from_f32(x, fmt: int) -> np.ndarray:
+    x = _c(x, np.float32).ravel()
+    out = np.zeros(x.size, np.uint8)
+    lib().fe2o3o_fnuz_from_f32_array(x, x.size, fmt, out)
+    return out
+
+
+def fnuz_decode_table(fmt: int) -> np.ndarray:
+    """f32 bit patterns of the 256 codes"""
+    return np.array([fnuz_to_f32_bits(i, fmt) for i in range(256)], np.uint32)
 
 
 def fp8_decode_table() -> np.ndarray:
