@@ -27,17 +27,33 @@ using namespace fe2o3;
 
 __global__ void zero_f32_kernel(float* p) { *p = 0.0f; }
 
+// A workgroup step covers 4096 elements as 1024 units of four (unit 256w + t
+// for thread t, w = 0..3): four 16-byte loads in flight per thread, each wave
+// access 1 KiB contiguous.  The rest
+// (fewer than 4096 elements) runs one unit, then one element, per thread.
+constexpr uint64_t kStepUnits = 1024;
+
 __global__ void __launch_bounds__(256) amax_kernel(const float* __restrict__ x, uint64_t n,
                                                    float* __restrict__ amax) {
   float m = 0.0f;
+  const uint64_t t = threadIdx.x;
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  const uint64_t n4 = n / 4;
+  const uint64_t units = n / 4, steps = units / kStepUnits;
   const f32x4_t* x4 = reinterpret_cast<const f32x4_t*>(x);
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-    const f32x4_t v = __builtin_nontemporal_load(x4 + i);
-    m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  auto max4 = [](f32x4_t v) {
+    return fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  };
+  for (uint64_t st = blockIdx.x; st < steps; st += gridDim.x) {
+    const uint64_t u0 = st * kStepUnits + t;
+    f32x4_t v[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) v[w] = __builtin_nontemporal_load(x4 + u0 + 256 * w);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) m = fmaxf(m, max4(v[w]));
   }
-  for (uint64_t i = n4 * 4 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+  for (uint64_t u = steps * kStepUnits + blockIdx.x * blockDim.x + t; u < units; u += stride)
+    m = fmaxf(m, max4(x4[u]));
+  for (uint64_t i = units * 4 + blockIdx.x * blockDim.x + t; i < n; i += stride)
     m = fmaxf(m, fabsf(x[i]));
   // One device-scope atomic per workgroup: atomics on one address from every
   // wave serialize and cost more than the read of the tensor.
@@ -57,22 +73,35 @@ __global__ void scale_kernel(const float* amax, float* scale) {
   *scale = a / 448.0f;
 }
 
+// Same step layout as amax_kernel: four units (16 elements) in flight per
+// thread, 16-byte loads and 4-byte stores of codes, each wave access
+// contiguous.
 __global__ void __launch_bounds__(256) quantize_kernel(const float* __restrict__ x, uint64_t n,
                                                        const float* __restrict__ scale,
                                                        uint8_t* __restrict__ q) {
   const float s = *scale;
+  const uint64_t t = threadIdx.x;
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  const uint64_t n4 = n / 4;
+  const uint64_t units = n / 4, steps = units / kStepUnits;
   const f32x4_t* x4 = reinterpret_cast<const f32x4_t*>(x);
   uint32_t* q4 = reinterpret_cast<uint32_t*>(q);
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-    const f32x4_t v = __builtin_nontemporal_load(x4 + i);
+  auto code4 = [s](f32x4_t v) {
     uint32_t packed = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) packed |= (uint32_t)e4m3_from_f32(v[e] / s) << (8 * e);
-    q4[i] = packed;
+    return packed;
+  };
+  for (uint64_t st = blockIdx.x; st < steps; st += gridDim.x) {
+    const uint64_t u0 = st * kStepUnits + t;
+    f32x4_t v[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) v[w] = __builtin_nontemporal_load(x4 + u0 + 256 * w);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) q4[u0 + 256 * w] = code4(v[w]);
   }
-  for (uint64_t i = n4 * 4 + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+  for (uint64_t u = steps * kStepUnits + blockIdx.x * blockDim.x + t; u < units; u += stride)
+    q4[u] = code4(x4[u]);
+  for (uint64_t i = units * 4 + blockIdx.x * blockDim.x + t; i < n; i += stride)
     q[i] = e4m3_from_f32(x[i] / s);
 }
 
@@ -238,8 +267,9 @@ __global__ void __launch_bounds__(256) zero_fill_bf16_kernel(uint16_t* __restric
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) c[i] = 0;
 }
 
+// one workgroup per 4096-element step, at most 8192 striding over the rest
 unsigned grid_for(uint64_t n) {
-  uint64_t b = (n / 4 + 255) / 256;
+  uint64_t b = (n + 4095) / 4096;
   if (b == 0) b = 1;
   return (unsigned)(b < 8192 ? b : 8192);
 }
