@@ -17,35 +17,29 @@
 
 namespace fe2o3 {
 
+// Branch-free (the kernels run it per lane, where a branch per case would
+// diverge): the magnitude is clamped to 448 (code 0x7e), which saturates
+// larger values and infinities; with E the biased binary32 exponent and sig
+// the 24-bit significand, the value in units of the target quantum
+// 2^(max(E-127, -6) - 3) is sig >> s, s = 20 + max(121 - E, 0) clamped to 31
+// (sig < 2^24, so any shift of 25 or more gives 0), rounded to nearest even
+// by adding half a unit less one plus the kept lsb.  The code is then
+// (max(E - 121, 0) << 3) + q: a carry into the next binade lands in the
+// exponent field, and a subnormal result needs no separate path.  Zero keeps
+// its sign (OCP E4M3FN has -0); NaN gives S.1111.111.
 FE2O3_HD uint8_t e4m3_from_bits(uint32_t bits) {
-  const uint8_t sign = (uint8_t)((bits >> 24) & 0x80u);
+  const uint32_t sign = (bits >> 24) & 0x80u;
   const uint32_t mag = bits & 0x7fffffffu;
-  if (mag > 0x7f800000u) return (uint8_t)(sign | 0x7f);   // NaN
-  if (mag >= 0x43e00000u) return (uint8_t)(sign | 0x7e);  // |x| >= 448 (and inf) saturate
-  const int exp = (int)(mag >> 23);                       // biased binary32 exponent
-  const uint32_t mant = (mag & 0x7fffffu) | (exp ? 0x800000u : 0u);
-  const int unbiased = exp ? exp - 127 : -126;
-  // quantum of the target e4m3 binade: 2^-9 when subnormal, else 2^(unbiased-3)
-  const int q = unbiased < -6 ? -9 : unbiased - 3;
-  // |x| = mant * 2^(unbiased-23); r = round(|x| / 2^q) = round(mant / 2^shift)
-  const int shift = q - unbiased + 23;  // >= 20
-  uint32_t r = 0;
-  if (shift < 32) {  // shift >= 32 leaves mant / 2^shift < 1/2: rounds to 0
-    const uint32_t whole = mant >> shift;
-    const uint32_t rem = mant & ((1u << shift) - 1u);
-    const uint32_t half = 1u << (shift - 1);
-    r = whole + ((rem > half || (rem == half && (whole & 1u))) ? 1u : 0u);
-  }
-  if (r == 0) return sign;
-  if (unbiased < -6) return (uint8_t)(sign | (r < 8 ? r : 0x08u));  // r == 8 is 2^-6, the first normal
-  int e = unbiased + 7;
-  if (r == 16) {  // rounding carried into the next binade
-    r = 8;
-    e += 1;
-  }
-  uint32_t code = ((uint32_t)e << 3) | (r - 8);
-  if (code > 0x7eu) code = 0x7eu;  // values rounding above 448 saturate
-  return (uint8_t)(sign | code);
+  const uint32_t m = mag < 0x43e00000u ? mag : 0x43e00000u;
+  const int E = (int)(m >> 23);
+  const uint32_t sig = (m & 0x7fffffu) | 0x800000u;
+  int s = 141 - E;
+  s = s > 20 ? s : 20;
+  s = s < 31 ? s : 31;
+  const uint32_t q = (sig + ((1u << (s - 1)) - 1u) + ((sig >> s) & 1u)) >> s;
+  const int ef = E - 121;
+  const uint32_t code = ((uint32_t)(ef > 0 ? ef : 0) << 3) + q;
+  return (uint8_t)(mag > 0x7f800000u ? (sign | 0x7fu) : (sign | code));
 }
 
 // E4M3FN -> bf16 bits, exact: every E4M3 value has at most 4 significant
