@@ -87,10 +87,12 @@ FE2O3_DEVICE float swap_half(float v) {
 // already touches every element.
 FE2O3_DEVICE float finite_probe(float acc, float x) { return __builtin_fmaf(x, 0.0f, acc); }
 
-// Marks the device's contract-status word (fe2o3_host::status_word) with a
-// vector atomic; only the rejecting path calls it.
+// Counts one rejection in the device's non-finite counter
+// (fe2o3_host::status_word) with a vector atomic add; only the rejecting
+// path calls it, from one lane.  The counter is never cleared: the host
+// reports each change of it once (status_track.hpp).
 FE2O3_DEVICE void mark_nonfinite(uint32_t* status) {
-  __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_add(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Canonical quiet NaN, the sentinel output of a rejected row or tile.

@@ -192,23 +192,24 @@ template <bool CAUSAL>
 __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse,
-    uint32_t seq, uint32_t heads, float scale_log2, uint32_t paired) {
+    uint32_t seq, uint32_t heads, float scale_log2, uint32_t paired, uint32_t xcds) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
   const uint32_t lr = lane & 31u, g = lane >> 5;
-  // Workgroup order.  Workgroup id i runs on XCD i % 8.  When heads % 8 == 0
-  // the ids are laid out so that XCD x walks heads x, x+8, x+16, ... and,
-  // for each, all of its query tiles back to back: the tiles of one head run
-  // together on one XCD and share their K/V through that XCD's L2.  Within a
-  // head the causal order is heaviest tile (most key tiles) first.
+  // Workgroup order.  Workgroup id i runs on XCD i % xcds (the device's XCD
+  // count, 8 on MI355X).  When xcds divides heads the ids are laid out so
+  // that XCD x walks heads x, x + xcds, x + 2 xcds, ... and, for each, all of
+  // its query tiles back to back: the tiles of one head run together on one
+  // XCD and share their K/V through that XCD's L2.  Within a head the causal
+  // order is heaviest tile (most key tiles) first.
   // With `paired`, a workgroup runs two query tiles of one head, r then
   // nq-1-r, so every causal workgroup does the same nq+1 key tiles.
   const uint32_t nq = (seq + BQ - 1u) / BQ;  // the last tile may be partial
   const uint32_t per_head = paired ? nq / 2u : nq;
   uint32_t bh, rank;
-  if (heads % 8u == 0u) {
-    const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
-    bh = (slot / per_head) * 8u + xcd;
+  if (xcds > 1u && heads % xcds == 0u) {
+    const uint32_t xcd = blockIdx.x % xcds, slot = blockIdx.x / xcds;
+    bh = (slot / per_head) * xcds + xcd;
     rank = slot % per_head;
   } else {
     bh = blockIdx.x / per_head;
@@ -466,13 +467,16 @@ int32_t fe2o3_flash_attention_fwd(const uint16_t* q, uint64_t q_len, const uint1
   const uint32_t paired = causal && nq % 2u == 0u ? 1u : 0u;
   const uint64_t wgs = (uint64_t)nq / (paired ? 2u : 1u) * bh;
   if (wgs > 0x7fffffffu) return FE2O3_ERR_SHAPE;
+  tile_plan::Topology topo;
+  const int32_t topo_rc = fe2o3_host::device_topology(&topo);
+  if (topo_rc != FE2O3_OK) return topo_rc;
   const dim3 grid((unsigned)wgs);
   if (causal)
     flash_fwd_kernel<true><<<grid, THREADS, SMEM_BYTES, (hipStream_t)stream>>>(
-        q, k, v, o, lse, seq, (uint32_t)bh, scale_log2, paired);
+        q, k, v, o, lse, seq, (uint32_t)bh, scale_log2, paired, topo.xcds);
   else
     flash_fwd_kernel<false><<<grid, THREADS, SMEM_BYTES, (hipStream_t)stream>>>(
-        q, k, v, o, lse, seq, (uint32_t)bh, scale_log2, paired);
+        q, k, v, o, lse, seq, (uint32_t)bh, scale_log2, paired, topo.xcds);
   return fe2o3_host::after_launch();
 }
 

@@ -119,12 +119,12 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
                                                           const float* __restrict__ scale_a,
                                                           const float* __restrict__ scale_b,
                                                           uint16_t* __restrict__ c, uint32_t m,
-                                                          uint32_t n, uint32_t k) {
+                                                          uint32_t n, uint32_t k, uint32_t xcds) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const uint32_t tiles_m = EDGE ? (m + 255u) / 256u : m / 256u;
   const uint32_t tiles_n = EDGE ? (n + 255u) / 256u : n / 256u;
   uint32_t tm, tn;
-  gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, xcds, &tm, &tn);
   const uint32_t rows_a = EDGE ? min(256u, m - tm * 256u) : 256u;
   const uint32_t rows_b = EDGE ? min(256u, n - tn * 256u) : 256u;
   const uint32_t k16 = k / 2;  // rows addressed in 16-bit units
@@ -168,13 +168,13 @@ template <int STAGES, bool WHOLE, bool TAIL = false>
 __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_fp8_128_kernel(
     const uint8_t* __restrict__ a, const uint8_t* __restrict__ b, const float* __restrict__ scale_a,
     const float* __restrict__ scale_b, uint16_t* __restrict__ c, uint32_t m, uint32_t n,
-    uint32_t k, uint32_t first_big = 0) {
+    uint32_t k, uint32_t xcds, uint32_t first_big = 0) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   uint32_t tm, tn;
   if constexpr (TAIL) {
-    if (!gemm_core::tail_quarter(blockIdx.x, first_big, m, n, &tm, &tn)) return;
+    if (!gemm_core::tail_quarter(blockIdx.x, first_big, m, n, xcds, &tm, &tn)) return;
   } else {
-    gemm_core::xcd_tile_order(blockIdx.x, (m + 127u) / 128u, (n + 127u) / 128u, &tm, &tn);
+    gemm_core::xcd_tile_order(blockIdx.x, (m + 127u) / 128u, (n + 127u) / 128u, xcds, &tm, &tn);
   }
   const uint32_t rows_a = WHOLE ? 128u : min(128u, m - tm * 128u);
   const uint32_t rows_b = WHOLE ? 128u : min(128u, n - tn * 128u);
@@ -196,12 +196,6 @@ __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_fp8_128_kernel(
   gemm_pipe::store_bf16_fp8_128<WHOLE>(acc, c + (uint64_t)tm * 128 * n + (uint64_t)tn * 128, n,
                                        rows_a, rows_b);
 }
-
-// MI355X's CUs, and at most this many 256 x 256 tiles (half of them) the
-// GEMM runs on 128 x 128 tiles (or, for the last of several rounds, its
-// tiles run as 128 x 128 quarters).
-constexpr uint64_t kFp8CUs = 256;
-constexpr uint64_t kFp8SmallGrid = 128;
 
 // ---- any shape ---------------------------------------------------------------------------
 // 64x64 output tiles, 32 k per step; each operand element is widened to bf16
@@ -351,81 +345,80 @@ int32_t fe2o3_gemm_fp8_nt(const uint8_t* a, uint64_t a_len, const uint8_t* b, ui
     gemm_fp8_generic_kernel<<<grid, 256, 0, s>>>(a, b, scale_a, scale_b, c, m, n, k);
     return fe2o3_host::after_launch();
   }
-  static const int32_t lds_rc = fe2o3_host::set_dynamic_lds(
-      {(const void*)gemm_fp8_kernel<false, false>, (const void*)gemm_fp8_kernel<true, false>,
-       (const void*)gemm_fp8_kernel<false, true>},
-      kFp8Smem);
+  // every kernel's LDS limit is raised before anything is launched, so a
+  // failure leaves C untouched
+  static const int32_t lds_rc = [] {
+    int32_t rc = fe2o3_host::set_dynamic_lds(
+        {(const void*)gemm_fp8_kernel<false, false>, (const void*)gemm_fp8_kernel<true, false>,
+         (const void*)gemm_fp8_kernel<false, true>},
+        kFp8Smem);
+    if (rc == FE2O3_OK)
+      rc = fe2o3_host::set_dynamic_lds(
+          {(const void*)gemm_fp8_128_kernel<2, true>, (const void*)gemm_fp8_128_kernel<2, false>,
+           (const void*)gemm_fp8_128_kernel<2, true, true>,
+           (const void*)gemm_fp8_128_kernel<2, false, true>},
+          kFp8SmallSmem<2>);
+    if (rc == FE2O3_OK)
+      rc = fe2o3_host::set_dynamic_lds(
+          {(const void*)gemm_fp8_128_kernel<3, true>, (const void*)gemm_fp8_128_kernel<3, false>,
+           (const void*)gemm_fp8_128_kernel<3, true, true>,
+           (const void*)gemm_fp8_128_kernel<3, false, true>},
+          kFp8SmallSmem<3>);
+    return rc;
+  }();
   if (lds_rc != FE2O3_OK) return lds_rc;
+  tile_plan::Topology topo;
+  const int32_t topo_rc = fe2o3_host::device_topology(&topo);
+  if (topo_rc != FE2O3_OK) return topo_rc;
+  const tile_plan::Plan plan = tile_plan::plan(m, n, topo);
+  if (plan.grid > 0x7fffffffu || plan.tail_grid > 0x7fffffffu) return FE2O3_ERR_SHAPE;
+  const uint32_t xcds = topo.xcds;
   const bool whole = m % 256 == 0 && n % 256 == 0 && ((uintptr_t)c & 15u) == 0;
-  const uint64_t tiles = (uint64_t)((m + 255) / 256) * ((n + 255) / 256);
-  if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
-  if (tiles <= kFp8SmallGrid) {  // 256 x 256 tiles would leave most CUs idle
-    static const int32_t small2_rc = fe2o3_host::set_dynamic_lds(
-        {(const void*)gemm_fp8_128_kernel<2, true>, (const void*)gemm_fp8_128_kernel<2, false>},
-        kFp8SmallSmem<2>);
-    static const int32_t small3_rc = fe2o3_host::set_dynamic_lds(
-        {(const void*)gemm_fp8_128_kernel<3, true>, (const void*)gemm_fp8_128_kernel<3, false>},
-        kFp8SmallSmem<3>);
-    if (small2_rc != FE2O3_OK) return small2_rc;
-    if (small3_rc != FE2O3_OK) return small3_rc;
-    const uint64_t t128 = (uint64_t)((m + 127) / 128) * ((n + 127) / 128);
-    const bool whole128 = m % 128 == 0 && n % 128 == 0 && ((uintptr_t)c & 15u) == 0;
-    const unsigned g = (unsigned)t128;
-    if (t128 > 2 * kFp8SmallGrid) {
+  const bool whole128 = m % 128 == 0 && n % 128 == 0 && ((uintptr_t)c & 15u) == 0;
+  const float* sa = scale_a;
+  const float* sb = scale_b;
+  if (plan.small) {  // 256 x 256 tiles would leave most CUs idle
+    const unsigned g = (unsigned)plan.grid;
+    if (plan.stages == 2) {
       if (whole128)
-        gemm_fp8_128_kernel<2, true><<<g, 256, kFp8SmallSmem<2>, s>>>(a, b, scale_a, scale_b, c,
-                                                                      m, n, k);
+        gemm_fp8_128_kernel<2, true><<<g, 256, kFp8SmallSmem<2>, s>>>(a, b, sa, sb, c, m, n, k,
+                                                                      xcds);
       else
-        gemm_fp8_128_kernel<2, false><<<g, 256, kFp8SmallSmem<2>, s>>>(a, b, scale_a, scale_b, c,
-                                                                       m, n, k);
+        gemm_fp8_128_kernel<2, false><<<g, 256, kFp8SmallSmem<2>, s>>>(a, b, sa, sb, c, m, n, k,
+                                                                       xcds);
     } else if (whole128) {
-      gemm_fp8_128_kernel<3, true><<<g, 256, kFp8SmallSmem<3>, s>>>(a, b, scale_a, scale_b, c, m,
-                                                                    n, k);
+      gemm_fp8_128_kernel<3, true><<<g, 256, kFp8SmallSmem<3>, s>>>(a, b, sa, sb, c, m, n, k, xcds);
     } else {
-      gemm_fp8_128_kernel<3, false><<<g, 256, kFp8SmallSmem<3>, s>>>(a, b, scale_a, scale_b, c,
-                                                                     m, n, k);
+      gemm_fp8_128_kernel<3, false><<<g, 256, kFp8SmallSmem<3>, s>>>(a, b, sa, sb, c, m, n, k,
+                                                                     xcds);
     }
     return fe2o3_host::after_launch();
   }
-  // A last round of at most kFp8SmallGrid tiles runs as 128 x 128 quarters
-  // on all CUs after the full rounds.
-  const uint64_t full = tiles / kFp8CUs * kFp8CUs, rest = tiles - full;
-  const bool tail = full > 0 && rest > 0 && rest <= kFp8SmallGrid;
-  const unsigned big = (unsigned)(tail ? full : tiles);
+  const unsigned big = (unsigned)plan.grid;
   if (!whole)
-    gemm_fp8_kernel<false, true><<<big, 256, kFp8Smem, s>>>(a, b, scale_a, scale_b, c, m, n, k);
+    gemm_fp8_kernel<false, true><<<big, 256, kFp8Smem, s>>>(a, b, sa, sb, c, m, n, k, xcds);
   else if (gemm_core::staged_epilogue(((uint64_t)m + n) * k))
-    gemm_fp8_kernel<true, false><<<big, 256, kFp8Smem, s>>>(a, b, scale_a, scale_b, c, m, n, k);
+    gemm_fp8_kernel<true, false><<<big, 256, kFp8Smem, s>>>(a, b, sa, sb, c, m, n, k, xcds);
   else
-    gemm_fp8_kernel<false, false><<<big, 256, kFp8Smem, s>>>(a, b, scale_a, scale_b, c, m, n, k);
-  if (tail) {
-    static const int32_t tail2_rc = fe2o3_host::set_dynamic_lds(
-        {(const void*)gemm_fp8_128_kernel<2, true, true>,
-         (const void*)gemm_fp8_128_kernel<2, false, true>},
-        kFp8SmallSmem<2>);
-    static const int32_t tail3_rc = fe2o3_host::set_dynamic_lds(
-        {(const void*)gemm_fp8_128_kernel<3, true, true>,
-         (const void*)gemm_fp8_128_kernel<3, false, true>},
-        kFp8SmallSmem<3>);
-    if (tail2_rc != FE2O3_OK) return tail2_rc;
-    if (tail3_rc != FE2O3_OK) return tail3_rc;
-    const bool whole128 = m % 128 == 0 && n % 128 == 0 && ((uintptr_t)c & 15u) == 0;
-    const unsigned g = (unsigned)((rest + 7) / 8 * 32);  // 4 quarters, 8 per XCD row
-    const uint32_t first = (uint32_t)full;
-    if (4 * rest > kFp8CUs) {  // more quarters than CUs: two-stage, two per CU
-      if (whole128)
-        gemm_fp8_128_kernel<2, true, true><<<g, 256, kFp8SmallSmem<2>, s>>>(
-            a, b, scale_a, scale_b, c, m, n, k, first);
-      else
-        gemm_fp8_128_kernel<2, false, true><<<g, 256, kFp8SmallSmem<2>, s>>>(
-            a, b, scale_a, scale_b, c, m, n, k, first);
-    } else if (whole128) {
-      gemm_fp8_128_kernel<3, true, true><<<g, 256, kFp8SmallSmem<3>, s>>>(
-          a, b, scale_a, scale_b, c, m, n, k, first);
-    } else {
-      gemm_fp8_128_kernel<3, false, true><<<g, 256, kFp8SmallSmem<3>, s>>>(
-          a, b, scale_a, scale_b, c, m, n, k, first);
-    }
+    gemm_fp8_kernel<false, false><<<big, 256, kFp8Smem, s>>>(a, b, sa, sb, c, m, n, k, xcds);
+  const int32_t big_rc = fe2o3_host::after_launch();
+  if (big_rc != FE2O3_OK || !plan.tail) return big_rc;
+  // the last round of at most half the CUs' tiles as 128 x 128 quarters
+  const unsigned g = (unsigned)plan.tail_grid;
+  const uint32_t first = plan.first_big;
+  if (plan.tail_stages == 2) {  // more quarters than CUs: two per CU
+    if (whole128)
+      gemm_fp8_128_kernel<2, true, true><<<g, 256, kFp8SmallSmem<2>, s>>>(a, b, sa, sb, c, m, n, k,
+                                                                          xcds, first);
+    else
+      gemm_fp8_128_kernel<2, false, true><<<g, 256, kFp8SmallSmem<2>, s>>>(a, b, sa, sb, c, m, n,
+                                                                           k, xcds, first);
+  } else if (whole128) {
+    gemm_fp8_128_kernel<3, true, true><<<g, 256, kFp8SmallSmem<3>, s>>>(a, b, sa, sb, c, m, n, k,
+                                                                        xcds, first);
+  } else {
+    gemm_fp8_128_kernel<3, false, true><<<g, 256, kFp8SmallSmem<3>, s>>>(a, b, sa, sb, c, m, n, k,
+                                                                         xcds, first);
   }
   return fe2o3_host::after_launch();
 }

@@ -409,11 +409,11 @@ FE2O3_DEVICE void general_epilogue(const Acc& acc, float* c_tile, uint32_t rows,
 __global__ void __launch_bounds__(256, 1) gemm_general_pipe_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, float* __restrict__ c,
     uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha,
-    float beta) {
+    float beta, uint32_t xcds) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const uint32_t tiles_m = (m + 255u) / 256u, tiles_n = (n + 255u) / 256u;
   uint32_t tm, tn;
-  gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, &tm, &tn);
+  gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, xcds, &tm, &tn);
   const uint32_t rows = min(256u, m - tm * 256u), cols = min(256u, n - tn * 256u);
   const auto ar = gemm_pipe::dense_rows<kGpRowBytes>(a + (uint64_t)tm * 256u * lda, lda, rows, k);
   const auto br = gemm_pipe::kn_rows(b + (uint64_t)tn * 256u, ldb, cols, k);
@@ -440,13 +440,13 @@ template <int STAGES, bool TAIL = false>
 __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_general_pipe128_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, float* __restrict__ c,
     uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha,
-    float beta, uint32_t first_big = 0) {
+    float beta, uint32_t xcds, uint32_t first_big = 0) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   uint32_t tm, tn;
   if constexpr (TAIL) {
-    if (!gemm_core::tail_quarter(blockIdx.x, first_big, m, n, &tm, &tn)) return;
+    if (!gemm_core::tail_quarter(blockIdx.x, first_big, m, n, xcds, &tm, &tn)) return;
   } else {
-    gemm_core::xcd_tile_order(blockIdx.x, (m + 127u) / 128u, (n + 127u) / 128u, &tm, &tn);
+    gemm_core::xcd_tile_order(blockIdx.x, (m + 127u) / 128u, (n + 127u) / 128u, xcds, &tm, &tn);
   }
   const uint32_t rows = min(128u, m - tm * 128u), cols = min(128u, n - tn * 128u);
   const auto ar =
@@ -469,13 +469,6 @@ const fe2o3_host::KernelRegistrar kRegisteredPipe[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<3>", (const void*)gemm_general_pipe128_kernel<3>, 256, kGp64Smem<3>}),
     fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<2, tail>", (const void*)gemm_general_pipe128_kernel<2, true>, 256, kGp64Smem<2>}),
     fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<3, tail>", (const void*)gemm_general_pipe128_kernel<3, true>, 256, kGp64Smem<3>})};
-
-// MI355X's CUs; at most kSmallGrid 256 x 256 tiles (half of them), the GEMM
-// runs on 128 x 128 tiles instead, three-stage up to 2 kSmallGrid of them
-// (one per CU), and a last round of at most kSmallGrid tiles after full
-// rounds runs as 128 x 128 quarters.
-constexpr uint64_t kCUs = 256;
-constexpr uint64_t kSmallGrid = 128;
 
 // Host: whether the pipelined tile takes this general GEMM: whole 64-k
 // stages, 16-byte aligned rows of A and B, and both operands' panels within
@@ -503,51 +496,48 @@ int32_t general_gemm(const uint16_t* a, uint64_t a_len, const uint16_t* b, uint6
   if (m == 0 || n == 0) return FE2O3_OK;  // empty output: no dispatch
   if ((ea && !a) || (eb && !b) || !c) return FE2O3_ERR_NULL;
   if (general_pipe_ok(a, b, k, lda, ldb)) {
-    static const int32_t lds_rc =
-        fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe_kernel}, kGpSmem);
+    // every kernel's LDS limit is raised before anything is launched, so a
+    // failure leaves C untouched
+    static const int32_t lds_rc = [] {
+      int32_t rc = fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe_kernel}, kGpSmem);
+      if (rc == FE2O3_OK)
+        rc = fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe128_kernel<2>,
+                                          (const void*)gemm_general_pipe128_kernel<2, true>},
+                                         kGp64Smem<2>);
+      if (rc == FE2O3_OK)
+        rc = fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe128_kernel<3>,
+                                          (const void*)gemm_general_pipe128_kernel<3, true>},
+                                         kGp64Smem<3>);
+      return rc;
+    }();
     if (lds_rc != FE2O3_OK) return lds_rc;
-    static const int32_t lds128_rc =
-        fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe128_kernel<2>}, kGp64Smem<2>);
-    static const int32_t lds128s3_rc =
-        fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe128_kernel<3>}, kGp64Smem<3>);
-    if (lds128_rc != FE2O3_OK) return lds128_rc;
-    if (lds128s3_rc != FE2O3_OK) return lds128s3_rc;
-    const uint64_t tiles = (uint64_t)((m + 255) / 256) * ((n + 255) / 256);
-    if (tiles > 0x7fffffffu) return FE2O3_ERR_SHAPE;
-    if (tiles <= kSmallGrid) {  // 256 x 256 tiles would leave most CUs idle
-      const uint64_t tiles128 = (uint64_t)((m + 127) / 128) * ((n + 127) / 128);
-      if (tiles128 > kSmallGrid * 2)
-        gemm_general_pipe128_kernel<2><<<(unsigned)tiles128, 256, kGp64Smem<2>,
-                                         (hipStream_t)stream>>>(a, b, c, m, n, k, lda, ldb, ldc,
-                                                                alpha, beta);
+    tile_plan::Topology topo;
+    const int32_t topo_rc = fe2o3_host::device_topology(&topo);
+    if (topo_rc != FE2O3_OK) return topo_rc;
+    const tile_plan::Plan plan = tile_plan::plan(m, n, topo);
+    if (plan.grid > 0x7fffffffu || plan.tail_grid > 0x7fffffffu) return FE2O3_ERR_SHAPE;
+    const uint32_t xcds = topo.xcds;
+    hipStream_t s = (hipStream_t)stream;
+    if (plan.small) {  // 256 x 256 tiles would leave most CUs idle
+      if (plan.stages == 2)
+        gemm_general_pipe128_kernel<2><<<(unsigned)plan.grid, 256, kGp64Smem<2>, s>>>(
+            a, b, c, m, n, k, lda, ldb, ldc, alpha, beta, xcds);
       else
-        gemm_general_pipe128_kernel<3><<<(unsigned)tiles128, 256, kGp64Smem<3>,
-                                         (hipStream_t)stream>>>(a, b, c, m, n, k, lda, ldb, ldc,
-                                                                alpha, beta);
+        gemm_general_pipe128_kernel<3><<<(unsigned)plan.grid, 256, kGp64Smem<3>, s>>>(
+            a, b, c, m, n, k, lda, ldb, ldc, alpha, beta, xcds);
       return fe2o3_host::after_launch();
     }
-    // a last round of at most kSmallGrid tiles runs as 128 x 128 quarters
-    // on all CUs after the full rounds
-    const uint64_t full = tiles / kCUs * kCUs, rest = tiles - full;
-    const bool tail = full > 0 && rest > 0 && rest <= kSmallGrid;
-    hipStream_t s = (hipStream_t)stream;
-    gemm_general_pipe_kernel<<<(unsigned)(tail ? full : tiles), 256, kGpSmem, s>>>(
-        a, b, c, m, n, k, lda, ldb, ldc, alpha, beta);
-    if (tail) {
-      static const int32_t tail2_rc = fe2o3_host::set_dynamic_lds(
-          {(const void*)gemm_general_pipe128_kernel<2, true>}, kGp64Smem<2>);
-      static const int32_t tail3_rc = fe2o3_host::set_dynamic_lds(
-          {(const void*)gemm_general_pipe128_kernel<3, true>}, kGp64Smem<3>);
-      if (tail2_rc != FE2O3_OK) return tail2_rc;
-      if (tail3_rc != FE2O3_OK) return tail3_rc;
-      const unsigned g = (unsigned)((rest + 7) / 8 * 32);  // 4 quarters, 8 per XCD row
-      if (4 * rest > kCUs)  // more quarters than CUs: two-stage, two per CU
-        gemm_general_pipe128_kernel<2, true><<<g, 256, kGp64Smem<2>, s>>>(
-            a, b, c, m, n, k, lda, ldb, ldc, alpha, beta, (uint32_t)full);
-      else
-        gemm_general_pipe128_kernel<3, true><<<g, 256, kGp64Smem<3>, s>>>(
-            a, b, c, m, n, k, lda, ldb, ldc, alpha, beta, (uint32_t)full);
-    }
+    gemm_general_pipe_kernel<<<(unsigned)plan.grid, 256, kGpSmem, s>>>(a, b, c, m, n, k, lda, ldb,
+                                                                        ldc, alpha, beta, xcds);
+    const int32_t big_rc = fe2o3_host::after_launch();
+    if (big_rc != FE2O3_OK || !plan.tail) return big_rc;
+    // the last round of at most half the CUs' tiles as 128 x 128 quarters
+    if (plan.tail_stages == 2)  // more quarters than CUs: two per CU
+      gemm_general_pipe128_kernel<2, true><<<(unsigned)plan.tail_grid, 256, kGp64Smem<2>, s>>>(
+          a, b, c, m, n, k, lda, ldb, ldc, alpha, beta, xcds, plan.first_big);
+    else
+      gemm_general_pipe128_kernel<3, true><<<(unsigned)plan.tail_grid, 256, kGp64Smem<3>, s>>>(
+          a, b, c, m, n, k, lda, ldb, ldc, alpha, beta, xcds, plan.first_big);
     return fe2o3_host::after_launch();
   }
   dim3 grid((n + G_BN - 1) / G_BN, (m + G_BM - 1) / G_BM);

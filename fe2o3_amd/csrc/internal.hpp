@@ -7,6 +7,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include "tile_plan.hpp"
+
 namespace fe2o3_host {
 
 // True when the environment variable FE2O3_FAULT_POINT names `entry`: the
@@ -25,13 +27,21 @@ inline int32_t set_dynamic_lds(std::initializer_list<const void*> fns, int bytes
   return 0;
 }
 
-// The current device's contract-status word: a device address that kernels
-// admitting only finite inputs receive as an argument and mark (atomic OR of
-// kStatusNonFinite) when they find a NaN or an infinity.  Each device has its
-// own copy of the word (a file-scope __device__ variable of runtime.hip,
-// located once per device with hipGetSymbolAddress).  nullptr on failure.
-constexpr uint32_t kStatusNonFinite = 1u;
+// The current device's non-finite counter: a device address that kernels
+// admitting only finite inputs receive as an argument and add 1 to
+// (mark_nonfinite) when they find a NaN or an infinity.  Each device has its
+// own counter (a file-scope __device__ variable of runtime.hip, located once
+// per device with hipGetSymbolAddress); nothing clears it, and a
+// synchronize reports a count it has not reported before as
+// FE2O3_ERR_NONFINITE (status_track.hpp).  nullptr on failure.
 uint32_t* status_word();
+
+// The current device's CU and XCD counts as the runtime reports them
+// (hipDeviceAttributeMultiprocessorCount, hipDeviceAttributeNumberOfXccs),
+// queried once per device and cached.  0, or the hipError_t of the query.
+// An XCD count the runtime does not report is taken as 1 (the tile orders
+// then stay in id order, which is correct on any part).
+int32_t device_topology(tile_plan::Topology* out);
 
 // Enqueue status: 0, or the hipError_t of the launch just made.
 inline int32_t after_launch() {

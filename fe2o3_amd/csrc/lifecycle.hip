@@ -47,6 +47,7 @@
 #include <unistd.h>
 
 #include "../../include/fe2o3_mi355x.h"
+#include "codeobj_inspect.hpp"
 #include "internal.hpp"
 
 #include "slice1_artifact.inc"
@@ -161,11 +162,6 @@ void hash_str(Sha256& d, const char* s) { hash_field(d, s, std::strlen(s)); }
 
 void put_le64(uint8_t* p, uint64_t v) {
   for (int i = 0; i < 8; ++i) p[i] = (uint8_t)(v >> (8 * i));
-}
-uint64_t get_le(const uint8_t* p, int n) {
-  uint64_t v = 0;
-  for (int i = 0; i < n; ++i) v |= (uint64_t)p[i] << (8 * i);
-  return v;
 }
 
 // ---- the exact profile ----------------------------------------------------------------
@@ -307,258 +303,8 @@ void import_identity(const uint8_t profile_identity[32], uint8_t out[32]) {
   d.finish(out);
 }
 
-// ---- code object inspection: ELF, kernel descriptor, metadata note --------------------
-
-// A small MessagePack reader for the NT_AMDGPU_METADATA note (maps, arrays,
-// strings, integers, booleans, nil).
-struct MsgValue {
-  enum Kind { kNil, kBool, kUInt, kInt, kStr, kArr, kMap } kind = kNil;
-  uint64_t u = 0;
-  int64_t i = 0;
-  std::string s;
-  std::vector<MsgValue> items;
-  std::vector<std::pair<std::string, MsgValue>> fields;
-  const MsgValue* get(const char* key) const {
-    for (const auto& f : fields)
-      if (f.first == key) return &f.second;
-    return nullptr;
-  }
-  bool uint_value(uint64_t* out) const {
-    if (kind == kUInt) {
-      *out = u;
-      return true;
-    }
-    if (kind == kInt && i >= 0) {
-      *out = (uint64_t)i;
-      return true;
-    }
-    return false;
-  }
-};
-
-class MsgReader {
- public:
-  MsgReader(const uint8_t* p, size_t n) : p_(p), n_(n) {}
-  bool read(MsgValue* v, int depth = 0) {
-    if (depth > 16 || pos_ >= n_) return false;
-    const uint8_t t = p_[pos_++];
-    if (t <= 0x7f) return set_uint(v, t);
-    if (t >= 0xe0) {
-      v->kind = MsgValue::kInt;
-      v->i = (int8_t)t;
-      return true;
-    }
-    if ((t & 0xf0) == 0x80) return read_map(v, t & 0x0f, depth);
-    if ((t & 0xf0) == 0x90) return read_arr(v, t & 0x0f, depth);
-    if ((t & 0xe0) == 0xa0) return read_str(v, t & 0x1f);
-    uint64_t x;
-    switch (t) {
-      case 0xc0: v->kind = MsgValue::kNil; return true;
-      case 0xc2: v->kind = MsgValue::kBool; v->u = 0; return true;
-      case 0xc3: v->kind = MsgValue::kBool; v->u = 1; return true;
-      case 0xcc: return be(1, &x) && set_uint(v, x);
-      case 0xcd: return be(2, &x) && set_uint(v, x);
-      case 0xce: return be(4, &x) && set_uint(v, x);
-      case 0xcf: return be(8, &x) && set_uint(v, x);
-      case 0xd0: if (!be(1, &x)) return false; v->kind = MsgValue::kInt; v->i = (int8_t)x; return true;
-      case 0xd1: if (!be(2, &x)) return false; v->kind = MsgValue::kInt; v->i = (int16_t)x; return true;
-      case 0xd2: if (!be(4, &x)) return false; v->kind = MsgValue::kInt; v->i = (int32_t)x; return true;
-      case 0xd3: if (!be(8, &x)) return false; v->kind = MsgValue::kInt; v->i = (int64_t)x; return true;
-      case 0xd9: return be(1, &x) && read_str(v, x);
-      case 0xda: return be(2, &x) && read_str(v, x);
-      case 0xdb: return be(4, &x) && read_str(v, x);
-      case 0xdc: return be(2, &x) && read_arr(v, x, depth);
-      case 0xdd: return be(4, &x) && read_arr(v, x, depth);
-      case 0xde: return be(2, &x) && read_map(v, x, depth);
-      case 0xdf: return be(4, &x) && read_map(v, x, depth);
-      default: return false;  // binary, ext and float forms do not occur in the note
-    }
-  }
-
- private:
-  static bool set_uint(MsgValue* v, uint64_t x) {
-    v->kind = MsgValue::kUInt;
-    v->u = x;
-    return true;
-  }
-  bool be(int bytes, uint64_t* out) {
-    if (n_ - pos_ < (size_t)bytes) return false;
-    uint64_t x = 0;
-    for (int i = 0; i < bytes; ++i) x = x << 8 | p_[pos_++];
-    *out = x;
-    return true;
-  }
-  bool read_str(MsgValue* v, uint64_t len) {
-    if (n_ - pos_ < len) return false;
-    v->kind = MsgValue::kStr;
-    v->s.assign(reinterpret_cast<const char*>(p_ + pos_), (size_t)len);
-    pos_ += len;
-    return true;
-  }
-  bool read_arr(MsgValue* v, uint64_t count, int depth) {
-    if (count > n_) return false;
-    v->kind = MsgValue::kArr;
-    v->items.resize((size_t)count);
-    for (auto& it : v->items)
-      if (!read(&it, depth + 1)) return false;
-    return true;
-  }
-  bool read_map(MsgValue* v, uint64_t count, int depth) {
-    if (count > n_) return false;
-    v->kind = MsgValue::kMap;
-    v->fields.resize((size_t)count);
-    for (auto& f : v->fields) {
-      MsgValue key;
-      if (!read(&key, depth + 1) || key.kind != MsgValue::kStr) return false;
-      f.first = std::move(key.s);
-      if (!read(&f.second, depth + 1)) return false;
-    }
-    return true;
-  }
-  const uint8_t* p_;
-  size_t n_;
-  size_t pos_ = 0;
-};
-
-constexpr uint16_t kEmAmdgpu = 224;
-constexpr uint8_t kOsAbiAmdgpuHsa = 64;
-constexpr uint32_t kMachMask = 0xffu, kMachGfx950 = 0x4fu;
-constexpr uint32_t kNtAmdgpuMetadata = 32;
-
-struct Section {
-  uint32_t name, type;
-  uint64_t addr, offset, size;
-  uint32_t link;
-  uint64_t entsize;
-};
-
-// Returns "" on success, else the first fact that could not be read.
-const char* inspect_code_object(const uint8_t* b, size_t n, Fe2o3Slice1InspectionV1* out) {
-  std::memset(out, 0, sizeof(*out));
-  out->byte_len = n;
-  if (n < 64 || std::memcmp(b, "\x7f" "ELF", 4) != 0 || b[4] != 2 || b[5] != 1)
-    return "ELF header";
-  if (get_le(b + 18, 2) != kEmAmdgpu || b[7] != kOsAbiAmdgpuHsa) return "ELF machine";
-  // EI_ABIVERSION: 2, 3, 4 = code object v4, v5, v6.
-  out->code_object_version = b[8] + 2u;
-  out->e_flags = (uint32_t)get_le(b + 48, 4);
-  const uint64_t shoff = get_le(b + 40, 8);
-  const uint64_t shentsize = get_le(b + 58, 2), shnum = get_le(b + 60, 2);
-  if (shentsize != 64 || shoff > n || shnum > (n - shoff) / 64) return "section table";
-  std::vector<Section> sec(shnum);
-  for (uint64_t i = 0; i < shnum; ++i) {
-    const uint8_t* s = b + shoff + 64 * i;
-    sec[i] = {(uint32_t)get_le(s, 4), (uint32_t)get_le(s + 4, 4), get_le(s + 16, 8),
-              get_le(s + 24, 8), get_le(s + 32, 8), (uint32_t)get_le(s + 40, 4), get_le(s + 56, 8)};
-    if (sec[i].type != 8 /* SHT_NOBITS */ && (sec[i].offset > n || sec[i].size > n - sec[i].offset))
-      return "section bounds";
-  }
-  // kernel descriptor through the symbol table
-  const uint8_t* kd = nullptr;
-  for (const auto& st : sec) {
-    if (st.type != 2 /* SHT_SYMTAB */ && st.type != 11 /* SHT_DYNSYM */) continue;
-    if (st.entsize != 24 || st.link >= shnum) return "symbol table";
-    const Section& strtab = sec[st.link];
-    for (uint64_t off = 0; off + 24 <= st.size; off += 24) {
-      const uint8_t* sym = b + st.offset + off;
-      const uint32_t name = (uint32_t)get_le(sym, 4);
-      if (name >= strtab.size) continue;
-      const char* nm = reinterpret_cast<const char*>(b + strtab.offset + name);
-      const size_t room = strtab.size - name;
-      if (strnlen(nm, room) == room || std::strcmp(nm, kDescriptorSymbol) != 0) continue;
-      const uint16_t shndx = (uint16_t)get_le(sym + 6, 2);
-      const uint64_t value = get_le(sym + 8, 8), size = get_le(sym + 16, 8);
-      if (size != 64 || shndx >= shnum) return "kernel descriptor symbol";
-      const Section& home = sec[shndx];
-      if (value < home.addr || value - home.addr + 64 > home.size) return "kernel descriptor";
-      kd = b + home.offset + (value - home.addr);
-    }
-    if (kd) break;
-  }
-  if (!kd) return "kernel descriptor symbol";
-  out->kd_group_segment_bytes = (uint32_t)get_le(kd + 0, 4);
-  out->kd_private_segment_bytes = (uint32_t)get_le(kd + 4, 4);
-  out->kd_kernarg_bytes = (uint32_t)get_le(kd + 8, 4);
-  // kernel_code_properties bit 10: ENABLE_WAVEFRONT_SIZE32
-  out->kd_wavefront_size = (get_le(kd + 56, 2) >> 10 & 1u) ? 32u : 64u;
-  // metadata note
-  MsgValue md;
-  bool have_md = false;
-  for (const auto& st : sec) {
-    if (st.type != 7 /* SHT_NOTE */) continue;
-    uint64_t off = 0;
-    while (off + 12 <= st.size && !have_md) {
-      const uint8_t* note = b + st.offset + off;
-      const uint64_t namesz = get_le(note, 4), descsz = get_le(note + 4, 4), type = get_le(note + 8, 4);
-      const uint64_t name_pad = (namesz + 3) & ~3ull, desc_pad = (descsz + 3) & ~3ull;
-      if (12 + name_pad + desc_pad > st.size - off) return "metadata note";
-      if (type == kNtAmdgpuMetadata && namesz == 7 && std::memcmp(note + 12, "AMDGPU", 7) == 0) {
-        MsgReader r(note + 12 + name_pad, descsz);
-        if (!r.read(&md) || md.kind != MsgValue::kMap) return "metadata";
-        have_md = true;
-      }
-      off += 12 + name_pad + desc_pad;
-    }
-  }
-  if (!have_md) return "metadata note";
-  const MsgValue* target = md.get("amdhsa.target");
-  if (!target || target->kind != MsgValue::kStr) return "metadata target";
-  const std::string triple = "amdgcn-amd-amdhsa--";
-  std::string t = target->s.compare(0, triple.size(), triple) == 0 ? target->s.substr(triple.size())
-                                                                  : target->s;
-  std::strncpy(out->target, t.c_str(), sizeof(out->target) - 1);
-  const MsgValue* kernels = md.get("amdhsa.kernels");
-  if (!kernels || kernels->kind != MsgValue::kArr) return "metadata kernels";
-  const MsgValue* k = nullptr;
-  for (const auto& kk : kernels->items) {
-    const MsgValue* name = kk.get(".name");
-    if (name && name->kind == MsgValue::kStr && name->s == kKernelSymbol) k = &kk;
-  }
-  if (!k) return "metadata kernel";
-  const MsgValue* sym = k->get(".symbol");
-  if (!sym || sym->kind != MsgValue::kStr || sym->s != kDescriptorSymbol) return "metadata symbol";
-  struct {
-    const char* key;
-    uint32_t* dst;
-  } ints[] = {{".kernarg_segment_size", &out->md_kernarg_bytes},
-              {".kernarg_segment_align", &out->md_kernarg_alignment},
-              {".group_segment_fixed_size", &out->md_group_segment_bytes},
-              {".private_segment_fixed_size", &out->md_private_segment_bytes},
-              {".wavefront_size", &out->md_wavefront_size},
-              {".max_flat_workgroup_size", &out->md_max_flat_workgroup_size},
-              {".sgpr_spill_count", &out->sgpr_spills},
-              {".vgpr_spill_count", &out->vgpr_spills}};
-  for (const auto& f : ints) {
-    const MsgValue* v = k->get(f.key);
-    uint64_t x;
-    if (!v || !v->uint_value(&x) || x > UINT32_MAX) return f.key;
-    *f.dst = (uint32_t)x;
-  }
-  const MsgValue* dyn = k->get(".uses_dynamic_stack");
-  out->uses_dynamic_stack = (dyn && dyn->kind == MsgValue::kBool) ? (uint32_t)dyn->u : 0u;
-  const MsgValue* args = k->get(".args");
-  if (!args || args->kind != MsgValue::kArr) return "metadata args";
-  uint64_t explicit_end = 0, implicit_off = out->md_kernarg_bytes;
-  for (const auto& a : args->items) {
-    const MsgValue* off = a.get(".offset");
-    const MsgValue* size = a.get(".size");
-    const MsgValue* kind = a.get(".value_kind");
-    uint64_t o, s;
-    if (!off || !size || !kind || kind->kind != MsgValue::kStr || !off->uint_value(&o) ||
-        !size->uint_value(&s))
-      return "metadata arg";
-    if (kind->s.compare(0, 7, "hidden_") == 0) {
-      implicit_off = std::min(implicit_off, o);
-    } else {
-      ++out->explicit_args;
-      explicit_end = std::max(explicit_end, o + s);
-    }
-  }
-  out->explicit_bytes = (uint32_t)explicit_end;
-  out->implicit_offset = (uint32_t)implicit_off;
-  out->implicit_bytes = out->md_kernarg_bytes - (uint32_t)std::min<uint64_t>(implicit_off, out->md_kernarg_bytes);
-  return "";
-}
+using fe2o3_inspect::kMachGfx950;
+using fe2o3_inspect::kMachMask;
 
 // The code object's own facts against the contract; "" when they agree.
 const char* inspection_drift(const Fe2o3Slice1InspectionV1& i, const Fe2o3Slice1ContractV1& c) {
@@ -607,8 +353,9 @@ const Artifact& artifact() {
     x.view.contract = exact_contract();
     std::memcpy(x.view.profile_identity, x.view.contract.identity, 32);
     import_identity(x.view.profile_identity, x.view.import_identity);
-    x.inspect_error = inspect_code_object(kSlice1CodeObject, sizeof(kSlice1CodeObject),
-                                          &x.view.inspection);
+    x.inspect_error =
+        fe2o3_inspect::inspect_code_object(kSlice1CodeObject, sizeof(kSlice1CodeObject),
+                                           kKernelSymbol, kDescriptorSymbol, &x.view.inspection);
     x.drift = x.inspect_error[0] ? x.inspect_error
                                  : inspection_drift(x.view.inspection, x.view.contract);
     return x;
@@ -1121,7 +868,8 @@ int32_t hip_load_executable(void* self, const uint8_t* bytes, uint64_t byte_len,
   if (!a->observed) return FE2O3_ERR_DEVICE;
   std::unique_ptr<HipExecutable> e(new HipExecutable{});
   e->magic = kHipExeMagic;
-  const char* bad = inspect_code_object(bytes, byte_len, &e->inspection);
+  const char* bad = fe2o3_inspect::inspect_code_object(bytes, byte_len, kKernelSymbol,
+                                                       kDescriptorSymbol, &e->inspection);
   if (bad[0]) return FE2O3_ERR_SHAPE;
   DeviceScope scope(a->device);
   if (!scope.ok()) return FE2O3_ERR_DEVICE;

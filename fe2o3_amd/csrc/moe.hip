@@ -275,8 +275,8 @@ __global__ void __launch_bounds__(256) gather_kernel(const uint16_t* __restrict_
 // tile), a wave scan sums the tile counts, a ballot finds the entry's
 // expert, and lane reads return its bounds as wave-uniform values.
 FE2O3_DEVICE bool expert_tile(const uint32_t* offsets, uint32_t e_begin, uint32_t e_end,
-                              uint32_t routes, uint32_t n_blocks, uint32_t* e_out, uint32_t* row0,
-                              uint32_t* rows, uint32_t* nb) {
+                              uint32_t routes, uint32_t n_blocks, uint32_t xcds, uint32_t* e_out,
+                              uint32_t* row0, uint32_t* rows, uint32_t* nb) {
   const uint32_t l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
   uint32_t lo = 0, n = 0;
   if (l < e_end - e_begin) expert_rows(offsets, e_begin + l, routes, &lo, &n);
@@ -287,10 +287,10 @@ FE2O3_DEVICE bool expert_tile(const uint32_t* offsets, uint32_t e_begin, uint32_
     if (l >= (uint32_t)o) incl += v;
   }
   const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
-  const uint32_t chunk = (total + 7u) / 8u;
-  const uint32_t slot = blockIdx.x >> 3;
+  const uint32_t chunk = (total + xcds - 1u) / xcds;
+  const uint32_t slot = blockIdx.x / xcds;
   if (slot >= chunk) return false;
-  const uint32_t x = (blockIdx.x & 7u) * chunk + slot;
+  const uint32_t x = (blockIdx.x % xcds) * chunk + slot;
   if (x >= total) return false;
   const int le = (int)__builtin_popcountll(__ballot(incl <= x));
   const uint32_t lo_e = (uint32_t)__builtin_amdgcn_readlane((int)lo, le);
@@ -401,10 +401,12 @@ FE2O3_DEVICE void gate_up_tile(const uint16_t* __restrict__ xc, const uint16_t* 
 __global__ void __launch_bounds__(256, 1) gate_up_kernel(
     const uint16_t* __restrict__ xc, const uint16_t* __restrict__ wg,
     const uint16_t* __restrict__ wu, const uint32_t* __restrict__ offsets, uint32_t e_begin,
-    uint32_t e_end, uint32_t hidden, uint32_t ffn, uint32_t routes, uint16_t* __restrict__ hc) {
+    uint32_t e_end, uint32_t hidden, uint32_t ffn, uint32_t routes, uint16_t* __restrict__ hc,
+    uint32_t xcds) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   uint32_t e, row0, rows, nb;
-  if (!expert_tile(offsets, e_begin, e_end, routes, ffn / 128u, &e, &row0, &rows, &nb)) return;
+  if (!expert_tile(offsets, e_begin, e_end, routes, ffn / 128u, xcds, &e, &row0, &rows, &nb))
+    return;
   by_tile_rows(rows, [&](auto rpw) {
     constexpr int R = decltype(rpw)::value;
     if constexpr (R == 0)
@@ -450,11 +452,11 @@ __global__ void __launch_bounds__(256, 1) down_kernel(const uint16_t* __restrict
                                                       uint32_t e_begin, uint32_t e_end,
                                                       uint32_t hidden, uint32_t ffn,
                                                       uint64_t routes, uint32_t kparts,
-                                                      float* __restrict__ yc) {
+                                                      float* __restrict__ yc, uint32_t xcds) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   uint32_t e, row0, rows, nb;
-  if (!expert_tile(offsets, e_begin, e_end, (uint32_t)routes, kparts * (hidden / 256u), &e, &row0,
-                   &rows, &nb))
+  if (!expert_tile(offsets, e_begin, e_end, (uint32_t)routes, kparts * (hidden / 256u), xcds, &e,
+                   &row0, &rows, &nb))
     return;
   by_tile_rows(rows, [&](auto rpw) {
     constexpr int R = decltype(rpw)::value;
@@ -828,25 +830,6 @@ uint64_t fe2o3_moe_ffn_workspace_bytes(uint32_t tokens, uint32_t hidden, uint32_
 
 namespace {
 
-// Compute units of the current device, cached per device (256 on MI355X;
-// 256 also if the query fails: the value only steers down_k_parts).
-uint32_t device_cus() {
-  static constexpr int kMaxDevices = 64;
-  static std::atomic<uint32_t> cus[kMaxDevices];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256u;
-  uint32_t c = cus[dev].load(std::memory_order_relaxed);
-  if (c == 0u) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        v <= 0)
-      v = 256;
-    c = (uint32_t)v;
-    cus[dev].store(c, std::memory_order_relaxed);
-  }
-  return c;
-}
-
 // K parts of the down GEMM: 2 (two half-K tiles per output tile, two fp32
 // partials) only when that fills the grid's rounds of `cus` tiles better
 // than whole-K tiles, each of which counts two half-K rounds.  The m-tile
@@ -907,19 +890,23 @@ int32_t ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate, uint
   hipStream_t s = (hipStream_t)stream;
   // the most m-tiles any routing yields for experts [b, e): routes/288
   // rounded up, plus one partial tile per expert
-  const uint32_t kparts = down_k_parts(routes, experts, hidden, device_cus());
+  tile_plan::Topology topo;
+  const int32_t topo_rc = fe2o3_host::device_topology(&topo);
+  if (topo_rc != FE2O3_OK) return topo_rc;
+  const uint32_t xcds = topo.xcds;
+  const uint32_t kparts = down_k_parts(routes, experts, hidden, topo.cus);
   auto grids = [&](uint32_t n_experts, uint64_t* gu, uint64_t* dn) {
-    *gu = expert_grid(routes, n_experts, ffn / 128u);
-    *dn = expert_grid(routes, n_experts, kparts * (hidden / 256u));
+    *gu = expert_grid(routes, n_experts, ffn / 128u, xcds);
+    *dn = expert_grid(routes, n_experts, kparts * (hidden / 256u), xcds);
     return *gu <= 0x7fffffffu && *dn <= 0x7fffffffu;
   };
   auto experts_ffn = [&](uint32_t b, uint32_t e, hipStream_t st) {
     uint64_t gu, dn;
     grids(e - b, &gu, &dn);
     gate_up_kernel<<<(unsigned)gu, 256, kSmem, st>>>(ws.xc, w_gate, w_up, expert_offsets, b, e,
-                                                     hidden, ffn, (uint32_t)routes, ws.hc);
+                                                     hidden, ffn, (uint32_t)routes, ws.hc, xcds);
     down_kernel<<<(unsigned)dn, 256, kSmem, st>>>(ws.hc, w_down, expert_offsets, b, e, hidden,
-                                                  ffn, routes, kparts, ws.yc);
+                                                  ffn, routes, kparts, ws.yc, xcds);
   };
   uint64_t gu_all, dn_all;
   if (!grids(experts, &gu_all, &dn_all)) return FE2O3_ERR_SHAPE;

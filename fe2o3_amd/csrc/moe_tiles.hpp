@@ -7,9 +7,9 @@
 // 32-row blocks are dealt out evenly (m_tile): 1033 rows are tiles of 288,
 // 256, 256 and 233 rows rather than four of 256 and a remainder of 9, and
 // every tile runs on an A tile of its own size rounded up to 32 rows.  Workgroup id i
-// runs on XCD i % 8; XCD x takes the x-th contiguous eighth of the list in
-// order, so the workgroups that share a weight block run at the same time
-// behind one L2.  The grid is sized for the most m-tiles routing can produce;
+// runs on XCD i % xcds (the device's XCD count, 8 on MI355X); XCD x takes
+// the x-th of xcds contiguous pieces of the list in order, so the workgroups
+// that share a weight block run at the same time behind one L2.  The grid is sized for the most m-tiles routing can produce;
 // entries past the list's end exit at once.
 //
 // Expert e's rows are offsets[e] .. offsets[e+1] clamped to [0, routes]
@@ -23,10 +23,12 @@
 
 #include <stdint.h>
 
+#ifndef FE2O3_HD
 #if defined(__HIPCC__)
 #define FE2O3_HD __host__ __device__ __forceinline__
 #else
 #define FE2O3_HD inline
+#endif
 #endif
 
 namespace fe2o3 {
@@ -63,17 +65,17 @@ FE2O3_HD void m_tile(uint32_t lo, uint32_t n, uint32_t m_tiles, uint32_t mt, uin
 // Entry of workgroup `block` in the list: expert, first row, row count
 // (1..288) and n-block; false when the workgroup has no entry.
 FE2O3_HD bool expert_tile_at(const uint32_t* offsets, uint32_t e_begin, uint32_t e_end,
-                             uint32_t routes, uint32_t n_blocks, uint32_t block, uint32_t* e_out,
-                             uint32_t* row0, uint32_t* rows, uint32_t* nb) {
+                             uint32_t routes, uint32_t n_blocks, uint32_t block, uint32_t xcds,
+                             uint32_t* e_out, uint32_t* row0, uint32_t* rows, uint32_t* nb) {
   uint32_t total = 0, lo, n;
   for (uint32_t e = e_begin; e < e_end; ++e) {
     expert_rows(offsets, e, routes, &lo, &n);
     total += expert_m_tiles(n) * n_blocks;
   }
-  const uint32_t chunk = (total + 7u) / 8u;
-  const uint32_t slot = block >> 3;
+  const uint32_t chunk = (total + xcds - 1u) / xcds;
+  const uint32_t slot = block / xcds;
   if (slot >= chunk) return false;
-  uint32_t x = (block & 7u) * chunk + slot;
+  uint32_t x = (block % xcds) * chunk + slot;
   if (x >= total) return false;
   for (uint32_t e = e_begin; e < e_end; ++e) {
     expert_rows(offsets, e, routes, &lo, &n);
@@ -97,7 +99,7 @@ FE2O3_HD bool expert_tile_at(const uint32_t* offsets, uint32_t e_begin, uint32_t
 // form (moe.hip) uses a wave scan, a ballot and lane reads, step for step.
 // Experts: at most 64.
 FE2O3_HD bool expert_tile_lanes(const uint32_t* offsets, uint32_t e_begin, uint32_t e_end,
-                                uint32_t routes, uint32_t n_blocks, uint32_t block,
+                                uint32_t routes, uint32_t n_blocks, uint32_t block, uint32_t xcds,
                                 uint32_t* e_out, uint32_t* row0, uint32_t* rows, uint32_t* nb) {
   uint32_t lo[64], n[64], incl[64];
   const uint32_t ne = e_end - e_begin;
@@ -109,10 +111,10 @@ FE2O3_HD bool expert_tile_lanes(const uint32_t* offsets, uint32_t e_begin, uint3
     incl[l] = run;
   }
   const uint32_t total = incl[63];
-  const uint32_t chunk = (total + 7u) / 8u;
-  const uint32_t slot = block >> 3;
+  const uint32_t chunk = (total + xcds - 1u) / xcds;
+  const uint32_t slot = block / xcds;
   if (slot >= chunk) return false;
-  const uint32_t x = (block & 7u) * chunk + slot;
+  const uint32_t x = (block % xcds) * chunk + slot;
   if (x >= total) return false;
   uint32_t l = 0;
   for (uint32_t i = 0; i < 64; ++i) l += incl[i] <= x ? 1u : 0u;
@@ -124,12 +126,13 @@ FE2O3_HD bool expert_tile_lanes(const uint32_t* offsets, uint32_t e_begin, uint3
   return true;
 }
 
-// Grid sizes (workgroups, a multiple of 8) of the gate/up and down launches
-// for experts [e_begin, e_end): routes/288 rounded up plus one partial tile
-// per expert bounds the m-tiles of any consistent routing.
-FE2O3_HD uint64_t expert_grid(uint64_t routes, uint32_t n_experts, uint32_t n_blocks) {
+// Grid sizes (workgroups, a multiple of xcds) of the gate/up and down
+// launches for experts [e_begin, e_end): routes/288 rounded up plus one
+// partial tile per expert bounds the m-tiles of any consistent routing.
+FE2O3_HD uint64_t expert_grid(uint64_t routes, uint32_t n_experts, uint32_t n_blocks,
+                              uint32_t xcds) {
   const uint64_t m_tiles = (routes + kMaxTileRows - 1u) / kMaxTileRows + n_experts;
-  return (m_tiles * n_blocks + 7u) / 8u * 8u;
+  return (m_tiles * n_blocks + xcds - 1u) / xcds * xcds;
 }
 
 }  // namespace fe2o3

@@ -5,10 +5,12 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "common.hpp"
 #include "internal.hpp"
+#include "status_track.hpp"
 
 static_assert(sizeof(Fe2o3HipDeviceProperties) == 312, "property record is 312 bytes");
 static_assert(offsetof(Fe2o3HipDeviceProperties, warp_size) == 256, "warp_size offset");
@@ -43,16 +45,20 @@ KernelRegistrar::KernelRegistrar(const KernelInfo& k) {
   if (r.n < kMaxKernels) r.k[r.n++] = k;
 }
 
-// One contract-status word per device.  The reference's kernels trap on a
-// non-finite input and the fault surfaces when the host synchronizes; here
-// the kernel marks this word instead, writes its documented sentinel
-// outputs and exits normally, and the next fe2o3_rt_stream_synchronize or
-// fe2o3_rt_device_synchronize on the device reports FE2O3_ERR_NONFINITE.
+// One non-finite rejection counter per device.  The reference's kernels
+// trap on a non-finite input and the fault surfaces when the host
+// synchronizes; here the kernel adds 1 to this counter instead, writes its
+// documented sentinel outputs and exits normally, and the next
+// fe2o3_rt_stream_synchronize or fe2o3_rt_device_synchronize on the device
+// that reads a count it has not reported yet returns FE2O3_ERR_NONFINITE
+// (the bookkeeping is StatusTracker, status_track.hpp).  Neither the kernels
+// nor the host ever clear the counter.
 static __device__ __align__(256) uint32_t status_word_dev;
 
 static constexpr int kMaxDevices = 64;
 static std::mutex status_mu;
 static uint32_t* status_ptrs[kMaxDevices];
+static StatusTracker status_seen[kMaxDevices];
 
 uint32_t* status_word() {
   int dev = 0;
@@ -66,21 +72,51 @@ uint32_t* status_word() {
   return status_ptrs[dev];
 }
 
-// Reads and clears the current device's status word after a successful
-// synchronize.  The word is per device: a report from a kernel that finished
-// on another stream of the device is returned here too.
+// Reads the current device's counter after a successful synchronize and
+// reports whether it moved since the device's last report.  The counter is
+// per device: a rejection by a kernel that finished on another stream of the
+// device is reported here too, once.
 static int32_t take_status(hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return (int32_t)hipErrorInvalidDevice;
   uint32_t* p = status_word();
   if (p == nullptr) return (int32_t)hipErrorInvalidSymbol;
   uint32_t v = 0;
   hipError_t e = hipMemcpyAsync(&v, p, sizeof v, hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) return (int32_t)e;
-  if (v == 0) return FE2O3_OK;
-  e = hipMemsetAsync(p, 0, sizeof v, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  std::lock_guard<std::mutex> lock(status_mu);
+  return status_seen[dev].report(v) ? FE2O3_ERR_NONFINITE : FE2O3_OK;
+}
+
+// CU and XCD counts per device, queried on first use.  A packed word per
+// device (cus << 8 | xcds; 0 = not yet queried), so concurrent first calls
+// may both query but every reader sees a whole value.
+static std::atomic<uint64_t> topology_word[kMaxDevices];
+
+int32_t device_topology(tile_plan::Topology* out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int32_t)e;
-  return (v & kStatusNonFinite) ? FE2O3_ERR_NONFINITE : FE2O3_OK;
+  if (dev < 0 || dev >= kMaxDevices) return (int32_t)hipErrorInvalidDevice;
+  uint64_t w = topology_word[dev].load(std::memory_order_acquire);
+  if (w == 0) {
+    int cus = 0, xcds = 0;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return (int32_t)e;
+    if (cus <= 0) return (int32_t)hipErrorInvalidDevice;
+    if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess) {
+      (void)hipGetLastError();  // the failed query must not surface as a launch error
+      xcds = 1;
+    }
+    if (xcds <= 0 || xcds > 255) xcds = 1;
+    w = (uint64_t)cus << 8 | (uint64_t)xcds;
+    topology_word[dev].store(w, std::memory_order_release);
+  }
+  out->cus = (uint32_t)(w >> 8);
+  out->xcds = (uint32_t)(w & 0xffu);
+  return 0;
 }
 
 }  // namespace fe2o3_host

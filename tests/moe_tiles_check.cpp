@@ -13,6 +13,8 @@
 //     expert's rows exactly once, in ceil(n / 288) tiles whose row counts
 //     differ by less than 64, each above 96 rows when there are two or more
 //     (no short remainder tile).
+// Every case runs for XCD counts 8 (MI355X), 1, 2, 3, 4 and 6: the list's
+// split over the XCDs must stay a bijection whatever the device reports.
 #include <stdint.h>
 #include <stdio.h>
 
@@ -54,17 +56,24 @@ int main() {
     }
     const uint32_t b = rnd() % experts;
     const uint32_t e_end = b + 1 + rnd() % (experts - b);
-    const uint64_t grid = fe2o3::expert_grid(routes, e_end - b, n_blocks);
+    // the device's XCD count: 8 on MI355X, fewer on partitioned parts
+    static const uint32_t kXcds[] = {8, 1, 2, 4, 3, 6};
+    const uint32_t xcds = kXcds[iter % 6];
+    const uint64_t grid = fe2o3::expert_grid(routes, e_end - b, n_blocks, xcds);
+    if (grid % xcds != 0) {
+      if (failures < 10) printf("grid %llu not a multiple of %u\n", (unsigned long long)grid, xcds);
+      ++failures;
+    }
     std::set<std::tuple<uint32_t, uint32_t, uint32_t>> seen;
     std::map<std::pair<uint32_t, uint32_t>, std::vector<std::pair<uint32_t, uint32_t>>> spans;
     bool dup = false;
     for (uint64_t blk = 0; blk < grid; ++blk) {
       uint32_t e, row0, rows, nb;
-      if (!fe2o3::expert_tile_at(off.data(), b, e_end, routes, n_blocks, (uint32_t)blk, &e, &row0,
-                                 &rows, &nb)) {
+      if (!fe2o3::expert_tile_at(off.data(), b, e_end, routes, n_blocks, (uint32_t)blk, xcds, &e,
+                                 &row0, &rows, &nb)) {
         uint32_t e2, r2, n2, b2;
-        if (fe2o3::expert_tile_lanes(off.data(), b, e_end, routes, n_blocks, (uint32_t)blk, &e2,
-                                     &r2, &n2, &b2)) {
+        if (fe2o3::expert_tile_lanes(off.data(), b, e_end, routes, n_blocks, (uint32_t)blk, xcds,
+                                     &e2, &r2, &n2, &b2)) {
           if (failures < 10) printf("lanes form has an extra tile: iter %d\n", iter);
           ++failures;
         }
@@ -73,7 +82,7 @@ int main() {
       ++tiles_checked;
       uint32_t e2, r2, n2, b2;
       const bool hit2 = fe2o3::expert_tile_lanes(off.data(), b, e_end, routes, n_blocks,
-                                                 (uint32_t)blk, &e2, &r2, &n2, &b2);
+                                                 (uint32_t)blk, xcds, &e2, &r2, &n2, &b2);
       if (!hit2 || e2 != e || r2 != row0 || n2 != rows || b2 != nb) {
         if (failures < 10) printf("lanes form differs: iter %d block %llu\n", iter,
                                   (unsigned long long)blk);
