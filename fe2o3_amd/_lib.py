@@ -220,6 +220,12 @@ SIGNATURES = {
     "fe2o3_rt_memcpy_async": (i32, [vp, vp, sz, u32, vp]),
     "fe2o3_rt_memcpy": (i32, [vp, vp, sz, u32]),
     "fe2o3_rt_memset_async": (i32, [vp, i32, sz, vp]),
+    "fe2o3_rt_module_load": (i32, [C.POINTER(vp), C.c_char_p]),
+    "fe2o3_rt_module_load_data": (i32, [C.POINTER(vp), vp]),
+    "fe2o3_rt_module_unload": (i32, [vp]),
+    "fe2o3_rt_module_get_function": (i32, [C.POINTER(vp), vp, C.c_char_p]),
+    "fe2o3_rt_module_launch_kernel": (i32, [vp, u32, u32, u32, u32, u32, u32, u32, vp,
+                                            C.POINTER(vp), C.POINTER(vp)]),
     "fe2o3_fill_normal_bf16": (i32, [vp, u64, u64, u64, f32, u64, vp]),
     "fe2o3_fill_normal_f32": (i32, [vp, u64, u64, u64, f32, u64, vp]),
     "fe2o3_fill_uniform_f32": (i32, [vp, u64, u64, u64, u64, vp]),

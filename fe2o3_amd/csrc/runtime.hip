@@ -300,6 +300,53 @@ int32_t fe2o3_rt_memset_async(void* dst, int32_t value, size_t bytes, void* stre
   return (int32_t)hipMemsetAsync(dst, value, bytes, (hipStream_t)stream);
 }
 
+// lib.rs:144-165: the module subset.  Handles are HIP's, passed through as
+// opaque pointers; null out-pointers and names are refused before any HIP
+// call.
+int32_t fe2o3_rt_module_load(void** module, const char* file_name) {
+  if (module == nullptr || file_name == nullptr) return FE2O3_ERR_NULL;
+  *module = nullptr;
+  hipModule_t m = nullptr;
+  const hipError_t e = hipModuleLoad(&m, file_name);
+  if (e == hipSuccess) *module = (void*)m;
+  return (int32_t)e;
+}
+
+int32_t fe2o3_rt_module_load_data(void** module, const void* image) {
+  if (module == nullptr || image == nullptr) return FE2O3_ERR_NULL;
+  *module = nullptr;
+  hipModule_t m = nullptr;
+  const hipError_t e = hipModuleLoadData(&m, image);
+  if (e == hipSuccess) *module = (void*)m;
+  return (int32_t)e;
+}
+
+int32_t fe2o3_rt_module_unload(void* module) {
+  if (module == nullptr) return FE2O3_ERR_NULL;
+  return (int32_t)hipModuleUnload((hipModule_t)module);
+}
+
+int32_t fe2o3_rt_module_get_function(void** function, void* module, const char* kernel_name) {
+  if (function == nullptr || module == nullptr || kernel_name == nullptr) return FE2O3_ERR_NULL;
+  *function = nullptr;
+  hipFunction_t f = nullptr;
+  const hipError_t e = hipModuleGetFunction(&f, (hipModule_t)module, kernel_name);
+  if (e == hipSuccess) *function = (void*)f;
+  return (int32_t)e;
+}
+
+int32_t fe2o3_rt_module_launch_kernel(void* function, uint32_t grid_dim_x, uint32_t grid_dim_y,
+                                      uint32_t grid_dim_z, uint32_t block_dim_x,
+                                      uint32_t block_dim_y, uint32_t block_dim_z,
+                                      uint32_t shared_mem_bytes, void* stream,
+                                      void** kernel_params, void** extra) {
+  if (function == nullptr) return FE2O3_ERR_NULL;
+  return (int32_t)hipModuleLaunchKernel((hipFunction_t)function, grid_dim_x, grid_dim_y,
+                                        grid_dim_z, block_dim_x, block_dim_y, block_dim_z,
+                                        shared_mem_bytes, (hipStream_t)stream, kernel_params,
+                                        extra);
+}
+
 int32_t fe2o3_kernel_resources(const char* entry, uint32_t index, Fe2o3KernelResources* out,
                                uint32_t* count) {
   if (!entry || !count) return FE2O3_ERR_NULL;

@@ -113,13 +113,15 @@ int32_t fe2o3_rt_require_gfx950(int32_t device_id);
  * contract rejects them, examples/row_softmax_v1/src/numerical_contract.rs:149).
  * Here such a kernel (fe2o3_row_softmax_v1, fe2o3_row_softmax,
  * fe2o3_flash_attention_causal_f32_b1_h1_n8_d16_v1, both top-2 routers)
- * writes the sentinel outputs its declaration states, marks the device's
- * contract-status word and exits normally; the next successful
+ * writes the sentinel outputs its declaration states, adds 1 to the device's
+ * non-finite counter and exits normally; the next successful
  * fe2o3_rt_device_synchronize or fe2o3_rt_stream_synchronize on that device
- * returns FE2O3_ERR_NONFINITE and clears the word.  The word is per device,
- * like the reference's context-wide fault: a synchronize reports what any
- * kernel that finished before it on the device found, whichever stream
- * launched it.  Event synchronization does not read the word. */
+ * that reads a count it has not reported yet returns FE2O3_ERR_NONFINITE.
+ * Nothing ever clears the counter, so a rejection that lands while a
+ * synchronize reads it is reported by the next one.  The counter is per
+ * device, like the reference's context-wide fault: a synchronize reports what
+ * any kernel that finished before it on the device found, whichever stream
+ * launched it, once.  Event synchronization does not read it. */
 int32_t fe2o3_rt_device_synchronize(void);
 
 /* lib.rs:109-111: hipStreamCreate / Destroy / Synchronize. */
@@ -146,6 +148,24 @@ int32_t fe2o3_rt_memcpy_async(void *dst, const void *src, size_t bytes,
                               uint32_t kind, void *stream);
 int32_t fe2o3_rt_memcpy(void *dst, const void *src, size_t bytes, uint32_t kind);
 int32_t fe2o3_rt_memset_async(void *dst, int32_t value, size_t bytes, void *stream);
+
+/* lib.rs:144-165: hipModuleLoad / hipModuleLoadData / hipModuleUnload /
+ * hipModuleGetFunction / hipModuleLaunchKernel, for callers that load code
+ * objects of their own.  Modules and functions are HIP handles passed as
+ * opaque pointers; kernel_params is HIP's array of pointers to each
+ * argument (or NULL with `extra`).  A NULL out-pointer, name, image or
+ * handle returns FE2O3_ERR_NULL without calling HIP; otherwise the HIP
+ * status is returned, and *module / *function are NULL on failure. */
+int32_t fe2o3_rt_module_load(void **module, const char *file_name);
+int32_t fe2o3_rt_module_load_data(void **module, const void *image);
+int32_t fe2o3_rt_module_unload(void *module);
+int32_t fe2o3_rt_module_get_function(void **function, void *module,
+                                     const char *kernel_name);
+int32_t fe2o3_rt_module_launch_kernel(void *function, uint32_t grid_dim_x,
+                                      uint32_t grid_dim_y, uint32_t grid_dim_z,
+                                      uint32_t block_dim_x, uint32_t block_dim_y,
+                                      uint32_t block_dim_z, uint32_t shared_mem_bytes,
+                                      void *stream, void **kernel_params, void **extra);
 
 /* ---- deterministic synthetic inputs --------------------------------------------
  * Counter-based fills that reproduce, bit for bit, the CPU generators of the

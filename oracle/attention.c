@@ -319,3 +319,66 @@ int32_t fe2o3o_row_softmax_rows(const float *input, uint64_t rows,
   }
   return status;
 }
+
+/* Row-by-row check of a device softmax over many rows: for each row the f64
+ * oracle (fe2o3o_row_softmax_oracle_v1) and the contract's comparison
+ * (fe2o3o_compare_row_softmax_v1) under the given policy, OpenMP over rows.
+ * stats[0] = rows failing the comparison, stats[1] = the first failing row
+ * (rows if none), stats[2] = max |actual - oracle| over all elements,
+ * stats[3] = max |oracle| over all elements, stats[4] = max |f64 row sum of
+ * actual - 1|.  Returns the first oracle error (FE2O3O_OK when every row's
+ * input is admitted); comparison failures are counted, not returned. */
+int32_t fe2o3o_row_softmax_check_rows(const float *input, const float *actual, uint64_t rows,
+                                      uint64_t cols, float abs_tol, float rel_tol, float sum_tol,
+                                      uint32_t max_ulps, int32_t threads, double *stats) {
+  int32_t status = FE2O3O_OK;
+  uint64_t failing = 0, first = rows;
+  double max_diff = 0.0, max_ref = 0.0, max_sum = 0.0;
+#pragma omp parallel num_threads(threads > 0 ? threads : 1)
+  {
+    float *ref = (float *)malloc(cols * sizeof(float));
+    uint64_t my_failing = 0, my_first = rows;
+    double my_diff = 0.0, my_ref = 0.0, my_sum = 0.0;
+    int32_t my_status = ref ? FE2O3O_OK : FE2O3O_ERR_INTERMEDIATE;
+#pragma omp for schedule(static)
+    for (uint64_t r = 0; r < rows; ++r) {
+      if (!ref) continue;
+      const float *x = input + r * cols, *y = actual + r * cols;
+      int32_t rc = fe2o3o_row_softmax_oracle_v1(x, cols, NULL, ref, NULL);
+      if (rc != FE2O3O_OK) {
+        my_status = rc;
+        continue;
+      }
+      if (fe2o3o_compare_row_softmax_v1(ref, y, cols, NULL, abs_tol, rel_tol, sum_tol, max_ulps,
+                                        NULL) != FE2O3O_OK) {
+        ++my_failing;
+        if (r < my_first) my_first = r;
+      }
+      double sum = 0.0;
+      for (uint64_t c = 0; c < cols; ++c) {
+        const double d = fabs((double)y[c] - (double)ref[c]);
+        if (!isnan(my_diff) && !(d <= my_diff)) my_diff = d; /* a NaN stays the maximum */
+        if (fabs((double)ref[c]) > my_ref) my_ref = fabs((double)ref[c]);
+        sum += (double)y[c];
+      }
+      const double e = fabs(sum - 1.0);
+      if (!isnan(my_sum) && !(e <= my_sum)) my_sum = e;
+    }
+    free(ref);
+#pragma omp critical
+    {
+      if (my_status != FE2O3O_OK) status = my_status;
+      failing += my_failing;
+      if (my_first < first) first = my_first;
+      if (!isnan(max_diff) && !(my_diff <= max_diff)) max_diff = my_diff;
+      if (my_ref > max_ref) max_ref = my_ref;
+      if (!isnan(max_sum) && !(my_sum <= max_sum)) max_sum = my_sum;
+    }
+  }
+  stats[0] = (double)failing;
+  stats[1] = (double)first;
+  stats[2] = max_diff;
+  stats[3] = max_ref;
+  stats[4] = max_sum;
+  return status;
+}

@@ -181,6 +181,14 @@ int32_t fe2o3o_row_softmax_reference_v1(const float *input, float *out);
 /* Many rows of fe2o3o_row_softmax_oracle_v1 (no mask), OpenMP over rows. */
 int32_t fe2o3o_row_softmax_rows(const float *input, uint64_t rows,
                                 uint64_t cols, float *out, int32_t threads);
+/* Each row of `actual` against fe2o3o_row_softmax_oracle_v1 of the same row
+ * of `input` under fe2o3o_compare_row_softmax_v1's policy, OpenMP over rows;
+ * stats[5] = {failing rows, first failing row (rows if none), max abs
+ * difference, max |oracle|, max |f64 row sum - 1|}. */
+int32_t fe2o3o_row_softmax_check_rows(const float *input, const float *actual,
+                                      uint64_t rows, uint64_t cols, float abs_tol,
+                                      float rel_tol, float sum_tol, uint32_t max_ulps,
+                                      int32_t threads, double *stats);
 
 /* ---- MoE top-2 router ---------------------------------------------------- */
 #define FE2O3O_DROP_ROUTE 0xffffffffu

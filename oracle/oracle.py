@@ -106,6 +106,8 @@ def _declare(L):
             i32, [f32p, f32p, u64, vp, f32, f32, f32, u32, C.POINTER(u64)]),
         "fe2o3o_row_softmax_reference_v1": (i32, [f32p, f32p]),
         "fe2o3o_row_softmax_rows": (i32, [f32p, u64, u64, f32p, i32]),
+        "fe2o3o_row_softmax_check_rows": (
+            i32, [f32p, f32p, u64, u64, f32, f32, f32, u32, i32, C.POINTER(C.c_double)]),
         "fe2o3o_moe_top2_route": (
             i32, [vp, u32, u32, u32, vp, vp, vp, vp, vp, vp, vp]),
         "fe2o3o_moe_select_top2_running": (None, [f32p, u32, u32p]),
@@ -148,13 +150,18 @@ def _ptr(a):
 
 
 def _threads() -> int:
-    """Default OpenMP width: the CPUs this process may run on, at most 16
-    (os.cpu_count() can report far more cores than a container grants)."""
+    """Default OpenMP width: the CPUs this process may run on (its affinity
+    set; os.cpu_count() can report far more cores than a container grants),
+    capped by OMP_NUM_THREADS when that is set (a GPU box sets it to the CPU
+    share of its GPU)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
-    return max(1, min(16, n))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
 
 
 def _c(a, dtype):
@@ -376,6 +383,22 @@ def row_softmax_reference_v1(x):
     out = np.zeros(64, np.float32)
     rc = lib().fe2o3o_row_softmax_reference_v1(x, out)
     return rc, out
+
+
+def row_softmax_check_rows(x, y, rows, cols, threads=0, abs_tol=3.0e-6, rel_tol=3.0e-5,
+                           sum_tol=6.0e-5, max_ulps=64):
+    """Every row of y against the f64 oracle of the same row of x under the
+    comparison policy (default: GFX_SOFTMAX_POLICY), in C over OpenMP.
+    Returns (rc, stats): failing rows, the first failing row (rows if none),
+    max abs difference, max |oracle|, max |f64 row sum - 1|."""
+    x = _c(x, np.float32).ravel()
+    y = _c(y, np.float32).ravel()
+    assert x.size == y.size == rows * cols
+    st = (C.c_double * 5)()
+    rc = lib().fe2o3o_row_softmax_check_rows(x, y, rows, cols, abs_tol, rel_tol, sum_tol,
+                                             max_ulps, threads or _threads(), st)
+    return rc, {"failing_rows": int(st[0]), "first_failing_row": int(st[1]),
+                "max_abs_diff": st[2], "max_ref": st[3], "max_row_sum_err": st[4]}
 
 
 def row_softmax_rows(x, rows, cols, threads=0):

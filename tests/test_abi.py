@@ -207,3 +207,35 @@ def test_lifecycle_record_layouts_match_the_header(tmp_path):
                    check=True)
     got = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
     assert got[:-1] == expect
+
+
+def test_module_seam_refuses_null_arguments_without_gpu():
+    """lib.rs:144-165's module subset: every NULL out-pointer, name, image or
+    handle is refused with FE2O3_ERR_NULL (-19) before HIP is called."""
+    from fe2o3_amd import _lib
+    L = _lib.lib()
+    null = -19
+    mod = C.c_void_p(0x1234)
+    fn = C.c_void_p(0x5678)
+    assert L.fe2o3_rt_module_load(None, b"x.co") == null
+    assert L.fe2o3_rt_module_load(C.byref(mod), None) == null
+    assert L.fe2o3_rt_module_load_data(None, C.c_void_p(1)) == null
+    assert L.fe2o3_rt_module_load_data(C.byref(mod), None) == null
+    assert L.fe2o3_rt_module_unload(None) == null
+    assert L.fe2o3_rt_module_get_function(None, C.c_void_p(1), b"k") == null
+    assert L.fe2o3_rt_module_get_function(C.byref(fn), None, b"k") == null
+    assert L.fe2o3_rt_module_get_function(C.byref(fn), C.c_void_p(1), None) == null
+    assert L.fe2o3_rt_module_launch_kernel(None, 1, 1, 1, 64, 1, 1, 0, None, None, None) == null
+    assert L.fe2o3_status_string(null) == b"required pointer is NULL"
+
+
+def test_published_code_object_is_the_embedded_one():
+    """The build places the slice-1 code object next to the library for the
+    module entry points; its SHA-256 is the lifecycle artifact's finalizer
+    identity, i.e. the bytes the library embeds."""
+    import hashlib
+    from fe2o3_amd import _lib, lifecycle
+    path = os.path.join(os.path.dirname(_lib.LIB_PATH), "tiled_gemm_lds_v1.co")
+    with open(path, "rb") as f:
+        data = f.read()
+    assert hashlib.sha256(data).digest() == bytes(lifecycle.artifact().finalizer_identity)

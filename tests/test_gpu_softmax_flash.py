@@ -99,12 +99,12 @@ def test_row_softmax_rows_against_oracle(gpu, oracle, rows, cols, masked):
         assert rc == 0, (r, rc, bad)
 
 
-def test_row_softmax_config3c_rows_sum_to_one(gpu, oracle):
+def test_row_softmax_config3c_every_row(gpu, oracle):
     """BASELINE config 3c at full size: 1,048,576 rows x 4096 fp32 (the
-    bench's N(0,1) input, seed 3).  Every row sums to 1 within the
-    reference's 6e-5 (read back in 1 GiB chunks), and 1024 rows spread over
-    all chunks, first and last rows included, match the oracle element by
-    element under the OCML policy."""
+    bench's N(0,1) input, seed 3).  Every row, element by element, against
+    the f64 oracle under the OCML comparison policy (abs 3e-6 + rel 3e-5 or
+    64 ULP per element, row sum within 6e-5), checked in C over the rows of
+    each 1 GiB chunk (oracle.row_softmax_check_rows)."""
     rows, cols = 8 * 32 * 4096, 4096
     kern = _k()
     x = gpu.alloc(rows * cols, np.float32)
@@ -114,20 +114,14 @@ def test_row_softmax_config3c_rows_sum_to_one(gpu, oracle):
     chunk = 65536
     checked = 0
     for c0 in range(0, rows, chunk):
-        out = y.view(c0 * cols, chunk * cols).download().reshape(chunk, cols)
-        sums = np.sum(out, axis=1, dtype=np.float64)
-        bad = np.nonzero(np.abs(sums - 1.0) > 6e-5)[0]
-        assert bad.size == 0, (c0 + int(bad[0]), float(sums[bad[0]]))
-        picks = sorted({0, chunk - 1} | {int(v) for v in np.random.default_rng(c0).choice(
-            np.arange(1, chunk - 1), 62, replace=False)})
-        xs = x.view(c0 * cols, chunk * cols).download().reshape(chunk, cols)[picks]
-        rc, ref = oracle.row_softmax_rows(xs, len(picks), cols)
-        assert rc == 0
-        for i, r in enumerate(picks):
-            assert oracle.compare_row_softmax_v1(ref[i], out[r], **oracle.GFX_SOFTMAX_POLICY)[0] == 0, \
-                c0 + r
-        checked += len(picks)
-    assert checked >= 1024
+        hx = x.view(c0 * cols, chunk * cols).download()
+        hy = y.view(c0 * cols, chunk * cols).download()
+        rc, st = oracle.row_softmax_check_rows(hx, hy, chunk, cols, **oracle.GFX_SOFTMAX_POLICY)
+        assert rc == 0, (c0, rc)
+        assert st["failing_rows"] == 0, (c0 + st["first_failing_row"], st)
+        assert st["max_row_sum_err"] <= 6e-5, (c0, st)
+        checked += chunk
+    assert checked == rows
 
 
 def test_row_softmax_rejects_zero_cols(gpu):
@@ -214,13 +208,14 @@ def test_flash_small_all_rows(gpu, oracle, b, h, s, causal):
 @pytest.mark.parametrize("causal", [False, True])
 def test_flash_config3_sampled_rows(gpu, oracle, causal):
     """B8 H32 S4096 D128, Q/K/V ~ N(0,1) bf16, scale
-    1/sqrt(128), against the two-pass f64 oracle with the LSE: 8 query rows
-    in every one of the 256 (batch, head), one per 512-row band at a
-    position that varies with the head, plus 64 rows (first, last and
-    128-row tile edges among them) in 16 heads spread over every batch."""
+    1/sqrt(128), against the two-pass f64 oracle with the LSE: 64 query rows
+    in every one of the 256 (batch, head), one per 64-row band at a position
+    that varies with the head and band (16,384 rows), plus 64 rows (first,
+    last and 128-row tile edges among them) in 16 heads spread over every
+    batch."""
     b, h, s = 8, 32, 4096
     (q, k, v), out, lse, scale = _flash(gpu, b, h, s, causal, seed=2)
-    per = 8
+    per = 64
     bh_all = np.repeat(np.arange(b * h, dtype=np.uint32), per)
     band = np.tile(np.arange(per, dtype=np.uint32), b * h)
     rows_all = band * (s // per) + (bh_all * 67 + band * 131) % (s // per)

@@ -210,3 +210,33 @@ def test_softmax_rows_is_rowwise_oracle(oracle):
     for r in range(8):
         _, one, _ = oracle.row_softmax_oracle_v1(x[r * 4096:(r + 1) * 4096])
         assert np.array_equal(out[r].view(np.uint32), one.view(np.uint32))
+
+
+def test_row_softmax_check_rows_counts_what_the_row_compare_rejects(oracle):
+    """The many-row check (fe2o3o_row_softmax_check_rows, used on config 3c's
+    million rows) is the per-row oracle plus the contract's comparison: it
+    passes the oracle's own output, and on planted mistakes (on the CPU) it
+    fails exactly the rows that compare_row_softmax_v1 rejects, reporting the
+    first one, a NaN as a NaN difference and the row-sum error."""
+    rng = np.random.default_rng(11)
+    rows, cols = 257, 4096
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    rc, ref = oracle.row_softmax_rows(x, rows, cols)
+    assert rc == 0
+    rc, st = oracle.row_softmax_check_rows(x, ref, rows, cols)
+    assert rc == 0 and st["failing_rows"] == 0 and st["first_failing_row"] == rows
+    assert st["max_abs_diff"] == 0.0 and st["max_row_sum_err"] < 1e-6
+    y = ref.copy()
+    y[200, 5] += 1e-4        # beyond abs 3e-6 + rel 3e-5 and 64 ULP
+    y[31, 4000] *= 1.5
+    y[100, 0] *= 1.0 + 1e-6  # within the policy
+    rc, st = oracle.row_softmax_check_rows(x, y, rows, cols)
+    assert rc == 0 and st["failing_rows"] == 2 and st["first_failing_row"] == 31
+    want = [r for r in range(rows)
+            if oracle.compare_row_softmax_v1(ref[r], y[r], **oracle.GFX_SOFTMAX_POLICY)[0] != 0]
+    assert want == [31, 200]
+    assert abs(st["max_abs_diff"] - float(np.max(np.abs(y.astype(np.float64) - ref)))) < 1e-12
+    y[7, 7] = np.nan
+    rc, st = oracle.row_softmax_check_rows(x, y, rows, cols)
+    assert st["failing_rows"] == 3 and st["first_failing_row"] == 7
+    assert np.isnan(st["max_abs_diff"]) and np.isnan(st["max_row_sum_err"])
