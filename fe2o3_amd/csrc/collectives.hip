@@ -106,7 +106,7 @@ int32_t fe2o3_wave64_collectives_v1(const float* input, uint64_t input_len, uint
                                     float* reduction, uint64_t reduction_len, float* inclusive,
                                     uint64_t inclusive_len, float* exclusive,
                                     uint64_t exclusive_len, void* stream) {
-  FE2O3_FAULT("fe2o3_wave64_collectives_v1");
+  FE2O3_ENTRY("fe2o3_wave64_collectives_v1");
   if (input_len != 64 || reduction_len != 64 || inclusive_len != 64 || exclusive_len != 64)
     return FE2O3_ERR_LENGTH;
   if (!input || !reduction || !inclusive || !exclusive) return FE2O3_ERR_NULL;
@@ -120,7 +120,7 @@ int32_t fe2o3_wave64_collectives_rows(const float* input, uint64_t input_len,
                                       uint64_t reduction_len, float* inclusive,
                                       uint64_t inclusive_len, float* exclusive,
                                       uint64_t exclusive_len, uint64_t rows, void* stream) {
-  FE2O3_FAULT("fe2o3_wave64_collectives_rows");
+  FE2O3_ENTRY("fe2o3_wave64_collectives_rows");
   if (rows > (UINT64_MAX / 64u)) return FE2O3_ERR_OVERFLOW;
   const uint64_t n = rows * 64u;
   if (input_len != n || masks_len != rows || reduction_len != n || inclusive_len != n ||
@@ -139,7 +139,7 @@ int32_t fe2o3_wave64_collectives_rows(const float* input, uint64_t input_len,
 
 int32_t fe2o3_lds_reduce_i32_v1(const int32_t* values, uint64_t values_len, int32_t* output,
                                 uint64_t output_len, void* stream) {
-  FE2O3_FAULT("fe2o3_lds_reduce_i32_v1");
+  FE2O3_ENTRY("fe2o3_lds_reduce_i32_v1");
   if (values_len != 64 || output_len != 1) return FE2O3_ERR_LENGTH;
   if (!values || !output) return FE2O3_ERR_NULL;
   lds_reduce_i32_kernel<<<1, 64, 0, (hipStream_t)stream>>>(values, output);
@@ -149,7 +149,7 @@ int32_t fe2o3_lds_reduce_i32_v1(const int32_t* values, uint64_t values_len, int3
 int32_t fe2o3_scoped_atomic_add_u32_v1(const uint32_t* values, uint64_t values_len,
                                        const uint32_t* eligible, uint64_t eligible_len,
                                        uint32_t* target, void* stream) {
-  FE2O3_FAULT("fe2o3_scoped_atomic_add_u32_v1");
+  FE2O3_ENTRY("fe2o3_scoped_atomic_add_u32_v1");
   if (values_len != 64 || eligible_len != 64) return FE2O3_ERR_LENGTH;
   if (!values || !eligible || !target) return FE2O3_ERR_NULL;
   if (((uintptr_t)target & 3u) != 0) return FE2O3_ERR_ALIGNMENT;

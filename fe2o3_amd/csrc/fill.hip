@@ -83,6 +83,7 @@ extern "C" {
 
 int32_t fe2o3_fill_normal_bf16(uint16_t* out, uint64_t n, uint64_t seed, uint64_t domain,
                                float scale, uint64_t first_index, void* stream) {
+  FE2O3_ENTRY("fe2o3_fill_normal_bf16");
   if (n == 0) return FE2O3_OK;
   if (out == nullptr) return FE2O3_ERR_NULL;
   fill_normal_bf16_kernel<<<fill_blocks(n), 256, 0, (hipStream_t)stream>>>(out, n, seed, domain,
@@ -92,6 +93,7 @@ int32_t fe2o3_fill_normal_bf16(uint16_t* out, uint64_t n, uint64_t seed, uint64_
 
 int32_t fe2o3_fill_normal_f32(float* out, uint64_t n, uint64_t seed, uint64_t domain, float scale,
                               uint64_t first_index, void* stream) {
+  FE2O3_ENTRY("fe2o3_fill_normal_f32");
   if (n == 0) return FE2O3_OK;
   if (out == nullptr) return FE2O3_ERR_NULL;
   fill_normal_f32_kernel<<<fill_blocks(n), 256, 0, (hipStream_t)stream>>>(out, n, seed, domain,
@@ -101,6 +103,7 @@ int32_t fe2o3_fill_normal_f32(float* out, uint64_t n, uint64_t seed, uint64_t do
 
 int32_t fe2o3_fill_uniform_f32(float* out, uint64_t n, uint64_t seed, uint64_t domain,
                                uint64_t first_index, void* stream) {
+  FE2O3_ENTRY("fe2o3_fill_uniform_f32");
   if (n == 0) return FE2O3_OK;
   if (out == nullptr) return FE2O3_ERR_NULL;
   fill_uniform_f32_kernel<<<fill_blocks(n), 256, 0, (hipStream_t)stream>>>(out, n, seed, domain,

@@ -427,7 +427,7 @@ int32_t fe2o3_flash_attention_causal_f32_b1_h1_n8_d16_v1(const float* q, uint64_
                                                           const float* v, uint64_t v_len,
                                                           float* output, uint64_t output_len,
                                                           void* stream) {
-  FE2O3_FAULT("fe2o3_flash_attention_causal_f32_b1_h1_n8_d16_v1");
+  FE2O3_ENTRY("fe2o3_flash_attention_causal_f32_b1_h1_n8_d16_v1");
   const uint64_t n = P_N * P_D;
   if (q_len != n || k_len != n || v_len != n || output_len != n) return FE2O3_ERR_LENGTH;
   if (!q || !k || !v || !output) return FE2O3_ERR_NULL;
@@ -442,7 +442,7 @@ int32_t fe2o3_flash_attention_fwd(const uint16_t* q, uint64_t q_len, const uint1
                                   uint64_t o_len, float* lse, uint64_t lse_len, uint32_t batch,
                                   uint32_t heads, uint32_t seq, uint32_t head_dim, int32_t causal,
                                   float scale, void* stream) {
-  FE2O3_FAULT("fe2o3_flash_attention_fwd");
+  FE2O3_ENTRY("fe2o3_flash_attention_fwd");
   if (head_dim != D) return FE2O3_ERR_SHAPE;
   const uint64_t bh = (uint64_t)batch * heads;
   const uint64_t n = bh * seq * head_dim;

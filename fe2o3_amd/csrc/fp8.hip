@@ -293,7 +293,7 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
 extern "C" {
 
 int32_t fe2o3_amax_f32(const float* x, uint64_t x_len, float* amax, void* stream) {
-  FE2O3_FAULT("fe2o3_amax_f32");
+  FE2O3_ENTRY("fe2o3_amax_f32");
   if (!amax || (x_len && !x)) return FE2O3_ERR_NULL;
   if (((uintptr_t)x & 15u) != 0) return FE2O3_ERR_ALIGNMENT;
   hipStream_t s = (hipStream_t)stream;
@@ -304,7 +304,7 @@ int32_t fe2o3_amax_f32(const float* x, uint64_t x_len, float* amax, void* stream
 }
 
 int32_t fe2o3_fp8_scale_from_amax(const float* amax, float* scale, void* stream) {
-  FE2O3_FAULT("fe2o3_fp8_scale_from_amax");
+  FE2O3_ENTRY("fe2o3_fp8_scale_from_amax");
   if (!amax || !scale) return FE2O3_ERR_NULL;
   scale_kernel<<<1, 1, 0, (hipStream_t)stream>>>(amax, scale);
   return fe2o3_host::after_launch();
@@ -312,7 +312,7 @@ int32_t fe2o3_fp8_scale_from_amax(const float* amax, float* scale, void* stream)
 
 int32_t fe2o3_quantize_e4m3(const float* x, uint64_t x_len, const float* scale, uint8_t* q,
                             uint64_t q_len, void* stream) {
-  FE2O3_FAULT("fe2o3_quantize_e4m3");
+  FE2O3_ENTRY("fe2o3_quantize_e4m3");
   if (x_len != q_len) return FE2O3_ERR_LENGTH;
   if (x_len == 0) return FE2O3_OK;
   if (!x || !scale || !q) return FE2O3_ERR_NULL;
@@ -324,7 +324,7 @@ int32_t fe2o3_quantize_e4m3(const float* x, uint64_t x_len, const float* scale, 
 int32_t fe2o3_gemm_fp8_nt(const uint8_t* a, uint64_t a_len, const uint8_t* b, uint64_t b_len,
                           const float* scale_a, const float* scale_b, uint16_t* c, uint64_t c_len,
                           uint32_t m, uint32_t n, uint32_t k, void* stream) {
-  FE2O3_FAULT("fe2o3_gemm_fp8_nt");
+  FE2O3_ENTRY("fe2o3_gemm_fp8_nt");
   if (a_len != (uint64_t)m * k || b_len != (uint64_t)n * k || c_len != (uint64_t)m * n)
     return FE2O3_ERR_LENGTH;
   if (c_len == 0) return FE2O3_OK;

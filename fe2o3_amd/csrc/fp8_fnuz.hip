@@ -154,7 +154,7 @@ extern "C" {
 
 int32_t fe2o3_fp8_fnuz_from_f32(const float* x, uint64_t x_len, uint8_t* q, uint64_t q_len,
                                 int32_t format, void* stream) {
-  FE2O3_FAULT("fe2o3_fp8_fnuz_from_f32");
+  FE2O3_ENTRY("fe2o3_fp8_fnuz_from_f32");
   if (format != FE2O3_FP8_FNUZ_E4M3 && format != FE2O3_FP8_FNUZ_E5M2) return FE2O3_ERR_SHAPE;
   if (x_len != q_len) return FE2O3_ERR_LENGTH;
   if (x_len == 0) return FE2O3_OK;
@@ -169,7 +169,7 @@ int32_t fe2o3_fp8_fnuz_from_f32(const float* x, uint64_t x_len, uint8_t* q, uint
 
 int32_t fe2o3_fp8_fnuz_to_f32(const uint8_t* q, uint64_t q_len, float* x, uint64_t x_len,
                               int32_t format, void* stream) {
-  FE2O3_FAULT("fe2o3_fp8_fnuz_to_f32");
+  FE2O3_ENTRY("fe2o3_fp8_fnuz_to_f32");
   if (format != FE2O3_FP8_FNUZ_E4M3 && format != FE2O3_FP8_FNUZ_E5M2) return FE2O3_ERR_SHAPE;
   if (x_len != q_len) return FE2O3_ERR_LENGTH;
   if (q_len == 0) return FE2O3_OK;

@@ -171,7 +171,7 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
 extern "C" int32_t fe2o3_gemm_bf16_nt(const uint16_t* a, uint64_t a_len, const uint16_t* b,
                                       uint64_t b_len, uint16_t* c, uint64_t c_len, uint32_t m,
                                       uint32_t n, uint32_t k, void* stream) {
-  FE2O3_FAULT("fe2o3_gemm_bf16_nt");
+  FE2O3_ENTRY("fe2o3_gemm_bf16_nt");
   if (a_len != (uint64_t)m * k || b_len != (uint64_t)n * k || c_len != (uint64_t)m * n)
     return FE2O3_ERR_LENGTH;
   if (c_len == 0) return FE2O3_OK;

@@ -291,7 +291,7 @@ extern "C" {
 
 int32_t fe2o3_tiled_gemm_lds_slice1_v1(const uint16_t* a, uint64_t a_len, const uint16_t* b,
                                        uint64_t b_len, float* c, uint64_t c_len, void* stream) {
-  FE2O3_FAULT("fe2o3_tiled_gemm_lds_slice1_v1");
+  FE2O3_ENTRY("fe2o3_tiled_gemm_lds_slice1_v1");
   return tile16(a, a_len, b, b_len, c, c_len, stream);
 }
 
@@ -300,14 +300,14 @@ int32_t fe2o3_moe_expert_gemm_bf16_m16_n16_k16_v1(const uint16_t* activations,
                                                   const uint16_t* weights, uint64_t weights_len,
                                                   float* output, uint64_t output_len,
                                                   void* stream) {
-  FE2O3_FAULT("fe2o3_moe_expert_gemm_bf16_m16_n16_k16_v1");
+  FE2O3_ENTRY("fe2o3_moe_expert_gemm_bf16_m16_n16_k16_v1");
   return tile16(activations, activations_len, weights, weights_len, output, output_len, stream);
 }
 
 int32_t fe2o3_tiled_gemm_v1(const uint16_t* a, uint64_t a_len, const uint16_t* b, uint64_t b_len,
                             float* c, uint64_t c_len, uint32_t m, uint32_t n, uint32_t k,
                             void* stream) {
-  FE2O3_FAULT("fe2o3_tiled_gemm_v1");
+  FE2O3_ENTRY("fe2o3_tiled_gemm_v1");
   // ShapeV1::checked (contract.rs:145-179): an empty output needs no
   // operand buffers; otherwise byte extents of A, B, C in that order
   if (m == 0 || n == 0) {
@@ -555,7 +555,7 @@ int32_t fe2o3_tiled_gemm_general_v1(const uint16_t* a, uint64_t a_len, const uin
                                     uint64_t b_len, float* c, uint64_t c_len, uint32_t m,
                                     uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb,
                                     uint32_t ldc, float alpha, float beta, void* stream) {
-  FE2O3_FAULT("fe2o3_tiled_gemm_general_v1");
+  FE2O3_ENTRY("fe2o3_tiled_gemm_general_v1");
   return general_gemm<false>(a, a_len, b, b_len, c, c_len, m, n, k, lda, ldb, ldc, alpha, beta,
                              stream);
 }
@@ -565,7 +565,7 @@ int32_t fe2o3_tiled_gemm_general_vector_a_v1(const uint16_t* a, uint64_t a_len,
                                              uint64_t c_len, uint32_t m, uint32_t n, uint32_t k,
                                              uint32_t lda, uint32_t ldb, uint32_t ldc,
                                              float alpha, float beta, void* stream) {
-  FE2O3_FAULT("fe2o3_tiled_gemm_general_vector_a_v1");
+  FE2O3_ENTRY("fe2o3_tiled_gemm_general_vector_a_v1");
   return general_gemm<true>(a, a_len, b, b_len, c, c_len, m, n, k, lda, ldb, ldc, alpha, beta,
                             stream);
 }
@@ -573,7 +573,7 @@ int32_t fe2o3_tiled_gemm_general_vector_a_v1(const uint16_t* a, uint64_t a_len,
 int32_t fe2o3_scalar_gemm_v1(const float* a, uint64_t a_len, const float* b, uint64_t b_len,
                              float* c, uint64_t c_len, uint32_t m, uint32_t n, uint32_t k,
                              void* stream) {
-  FE2O3_FAULT("fe2o3_scalar_gemm_v1");
+  FE2O3_ENTRY("fe2o3_scalar_gemm_v1");
   const uint64_t ea = (uint64_t)m * k, eb = (uint64_t)k * n, ec = (uint64_t)m * n;
   if (a_len < ea || b_len < eb || c_len < ec) return FE2O3_ERR_LENGTH;
   if (ec == 0) return FE2O3_OK;

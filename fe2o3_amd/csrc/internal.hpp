@@ -66,7 +66,16 @@ struct KernelRegistrar {
 
 }  // namespace fe2o3_host
 
-#define FE2O3_FAULT(entry)                                   \
-  do {                                                      \
-    if (fe2o3_host::fault_point(entry)) return FE2O3_ERR_INJECTED; \
+// First statement of every C-ABI entry point that launches kernels:
+//  - FE2O3_FAULT_POINT naming `entry` fails it with FE2O3_ERR_INJECTED
+//    before anything else;
+//  - the calling thread's last HIP error is cleared, so after_launch()
+//    reports the entry's own launches only.  HIP keeps the last failed call
+//    of any API in thread-local state until it is read (a failed
+//    hipModuleGetFunction, say, or the caller's own failed launch), and
+//    successful calls do not reset it.
+#define FE2O3_ENTRY(entry)                                             \
+  do {                                                                \
+    if (fe2o3_host::fault_point(entry)) return FE2O3_ERR_INJECTED;     \
+    (void)hipGetLastError();                                          \
   } while (0)

@@ -1066,7 +1066,7 @@ int32_t fe2o3_lds_gemm_slice1_join_v1(const uint16_t* a, uint64_t a_len, const u
                                       uint64_t b_len, float* c, uint64_t c_len, int32_t device,
                                       void (*release)(void*), void* user,
                                       Fe2o3Slice1Lifecycle** out, Fe2o3Slice1ErrorV1* error) {
-  FE2O3_FAULT("fe2o3_lds_gemm_slice1_join_v1");
+  FE2O3_ENTRY("fe2o3_lds_gemm_slice1_join_v1");
   if (!out) return FE2O3_ERR_NULL;
   *out = nullptr;
   // The leases are released exactly once, also when the join is refused.
@@ -1141,7 +1141,7 @@ int32_t fe2o3_lds_gemm_slice1_hip_adapter_v1(int32_t device, Fe2o3Slice1AdapterV
 int32_t fe2o3_lds_gemm_slice1_load_v1(Fe2o3Slice1Lifecycle* lc,
                                       const Fe2o3Slice1AdapterV1* adapter,
                                       Fe2o3Slice1ErrorV1* error) {
-  FE2O3_FAULT("fe2o3_lds_gemm_slice1_load_v1");
+  FE2O3_ENTRY("fe2o3_lds_gemm_slice1_load_v1");
   if (!lc || !adapter) return FE2O3_ERR_NULL;
   if (lc->state != FE2O3_SLICE1_JOINED) return state_error(error, lc->state);
   lc->adapter = *adapter;
@@ -1156,7 +1156,7 @@ int32_t fe2o3_lds_gemm_slice1_load_v1(Fe2o3Slice1Lifecycle* lc,
 
 int32_t fe2o3_lds_gemm_slice1_dispatch_and_wait_v1(Fe2o3Slice1Lifecycle* lc,
                                                    Fe2o3Slice1ErrorV1* error) {
-  FE2O3_FAULT("fe2o3_lds_gemm_slice1_dispatch_and_wait_v1");
+  FE2O3_ENTRY("fe2o3_lds_gemm_slice1_dispatch_and_wait_v1");
   if (!lc) return FE2O3_ERR_NULL;
   if (lc->state != FE2O3_SLICE1_LOADED) return state_error(error, lc->state);
   return do_dispatch(lc, error);

@@ -780,7 +780,7 @@ int32_t fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1(
     uint64_t admitted_len, uint32_t* expert_offsets, uint64_t offsets_len, uint32_t* route_slots,
     uint64_t slots_len, uint32_t* permutation, uint64_t permutation_len, uint32_t* inverse,
     uint64_t inverse_len, void* stream) {
-  FE2O3_FAULT("fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1");
+  FE2O3_ENTRY("fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1");
   // examples/moe_top2_v1/src/contract.rs:3-29: T=8, E=4, K=2, C=4
   if (logits_len != 32 || top2_len != 16 || requested_len != 4 || admitted_len != 4 ||
       offsets_len != 5 || slots_len != 16 || permutation_len != 16 || inverse_len != 16)
@@ -798,7 +798,7 @@ int32_t fe2o3_moe_top2_route(const void* logits, uint64_t logits_len, uint32_t l
                              uint64_t permutation_len, uint32_t* inverse, uint64_t inverse_len,
                              float* route_weights, uint64_t weights_len, uint32_t tokens,
                              uint32_t experts, uint32_t capacity, void* stream) {
-  FE2O3_FAULT("fe2o3_moe_top2_route");
+  FE2O3_ENTRY("fe2o3_moe_top2_route");
   return route(logits, logits_len, logits_dtype, top2_experts, top2_len, requested_counts,
                requested_len, admitted_counts, admitted_len, expert_offsets, offsets_len,
                route_slots, slots_len, permutation, permutation_len, inverse, inverse_len,
@@ -811,7 +811,7 @@ int32_t fe2o3_moe_expert_combine_f32_t8_k2_o16_v1(const float* compact_output,
                                                   const float* route_weights, uint64_t weights_len,
                                                   float* combined_output, uint64_t combined_len,
                                                   void* stream) {
-  FE2O3_FAULT("fe2o3_moe_expert_combine_f32_t8_k2_o16_v1");
+  FE2O3_ENTRY("fe2o3_moe_expert_combine_f32_t8_k2_o16_v1");
   if (compact_len != 256 || inverse_len != 16 || weights_len != 16 || combined_len != 128)
     return FE2O3_ERR_LENGTH;
   if (!compact_output || !inverse || !route_weights || !combined_output) return FE2O3_ERR_NULL;
@@ -974,7 +974,7 @@ int32_t fe2o3_moe_ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_
                            uint64_t out_len, void* workspace, uint64_t workspace_bytes,
                            uint32_t tokens, uint32_t hidden, uint32_t ffn, uint32_t experts,
                            void* stream) {
-  FE2O3_FAULT("fe2o3_moe_ffn_top2");
+  FE2O3_ENTRY("fe2o3_moe_ffn_top2");
   (void)top2_experts;
   return ffn_top2(x, x_len, w_gate, w_gate_len, w_up, w_up_len, w_down, w_down_len, top2_len,
                   expert_offsets, offsets_len, permutation, permutation_len, inverse, inverse_len,
@@ -993,7 +993,7 @@ int32_t fe2o3_moe_ffn_top2_noalloc(const uint16_t* x, uint64_t x_len, const uint
                                    uint16_t* out, uint64_t out_len, uint32_t tokens,
                                    uint32_t hidden, uint32_t ffn, uint32_t experts,
                                    void* stream) {
-  FE2O3_FAULT("fe2o3_moe_ffn_top2_noalloc");
+  FE2O3_ENTRY("fe2o3_moe_ffn_top2_noalloc");
   (void)top2_experts;
   if (fe2o3_moe_ffn_workspace_bytes(tokens, hidden, ffn, experts) > kNoAllocScratchBytes)
     return FE2O3_ERR_WORKSPACE;
@@ -1014,7 +1014,7 @@ int32_t fe2o3_moe_routing_check(const uint32_t* top2_experts, uint64_t top2_len,
                                 const uint32_t* inverse, uint64_t inverse_len, uint32_t tokens,
                                 uint32_t experts, uint32_t capacity, uint32_t* record,
                                 uint64_t record_len, void* stream) {
-  FE2O3_FAULT("fe2o3_moe_routing_check");
+  FE2O3_ENTRY("fe2o3_moe_routing_check");
   if (experts < 1 || experts > MAX_EXPERTS) return FE2O3_ERR_SHAPE;
   const uint64_t routes = 2ull * tokens;
   if (routes > CHECK_MAX_ROUTES) return FE2O3_ERR_SHAPE;

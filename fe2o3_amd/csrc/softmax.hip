@@ -189,7 +189,7 @@ extern "C" {
 
 int32_t fe2o3_row_softmax_v1(const float* input, uint64_t input_len, float* output,
                              uint64_t output_len, void* stream) {
-  FE2O3_FAULT("fe2o3_row_softmax_v1");
+  FE2O3_ENTRY("fe2o3_row_softmax_v1");
   // examples/row_softmax_v1: exactly one 64-element row.
   if (input_len != 64 || output_len != 64) return FE2O3_ERR_LENGTH;
   return row_softmax(input, input_len, output, output_len, nullptr, 0, 1, 64, stream);
@@ -198,7 +198,7 @@ int32_t fe2o3_row_softmax_v1(const float* input, uint64_t input_len, float* outp
 int32_t fe2o3_row_softmax(const float* input, uint64_t input_len, float* output,
                           uint64_t output_len, const uint8_t* mask, uint64_t mask_len,
                           uint64_t rows, uint64_t cols, void* stream) {
-  FE2O3_FAULT("fe2o3_row_softmax");
+  FE2O3_ENTRY("fe2o3_row_softmax");
   return row_softmax(input, input_len, output, output_len, mask, mask_len, rows, cols, stream);
 }
 

@@ -103,9 +103,11 @@ def test_module_seam_six_cases(gpu, oracle, from_file):
         _check(L.fe2o3_rt_module_unload(module), "unload")
 
 
-def test_module_seam_unknown_symbol_is_an_error(gpu):
+def test_module_seam_unknown_symbol_is_an_error(gpu, oracle):
     """A symbol the module does not hold is HIP's error (a positive status)
-    and leaves the function handle NULL; the module still unloads."""
+    and leaves the function handle NULL; the module still unloads.  The
+    failed lookup stays in HIP's thread-local last error; the next entry
+    point still reports its own launch (0) and computes its product."""
     from fe2o3_amd import _lib
     L = _lib.lib()
     _, data = _code_object()
@@ -116,3 +118,14 @@ def test_module_seam_unknown_symbol_is_an_error(gpu):
     rc = L.fe2o3_rt_module_get_function(C.byref(fn), module, b"tiled_gemm_lds_v2")
     assert rc > 0 and not fn.value
     _check(L.fe2o3_rt_module_unload(module), "unload")
+    m = n = k = 256
+    a = oracle.fill_normal_bf16(m * k, 1, 0xA, 1.0 / 16.0)
+    b = oracle.fill_normal_bf16(n * k, 1, 0xB, 1.0 / 16.0)
+    da, db = gpu.to_device(a), gpu.to_device(b)
+    dc = gpu.alloc(m * n, np.uint16)
+    rc = L.fe2o3_gemm_bf16_nt(da.ptr, da.count, db.ptr, db.count, dc.ptr, dc.count, m, n, k, None)
+    assert rc == 0, rc
+    _check(L.fe2o3_rt_device_synchronize(), "synchronize")
+    got = oracle.bf16_to_f32(dc.download()).reshape(m, n)
+    ref = oracle.gemm_bf16_nt_rows(m, n, k, a, b, 0, m).reshape(m, n)
+    assert float(np.max(np.abs(got - ref)) / np.max(np.abs(ref))) <= 1e-2
