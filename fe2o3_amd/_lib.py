@@ -263,6 +263,7 @@ SIGNATURES = {
     "fe2o3_quantize_e4m3": (i32, [vp, u64, vp, vp, u64, vp]),
     "fe2o3_fp8_fnuz_from_f32": (i32, [vp, u64, vp, u64, i32, vp]),
     "fe2o3_fp8_fnuz_to_f32": (i32, [vp, u64, vp, u64, i32, vp]),
+    "fe2o3_bf16_from_f32": (i32, [vp, u64, vp, u64, vp]),
     "fe2o3_gemm_fp8_nt": (i32, [vp, u64, vp, u64, vp, vp, vp, u64, u32, u32, u32, vp]),
     "fe2o3_moe_routing_check": (
         i32, [vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, vp, u64, u32, u32, u32, vp,

@@ -234,6 +234,11 @@ def fp8_fnuz_to_f32(q: DeviceBuffer, x: DeviceBuffer, fmt: int, stream=None,
           sync=sync)
 
 
+def bf16_from_f32(x: DeviceBuffer, out: DeviceBuffer, stream=None, sync=True) -> None:
+    """out = Bf16::from_f32(x) elementwise (crates/fe2o3-device/src/half.rs:182-190)."""
+    _call("fe2o3_bf16_from_f32", x.ptr, x.count, out.ptr, out.count, stream=stream, sync=sync)
+
+
 def gemm_fp8_nt(a, b, scale_a, scale_b, c, m, n, k, stream=None, sync=True) -> None:
     _call("fe2o3_gemm_fp8_nt", a.ptr, a.count, b.ptr, b.count, scale_a.ptr, scale_b.ptr,
           c.ptr, c.count, m, n, k, stream=stream, sync=sync)

@@ -445,6 +445,16 @@ int32_t fe2o3_fp8_fnuz_from_f32(const float *x, uint64_t x_len, uint8_t *q,
 int32_t fe2o3_fp8_fnuz_to_f32(const uint8_t *q, uint64_t q_len, float *x,
                               uint64_t x_len, int32_t format, void *stream);
 
+/* crates/fe2o3-device/src/half.rs:182-190 (Bf16::from_f32) over an array:
+ * out[i] = the bf16 bits of x[i], round to nearest, ties to even; a NaN
+ * keeps its sign and high payload bits and is quieted (| 0x0040).  The
+ * narrowing every bf16 output of the library goes through (gfx950's
+ * v_cvt_pk_bf16_f32).  Any alignment (16-byte loads and 8-byte stores when
+ * x is 16-byte and out 8-byte aligned).  FE2O3_ERR_LENGTH when the lengths
+ * differ; n = 0 launches nothing. */
+int32_t fe2o3_bf16_from_f32(const float *x, uint64_t x_len, uint16_t *out,
+                            uint64_t out_len, void *stream);
+
 /* ---- fp8 (OCP E4M3FN, per-tensor scale) ---------------------------------------------
  * Not in the reference (its only fp8 type is gfx942 FNUZ,
  * crates/fe2o3-device/src/fp8.rs:53-110, which gfx950's MFMA does not take):
