@@ -523,13 +523,54 @@ def sec_gemm_f32(ctx, stream, args):
                                  f"256^3 problem, {dt * 1e3:.1f} ms")}
 
 
+def sec_gemm_bf16_k4000(ctx, stream, args):
+    """The config-2 GEMM with K = 4000 (a multiple of 8, not of 64): the
+    pipelined tile with a partial last stage, beside the whole-stage K = 4096
+    of the main line (same M, N, data generator and seed)."""
+    from fe2o3_amd import kernels
+    from oracle import oracle as orc
+    m = n = 4096
+    res = {"workload": "bf16 GEMM M=N=4096, K=4000 (partial last k stage), else as config 2",
+           "kernel": "gemm_bf16_nt_256_kernel<k tail>", "unit": "TFLOP/s"}
+    vals = {}
+    for k in (4000, 4096):
+        a, b = ctx.alloc(m * k, np.uint16), ctx.alloc(n * k, np.uint16)
+        c = ctx.alloc(m * n, np.uint16)
+        kernels.fill_normal_bf16(a, 1, 0xA, float(1.0 / np.sqrt(k)), stream=stream)
+        kernels.fill_normal_bf16(b, 1, 0xB, float(1.0 / np.sqrt(k)), stream=stream)
+        prep = kernels.gemm_bf16_nt_gpu.Kernel.load(ctx).prepare(a, b, c, m, n, k)
+        ms = _timed(ctx, stream, lambda: prep.launch_async(stream), args)
+        vals[k] = (ms, 2.0 * m * n * k / (ms * 1e-3) / 1e12, a, b, c)
+    ms, tf, a, b, c = vals[4000]
+    res.update({"ms": ms, "value": round(tf, 2), "k4096_value": round(vals[4096][1], 2),
+                "ratio_to_k4096": round(tf / vals[4096][1], 4),
+                "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK["bf16"],
+                             "unit": "TFLOP/s", "frac": round(tf / PEAK["bf16"], 4)}})
+    if not args.cpu_baseline:
+        return res
+    k = 4000
+    ha, hb = a.download(), b.download()
+    got = _bf16(c.download()).reshape(m, n)
+    rows = 64
+    t0 = time.perf_counter()
+    ref = orc.gemm_bf16_nt_rows(m, n, k, ha, hb, 2048, 2048 + rows,
+                                threads=_cpu_threads()).reshape(rows, n)
+    dt = time.perf_counter() - t0
+    res["parity"] = {"max_rel_err": _rel(got[2048:2048 + rows], ref), "tolerance": 1e-2,
+                     "coverage": f"output rows 2048..{2048 + rows - 1}, every column"}
+    res["cpu_baseline"] = _cpu(2.0 * rows * n * k / dt / 1e12, "TFLOP/s", _cpu_threads(),
+                               f"oracle/gemm.c fe2o3o_gemm_bf16_nt_rows on the {rows} parity "
+                               f"rows, {dt:.2f} s")
+    return res
+
+
 def sec_gemm_general(ctx, stream, args):
     """tiled_gemm_general_v1 at 2048^3 with padded strides and alpha/beta
-    (C = 1.5 A B + 0.5 C, lda = ldb = ldc = 2056): the pipelined tile (the
-    shape qualifies; its 64 tiles of 256x256 would leave most CUs idle, so
-    it runs 256 tiles of 128x128), and both staged schedules on the same
-    data with A two bytes past a 16-byte boundary (which the tiles do not
-    take).
+    (C = 1.5 A B + 0.5 C, lda = ldb = ldc = 2056): the pipelined tile (its 64
+    tiles of 256x256 would leave most CUs idle, so it runs 256 tiles of
+    128x128), then the same data with A two bytes past a 16-byte boundary
+    through both schedules' entry points (the tiles cannot read such rows in
+    place; A is repacked into aligned rows first).
     Each launch reads and rewrites C (C converges to 3 A B); it is restored
     before the parity call."""
     from fe2o3_amd import _lib, kernels
@@ -551,10 +592,10 @@ def sec_gemm_general(ctx, stream, args):
                        "(tiled_gemm_general_v1)", "unit": "TFLOP/s"}
     outs = {}
     runs = (("pipelined", kernels.tiled_gemm_general_v1_gpu, a),
-            ("reference", kernels.tiled_gemm_general_v1_gpu, None),
-            ("vector_a", kernels.tiled_gemm_general_vector_a_v1_gpu, None))
+            ("a_offset_2_bytes", kernels.tiled_gemm_general_v1_gpu, None),
+            ("a_offset_2_bytes_vector_a", kernels.tiled_gemm_general_vector_a_v1_gpu, None))
     for name, kern, a_in in runs:
-        if a_in is None:  # A's data moved to the 2-byte offset: the staged kernels
+        if a_in is None:  # A's data moved to the 2-byte offset: repacked first
             check(_lib.lib().fe2o3_rt_memcpy_async(a_off.ptr, a.ptr, a.nbytes, 3, stream.handle),
                   "copy")
             a_in = a_off
@@ -568,8 +609,8 @@ def sec_gemm_general(ctx, stream, args):
         res[name] = {"ms": round(ms, 5), "value": round(tf, 2),
                      "frac": round(tf / PEAK["bf16"], 4)}
     res["kernel"] = ("gemm_general_pipe128_kernel<3> (pipelined, 128x128 tiles at this size); "
-                     "gemm_general_kernel<false> / <true> "
-                     "(staged schedules)")
+                     "with A at a 2-byte offset repack_rows_kernel, then the same tile")
+    res["a_offset_ratio"] = round(res["a_offset_2_bytes"]["value"] / res["pipelined"]["value"], 4)
     res["ms"] = res["pipelined"]["ms"]
     res["value"] = res["pipelined"]["value"]
     res["roofline"] = {"bound": "mfma", "achieved": res["value"], "peak": PEAK["bf16"],
@@ -585,11 +626,12 @@ def sec_gemm_general(ctx, stream, args):
                                           hc[r0 * ld:r0 * ld + (rows - 1) * ld + n], alpha, beta)
     dt = time.perf_counter() - t0
     got = np.stack([outs["pipelined"][(r0 + r) * ld:(r0 + r) * ld + n] for r in range(rows)])
-    same = all(outs[x].tobytes() == outs["pipelined"].tobytes() for x in ("reference", "vector_a"))
+    same = all(outs[x].tobytes() == outs["pipelined"].tobytes()
+               for x in ("a_offset_2_bytes", "a_offset_2_bytes_vector_a"))
     res["parity"] = {"max_rel_err": _rel(got.ravel(), ref) if rc == 0 else None,
                      "tolerance": 1e-5, "paths_bit_identical": bool(same),
                      "coverage": f"output rows {r0}..{r0 + rows - 1} (every column) against the "
-                                 "tiled CPU schedule; the three paths' whole outputs compared"}
+                                 "tiled CPU schedule; the three runs' whole outputs compared"}
     res["cpu_baseline"] = _cpu(2.0 * rows * n * k / dt / 1e12, "TFLOP/s", 1,
                                f"oracle/gemm.c fe2o3o_general_reference_v1 (tiled schedule, one "
                                f"thread) on the {rows}-row parity block, {dt:.2f} s")
@@ -747,6 +789,7 @@ SECONDARY = {
     "fp8_gemm": sec_fp8,
     "moe": sec_moe,
     "gemm_f32": sec_gemm_f32,
+    "gemm_bf16_k4000": sec_gemm_bf16_k4000,
     "gemm_general": sec_gemm_general,
     "gemm_general_4096": sec_gemm_general_4096,
     "collectives": sec_collectives,

@@ -125,9 +125,11 @@ FE2O3_DEVICE uint32_t swz_v(uint32_t r) { return ((r & 3u) << 1) ^ ((r & 3u) << 
 
 // K and V of one head are read through buffer resources (base = the head,
 // range = its seq * 256 bytes).  A partial last key tile (seq not a multiple
-// of 64) has rows past seq: the range check returns zero for them, and the
-// LDS-direct load writes those zeros into the tile, so the masked keys'
-// P = 0 meets V = 0 there, never a stale value of another tile or launch.  One tile is 16 loads of 1 KiB (4 rows of
+// of 64) has rows past seq: their loads take a VGPR offset past the range
+// (the range check covers the VGPR offset, not the scalar tile offset), so
+// the LDS-direct load writes zeros into the tile and the masked keys' P = 0
+// meets V = 0 there, never a value of the next head, of another tile or of
+// memory past the tensor.  One tile is 16 loads of 1 KiB (4 rows of
 // 256 B), wave w issuing loads j = 0 .. 16/WAVES - 1 of rows
 // 4 (WAVES j + w) .. +3.  The chunk swizzles depend on the row mod 16 only,
 // and 4 WAVES is a multiple of 16, so a thread's byte offset within the tile
@@ -156,16 +158,27 @@ constexpr int kAhead = 2;
 constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
 static_assert(16 % (2 * kLoadsPerTile) == 0, "a tile's copies spread evenly over 16 MFMAs");
 
+// past any head's range (seq * 256 < 2^31)
+constexpr uint32_t kKeyOutOfRange = 0x80000000u;
+
+// Load j of this thread's chunk of the tile at byte tile_byte.  RAGGED
+// (seq not a multiple of 64): a chunk of a row at or past the head's `bytes`
+// (seq * 256) loads zeros; otherwise every row of every tile is in range.
+template <bool RAGGED>
 FE2O3_DEVICE void copy_load(__amdgpu_buffer_rsrc_t src, uint32_t voff, uint32_t tile_byte,
-                            uint8_t* lds, uint32_t wave, int j) {
+                            uint32_t bytes, uint8_t* lds, uint32_t wave, int j) {
+  const uint32_t soff = tile_byte + 1024u * WAVES * j;
+  const uint32_t off = !RAGGED || voff + soff < bytes ? voff : kKeyOutOfRange;
   __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (lds_void_t*)(lds + (WAVES * j + wave) * 1024u),
-                                           16, voff, tile_byte + 1024u * WAVES * j, 0, 0);
+                                           16, off, soff, 0, 0);
 }
 
+template <bool RAGGED>
 FE2O3_DEVICE void issue_tile(__amdgpu_buffer_rsrc_t src, uint32_t voff, uint32_t tile_byte,
-                             uint8_t* lds, uint32_t wave) {
+                             uint32_t bytes, uint8_t* lds, uint32_t wave) {
 #pragma unroll
-  for (int j = 0; j < kLoadsPerTile; ++j) copy_load(src, voff, tile_byte, lds, wave, j);
+  for (int j = 0; j < kLoadsPerTile; ++j)
+    copy_load<RAGGED>(src, voff, tile_byte, bytes, lds, wave, j);
 }
 
 // V^T operand of one O^T MFMA (d rows 32*db.., keys of half h of 32-key block
@@ -188,7 +201,9 @@ FE2O3_DEVICE bf16x8_t read_vt(const uint8_t* vt, uint32_t db, uint32_t kb, uint3
   return __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-template <bool CAUSAL>
+// RAGGED: seq is not a multiple of 64, so the last key tile is partial and
+// its copies mask the rows past seq (copy_load).
+template <bool CAUSAL, bool RAGGED = false>
 __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse,
@@ -220,8 +235,9 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
   const uint16_t* kh = k + head;
   const uint16_t* vh = v + head;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(w);  // wave-uniform
-  const __amdgpu_buffer_rsrc_t ksrc = head_rsrc(kh, seq * (uint32_t)(D * 2));
-  const __amdgpu_buffer_rsrc_t vsrc = head_rsrc(vh, seq * (uint32_t)(D * 2));
+  const uint32_t head_bytes = seq * (uint32_t)(D * 2);
+  const __amdgpu_buffer_rsrc_t ksrc = head_rsrc(kh, head_bytes);
+  const __amdgpu_buffer_rsrc_t vsrc = head_rsrc(vh, head_bytes);
   const uint32_t k_off = tile_voffset<false>(), v_off = tile_voffset<true>();
   for (uint32_t item = 0; item < (paired ? 2u : 1u); ++item) {
   // heaviest first: the higher query tile of the pair, or rank order reversed
@@ -248,8 +264,8 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
 
   const uint32_t kv_tiles = (seq + BKV - 1u) / BKV;
   const uint32_t n_kv = CAUSAL ? min((qt + 1u) * (BQ / BKV), kv_tiles) : kv_tiles;
-  issue_tile(ksrc, k_off, 0u, smem, wave);
-  issue_tile(vsrc, v_off, 0u, smem + TILE_BYTES, wave);
+  issue_tile<RAGGED>(ksrc, k_off, 0u, head_bytes, smem, wave);
+  issue_tile<RAGGED>(vsrc, v_off, 0u, head_bytes, smem + TILE_BYTES, wave);
   wait_vmcnt0();
   lds_barrier();
 
@@ -264,8 +280,8 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
     // keys key0..key0+63 vs. rows q_row0..q_row0+31
     const bool active = !CAUSAL || key0 <= q_row0 + 31u;
     if (!active) {
-      issue_tile(ksrc, k_off, nt, nxt, wave);
-      issue_tile(vsrc, v_off, nt, nxt + TILE_BYTES, wave);
+      issue_tile<RAGGED>(ksrc, k_off, nt, head_bytes, nxt, wave);
+      issue_tile<RAGGED>(vsrc, v_off, nt, head_bytes, nxt + TILE_BYTES, wave);
     }
     if (active) {
       // S^T = K Q^T : two 32-key blocks.  MFMA i (0..15) is key block kb = i%2
@@ -296,7 +312,7 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
         if (i % kCopyEvery == 0) {
           const int n = i / kCopyEvery, jj = n % kLoadsPerTile;
           const bool is_v = n >= kLoadsPerTile;
-          copy_load(is_v ? vsrc : ksrc, is_v ? v_off : k_off, nt,
+          copy_load<RAGGED>(is_v ? vsrc : ksrc, is_v ? v_off : k_off, nt, head_bytes,
                     nxt + (is_v ? TILE_BYTES : 0), wave, jj);
         }
         if (i + kAhead < 16) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
@@ -416,7 +432,9 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
 const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_flash_attention_causal_f32_b1_h1_n8_d16_v1", "flash_profile_kernel", (const void*)flash_profile_kernel, 64, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_flash_attention_fwd", "flash_fwd_kernel<false>", (const void*)flash_fwd_kernel<false>, THREADS, SMEM_BYTES}),
-    fe2o3_host::KernelRegistrar({"fe2o3_flash_attention_fwd", "flash_fwd_kernel<true>", (const void*)flash_fwd_kernel<true>, THREADS, SMEM_BYTES})};
+    fe2o3_host::KernelRegistrar({"fe2o3_flash_attention_fwd", "flash_fwd_kernel<true>", (const void*)flash_fwd_kernel<true>, THREADS, SMEM_BYTES}),
+    fe2o3_host::KernelRegistrar({"fe2o3_flash_attention_fwd", "flash_fwd_kernel<false, ragged>", (const void*)flash_fwd_kernel<false, true>, THREADS, SMEM_BYTES}),
+    fe2o3_host::KernelRegistrar({"fe2o3_flash_attention_fwd", "flash_fwd_kernel<true, ragged>", (const void*)flash_fwd_kernel<true, true>, THREADS, SMEM_BYTES})};
 
 }  // namespace
 
@@ -458,7 +476,9 @@ int32_t fe2o3_flash_attention_fwd(const uint16_t* q, uint64_t q_len, const uint1
   if (!(scale > 0.0f) || !__builtin_isfinite(scale)) return FE2O3_ERR_SHAPE;
   const float scale_log2 = scale * 1.4426950408889634f;
   static const int32_t lds_rc = fe2o3_host::set_dynamic_lds(
-      {(const void*)flash_fwd_kernel<true>, (const void*)flash_fwd_kernel<false>}, SMEM_BYTES);
+      {(const void*)flash_fwd_kernel<true>, (const void*)flash_fwd_kernel<false>,
+       (const void*)flash_fwd_kernel<true, true>, (const void*)flash_fwd_kernel<false, true>},
+      SMEM_BYTES);
   if (lds_rc != FE2O3_OK) return lds_rc;
   // one linear workgroup id per (query tile, batch*head); see the kernel
   // causal: pairs of query tiles per workgroup (every workgroup the same
@@ -471,11 +491,19 @@ int32_t fe2o3_flash_attention_fwd(const uint16_t* q, uint64_t q_len, const uint1
   const int32_t topo_rc = fe2o3_host::device_topology(&topo);
   if (topo_rc != FE2O3_OK) return topo_rc;
   const dim3 grid((unsigned)wgs);
-  if (causal)
-    flash_fwd_kernel<true><<<grid, THREADS, SMEM_BYTES, (hipStream_t)stream>>>(
+  hipStream_t s = (hipStream_t)stream;
+  const bool ragged = seq % BKV != 0u;  // a partial last key tile
+  if (causal && ragged)
+    flash_fwd_kernel<true, true><<<grid, THREADS, SMEM_BYTES, s>>>(
+        q, k, v, o, lse, seq, (uint32_t)bh, scale_log2, paired, topo.xcds);
+  else if (causal)
+    flash_fwd_kernel<true><<<grid, THREADS, SMEM_BYTES, s>>>(
+        q, k, v, o, lse, seq, (uint32_t)bh, scale_log2, paired, topo.xcds);
+  else if (ragged)
+    flash_fwd_kernel<false, true><<<grid, THREADS, SMEM_BYTES, s>>>(
         q, k, v, o, lse, seq, (uint32_t)bh, scale_log2, paired, topo.xcds);
   else
-    flash_fwd_kernel<false><<<grid, THREADS, SMEM_BYTES, (hipStream_t)stream>>>(
+    flash_fwd_kernel<false><<<grid, THREADS, SMEM_BYTES, s>>>(
         q, k, v, o, lse, seq, (uint32_t)bh, scale_log2, paired, topo.xcds);
   return fe2o3_host::after_launch();
 }

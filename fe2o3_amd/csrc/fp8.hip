@@ -21,6 +21,8 @@
 #include "gemm_pipe.hpp"
 #include "internal.hpp"
 
+#include <type_traits>
+
 namespace {
 
 using namespace fe2o3;
@@ -113,7 +115,10 @@ constexpr int kFp8Smem = kFp8Stages * 2 * gemm_pipe::Geo<kFp8RowBytes>::kTileByt
 // EDGE: M or N is not a multiple of 256 (or C is not 16-byte aligned): the
 // grid covers ceil(M/256) x ceil(N/256) tiles, operand rows past M (N) repeat
 // the last valid row, and each tile stores only its valid rows and columns.
-template <bool STAGED, bool EDGE>
+// KT: K is a multiple of 16 but not of 128; the last stage is partial and
+// its chunks past K load zeros (gemm_pipe::Rows MASK), whose products are
+// zero (the generic kernel's zero padding of its last k step).
+template <bool STAGED, bool EDGE, bool KT = false>
 __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restrict__ a,
                                                           const uint8_t* __restrict__ b,
                                                           const float* __restrict__ scale_a,
@@ -130,11 +135,13 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
   const uint32_t k16 = k / 2;  // rows addressed in 16-bit units
   const uint16_t* a16 = reinterpret_cast<const uint16_t*>(a + (uint64_t)tm * 256 * k);
   const uint16_t* b16 = reinterpret_cast<const uint16_t*>(b + (uint64_t)tn * 256 * k);
-  const auto ar = gemm_pipe::dense_rows<kFp8RowBytes>(a16, k16, rows_a, k16);
-  const auto br = gemm_pipe::dense_rows<kFp8RowBytes>(b16, k16, rows_b, k16);
+  const auto ar = gemm_pipe::dense_rows<kFp8RowBytes, 256, KT>(a16, k16, rows_a, k16);
+  const auto br = gemm_pipe::dense_rows<kFp8RowBytes, 256, KT>(b16, k16, rows_b, k16);
+  // the wave index, read before the K loop: the epilogue needs no thread id
+  const uint32_t wave = gemm_pipe::wave_id();
   gemm_pipe::Acc32 acc;
-  gemm_pipe::mainloop<gemm_pipe::Fp8Mma<kFp8RowBytes>, kFp8RowBytes, kFp8Stages>(ar, br, k16,
-                                                                                 smem, acc);
+  gemm_pipe::mainloop<gemm_pipe::Fp8Mma<kFp8RowBytes>, kFp8RowBytes, kFp8Stages, KT>(
+      ar, br, k16, smem, acc);
   const float sab = scale_a[0] * scale_b[0];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -144,11 +151,11 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
       for (int e = 0; e < 16; ++e) acc.v[i][j][e] *= sab;
   uint16_t* c_tile = c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256;
   if constexpr (EDGE)
-    gemm_pipe::store_bf16_edge(acc, c_tile, n, rows_a, rows_b);
+    gemm_pipe::store_bf16_edge(acc, c_tile, n, rows_a, rows_b, wave);
   else if constexpr (STAGED)
-    gemm_pipe::store_bf16_staged(acc, smem, c_tile, n);
+    gemm_pipe::store_bf16_staged(acc, smem, c_tile, n, wave);
   else
-    gemm_pipe::store_bf16(acc, c_tile, n);
+    gemm_pipe::store_bf16(acc, c_tile, n, wave);
 }
 
 // The small-grid form: 128 x 128 tiles (Fp8Mma64) for GEMMs whose 256 x 256
@@ -164,7 +171,7 @@ constexpr int kFp8SmallSmem = STAGES * 2 * 128 * kFp8RowBytes;
 // TAIL: the last, partial round of a 256 x 256 grid (tiles first_big .. end
 // of gemm_core::xcd_tile_order's list), each as four 128 x 128 quarters
 // (gemm_core::tail_quarter).
-template <int STAGES, bool WHOLE, bool TAIL = false>
+template <int STAGES, bool WHOLE, bool TAIL = false, bool KT = false>
 __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_fp8_128_kernel(
     const uint8_t* __restrict__ a, const uint8_t* __restrict__ b, const float* __restrict__ scale_a,
     const float* __restrict__ scale_b, uint16_t* __restrict__ c, uint32_t m, uint32_t n,
@@ -181,11 +188,11 @@ __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_fp8_128_kernel(
   const uint32_t k16 = k / 2;  // rows addressed in 16-bit units
   const uint16_t* a16 = reinterpret_cast<const uint16_t*>(a + (uint64_t)tm * 128 * k);
   const uint16_t* b16 = reinterpret_cast<const uint16_t*>(b + (uint64_t)tn * 128 * k);
-  const auto ar = gemm_pipe::dense_rows<kFp8RowBytes, 128>(a16, k16, rows_a, k16);
-  const auto br = gemm_pipe::dense_rows<kFp8RowBytes, 128>(b16, k16, rows_b, k16);
+  const auto ar = gemm_pipe::dense_rows<kFp8RowBytes, 128, KT>(a16, k16, rows_a, k16);
+  const auto br = gemm_pipe::dense_rows<kFp8RowBytes, 128, KT>(b16, k16, rows_b, k16);
   typename gemm_pipe::Fp8Mma64<kFp8RowBytes>::Acc acc;
-  gemm_pipe::mainloop<gemm_pipe::Fp8Mma64<kFp8RowBytes>, kFp8RowBytes, STAGES>(ar, br, k16,
-                                                                               smem, acc);
+  gemm_pipe::mainloop<gemm_pipe::Fp8Mma64<kFp8RowBytes>, kFp8RowBytes, STAGES, KT>(ar, br, k16,
+                                                                                   smem, acc);
   const float sab = scale_a[0] * scale_b[0];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -277,6 +284,12 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel", (const void*)gemm_fp8_kernel<false, false>, 256, kFp8Smem}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel<staged>", (const void*)gemm_fp8_kernel<true, false>, 256, kFp8Smem}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel<edge>", (const void*)gemm_fp8_kernel<false, true>, 256, kFp8Smem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel<edge, k tail>", (const void*)gemm_fp8_kernel<false, true, true>, 256, kFp8Smem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_kernel<k tail>", (const void*)gemm_fp8_kernel<false, false, true>, 256, kFp8Smem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<2, k tail>", (const void*)gemm_fp8_128_kernel<2, true, false, true>, 256, kFp8SmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<3, k tail>", (const void*)gemm_fp8_128_kernel<3, true, false, true>, 256, kFp8SmallSmem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<2, tail, k tail>", (const void*)gemm_fp8_128_kernel<2, true, true, true>, 256, kFp8SmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<3, tail, k tail>", (const void*)gemm_fp8_128_kernel<3, true, true, true>, 256, kFp8SmallSmem<3>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<2>", (const void*)gemm_fp8_128_kernel<2, true>, 256, kFp8SmallSmem<2>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<2, edge>", (const void*)gemm_fp8_128_kernel<2, false>, 256, kFp8SmallSmem<2>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<3>", (const void*)gemm_fp8_128_kernel<3, true>, 256, kFp8SmallSmem<3>}),
@@ -285,8 +298,93 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<2, edge, tail>", (const void*)gemm_fp8_128_kernel<2, false, true>, 256, kFp8SmallSmem<2>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<3, tail>", (const void*)gemm_fp8_128_kernel<3, true, true>, 256, kFp8SmallSmem<3>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<3, edge, tail>", (const void*)gemm_fp8_128_kernel<3, false, true>, 256, kFp8SmallSmem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<2, edge, k tail>", (const void*)gemm_fp8_128_kernel<2, false, false, true>, 256, kFp8SmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<3, edge, k tail>", (const void*)gemm_fp8_128_kernel<3, false, false, true>, 256, kFp8SmallSmem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<2, edge, tail, k tail>", (const void*)gemm_fp8_128_kernel<2, false, true, true>, 256, kFp8SmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<3, edge, tail, k tail>", (const void*)gemm_fp8_128_kernel<3, false, true, true>, 256, kFp8SmallSmem<3>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_generic_kernel", (const void*)gemm_fp8_generic_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "zero_fill_bf16_kernel", (const void*)zero_fill_bf16_kernel, 256, 0})};
+
+}  // namespace
+
+namespace {
+
+// Raises every fast-path kernel's dynamic-LDS limit once per process.
+int32_t set_fp8_lds() {
+  static const int32_t rc = [] {
+    int32_t r = fe2o3_host::set_dynamic_lds(
+        {(const void*)gemm_fp8_kernel<false, false>, (const void*)gemm_fp8_kernel<true, false>,
+         (const void*)gemm_fp8_kernel<false, true>, (const void*)gemm_fp8_kernel<false, true, true>,
+         (const void*)gemm_fp8_kernel<false, false, true>},
+        kFp8Smem);
+    if (r == FE2O3_OK)
+      r = fe2o3_host::set_dynamic_lds(
+          {(const void*)gemm_fp8_128_kernel<2, true>, (const void*)gemm_fp8_128_kernel<2, false>,
+           (const void*)gemm_fp8_128_kernel<2, true, true>,
+           (const void*)gemm_fp8_128_kernel<2, false, true>,
+           (const void*)gemm_fp8_128_kernel<2, false, false, true>,
+           (const void*)gemm_fp8_128_kernel<2, false, true, true>,
+           (const void*)gemm_fp8_128_kernel<2, true, false, true>,
+           (const void*)gemm_fp8_128_kernel<2, true, true, true>},
+          kFp8SmallSmem<2>);
+    if (r == FE2O3_OK)
+      r = fe2o3_host::set_dynamic_lds(
+          {(const void*)gemm_fp8_128_kernel<3, true>, (const void*)gemm_fp8_128_kernel<3, false>,
+           (const void*)gemm_fp8_128_kernel<3, true, true>,
+           (const void*)gemm_fp8_128_kernel<3, false, true>,
+           (const void*)gemm_fp8_128_kernel<3, false, false, true>,
+           (const void*)gemm_fp8_128_kernel<3, false, true, true>,
+           (const void*)gemm_fp8_128_kernel<3, true, false, true>,
+           (const void*)gemm_fp8_128_kernel<3, true, true, true>},
+          kFp8SmallSmem<3>);
+    return r;
+  }();
+  return rc;
+}
+
+// The launches of `plan` (tile_plan.hpp).  KT: K not a multiple of 128 (a
+// partial last stage in every tile).
+template <bool KT>
+int32_t launch_fp8(const uint8_t* a, const uint8_t* b, const float* sa, const float* sb,
+                   uint16_t* c, uint32_t m, uint32_t n, uint32_t k, const tile_plan::Plan& plan,
+                   uint32_t xcds, hipStream_t s) {
+  const bool whole = m % 256 == 0 && n % 256 == 0 && ((uintptr_t)c & 15u) == 0;
+  const bool whole128 = m % 128 == 0 && n % 128 == 0 && ((uintptr_t)c & 15u) == 0;
+  // one launch of 128 x 128 tiles: the whole GEMM (TAIL false) or the tail
+  // round's quarters
+  auto small = [&](auto stages, auto tail, unsigned grid, uint32_t first) {
+    constexpr int S = decltype(stages)::value;
+    constexpr bool T = decltype(tail)::value;
+    if (whole128)
+      gemm_fp8_128_kernel<S, true, T, KT><<<grid, 256, kFp8SmallSmem<S>, s>>>(a, b, sa, sb, c, m,
+                                                                              n, k, xcds, first);
+    else
+      gemm_fp8_128_kernel<S, false, T, KT><<<grid, 256, kFp8SmallSmem<S>, s>>>(a, b, sa, sb, c, m,
+                                                                               n, k, xcds, first);
+    return fe2o3_host::after_launch();
+  };
+  using Two = std::integral_constant<int, 2>;
+  using Three = std::integral_constant<int, 3>;
+  using Whole = std::false_type;
+  using Tail = std::true_type;
+  if (plan.small)  // 256 x 256 tiles would leave most CUs idle
+    return plan.stages == 2 ? small(Two{}, Whole{}, (unsigned)plan.grid, 0u)
+                            : small(Three{}, Whole{}, (unsigned)plan.grid, 0u);
+  const unsigned big = (unsigned)plan.grid;
+  if (!whole)
+    gemm_fp8_kernel<false, true, KT><<<big, 256, kFp8Smem, s>>>(a, b, sa, sb, c, m, n, k, xcds);
+  else if (!KT && gemm_core::staged_epilogue(((uint64_t)m + n) * k))
+    gemm_fp8_kernel<true, false><<<big, 256, kFp8Smem, s>>>(a, b, sa, sb, c, m, n, k, xcds);
+  else
+    gemm_fp8_kernel<false, false, KT><<<big, 256, kFp8Smem, s>>>(a, b, sa, sb, c, m, n, k, xcds);
+  const int32_t big_rc = fe2o3_host::after_launch();
+  if (big_rc != FE2O3_OK || !plan.tail) return big_rc;
+  // the last round of at most half the CUs' tiles as 128 x 128 quarters; two
+  // per CU when there are more quarters than CUs
+  return plan.tail_stages == 2
+             ? small(Two{}, Tail{}, (unsigned)plan.tail_grid, plan.first_big)
+             : small(Three{}, Tail{}, (unsigned)plan.tail_grid, plan.first_big);
+}
 
 }  // namespace
 
@@ -335,9 +433,10 @@ int32_t fe2o3_gemm_fp8_nt(const uint8_t* a, uint64_t a_len, const uint8_t* b, ui
     zero_fill_bf16_kernel<<<(unsigned)(blocks < 4096u ? blocks : 4096u), 256, 0, s>>>(c, c_len);
     return fe2o3_host::after_launch();
   }
-  // fast path: whole 128-k stages, 16-byte operand rows, and a 256-row fp8
-  // panel (256 * k bytes) within its buffer resource's 32-bit range
-  const bool fast = k % 128 == 0 && 256ull * k < (1ull << 31) &&
+  // fast path: 16-byte operand rows (K a multiple of 16) and a 256-row fp8
+  // panel (256 * k bytes) within its buffer resource's 32-bit range; K not a
+  // multiple of 128 takes the edge tiles with a partial last stage
+  const bool fast = k % 16 == 0 && 256ull * k < (1ull << 31) &&
                     (((uintptr_t)a | (uintptr_t)b) & 15u) == 0;
   if (!fast) {
     const dim3 grid((n + G8_BN - 1) / G8_BN, (m + G8_BM - 1) / G8_BM);
@@ -345,82 +444,16 @@ int32_t fe2o3_gemm_fp8_nt(const uint8_t* a, uint64_t a_len, const uint8_t* b, ui
     gemm_fp8_generic_kernel<<<grid, 256, 0, s>>>(a, b, scale_a, scale_b, c, m, n, k);
     return fe2o3_host::after_launch();
   }
-  // every kernel's LDS limit is raised before anything is launched, so a
-  // failure leaves C untouched
-  static const int32_t lds_rc = [] {
-    int32_t rc = fe2o3_host::set_dynamic_lds(
-        {(const void*)gemm_fp8_kernel<false, false>, (const void*)gemm_fp8_kernel<true, false>,
-         (const void*)gemm_fp8_kernel<false, true>},
-        kFp8Smem);
-    if (rc == FE2O3_OK)
-      rc = fe2o3_host::set_dynamic_lds(
-          {(const void*)gemm_fp8_128_kernel<2, true>, (const void*)gemm_fp8_128_kernel<2, false>,
-           (const void*)gemm_fp8_128_kernel<2, true, true>,
-           (const void*)gemm_fp8_128_kernel<2, false, true>},
-          kFp8SmallSmem<2>);
-    if (rc == FE2O3_OK)
-      rc = fe2o3_host::set_dynamic_lds(
-          {(const void*)gemm_fp8_128_kernel<3, true>, (const void*)gemm_fp8_128_kernel<3, false>,
-           (const void*)gemm_fp8_128_kernel<3, true, true>,
-           (const void*)gemm_fp8_128_kernel<3, false, true>},
-          kFp8SmallSmem<3>);
-    return rc;
-  }();
+  const int32_t lds_rc = set_fp8_lds();  // before any launch: a failure leaves C untouched
   if (lds_rc != FE2O3_OK) return lds_rc;
   tile_plan::Topology topo;
   const int32_t topo_rc = fe2o3_host::device_topology(&topo);
   if (topo_rc != FE2O3_OK) return topo_rc;
   const tile_plan::Plan plan = tile_plan::plan(m, n, topo);
   if (plan.grid > 0x7fffffffu || plan.tail_grid > 0x7fffffffu) return FE2O3_ERR_SHAPE;
-  const uint32_t xcds = topo.xcds;
-  const bool whole = m % 256 == 0 && n % 256 == 0 && ((uintptr_t)c & 15u) == 0;
-  const bool whole128 = m % 128 == 0 && n % 128 == 0 && ((uintptr_t)c & 15u) == 0;
-  const float* sa = scale_a;
-  const float* sb = scale_b;
-  if (plan.small) {  // 256 x 256 tiles would leave most CUs idle
-    const unsigned g = (unsigned)plan.grid;
-    if (plan.stages == 2) {
-      if (whole128)
-        gemm_fp8_128_kernel<2, true><<<g, 256, kFp8SmallSmem<2>, s>>>(a, b, sa, sb, c, m, n, k,
-                                                                      xcds);
-      else
-        gemm_fp8_128_kernel<2, false><<<g, 256, kFp8SmallSmem<2>, s>>>(a, b, sa, sb, c, m, n, k,
-                                                                       xcds);
-    } else if (whole128) {
-      gemm_fp8_128_kernel<3, true><<<g, 256, kFp8SmallSmem<3>, s>>>(a, b, sa, sb, c, m, n, k, xcds);
-    } else {
-      gemm_fp8_128_kernel<3, false><<<g, 256, kFp8SmallSmem<3>, s>>>(a, b, sa, sb, c, m, n, k,
-                                                                     xcds);
-    }
-    return fe2o3_host::after_launch();
-  }
-  const unsigned big = (unsigned)plan.grid;
-  if (!whole)
-    gemm_fp8_kernel<false, true><<<big, 256, kFp8Smem, s>>>(a, b, sa, sb, c, m, n, k, xcds);
-  else if (gemm_core::staged_epilogue(((uint64_t)m + n) * k))
-    gemm_fp8_kernel<true, false><<<big, 256, kFp8Smem, s>>>(a, b, sa, sb, c, m, n, k, xcds);
-  else
-    gemm_fp8_kernel<false, false><<<big, 256, kFp8Smem, s>>>(a, b, sa, sb, c, m, n, k, xcds);
-  const int32_t big_rc = fe2o3_host::after_launch();
-  if (big_rc != FE2O3_OK || !plan.tail) return big_rc;
-  // the last round of at most half the CUs' tiles as 128 x 128 quarters
-  const unsigned g = (unsigned)plan.tail_grid;
-  const uint32_t first = plan.first_big;
-  if (plan.tail_stages == 2) {  // more quarters than CUs: two per CU
-    if (whole128)
-      gemm_fp8_128_kernel<2, true, true><<<g, 256, kFp8SmallSmem<2>, s>>>(a, b, sa, sb, c, m, n, k,
-                                                                          xcds, first);
-    else
-      gemm_fp8_128_kernel<2, false, true><<<g, 256, kFp8SmallSmem<2>, s>>>(a, b, sa, sb, c, m, n,
-                                                                           k, xcds, first);
-  } else if (whole128) {
-    gemm_fp8_128_kernel<3, true, true><<<g, 256, kFp8SmallSmem<3>, s>>>(a, b, sa, sb, c, m, n, k,
-                                                                        xcds, first);
-  } else {
-    gemm_fp8_128_kernel<3, false, true><<<g, 256, kFp8SmallSmem<3>, s>>>(a, b, sa, sb, c, m, n, k,
-                                                                         xcds, first);
-  }
-  return fe2o3_host::after_launch();
+  if (k % 128 != 0)
+    return launch_fp8<true>(a, b, scale_a, scale_b, c, m, n, k, plan, topo.xcds, s);
+  return launch_fp8<false>(a, b, scale_a, scale_b, c, m, n, k, plan, topo.xcds, s);
 }
 
 }  // extern "C"

@@ -2,15 +2,19 @@
 // A[m,k] (row-major) * B^T with B stored [n,k] (k contiguous, i.e. the
 // BASELINE's column-major B), fp32 accumulation, RNE bf16 output.
 //
-// Fast path (k a multiple of 64 below 2^22, A and B 16-byte aligned): the
+// Fast path (k a multiple of 8 below 2^22, A and B 16-byte aligned): the
 // 256x256 pipelined MFMA tile of gemm_pipe.hpp with 64 k per LDS stage and
 // two stages, workgroups ordered XCD-aware (gemm_core.hpp); m or n not a
-// multiple of 256 (or an unaligned C) runs its edge form.  Any other shape
-// uses a bounds-checked 64x64-tile MFMA kernel.
+// multiple of 256 (or an unaligned C) runs its edge form, and k not a
+// multiple of 64 either form with a partial last stage.  Any other shape
+// (k not a multiple of 8, misaligned A or B) uses a bounds-checked
+// 64x64-tile MFMA kernel.
 #include "common.hpp"
 #include "gemm_core.hpp"
 #include "gemm_pipe.hpp"
 #include "internal.hpp"
+
+#include <type_traits>
 
 namespace {
 
@@ -81,7 +85,11 @@ constexpr int kFastSmem = kStages * 2 * gemm_pipe::Geo<kRowBytes>::kTileBytes;  
 // ceil(N/256) tiles, operand rows past M (N) repeat the last valid row
 // (their products reach only outputs that are not stored), and each tile
 // stores only its valid rows and columns, element by element.
-template <bool STAGED, bool EDGE>
+//
+// KT: K is a multiple of 8 but not of 64; the last stage is partial and its
+// chunks past K load zeros (gemm_pipe::Rows MASK), the zero padding the
+// generic kernel gives its last k step, so C is bit-identical to it.
+template <bool STAGED, bool EDGE, bool KT = false>
 __global__ void __launch_bounds__(256, 1) gemm_bf16_nt_256_kernel(const uint16_t* __restrict__ a,
                                                                    const uint16_t* __restrict__ b,
                                                                    uint16_t* __restrict__ c,
@@ -94,10 +102,13 @@ __global__ void __launch_bounds__(256, 1) gemm_bf16_nt_256_kernel(const uint16_t
   gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, xcds, &tm, &tn);
   const uint32_t rows_a = EDGE ? min(256u, m - tm * 256u) : 256u;
   const uint32_t rows_b = EDGE ? min(256u, n - tn * 256u) : 256u;
-  const auto ar = gemm_pipe::dense_rows<kRowBytes>(a + (uint64_t)tm * 256 * k, k, rows_a, k);
-  const auto br = gemm_pipe::dense_rows<kRowBytes>(b + (uint64_t)tn * 256 * k, k, rows_b, k);
+  const auto ar =
+      gemm_pipe::dense_rows<kRowBytes, 256, KT>(a + (uint64_t)tm * 256 * k, k, rows_a, k);
+  const auto br =
+      gemm_pipe::dense_rows<kRowBytes, 256, KT>(b + (uint64_t)tn * 256 * k, k, rows_b, k);
   gemm_pipe::Acc16 acc;
-  gemm_pipe::mainloop<gemm_pipe::Bf16Mma<kRowBytes>, kRowBytes, kStages>(ar, br, k, smem, acc);
+  gemm_pipe::mainloop<gemm_pipe::Bf16Mma<kRowBytes>, kRowBytes, kStages, KT>(ar, br, k, smem,
+                                                                              acc);
   uint16_t* c_tile = c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256;
   if constexpr (EDGE)
     gemm_pipe::store_bf16_edge(acc, c_tile, n, rows_a, rows_b);
@@ -120,7 +131,7 @@ constexpr int kSmallSmem = STAGES * (128 * kRowBytes + gemm_pipe::Bf16Mma64::kBT
 // TAIL: the last, partial round of a 256 x 256 grid (tiles first_big .. end
 // of gemm_core::xcd_tile_order's list), each as four 128 x 128 quarters
 // (gemm_core::tail_quarter).
-template <int STAGES, bool WHOLE, bool TAIL = false>
+template <int STAGES, bool WHOLE, bool TAIL = false, bool KT = false>
 __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_bf16_nt_128_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint16_t* __restrict__ c,
     uint32_t m, uint32_t n, uint32_t k, uint32_t xcds, uint32_t first_big = 0) {
@@ -133,10 +144,12 @@ __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_bf16_nt_128_ker
   }
   const uint32_t rows_a = WHOLE ? 128u : min(128u, m - tm * 128u);
   const uint32_t rows_b = WHOLE ? 128u : min(128u, n - tn * 128u);
-  const auto ar = gemm_pipe::dense_rows<kRowBytes, 128>(a + (uint64_t)tm * 128 * k, k, rows_a, k);
-  const auto br = gemm_pipe::dense_rows<kRowBytes, 128>(b + (uint64_t)tn * 128 * k, k, rows_b, k);
+  const auto ar =
+      gemm_pipe::dense_rows<kRowBytes, 128, KT>(a + (uint64_t)tm * 128 * k, k, rows_a, k);
+  const auto br =
+      gemm_pipe::dense_rows<kRowBytes, 128, KT>(b + (uint64_t)tn * 128 * k, k, rows_b, k);
   gemm_pipe::Bf16Mma64::Acc acc;
-  gemm_pipe::mainloop<gemm_pipe::Bf16Mma64, kRowBytes, STAGES>(ar, br, k, smem, acc);
+  gemm_pipe::mainloop<gemm_pipe::Bf16Mma64, kRowBytes, STAGES, KT>(ar, br, k, smem, acc);
   gemm_pipe::store_bf16_128<WHOLE>(acc, c + (uint64_t)tm * 128 * n + (uint64_t)tn * 128, n,
                                    rows_a, rows_b);
 }
@@ -163,8 +176,98 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<2, edge, tail>", (const void*)gemm_bf16_nt_128_kernel<2, false, true>, 256, kSmallSmem<2>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<3, tail>", (const void*)gemm_bf16_nt_128_kernel<3, true, true>, 256, kSmallSmem<3>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<3, edge, tail>", (const void*)gemm_bf16_nt_128_kernel<3, false, true>, 256, kSmallSmem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel<edge, k tail>", (const void*)gemm_bf16_nt_256_kernel<false, true, true>, 256, kFastSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_256_kernel<k tail>", (const void*)gemm_bf16_nt_256_kernel<false, false, true>, 256, kFastSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<2, k tail>", (const void*)gemm_bf16_nt_128_kernel<2, true, false, true>, 256, kSmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<3, k tail>", (const void*)gemm_bf16_nt_128_kernel<3, true, false, true>, 256, kSmallSmem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<2, tail, k tail>", (const void*)gemm_bf16_nt_128_kernel<2, true, true, true>, 256, kSmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<3, tail, k tail>", (const void*)gemm_bf16_nt_128_kernel<3, true, true, true>, 256, kSmallSmem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<2, edge, k tail>", (const void*)gemm_bf16_nt_128_kernel<2, false, false, true>, 256, kSmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<3, edge, k tail>", (const void*)gemm_bf16_nt_128_kernel<3, false, false, true>, 256, kSmallSmem<3>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<2, edge, tail, k tail>", (const void*)gemm_bf16_nt_128_kernel<2, false, true, true>, 256, kSmallSmem<2>}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_128_kernel<3, edge, tail, k tail>", (const void*)gemm_bf16_nt_128_kernel<3, false, true, true>, 256, kSmallSmem<3>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "gemm_bf16_nt_generic_kernel", (const void*)gemm_bf16_nt_generic_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "zero_fill_bf16_kernel", (const void*)zero_fill_bf16_kernel, 256, 0})};
+
+// Raises every fast-path kernel's dynamic-LDS limit once per process.
+int32_t set_fast_lds() {
+  static const int32_t rc = [] {
+    int32_t r = fe2o3_host::set_dynamic_lds(
+        {(const void*)gemm_bf16_nt_256_kernel<false, false>,
+         (const void*)gemm_bf16_nt_256_kernel<true, false>,
+         (const void*)gemm_bf16_nt_256_kernel<false, true>,
+         (const void*)gemm_bf16_nt_256_kernel<false, true, true>,
+         (const void*)gemm_bf16_nt_256_kernel<false, false, true>},
+        kFastSmem);
+    if (r == FE2O3_OK)
+      r = fe2o3_host::set_dynamic_lds(
+          {(const void*)gemm_bf16_nt_128_kernel<2, true>,
+           (const void*)gemm_bf16_nt_128_kernel<2, false>,
+           (const void*)gemm_bf16_nt_128_kernel<2, true, true>,
+           (const void*)gemm_bf16_nt_128_kernel<2, false, true>,
+           (const void*)gemm_bf16_nt_128_kernel<2, false, false, true>,
+           (const void*)gemm_bf16_nt_128_kernel<2, false, true, true>,
+           (const void*)gemm_bf16_nt_128_kernel<2, true, false, true>,
+           (const void*)gemm_bf16_nt_128_kernel<2, true, true, true>},
+          kSmallSmem<2>);
+    if (r == FE2O3_OK)
+      r = fe2o3_host::set_dynamic_lds(
+          {(const void*)gemm_bf16_nt_128_kernel<3, true>,
+           (const void*)gemm_bf16_nt_128_kernel<3, false>,
+           (const void*)gemm_bf16_nt_128_kernel<3, true, true>,
+           (const void*)gemm_bf16_nt_128_kernel<3, false, true>,
+           (const void*)gemm_bf16_nt_128_kernel<3, false, false, true>,
+           (const void*)gemm_bf16_nt_128_kernel<3, false, true, true>,
+           (const void*)gemm_bf16_nt_128_kernel<3, true, false, true>,
+           (const void*)gemm_bf16_nt_128_kernel<3, true, true, true>},
+          kSmallSmem<3>);
+    return r;
+  }();
+  return rc;
+}
+
+// The launches of `plan` (tile_plan.hpp).  KT: K not a multiple of 64 (a
+// partial last stage in every tile).
+template <bool KT>
+int32_t launch_fast(const uint16_t* a, const uint16_t* b, uint16_t* c, uint32_t m, uint32_t n,
+                    uint32_t k, const tile_plan::Plan& plan, uint32_t xcds, hipStream_t s) {
+  const bool whole = m % 256 == 0 && n % 256 == 0 && aligned16(c);
+  const bool whole128 = m % 128 == 0 && n % 128 == 0 && aligned16(c);
+  // one launch of 128 x 128 tiles: the whole GEMM (TAIL false) or the tail
+  // round's quarters
+  auto small = [&](auto stages, auto tail, unsigned grid, uint32_t first) {
+    constexpr int S = decltype(stages)::value;
+    constexpr bool T = decltype(tail)::value;
+    if (whole128)
+      gemm_bf16_nt_128_kernel<S, true, T, KT><<<grid, 256, kSmallSmem<S>, s>>>(a, b, c, m, n, k,
+                                                                               xcds, first);
+    else
+      gemm_bf16_nt_128_kernel<S, false, T, KT><<<grid, 256, kSmallSmem<S>, s>>>(a, b, c, m, n, k,
+                                                                                xcds, first);
+    return fe2o3_host::after_launch();
+  };
+  using Two = std::integral_constant<int, 2>;
+  using Three = std::integral_constant<int, 3>;
+  using Whole = std::false_type;
+  using Tail = std::true_type;
+  if (plan.small)  // 256 x 256 tiles would leave most CUs idle
+    return plan.stages == 2 ? small(Two{}, Whole{}, (unsigned)plan.grid, 0u)
+                            : small(Three{}, Whole{}, (unsigned)plan.grid, 0u);
+  const unsigned big = (unsigned)plan.grid;
+  if (!whole)
+    gemm_bf16_nt_256_kernel<false, true, KT><<<big, 256, kFastSmem, s>>>(a, b, c, m, n, k, xcds);
+  else if (!KT && gemm_core::staged_epilogue(((uint64_t)m + n) * k * 2u))
+    gemm_bf16_nt_256_kernel<true, false><<<big, 256, kFastSmem, s>>>(a, b, c, m, n, k, xcds);
+  else
+    gemm_bf16_nt_256_kernel<false, false, KT><<<big, 256, kFastSmem, s>>>(a, b, c, m, n, k, xcds);
+  const int32_t big_rc = fe2o3_host::after_launch();
+  if (big_rc != FE2O3_OK || !plan.tail) return big_rc;
+  // the last round of at most half the CUs' tiles as 128 x 128 quarters; two
+  // per CU when there are more quarters than CUs
+  return plan.tail_stages == 2
+             ? small(Two{}, Tail{}, (unsigned)plan.tail_grid, plan.first_big)
+             : small(Three{}, Tail{}, (unsigned)plan.tail_grid, plan.first_big);
+}
 
 }  // namespace
 
@@ -182,88 +285,23 @@ extern "C" int32_t fe2o3_gemm_bf16_nt(const uint16_t* a, uint64_t a_len, const u
                             (hipStream_t)stream>>>(c, c_len);
     return fe2o3_host::after_launch();
   }
-  // fast path: whole stages, 16-byte operand rows, and a 256-row panel
+  // fast path: 16-byte operand rows (K a multiple of 8), and a 256-row panel
   // (512 * k bytes) inside the 32-bit range of its buffer resource; whole
   // tiles with a 16-byte aligned C take the plain tile, any other M and N
-  // the edge tile
-  const bool fast = k % gemm_pipe::Geo<kRowBytes>::kK16 == 0 && 512ull * k < (1ull << 31) &&
-                    aligned16(a) && aligned16(b);
+  // the edge tile; K not a multiple of 64 the same tiles with a partial last
+  // stage (KT)
+  const bool fast = k % 8 == 0 && 512ull * k < (1ull << 31) && aligned16(a) && aligned16(b);
   if (fast) {
-    // every kernel's LDS limit is raised before anything is launched, so a
-    // failure leaves C untouched
-    static const int32_t lds_rc = [] {
-      int32_t rc = fe2o3_host::set_dynamic_lds(
-          {(const void*)gemm_bf16_nt_256_kernel<false, false>,
-           (const void*)gemm_bf16_nt_256_kernel<true, false>,
-           (const void*)gemm_bf16_nt_256_kernel<false, true>},
-          kFastSmem);
-      if (rc == FE2O3_OK)
-        rc = fe2o3_host::set_dynamic_lds(
-            {(const void*)gemm_bf16_nt_128_kernel<2, true>,
-             (const void*)gemm_bf16_nt_128_kernel<2, false>,
-             (const void*)gemm_bf16_nt_128_kernel<2, true, true>,
-             (const void*)gemm_bf16_nt_128_kernel<2, false, true>},
-            kSmallSmem<2>);
-      if (rc == FE2O3_OK)
-        rc = fe2o3_host::set_dynamic_lds(
-            {(const void*)gemm_bf16_nt_128_kernel<3, true>,
-             (const void*)gemm_bf16_nt_128_kernel<3, false>,
-             (const void*)gemm_bf16_nt_128_kernel<3, true, true>,
-             (const void*)gemm_bf16_nt_128_kernel<3, false, true>},
-            kSmallSmem<3>);
-      return rc;
-    }();
+    const int32_t lds_rc = set_fast_lds();  // before any launch: a failure leaves C untouched
     if (lds_rc != FE2O3_OK) return lds_rc;
     tile_plan::Topology topo;
     const int32_t topo_rc = fe2o3_host::device_topology(&topo);
     if (topo_rc != FE2O3_OK) return topo_rc;
     const tile_plan::Plan plan = tile_plan::plan(m, n, topo);
     if (plan.grid > 0x7fffffffu || plan.tail_grid > 0x7fffffffu) return FE2O3_ERR_SHAPE;
-    const uint32_t xcds = topo.xcds;
-    const bool whole = m % 256 == 0 && n % 256 == 0 && aligned16(c);
-    const bool whole128 = m % 128 == 0 && n % 128 == 0 && aligned16(c);
-    hipStream_t s = (hipStream_t)stream;
-    if (plan.small) {  // 256 x 256 tiles would leave most CUs idle
-      const unsigned g = (unsigned)plan.grid;
-      if (plan.stages == 2) {
-        if (whole128)
-          gemm_bf16_nt_128_kernel<2, true><<<g, 256, kSmallSmem<2>, s>>>(a, b, c, m, n, k, xcds);
-        else
-          gemm_bf16_nt_128_kernel<2, false><<<g, 256, kSmallSmem<2>, s>>>(a, b, c, m, n, k, xcds);
-      } else if (whole128) {
-        gemm_bf16_nt_128_kernel<3, true><<<g, 256, kSmallSmem<3>, s>>>(a, b, c, m, n, k, xcds);
-      } else {
-        gemm_bf16_nt_128_kernel<3, false><<<g, 256, kSmallSmem<3>, s>>>(a, b, c, m, n, k, xcds);
-      }
-      return fe2o3_host::after_launch();
-    }
-    const unsigned big = (unsigned)plan.grid;
-    if (!whole)
-      gemm_bf16_nt_256_kernel<false, true><<<big, 256, kFastSmem, s>>>(a, b, c, m, n, k, xcds);
-    else if (gemm_core::staged_epilogue(((uint64_t)m + n) * k * 2u))
-      gemm_bf16_nt_256_kernel<true, false><<<big, 256, kFastSmem, s>>>(a, b, c, m, n, k, xcds);
-    else
-      gemm_bf16_nt_256_kernel<false, false><<<big, 256, kFastSmem, s>>>(a, b, c, m, n, k, xcds);
-    const int32_t big_rc = fe2o3_host::after_launch();
-    if (big_rc != FE2O3_OK || !plan.tail) return big_rc;
-    // the last round of at most half the CUs' tiles as 128 x 128 quarters
-    const unsigned g = (unsigned)plan.tail_grid;
-    const uint32_t first = plan.first_big;
-    if (plan.tail_stages == 2) {  // more quarters than CUs: two per CU
-      if (whole128)
-        gemm_bf16_nt_128_kernel<2, true, true><<<g, 256, kSmallSmem<2>, s>>>(a, b, c, m, n, k,
-                                                                             xcds, first);
-      else
-        gemm_bf16_nt_128_kernel<2, false, true><<<g, 256, kSmallSmem<2>, s>>>(a, b, c, m, n, k,
-                                                                              xcds, first);
-    } else if (whole128) {
-      gemm_bf16_nt_128_kernel<3, true, true><<<g, 256, kSmallSmem<3>, s>>>(a, b, c, m, n, k, xcds,
-                                                                           first);
-    } else {
-      gemm_bf16_nt_128_kernel<3, false, true><<<g, 256, kSmallSmem<3>, s>>>(a, b, c, m, n, k,
-                                                                            xcds, first);
-    }
-    return fe2o3_host::after_launch();
+    if (k % gemm_pipe::Geo<kRowBytes>::kK16 != 0)
+      return launch_fast<true>(a, b, c, m, n, k, plan, topo.xcds, (hipStream_t)stream);
+    return launch_fast<false>(a, b, c, m, n, k, plan, topo.xcds, (hipStream_t)stream);
   }
   dim3 grid((n + N_BN - 1) / N_BN, (m + N_BM - 1) / N_BM);
   if (grid.y > 65535u) return FE2O3_ERR_SHAPE;

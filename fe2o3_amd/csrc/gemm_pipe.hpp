@@ -73,13 +73,42 @@ struct Geo {
 // kARows rows (256, or fewer for short tiles).  KN: the operand is stored
 // [k][n] (rows of n, kn_rows) and a stage's k offset `kbytes` (the byte
 // offset along a k-contiguous row) becomes kbytes * kmul bytes down the rows.
-template <int ROW_BYTES, int N = Geo<ROW_BYTES>::kInstPerWave, bool KN = false>
-struct Rows {
+// MASK: the rows hold k_end bytes of k, not a whole number of stages; a
+// chunk at or past k_end (chunk byte offset cbytes[j] along k within its
+// stage, plus the stage's kbytes) loads from a VGPR offset past the
+// buffer's extent, which the range check turns into 16 zero bytes in LDS.
+// The range check covers the VGPR offset only, not the scalar offset soff
+// carries, so a stage offset alone never makes a load return zeros: every
+// load past the operand's k goes through this mask.  For a [k][n] operand a
+// chunk is one k row (cbytes = 2 * its row within the stage).  Dense rows
+// have k_end a multiple of 16 bytes, so no chunk straddles it.  The zeros'
+// products are zero, the zero padding the staged kernels give a partial k
+// step.
+constexpr uint32_t kOutOfRange = 0x80000000u;  // past any extent (extents are < 2^31)
+
+// the mask's per-slot chunk offsets and k extent (no members without MASK)
+template <bool MASK, int N>
+struct RowsMask {
+  uint32_t cbytes[N];
+  uint32_t k_end;
+};
+template <int N>
+struct RowsMask<false, N> {};
+
+template <int ROW_BYTES, int N = Geo<ROW_BYTES>::kInstPerWave, bool KN = false,
+          bool MASK = false>
+struct Rows : RowsMask<MASK, N> {
+  static constexpr bool kMask = MASK;
   const void* base[N];
   uint32_t bytes;
   uint32_t voff[N];
   uint32_t kmul;
   FE2O3_DEVICE uint32_t soff(uint32_t kbytes) const { return KN ? kbytes * kmul : kbytes; }
+  // this lane's offset for load slot j of the stage at kbytes
+  FE2O3_DEVICE uint32_t off(int j, uint32_t kbytes) const {
+    if constexpr (MASK) return this->cbytes[j] < this->k_end - kbytes ? voff[j] : kOutOfRange;
+    else return voff[j];
+  }
 };
 
 FE2O3_DEVICE __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
@@ -96,15 +125,15 @@ FE2O3_DEVICE void b2l_b128(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, u
 // Dense operand: rows `ld` 16-bit elements apart from `base`, k16 elements
 // read per row; rows at or beyond valid_rows are clamped to the last valid
 // row (their products only reach outputs that are never stored).  The
-// caller guarantees ((valid_rows - 1) * ld + k16) * 2 < 2^31.
-template <int ROW_BYTES, int ROWS = 256>
-FE2O3_DEVICE Rows<ROW_BYTES, Geo<ROW_BYTES>::insts(ROWS)> dense_rows(const uint16_t* base,
-                                                                      uint32_t ld,
-                                                                      uint32_t valid_rows,
-                                                                      uint32_t k16) {
+// caller guarantees ((valid_rows - 1) * ld + k16) * 2 < 2^31.  MASK: k16 is
+// a multiple of 8 but not of the stage's k (Rows::off).
+template <int ROW_BYTES, int ROWS = 256, bool MASK = false>
+FE2O3_DEVICE Rows<ROW_BYTES, Geo<ROW_BYTES>::insts(ROWS), false, MASK> dense_rows(
+    const uint16_t* base, uint32_t ld, uint32_t valid_rows, uint32_t k16) {
   using G = Geo<ROW_BYTES>;
-  Rows<ROW_BYTES, G::insts(ROWS)> t;
+  Rows<ROW_BYTES, G::insts(ROWS), false, MASK> t;
   t.bytes = ((valid_rows - 1u) * ld + k16) * 2u;
+  if constexpr (MASK) t.k_end = k16 * 2u;
 #pragma unroll
   for (int j = 0; j < G::insts(ROWS); ++j) {
     uint32_t row = G::inst_row(j);
@@ -112,19 +141,20 @@ FE2O3_DEVICE Rows<ROW_BYTES, Geo<ROW_BYTES>::insts(ROWS)> dense_rows(const uint1
     if (row >= valid_rows) row = valid_rows - 1u;
     t.base[j] = base;
     t.voff[j] = (row * ld + chunk * 8u) * 2u;
+    if constexpr (MASK) t.cbytes[j] = chunk * 16u;
   }
   return t;
 }
 
 // Loads j in [J0, J1) of one operand tile into the LDS tile at byte offset
 // `tile` of smem, k offset `kbytes` (wave-uniform).
-template <int ROW_BYTES, int J0, int J1, int N, bool KN>
-FE2O3_DEVICE void issue_part(const Rows<ROW_BYTES, N, KN>& rows, uint32_t kbytes, uint8_t* smem,
-                             uint32_t tile, uint32_t wave) {
+template <int ROW_BYTES, int J0, int J1, int N, bool KN, bool MASK>
+FE2O3_DEVICE void issue_part(const Rows<ROW_BYTES, N, KN, MASK>& rows, uint32_t kbytes,
+                             uint8_t* smem, uint32_t tile, uint32_t wave) {
 #pragma unroll
   for (int j = J0; j < J1; ++j)
-    b2l_b128(rsrc(rows.base[j], rows.bytes), smem + tile + (4u * j + wave) * 1024u, rows.voff[j],
-             rows.soff(kbytes));
+    b2l_b128(rsrc(rows.base[j], rows.bytes), smem + tile + (4u * j + wave) * 1024u,
+             rows.off(j, kbytes), rows.soff(kbytes));
 }
 
 // B stored [k][n] (row-major, ldb elements apart), 256 columns from `base`:
@@ -141,13 +171,17 @@ FE2O3_DEVICE uint32_t kn_swz(uint32_t krow) {
   // 8-byte pieces fill 32 distinct 16-byte positions of the 512-byte rows
   return 2u * ((krow & 3u) | (((krow >> 3) & 3u) << 2));
 }
-FE2O3_DEVICE Rows<128, 8, true> kn_rows(const uint16_t* base, uint32_t ld, uint32_t valid_cols,
-                                        uint32_t k16) {
-  Rows<128, 8, true> t;
+// MASK: k16 is not a multiple of 64 and the last stage's rows from k16 on
+// load zeros (Rows::off).
+template <bool MASK = false>
+FE2O3_DEVICE Rows<128, 8, true, MASK> kn_rows(const uint16_t* base, uint32_t ld,
+                                              uint32_t valid_cols, uint32_t k16) {
+  Rows<128, 8, true, MASK> t;
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
   const uint32_t last_chunk = (valid_cols - 1u) / 8u;
-  t.bytes = ((k16 - 1u) * ld + valid_cols) * 2u;  // reads past C's columns return 0
+  t.bytes = ((k16 - 1u) * ld + valid_cols) * 2u;
   t.kmul = ld;  // a stage of 64 k (128 bytes along a k row) is 64 rows of ld elements
+  if constexpr (MASK) t.k_end = k16 * 2u;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const uint32_t krow = 2u * (4u * j + w) + lane / 32u;
@@ -155,6 +189,7 @@ FE2O3_DEVICE Rows<128, 8, true> kn_rows(const uint16_t* base, uint32_t ld, uint3
     if (chunk > last_chunk) chunk = last_chunk;
     t.base[j] = base;
     t.voff[j] = (krow * ld + chunk * 8u) * 2u;
+    if constexpr (MASK) t.cbytes[j] = 2u * krow;
   }
   return t;
 }
@@ -198,13 +233,15 @@ FE2O3_DEVICE uint32_t kn_swz16(uint32_t krow) {
   // 8-byte pieces fill 16 distinct 16-byte positions of the 256-byte rows
   return 2u * ((krow & 3u) | (((krow >> 3) & 1u) << 2));
 }
-FE2O3_DEVICE Rows<128, 4, true> kn_rows128(const uint16_t* base, uint32_t ld, uint32_t valid_cols,
-                                           uint32_t k16) {
-  Rows<128, 4, true> t;
+template <bool MASK = false>
+FE2O3_DEVICE Rows<128, 4, true, MASK> kn_rows128(const uint16_t* base, uint32_t ld,
+                                                 uint32_t valid_cols, uint32_t k16) {
+  Rows<128, 4, true, MASK> t;
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
   const uint32_t last_chunk = (valid_cols - 1u) / 8u;
-  t.bytes = ((k16 - 1u) * ld + valid_cols) * 2u;  // reads past C's columns return 0
+  t.bytes = ((k16 - 1u) * ld + valid_cols) * 2u;
   t.kmul = ld;  // a stage of 64 k (128 bytes along a k row) is 64 rows of ld elements
+  if constexpr (MASK) t.k_end = k16 * 2u;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t krow = 4u * (4u * j + w) + lane / 16u;
@@ -212,6 +249,7 @@ FE2O3_DEVICE Rows<128, 4, true> kn_rows128(const uint16_t* base, uint32_t ld, ui
     if (chunk > last_chunk) chunk = last_chunk;
     t.base[j] = base;
     t.voff[j] = (krow * ld + chunk * 8u) * 2u;
+    if constexpr (MASK) t.cbytes[j] = 2u * krow;
   }
   return t;
 }
@@ -753,31 +791,33 @@ struct CopyOrder {
 };
 
 // Copy C of the stage at k offset `kbytes` into LDS buffer `buf`.
-template <int ROW_BYTES, int STAGES, int A_ROWS, int C, int NA, int NB, bool BKN>
-FE2O3_DEVICE void copy_one(const Rows<ROW_BYTES, NA>& ar, const Rows<ROW_BYTES, NB, BKN>& br,
-                           uint32_t kbytes, uint8_t* smem, uint32_t wave, int buf) {
+template <int ROW_BYTES, int STAGES, int A_ROWS, int C, class RA, class RB>
+FE2O3_DEVICE void copy_one(const RA& ar, const RB& br, uint32_t kbytes, uint8_t* smem,
+                           uint32_t wave, int buf) {
+  constexpr int NA = sizeof(ar.voff) / sizeof(uint32_t), NB = sizeof(br.voff) / sizeof(uint32_t);
   using L = Lay<ROW_BYTES, STAGES, A_ROWS, NB * 4096>;  // NB 1-KiB loads per wave
   using O = CopyOrder<NA, NB>;
   constexpr int j = O::slot(C);
   if constexpr (O::is_a(C))
-    b2l_b128(rsrc(ar.base[j], ar.bytes), smem + L::a(buf) + (4u * j + wave) * 1024u, ar.voff[j],
-             kbytes);
+    b2l_b128(rsrc(ar.base[j], ar.bytes), smem + L::a(buf) + (4u * j + wave) * 1024u,
+             ar.off(j, kbytes), kbytes);
   else
     b2l_b128(rsrc(br.base[j], br.bytes), smem + L::b_region + L::b(buf) + (4u * j + wave) * 1024u,
-             br.voff[j], br.soff(kbytes));
+             br.off(j, kbytes), br.soff(kbytes));
 }
 
 // Substep S_ of a K step held in stage buffer P.  FIRST: the K loop's first
 // substep (accumulators written, not added to).  k_next / k_next2: k byte
 // offsets of the stages one and two ahead (clamped to the last stage).
-template <class M, int ROW_BYTES, int STAGES, int P, int S_, bool FIRST>
+// MASK: the operands' rows end inside the last stage (Rows::off).
+template <class M, int ROW_BYTES, int STAGES, int P, int S_, bool FIRST, bool MASK = false>
 struct Substep {
   using G = Geo<ROW_BYTES>;
   using L = Lay<ROW_BYTES, STAGES, M::kARows, M::kBTileBytes>;
   static constexpr int S = M::kSubsteps, MF = M::kMfma;
   static constexpr int NA = G::insts(M::kARows), NB = M::kBTileBytes / 4096;
-  using RA_ = Rows<ROW_BYTES, NA>;
-  using RB_ = Rows<ROW_BYTES, NB, M::kBKN>;
+  using RA_ = Rows<ROW_BYTES, NA, false, MASK>;
+  using RB_ = Rows<ROW_BYTES, NB, M::kBKN, MASK>;
   static constexpr int NC = NA + NB;              // copies per stage and wave
   static constexpr int kEarly = NC / 2;           // copies started at the barrier
   static constexpr int PN = (P + 1) % STAGES;     // buffer of the next step
@@ -833,56 +873,59 @@ struct Substep {
     __builtin_amdgcn_sched_barrier(0);
     slot<0>(ar, br, k_next, k_next2, smem, wave, ln, f, acc);
     if constexpr (!LAST)
-      Substep<M, ROW_BYTES, STAGES, P, S_ + 1, FIRST>::run(ar, br, k_next, k_next2, smem, wave,
-                                                           ln, f, acc);
+      Substep<M, ROW_BYTES, STAGES, P, S_ + 1, FIRST, MASK>::run(ar, br, k_next, k_next2, smem,
+                                                                 wave, ln, f, acc);
   }
 };
 
 // Steps kt .. kt+STAGES-1 in buffers P .. STAGES-1 (TAIL: stop at the last
 // step; FIRST: kt is the K loop's first step).
-template <class M, int ROW_BYTES, int STAGES, int P, bool TAIL, bool FIRST>
+template <class M, int ROW_BYTES, int STAGES, int P, bool TAIL, bool FIRST, bool MASK = false>
 struct Steps {
   static FE2O3_DEVICE uint32_t stage_k(int st, int steps) {
     using G = Geo<ROW_BYTES>;
     return __builtin_amdgcn_readfirstlane((uint32_t)(st < steps ? st : steps - 1) *
                                           (G::kK16 * 2u));
   }
-  using Sub0 = Substep<M, ROW_BYTES, STAGES, 0, 0, false>;
+  using Sub0 = Substep<M, ROW_BYTES, STAGES, 0, 0, false, MASK>;
   static FE2O3_DEVICE void run(const typename Sub0::RA_& ar, const typename Sub0::RB_& br, int kt,
                                int steps, uint8_t* smem, uint32_t wave,
                                const typename M::Lanes& ln, typename M::Frags* f,
                                typename M::Acc& acc) {
     if (TAIL && kt >= steps) return;
-    Substep<M, ROW_BYTES, STAGES, P, 0, FIRST && P == 0>::run(
+    Substep<M, ROW_BYTES, STAGES, P, 0, FIRST && P == 0, MASK>::run(
         ar, br, stage_k(kt + STAGES - 1, steps), stage_k(kt + STAGES, steps), smem, wave, ln, f,
         acc);
     if constexpr (P + 1 < STAGES)
-      Steps<M, ROW_BYTES, STAGES, P + 1, TAIL, FIRST>::run(ar, br, kt + 1, steps, smem, wave, ln,
-                                                           f, acc);
+      Steps<M, ROW_BYTES, STAGES, P + 1, TAIL, FIRST, MASK>::run(ar, br, kt + 1, steps, smem,
+                                                                 wave, ln, f, acc);
   }
 };
 
-// K loop over k16 16-bit units per row (a multiple of Geo::kK16, at least one
-// stage); every accumulator is written (no zeroing beforehand).
-template <class M, int ROW_BYTES, int STAGES>
-FE2O3_DEVICE void mainloop(const typename Substep<M, ROW_BYTES, STAGES, 0, 0, false>::RA_& ar,
-                           const typename Substep<M, ROW_BYTES, STAGES, 0, 0, false>::RB_& br,
-                           uint32_t k16, uint8_t* smem, typename M::Acc& acc) {
+// K loop over k16 16-bit units per row (at least one); every accumulator is
+// written (no zeroing beforehand).  k16 is a multiple of Geo::kK16, or, with
+// MASK, of 8: the last stage is then partial and its chunks past k16 load
+// zeros.
+template <class M, int ROW_BYTES, int STAGES, bool MASK = false>
+FE2O3_DEVICE void mainloop(
+    const typename Substep<M, ROW_BYTES, STAGES, 0, 0, false, MASK>::RA_& ar,
+    const typename Substep<M, ROW_BYTES, STAGES, 0, 0, false, MASK>::RB_& br, uint32_t k16,
+    uint8_t* smem, typename M::Acc& acc) {
   using G = Geo<ROW_BYTES>;
   using L = Lay<ROW_BYTES, STAGES, M::kARows, M::kBTileBytes>;
-  using Sub = Substep<M, ROW_BYTES, STAGES, 0, 0, false>;
+  using Sub = Substep<M, ROW_BYTES, STAGES, 0, 0, false, MASK>;
   static_assert((ROW_BYTES == 128 && (STAGES == 2 || STAGES == 3)) ||
                     (ROW_BYTES == 64 && STAGES == 4),
                 "two or three 64-k stages, or four 32-k stages");
   static_assert(M::kSubsteps % 2 == 0 || STAGES % 2 == 0,
                 "fragment buffers alternate across the unrolled steps");
   constexpr int NA = Sub::NA, NB = Sub::NB;
-  const int steps = (int)(k16 / G::kK16);
+  const int steps = (int)(MASK ? (k16 + G::kK16 - 1u) / G::kK16 : k16 / G::kK16);
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const typename M::Lanes ln = M::lanes(L::b_region);
   // stages 0 .. STAGES-2 whole, and stage STAGES-1's early copies (those a
   // step -1 would issue)
-  using St = Steps<M, ROW_BYTES, STAGES, 0, false, false>;
+  using St = Steps<M, ROW_BYTES, STAGES, 0, false, false, MASK>;
 #pragma unroll
   for (int st = 0; st + 1 < STAGES; ++st) {
     const uint32_t kb = st == 0 ? 0u : St::stage_k(st, steps);
@@ -913,21 +956,23 @@ FE2O3_DEVICE void mainloop(const typename Substep<M, ROW_BYTES, STAGES, 0, 0, fa
   __builtin_amdgcn_sched_barrier(0);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
-  int kt = 0;
-  if (steps >= STAGES) {
-    Steps<M, ROW_BYTES, STAGES, 0, false, true>::run(ar, br, 0, steps, smem, wave, ln, f, acc);
-    for (kt = STAGES; kt + STAGES <= steps; kt += STAGES)
-      Steps<M, ROW_BYTES, STAGES, 0, false, false>::run(ar, br, kt, steps, smem, wave, ln, f,
-                                                        acc);
-    if (kt < steps)  // fewer than STAGES steps left; they start in buffer 0
-      Steps<M, ROW_BYTES, STAGES, 0, true, false>::run(ar, br, kt, steps, smem, wave, ln, f, acc);
-  } else {
-    Steps<M, ROW_BYTES, STAGES, 0, true, true>::run(ar, br, 0, steps, smem, wave, ln, f, acc);
-  }
+  // the first group bounded (it may hold every step), then whole groups,
+  // then the rest; one code path whatever the step count
+  Steps<M, ROW_BYTES, STAGES, 0, true, true, MASK>::run(ar, br, 0, steps, smem, wave, ln, f, acc);
+  int kt = STAGES;
+  for (; kt + STAGES <= steps; kt += STAGES)
+    Steps<M, ROW_BYTES, STAGES, 0, false, false, MASK>::run(ar, br, kt, steps, smem, wave, ln, f,
+                                                            acc);
+  if (kt < steps)  // fewer than STAGES steps left; they start in buffer 0
+    Steps<M, ROW_BYTES, STAGES, 0, true, false, MASK>::run(ar, br, kt, steps, smem, wave, ln, f,
+                                                           acc);
   __builtin_amdgcn_sched_barrier(0);
-  // the last steps' early copies (of clamped stages nobody reads) land before
-  // the workgroup can end and its LDS be handed to another
-  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  // The last steps' early copies (of clamped stages nobody reads) land
+  // before the workgroup can end and its LDS be handed to another, and the
+  // last substep's reads of a next stage that does not exist land before
+  // the epilogue may reuse their registers (a policy's inline-asm reads are
+  // invisible to the compiler's own wait tracking).
+  __builtin_amdgcn_s_waitcnt(kWaitVm0Lgkm0);
   M::finish(acc);
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -949,21 +994,50 @@ FE2O3_DEVICE uint32_t acc16_col0() { return (wave_id() & 1u) * CPW + 4u * (lane_
 
 // Acc32T (i, j, e): tile row wm*RPW + 32i + lane%32, tile column
 // wn*RPW + 32j + 8(e/4) + 4(lane/32) + e%4 (RPW = 128, or 64 for Fp8Mma64).
+// (`w`: the wave index, when the caller read it before the K loop, so that
+// the thread id need not stay live across the loop)
 template <int RPW = 128>
-FE2O3_DEVICE uint32_t acc32_row0() { return (wave_id() >> 1) * RPW + (lane_id() & 31u); }
+FE2O3_DEVICE uint32_t acc32_row0(uint32_t w) { return (w >> 1) * RPW + (lane_id() & 31u); }
+template <int RPW = 128>
+FE2O3_DEVICE uint32_t acc32_row0() { return acc32_row0<RPW>(wave_id()); }
 
-FE2O3_DEVICE void store_bf16(const Acc16& acc, uint16_t* c_tile, uint64_t ldc) {
-  const uint32_t row0 = acc16_row0(), col0 = acc16_col0();
+// Acc16 (i, j, e) holds column 16j + 4g + e of the wave's block, g = lane /
+// 16 (the lane's 16-lane row of the wave).  For a pair of column blocks
+// (j, j + 1), v_permlane16_swap exchanges rows 1 and 3 of block j's packed
+// values with rows 0 and 2 of block j + 1's: afterwards lanes of row g hold
+// columns 8 (g / 2) .. + 7 of block j + g % 2, 16 bytes per lane, and each
+// store writes 64 contiguous bytes of 16 rows (half the stores of writing
+// the 8-byte pieces in place).
+// row0, col0: this lane's first row and column (columns of a pair start
+// 32 apart).
+template <int RB, int CB>
+FE2O3_DEVICE void store_bf16_pairs(const Acc16T<RB, CB>& acc, uint16_t* c_tile, uint64_t ldc,
+                                   uint32_t row0, uint32_t col0) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < RB; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      u32x2_t packed;
-      packed[0] = pack_bf16x2(acc.v[i][j][0], acc.v[i][j][1]);
-      packed[1] = pack_bf16x2(acc.v[i][j][2], acc.v[i][j][3]);
-      *reinterpret_cast<u32x2_t*>(c_tile + (uint64_t)(row0 + 16u * i) * ldc + col0 + 16u * j) =
+    for (int jp = 0; jp < CB / 2; ++jp) {
+      const int ja = 2 * jp, jb = 2 * jp + 1;
+      const uint32_t y0 = pack_bf16x2(acc.v[i][ja][0], acc.v[i][ja][1]);
+      const uint32_t y1 = pack_bf16x2(acc.v[i][ja][2], acc.v[i][ja][3]);
+      const uint32_t x0 = pack_bf16x2(acc.v[i][jb][0], acc.v[i][jb][1]);
+      const uint32_t x1 = pack_bf16x2(acc.v[i][jb][2], acc.v[i][jb][3]);
+      const auto s0 = __builtin_amdgcn_permlane16_swap(y0, x0, false, false);
+      const auto s1 = __builtin_amdgcn_permlane16_swap(y1, x1, false, false);
+      u32x4_t packed;
+      packed[0] = s0[0];
+      packed[1] = s1[0];
+      packed[2] = s0[1];
+      packed[3] = s1[1];
+      *reinterpret_cast<u32x4_t*>(c_tile + (uint64_t)(row0 + 16u * i) * ldc + col0 + 32u * jp) =
           packed;
     }
+}
+
+FE2O3_DEVICE void store_bf16(const Acc16& acc, uint16_t* c_tile, uint64_t ldc) {
+  const uint32_t g = lane_id() >> 4;
+  const uint32_t col0 = (wave_id() & 1u) * 128u + 16u * (g & 1u) + 8u * (g >> 1);
+  store_bf16_pairs(acc, c_tile, ldc, acc16_row0(), col0);
 }
 
 // Edge tiles (the last tile row or column of a C whose M or N is not a
@@ -989,39 +1063,39 @@ FE2O3_DEVICE void store_bf16_edge(const Acc16& acc, uint16_t* c_tile, uint64_t l
 }
 
 // A 128 x 128 tile of Acc16T<4, 4> (waves of 64 x 64): whole tiles of a
-// 16-byte aligned C (WHOLE) as 8-byte pieces; otherwise only rows <
-// rows_valid and columns < cols_valid, one 2-byte store per element.
+// 16-byte aligned C (WHOLE) with store_bf16's pair exchange, 16 bytes per
+// lane; otherwise only rows < rows_valid and columns < cols_valid, one
+// 2-byte store per element.
 template <bool WHOLE>
 FE2O3_DEVICE void store_bf16_128(const Acc16T<4, 4>& acc, uint16_t* c_tile, uint64_t ldc,
                                  uint32_t rows_valid, uint32_t cols_valid) {
+  if constexpr (WHOLE) {
+    const uint32_t g = lane_id() >> 4;
+    const uint32_t col0 = (wave_id() & 1u) * 64u + 16u * (g & 1u) + 8u * (g >> 1);
+    store_bf16_pairs(acc, c_tile, ldc, acc16_row0<64>(), col0);
+    return;
+  }
   const uint32_t row0 = acc16_row0<64>(), col0 = acc16_col0<64>();
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t r = row0 + 16u * i;
-    if (!WHOLE && r >= rows_valid) continue;
+    if (r >= rows_valid) continue;
     uint16_t* out = c_tile + (uint64_t)r * ldc;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if constexpr (WHOLE) {
-        u32x2_t packed;
-        packed[0] = pack_bf16x2(acc.v[i][j][0], acc.v[i][j][1]);
-        packed[1] = pack_bf16x2(acc.v[i][j][2], acc.v[i][j][3]);
-        *reinterpret_cast<u32x2_t*>(out + col0 + 16u * j) = packed;
-      } else {
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t c = col0 + 16u * j + e;
-          if (c < cols_valid) out[c] = bf16_bits_from_f32(acc.v[i][j][e]);
-        }
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t c = col0 + 16u * j + e;
+        if (c < cols_valid) out[c] = bf16_bits_from_f32(acc.v[i][j][e]);
       }
-    }
   }
 }
 
 FE2O3_DEVICE void store_bf16_edge(const Acc32& acc, uint16_t* c_tile, uint64_t ldc,
-                                  uint32_t rows_valid, uint32_t cols_valid) {
-  const uint32_t row0 = acc32_row0();
-  const uint32_t col0 = (wave_id() & 1u) * 128u + 4u * (lane_id() >> 5);
+                                  uint32_t rows_valid, uint32_t cols_valid,
+                                  uint32_t w = wave_id()) {
+  const uint32_t row0 = acc32_row0(w);
+  const uint32_t col0 = (w & 1u) * 128u + 4u * (lane_id() >> 5);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t r = row0 + 32u * i;
@@ -1081,8 +1155,8 @@ FE2O3_DEVICE void stage_bf16(const Acc32& acc, uint8_t* region) {
 // `smem` needs 128 KiB, and the caller's copies must all have landed.
 template <class Acc>
 FE2O3_DEVICE void store_bf16_staged(const Acc& acc, uint8_t* smem, uint16_t* c_tile,
-                                    uint64_t ldc) {
-  const uint32_t l = lane_id(), w = wave_id();
+                                    uint64_t ldc, uint32_t w = wave_id()) {
+  const uint32_t l = lane_id();
   uint8_t* region = smem + w * 32768u;
   __syncthreads();  // every wave is past its last fragment read and copy
   stage_bf16(acc, region);
@@ -1104,9 +1178,10 @@ FE2O3_DEVICE void store_bf16_staged(const Acc& acc, uint8_t* smem, uint16_t* c_t
 // 0..7 and lanes 32-63 columns 32j + 16p + 8..15: 16 bytes per lane and 32
 // bytes per row per store, twice the run and half the stores of storing the
 // 8-byte pieces in place.
-FE2O3_DEVICE void store_bf16(const Acc32& acc, uint16_t* c_tile, uint64_t ldc) {
-  const uint32_t row0 = acc32_row0();
-  const uint32_t col0 = (wave_id() & 1u) * 128u + 8u * (lane_id() >> 5);
+FE2O3_DEVICE void store_bf16(const Acc32& acc, uint16_t* c_tile, uint64_t ldc,
+                            uint32_t w = wave_id()) {
+  const uint32_t row0 = acc32_row0(w);
+  const uint32_t col0 = (w & 1u) * 128u + 8u * (lane_id() >> 5);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll

@@ -406,19 +406,25 @@ FE2O3_DEVICE void general_epilogue(const Acc& acc, float* c_tile, uint32_t rows,
   }
 }
 
+// k: A's k extent and the K loop's; kb: B's rows (its k extent), at most k
+// and more than k - 64.  KT: k or kb is not a multiple of 64; A's chunks
+// past k and B's rows past kb load zeros (gemm_pipe::Rows MASK), so each
+// accumulator gets the staged kernel's zero-padded 32-k blocks.
+template <bool KT = false>
 __global__ void __launch_bounds__(256, 1) gemm_general_pipe_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, float* __restrict__ c,
-    uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha,
-    float beta, uint32_t xcds) {
+    uint32_t m, uint32_t n, uint32_t k, uint32_t kb, uint32_t lda, uint32_t ldb, uint32_t ldc,
+    float alpha, float beta, uint32_t xcds) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   const uint32_t tiles_m = (m + 255u) / 256u, tiles_n = (n + 255u) / 256u;
   uint32_t tm, tn;
   gemm_core::xcd_tile_order(blockIdx.x, tiles_m, tiles_n, xcds, &tm, &tn);
   const uint32_t rows = min(256u, m - tm * 256u), cols = min(256u, n - tn * 256u);
-  const auto ar = gemm_pipe::dense_rows<kGpRowBytes>(a + (uint64_t)tm * 256u * lda, lda, rows, k);
-  const auto br = gemm_pipe::kn_rows(b + (uint64_t)tn * 256u, ldb, cols, k);
+  const auto ar =
+      gemm_pipe::dense_rows<kGpRowBytes, 256, KT>(a + (uint64_t)tm * 256u * lda, lda, rows, k);
+  const auto br = gemm_pipe::kn_rows<KT>(b + (uint64_t)tn * 256u, ldb, cols, kb);
   gemm_pipe::Acc16 acc;
-  gemm_pipe::mainloop<gemm_pipe::Bf16MmaKN, kGpRowBytes, kGpStages>(ar, br, k, smem, acc);
+  gemm_pipe::mainloop<gemm_pipe::Bf16MmaKN, kGpRowBytes, kGpStages, KT>(ar, br, k, smem, acc);
   general_epilogue<256, 128, 128>(acc, c + (uint64_t)tm * 256u * ldc + (uint64_t)tn * 256u, rows,
                                   cols, ldc, ((uintptr_t)c & 15u) == 0u, alpha, beta);
 }
@@ -436,11 +442,12 @@ constexpr int kGp64Smem =
 // TAIL: the last, partial round of a 256 x 256 grid (tiles first_big .. end
 // of gemm_core::xcd_tile_order's list), each as four 128 x 128 quarters
 // (gemm_core::tail_quarter).
-template <int STAGES, bool TAIL = false>
+// k, kb, KT: as for gemm_general_pipe_kernel.
+template <int STAGES, bool TAIL = false, bool KT = false>
 __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_general_pipe128_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, float* __restrict__ c,
-    uint32_t m, uint32_t n, uint32_t k, uint32_t lda, uint32_t ldb, uint32_t ldc, float alpha,
-    float beta, uint32_t xcds, uint32_t first_big = 0) {
+    uint32_t m, uint32_t n, uint32_t k, uint32_t kb, uint32_t lda, uint32_t ldb, uint32_t ldc,
+    float alpha, float beta, uint32_t xcds, uint32_t first_big = 0) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   uint32_t tm, tn;
   if constexpr (TAIL) {
@@ -450,35 +457,136 @@ __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_general_pipe128
   }
   const uint32_t rows = min(128u, m - tm * 128u), cols = min(128u, n - tn * 128u);
   const auto ar =
-      gemm_pipe::dense_rows<kGpRowBytes, 128>(a + (uint64_t)tm * 128u * lda, lda, rows, k);
-  const auto br = gemm_pipe::kn_rows128(b + (uint64_t)tn * 128u, ldb, cols, k);
+      gemm_pipe::dense_rows<kGpRowBytes, 128, KT>(a + (uint64_t)tm * 128u * lda, lda, rows, k);
+  const auto br = gemm_pipe::kn_rows128<KT>(b + (uint64_t)tn * 128u, ldb, cols, kb);
   gemm_pipe::Bf16MmaKN64::Acc acc;
-  gemm_pipe::mainloop<gemm_pipe::Bf16MmaKN64, kGpRowBytes, STAGES>(ar, br, k, smem, acc);
+  gemm_pipe::mainloop<gemm_pipe::Bf16MmaKN64, kGpRowBytes, STAGES, KT>(ar, br, k, smem, acc);
   general_epilogue<128, 64, 64>(acc, c + (uint64_t)tm * 128u * ldc + (uint64_t)tn * 128u, rows,
                                 cols, ldc, ((uintptr_t)c & 15u) == 0u, alpha, beta);
 }
 
-const fe2o3_host::KernelRegistrar kRegisteredPipe[] = {
-    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe_kernel", (const void*)gemm_general_pipe_kernel, 256, kGpSmem}),
-    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe128_kernel<2>", (const void*)gemm_general_pipe128_kernel<2>, 256, kGp64Smem<2>}),
-    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe128_kernel<3>", (const void*)gemm_general_pipe128_kernel<3>, 256, kGp64Smem<3>}),
-    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe128_kernel<2, tail>", (const void*)gemm_general_pipe128_kernel<2, true>, 256, kGp64Smem<2>}),
-    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_v1", "gemm_general_pipe128_kernel<3, tail>", (const void*)gemm_general_pipe128_kernel<3, true>, 256, kGp64Smem<3>}),
-    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe_kernel", (const void*)gemm_general_pipe_kernel, 256, kGpSmem}),
-    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<2>", (const void*)gemm_general_pipe128_kernel<2>, 256, kGp64Smem<2>}),
-    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<3>", (const void*)gemm_general_pipe128_kernel<3>, 256, kGp64Smem<3>}),
-    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<2, tail>", (const void*)gemm_general_pipe128_kernel<2, true>, 256, kGp64Smem<2>}),
-    fe2o3_host::KernelRegistrar({"fe2o3_tiled_gemm_general_vector_a_v1", "gemm_general_pipe128_kernel<3, tail>", (const void*)gemm_general_pipe128_kernel<3, true>, 256, kGp64Smem<3>})};
+// ---- operands the pipelined tile cannot read directly ---------------------------
+// Rows that are not 16-byte aligned (A or B two bytes past a boundary, a
+// stride that is not a multiple of 8) or an A whose K is not a multiple of
+// 8 are first copied into aligned scratch rows: A as [m][kp] with kp = K
+// rounded up to 64 and zeros from K on, B as [K][np] with np = N rounded up
+// to 8.  The pipelined tile then reads the copies; its products are the same
+// MFMAs over the same zero-padded 32-k blocks.  8 elements (16 bytes) per
+// thread per step, written as one 16-byte store.  A whole 8-element piece
+// of a source row is read as one 16-byte load at its own (2-byte) alignment
+// (gfx950 global loads take any alignment); the piece that holds a row's
+// end is read element by element.
+__global__ void __launch_bounds__(256) repack_rows_kernel(const uint16_t* __restrict__ src,
+                                                          uint32_t rows, uint32_t cols,
+                                                          uint32_t ld, uint16_t* __restrict__ dst,
+                                                          uint32_t dst_cols) {
+  const uint64_t per_row = dst_cols / 8u, groups = (uint64_t)rows * per_row;
+  for (uint64_t g = (uint64_t)blockIdx.x * 256u + threadIdx.x; g < groups;
+       g += (uint64_t)gridDim.x * 256u) {
+    const uint64_t r = g / per_row;
+    const uint32_t c0 = (uint32_t)(g % per_row) * 8u;
+    const uint16_t* row = src + r * ld;
+    u32x4_t p;
+    if (c0 + 8u <= cols) {
+      __builtin_memcpy(&p, row + c0, 16);
+    } else {
+      uint16_t v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = c0 + e < cols ? row[c0 + e] : (uint16_t)0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) p[q] = (uint32_t)v[2 * q] | ((uint32_t)v[2 * q + 1] << 16);
+    }
+    *reinterpret_cast<u32x4_t*>(dst + r * dst_cols + c0) = p;
+  }
+}
 
-// Host: whether the pipelined tile takes this general GEMM: whole 64-k
-// stages, 16-byte aligned rows of A and B, and both operands' panels within
-// a buffer resource's 32-bit range.
-bool general_pipe_ok(const uint16_t* a, const uint16_t* b, uint32_t k, uint32_t lda,
-                     uint32_t ldb) {
-  return k != 0 && k % 64 == 0 && lda % 8 == 0 && ldb % 8 == 0 &&
-         (((uintptr_t)a | (uintptr_t)b) & 15u) == 0 && (255ull * lda + k) * 2 < (1ull << 31) &&
+#define FE2O3_GENERAL_PIPE_KERNELS(entry)                                                        \
+  fe2o3_host::KernelRegistrar({entry, "gemm_general_pipe_kernel", (const void*)gemm_general_pipe_kernel<false>, 256, kGpSmem}), \
+  fe2o3_host::KernelRegistrar({entry, "gemm_general_pipe_kernel<k tail>", (const void*)gemm_general_pipe_kernel<true>, 256, kGpSmem}), \
+  fe2o3_host::KernelRegistrar({entry, "gemm_general_pipe128_kernel<2>", (const void*)gemm_general_pipe128_kernel<2>, 256, kGp64Smem<2>}), \
+  fe2o3_host::KernelRegistrar({entry, "gemm_general_pipe128_kernel<3>", (const void*)gemm_general_pipe128_kernel<3>, 256, kGp64Smem<3>}), \
+  fe2o3_host::KernelRegistrar({entry, "gemm_general_pipe128_kernel<2, tail>", (const void*)gemm_general_pipe128_kernel<2, true>, 256, kGp64Smem<2>}), \
+  fe2o3_host::KernelRegistrar({entry, "gemm_general_pipe128_kernel<3, tail>", (const void*)gemm_general_pipe128_kernel<3, true>, 256, kGp64Smem<3>}), \
+  fe2o3_host::KernelRegistrar({entry, "gemm_general_pipe128_kernel<2, k tail>", (const void*)gemm_general_pipe128_kernel<2, false, true>, 256, kGp64Smem<2>}), \
+  fe2o3_host::KernelRegistrar({entry, "gemm_general_pipe128_kernel<3, k tail>", (const void*)gemm_general_pipe128_kernel<3, false, true>, 256, kGp64Smem<3>}), \
+  fe2o3_host::KernelRegistrar({entry, "gemm_general_pipe128_kernel<2, tail, k tail>", (const void*)gemm_general_pipe128_kernel<2, true, true>, 256, kGp64Smem<2>}), \
+  fe2o3_host::KernelRegistrar({entry, "gemm_general_pipe128_kernel<3, tail, k tail>", (const void*)gemm_general_pipe128_kernel<3, true, true>, 256, kGp64Smem<3>}), \
+  fe2o3_host::KernelRegistrar({entry, "repack_rows_kernel", (const void*)repack_rows_kernel, 256, 0})
+
+const fe2o3_host::KernelRegistrar kRegisteredPipe[] = {
+    FE2O3_GENERAL_PIPE_KERNELS("fe2o3_tiled_gemm_general_v1"),
+    FE2O3_GENERAL_PIPE_KERNELS("fe2o3_tiled_gemm_general_vector_a_v1")};
+
+// Raises every pipelined kernel's dynamic-LDS limit once per process.
+int32_t set_general_lds() {
+  static const int32_t rc = [] {
+    int32_t r = fe2o3_host::set_dynamic_lds(
+        {(const void*)gemm_general_pipe_kernel<false>, (const void*)gemm_general_pipe_kernel<true>},
+        kGpSmem);
+    if (r == FE2O3_OK)
+      r = fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe128_kernel<2>,
+                                       (const void*)gemm_general_pipe128_kernel<2, true>,
+                                       (const void*)gemm_general_pipe128_kernel<2, false, true>,
+                                       (const void*)gemm_general_pipe128_kernel<2, true, true>},
+                                      kGp64Smem<2>);
+    if (r == FE2O3_OK)
+      r = fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe128_kernel<3>,
+                                       (const void*)gemm_general_pipe128_kernel<3, true>,
+                                       (const void*)gemm_general_pipe128_kernel<3, false, true>,
+                                       (const void*)gemm_general_pipe128_kernel<3, true, true>},
+                                      kGp64Smem<3>);
+    return r;
+  }();
+  return rc;
+}
+
+// The launches of `plan` over A (lda, k) and B (ldb, kb rows); KT: k or kb
+// is not a multiple of 64.
+template <bool KT>
+int32_t launch_general_pipe(const uint16_t* a, const uint16_t* b, float* c, uint32_t m,
+                            uint32_t n, uint32_t k, uint32_t kb, uint32_t lda, uint32_t ldb,
+                            uint32_t ldc, float alpha, float beta, const tile_plan::Plan& plan,
+                            uint32_t xcds, hipStream_t s) {
+  if (plan.small) {  // 256 x 256 tiles would leave most CUs idle
+    if (plan.stages == 2)
+      gemm_general_pipe128_kernel<2, false, KT><<<(unsigned)plan.grid, 256, kGp64Smem<2>, s>>>(
+          a, b, c, m, n, k, kb, lda, ldb, ldc, alpha, beta, xcds);
+    else
+      gemm_general_pipe128_kernel<3, false, KT><<<(unsigned)plan.grid, 256, kGp64Smem<3>, s>>>(
+          a, b, c, m, n, k, kb, lda, ldb, ldc, alpha, beta, xcds);
+    return fe2o3_host::after_launch();
+  }
+  gemm_general_pipe_kernel<KT><<<(unsigned)plan.grid, 256, kGpSmem, s>>>(
+      a, b, c, m, n, k, kb, lda, ldb, ldc, alpha, beta, xcds);
+  const int32_t big_rc = fe2o3_host::after_launch();
+  if (big_rc != FE2O3_OK || !plan.tail) return big_rc;
+  // the last round of at most half the CUs' tiles as 128 x 128 quarters
+  if (plan.tail_stages == 2)  // more quarters than CUs: two per CU
+    gemm_general_pipe128_kernel<2, true, KT><<<(unsigned)plan.tail_grid, 256, kGp64Smem<2>, s>>>(
+        a, b, c, m, n, k, kb, lda, ldb, ldc, alpha, beta, xcds, plan.first_big);
+  else
+    gemm_general_pipe128_kernel<3, true, KT><<<(unsigned)plan.tail_grid, 256, kGp64Smem<3>, s>>>(
+        a, b, c, m, n, k, kb, lda, ldb, ldc, alpha, beta, xcds, plan.first_big);
+  return fe2o3_host::after_launch();
+}
+
+// Whether the pipelined tile reads an operand in place: 16-byte aligned
+// rows, and its 256-row (A) or K-row (B) panel within a buffer resource's
+// 32-bit range.  A also needs K a multiple of 8 (chunks past K are masked
+// whole).
+bool a_direct(const uint16_t* a, uint32_t k, uint32_t lda) {
+  return k % 8 == 0 && lda % 8 == 0 && ((uintptr_t)a & 15u) == 0 &&
+         (255ull * lda + k) * 2 < (1ull << 31);
+}
+bool b_direct(const uint16_t* b, uint32_t k, uint32_t ldb) {
+  return ldb % 8 == 0 && ((uintptr_t)b & 15u) == 0 &&
          ((uint64_t)(k - 1) * ldb + 256) * 2 < (1ull << 31);
 }
+
+// Operands the tile cannot read in place are repacked (repack_rows_kernel)
+// when M and N are at least one 128 x 128 tile; smaller problems stay on
+// the staged kernel.
+constexpr uint32_t kRepackMin = 128;
 
 template <bool VEC_A>
 int32_t general_gemm(const uint16_t* a, uint64_t a_len, const uint16_t* b, uint64_t b_len,
@@ -495,51 +603,68 @@ int32_t general_gemm(const uint16_t* a, uint64_t a_len, const uint16_t* b, uint6
   if (a_len < ea || b_len < eb || c_len < ec) return FE2O3_ERR_LENGTH;
   if (m == 0 || n == 0) return FE2O3_OK;  // empty output: no dispatch
   if ((ea && !a) || (eb && !b) || !c) return FE2O3_ERR_NULL;
-  if (general_pipe_ok(a, b, k, lda, ldb)) {
+  const bool ad = k != 0 && a_direct(a, k, lda), bd = k != 0 && b_direct(b, k, ldb);
+  const bool repack = k != 0 && (!ad || !bd) && m >= kRepackMin && n >= kRepackMin;
+  if (k != 0 && ((ad && bd) || repack)) {
     // every kernel's LDS limit is raised before anything is launched, so a
     // failure leaves C untouched
-    static const int32_t lds_rc = [] {
-      int32_t rc = fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe_kernel}, kGpSmem);
-      if (rc == FE2O3_OK)
-        rc = fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe128_kernel<2>,
-                                          (const void*)gemm_general_pipe128_kernel<2, true>},
-                                         kGp64Smem<2>);
-      if (rc == FE2O3_OK)
-        rc = fe2o3_host::set_dynamic_lds({(const void*)gemm_general_pipe128_kernel<3>,
-                                          (const void*)gemm_general_pipe128_kernel<3, true>},
-                                         kGp64Smem<3>);
-      return rc;
-    }();
+    const int32_t lds_rc = set_general_lds();
     if (lds_rc != FE2O3_OK) return lds_rc;
     tile_plan::Topology topo;
     const int32_t topo_rc = fe2o3_host::device_topology(&topo);
     if (topo_rc != FE2O3_OK) return topo_rc;
     const tile_plan::Plan plan = tile_plan::plan(m, n, topo);
     if (plan.grid > 0x7fffffffu || plan.tail_grid > 0x7fffffffu) return FE2O3_ERR_SHAPE;
-    const uint32_t xcds = topo.xcds;
     hipStream_t s = (hipStream_t)stream;
-    if (plan.small) {  // 256 x 256 tiles would leave most CUs idle
-      if (plan.stages == 2)
-        gemm_general_pipe128_kernel<2><<<(unsigned)plan.grid, 256, kGp64Smem<2>, s>>>(
-            a, b, c, m, n, k, lda, ldb, ldc, alpha, beta, xcds);
-      else
-        gemm_general_pipe128_kernel<3><<<(unsigned)plan.grid, 256, kGp64Smem<3>, s>>>(
-            a, b, c, m, n, k, lda, ldb, ldc, alpha, beta, xcds);
-      return fe2o3_host::after_launch();
+    if (!repack) {
+      if (k % 64 != 0)
+        return launch_general_pipe<true>(a, b, c, m, n, k, k, lda, ldb, ldc, alpha, beta, plan,
+                                         topo.xcds, s);
+      return launch_general_pipe<false>(a, b, c, m, n, k, k, lda, ldb, ldc, alpha, beta, plan,
+                                        topo.xcds, s);
     }
-    gemm_general_pipe_kernel<<<(unsigned)plan.grid, 256, kGpSmem, s>>>(a, b, c, m, n, k, lda, ldb,
-                                                                        ldc, alpha, beta, xcds);
-    const int32_t big_rc = fe2o3_host::after_launch();
-    if (big_rc != FE2O3_OK || !plan.tail) return big_rc;
-    // the last round of at most half the CUs' tiles as 128 x 128 quarters
-    if (plan.tail_stages == 2)  // more quarters than CUs: two per CU
-      gemm_general_pipe128_kernel<2, true><<<(unsigned)plan.tail_grid, 256, kGp64Smem<2>, s>>>(
-          a, b, c, m, n, k, lda, ldb, ldc, alpha, beta, xcds, plan.first_big);
-    else
-      gemm_general_pipe128_kernel<3, true><<<(unsigned)plan.tail_grid, 256, kGp64Smem<3>, s>>>(
-          a, b, c, m, n, k, lda, ldb, ldc, alpha, beta, xcds, plan.first_big);
-    return fe2o3_host::after_launch();
+    // repack what cannot be read in place into one stream-ordered scratch
+    // block: A as [m][kp] (zeros from K on), B as [K][np]
+    const uint32_t kp = (k + 63u) & ~63u, np = (n + 7u) & ~7u;
+    const uint64_t a_elems = ad ? 0 : (uint64_t)m * kp, b_elems = bd ? 0 : (uint64_t)k * np;
+    if ((!ad && 256ull * kp * 2 >= (1ull << 31)) ||
+        (!bd && ((uint64_t)(k - 1) * np + 256) * 2 >= (1ull << 31)))
+      return FE2O3_ERR_SHAPE;
+    void* scratch = nullptr;
+    int32_t rc = fe2o3_host::scratch_alloc(&scratch, (a_elems + b_elems) * 2, s);
+    if (rc != FE2O3_OK) {
+      // no stream-ordered scratch on this device or process: the staged
+      // kernel reads the operands as they are
+      (void)hipGetLastError();
+      goto staged;
+    }
+    uint16_t* ap = static_cast<uint16_t*>(scratch);
+    uint16_t* bp = ap + a_elems;
+    auto grid = [](uint64_t groups) {
+      const uint64_t g = (groups + 255) / 256;
+      return (unsigned)(g < 16384 ? g : 16384);
+    };
+    if (!ad) repack_rows_kernel<<<grid((uint64_t)m * (kp / 8)), 256, 0, s>>>(a, m, k, lda, ap, kp);
+    if (!bd) repack_rows_kernel<<<grid((uint64_t)k * (np / 8)), 256, 0, s>>>(b, k, n, ldb, bp, np);
+    rc = fe2o3_host::after_launch();
+    if (rc == FE2O3_OK) {
+      const uint16_t* ra = ad ? a : ap;
+      const uint16_t* rb = bd ? b : bp;
+      const uint32_t rlda = ad ? lda : kp, rldb = bd ? ldb : np;
+      // a repacked A holds zeros up to kp: the K loop runs whole stages over
+      // it; an A read in place masks its chunks past K.  B's rows past K
+      // are masked either way.
+      const uint32_t kloop = ad ? k : kp;
+      rc = k % 64 != 0
+               ? launch_general_pipe<true>(ra, rb, c, m, n, kloop, k, rlda, rldb, ldc, alpha,
+                                           beta, plan, topo.xcds, s)
+               : launch_general_pipe<false>(ra, rb, c, m, n, kloop, k, rlda, rldb, ldc, alpha,
+                                            beta, plan, topo.xcds, s);
+    }
+    const int32_t free_rc = fe2o3_host::scratch_free(scratch, s);
+    return rc != FE2O3_OK ? rc : free_rc;
   }
+staged:
   dim3 grid((n + G_BN - 1) / G_BN, (m + G_BM - 1) / G_BM);
   if (grid.y > 65535u) return FE2O3_ERR_SHAPE;
   gemm_general_kernel<VEC_A><<<grid, 256, 0, (hipStream_t)stream>>>(a, b, c, m, n, k, lda, ldb,

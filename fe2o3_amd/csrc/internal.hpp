@@ -43,6 +43,13 @@ uint32_t* status_word();
 // then stay in id order, which is correct on any part).
 int32_t device_topology(tile_plan::Topology* out);
 
+// Stream-ordered device scratch for entry points that stage operands (a
+// library-owned pool per device; runtime.hip): scratch_alloc enqueues the
+// allocation on stream s, scratch_free its release after the work enqueued
+// before it.  0, or a hipError_t.
+int32_t scratch_alloc(void** p, size_t bytes, hipStream_t s);
+int32_t scratch_free(void* p, hipStream_t s);
+
 // Enqueue status: 0, or the hipError_t of the launch just made.
 inline int32_t after_launch() {
   hipError_t e = hipGetLastError();

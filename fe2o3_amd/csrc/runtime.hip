@@ -31,10 +31,13 @@ bool fault_point(const char* entry) {
 // Registered kernels, filled by the static tables of every source file when
 // the library loads (a function-local static, so registration order across
 // files does not matter).
-static constexpr int kMaxKernels = 128;
+// A table that would overflow is recorded (`dropped`) and every query then
+// fails with FE2O3_ERR_OVERFLOW rather than answer from a partial table.
+static constexpr int kMaxKernels = 512;
 struct Registry {
   KernelInfo k[kMaxKernels];
   int n = 0;
+  int dropped = 0;
 };
 static Registry& registry() {
   static Registry r;
@@ -42,7 +45,10 @@ static Registry& registry() {
 }
 KernelRegistrar::KernelRegistrar(const KernelInfo& k) {
   Registry& r = registry();
-  if (r.n < kMaxKernels) r.k[r.n++] = k;
+  if (r.n < kMaxKernels)
+    r.k[r.n++] = k;
+  else
+    ++r.dropped;
 }
 
 // One non-finite rejection counter per device.  The reference's kernels
@@ -117,6 +123,55 @@ int32_t device_topology(tile_plan::Topology* out) {
   out->cus = (uint32_t)(w >> 8);
   out->xcds = (uint32_t)(w & 0xffu);
   return 0;
+}
+
+// Stream-ordered scratch: one library-owned memory pool per device, its
+// release threshold at the maximum so blocks freed at the end of one call
+// stay in the pool for the next (a pool of the device's own would hand them
+// back at every synchronize).  Allocation and free are ordered on the
+// caller's stream, so concurrent calls on different streams get different
+// blocks and a call never frees memory its kernels still use.
+static hipMemPool_t scratch_pools[kMaxDevices];
+static std::mutex scratch_mu;
+
+static int32_t scratch_pool(hipMemPool_t* out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int32_t)e;
+  if (dev < 0 || dev >= kMaxDevices) return (int32_t)hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_pools[dev] == nullptr) {
+    hipMemPoolProps props;
+    memset(&props, 0, sizeof props);
+    props.allocType = hipMemAllocationTypePinned;
+    props.handleTypes = hipMemHandleTypeNone;
+    props.location.type = hipMemLocationTypeDevice;
+    props.location.id = dev;
+    hipMemPool_t pool = nullptr;
+    e = hipMemPoolCreate(&pool, &props);
+    if (e != hipSuccess) return (int32_t)e;
+    uint64_t keep = ~0ull;
+    e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+    if (e != hipSuccess) {
+      (void)hipMemPoolDestroy(pool);
+      return (int32_t)e;
+    }
+    scratch_pools[dev] = pool;
+  }
+  *out = scratch_pools[dev];
+  return 0;
+}
+
+int32_t scratch_alloc(void** p, size_t bytes, hipStream_t s) {
+  *p = nullptr;
+  hipMemPool_t pool = nullptr;
+  const int32_t rc = scratch_pool(&pool);
+  if (rc != 0) return rc;
+  return (int32_t)hipMallocFromPoolAsync(p, bytes == 0 ? 16 : bytes, pool, s);
+}
+
+int32_t scratch_free(void* p, hipStream_t s) {
+  return p == nullptr ? 0 : (int32_t)hipFreeAsync(p, s);
 }
 
 }  // namespace fe2o3_host
@@ -351,6 +406,10 @@ int32_t fe2o3_kernel_resources(const char* entry, uint32_t index, Fe2o3KernelRes
                                uint32_t* count) {
   if (!entry || !count) return FE2O3_ERR_NULL;
   const fe2o3_host::Registry& r = fe2o3_host::registry();
+  if (r.dropped != 0) {
+    *count = 0;
+    return FE2O3_ERR_OVERFLOW;
+  }
   const fe2o3_host::KernelInfo* hit = nullptr;
   uint32_t n = 0;
   for (int i = 0; i < r.n; ++i)

@@ -12,8 +12,10 @@ element type and length against the kernel signature and fails closed with
 ``Fe2o3Error`` before any launch, and ``launch`` enqueues on the stream and
 then synchronizes it, so buffers are quiescent when it returns, as the
 reference's typed launch is synchronous by design
-(crates/fe2o3-host/src/loaded_kernel.rs:420-432).  ``launch_async`` only
-enqueues.  The physical argument order is the reference's: one
+(crates/fe2o3-host/src/loaded_kernel.rs:420-432).  The prepared launch holds
+its slices, so buffers handed in as temporaries live until it is dropped.
+``launch_async`` only enqueues: keep the prepared launch (or the buffers)
+until the stream has been synchronized.  The physical argument order is the reference's: one
 (pointer, length) pair per slice in declaration order, then the scalars
 (examples/tiled_gemm_general_v1/hardware-harness/src/lib.rs:578-597).
 """
@@ -31,9 +33,15 @@ ERR_LENGTH = -2
 
 
 class _Prepared:
-    def __init__(self, kernel: "_TypedKernel", args: tuple):
+    """A checked launch: the flattened arguments, plus the slices themselves,
+    held so that a buffer passed as a temporary (``prepare(ctx.to_device(x),
+    ...)``) stays allocated until the launch has run; a DeviceBuffer frees
+    its memory when it is collected."""
+
+    def __init__(self, kernel: "_TypedKernel", args: tuple, buffers: tuple):
         self.kernel = kernel
         self.args = args
+        self.buffers = buffers
 
     def launch_async(self, stream: Stream | None = None) -> None:
         fn = getattr(_lib.lib(), self.kernel.ENTRY)
@@ -80,7 +88,7 @@ class _TypedKernel:
             flat += [buf.ptr, buf.count]
         for (name, ctype), value in zip(self.SCALARS, args[ns:]):
             flat.append(ctype(value))
-        return _Prepared(self, tuple(flat))
+        return _Prepared(self, tuple(flat), tuple(args[:ns]))
 
 
 def _typed(entry, slices, scalars=()):

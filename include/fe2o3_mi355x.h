@@ -530,7 +530,9 @@ int32_t fe2o3_moe_routing_check(const uint32_t *top2_experts, uint64_t top2_len,
  * bytes per lane (0 = no scratch, no register spills) and registers as the
  * runtime reports them for the loaded code object.  *count is always set
  * to the number of kernels behind `entry`; FE2O3_ERR_LENGTH when
- * index >= *count (0 for an unknown entry).  120-byte record. */
+ * index >= *count (0 for an unknown entry); FE2O3_ERR_OVERFLOW (and
+ * *count 0) if the library's kernel table overflowed when it loaded.
+ * 120-byte record. */
 typedef struct Fe2o3KernelResources {
   char kernel[96];
   uint32_t workgroup_size;

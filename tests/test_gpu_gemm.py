@@ -157,14 +157,28 @@ def test_general_random_within_tolerance(gpu, oracle, dims, strides, alpha, beta
     ((17, 1000, 128), (136, 1003, 1003), 1.0, 1.0),
     ((64, 300, 64), (64, 304, 301), 0.5, -1.0),  # last column chunk reads B's padding
     ((3000, 2900, 128), (136, 2904, 2910), 1.25, -0.5),  # 144 tiles of 256: the 256x256 tile
+    # K not a multiple of 64: the partial last stage (A's chunks and B's rows
+    # past K masked to zeros)
+    ((300, 520, 520), (528, 528, 530), 1.5, 0.5),
+    ((256, 384, 72), (72, 384, 390), -1.0, 0.25),
+    ((3000, 2900, 200), (200, 2904, 2910), 0.75, 1.0),
+    # K not a multiple of 8: A repacked even when aligned
+    ((300, 520, 77), (80, 520, 530), 1.0, -0.5),
+    # B's stride not a multiple of 8: B repacked
+    ((300, 260, 256), (264, 261, 270), 2.0, 0.0),
+    # both repacked, K not a multiple of 64 (B's repacked rows end inside the
+    # last stage)
+    ((200, 130, 77), (77, 131, 140), -2.0, 0.125),
 ])
 def test_general_pipelined_tile_matches_staged_kernel(gpu, oracle, dims, strides, alpha, beta):
-    """Shapes the pipelined tiles take (whole 64-k stages, 16-byte aligned A
-    and B rows; 128x128 tiles up to 128 tiles of 256x256, the 256x256 tile
-    beyond) against the same data through the 64x64 staged kernel (A moved
-    to a 2-byte offset, which the tiles do not take): the same bits, also
-    with NaN and infinity in A's and B's stride padding; C's padding
-    untouched; rel-err <= 1e-5 against the tiled CPU schedule."""
+    """One GEMM three ways, the same bits: the pipelined tiles on the
+    operands as given; the same with A two bytes past a 16-byte boundary
+    (the tiles cannot read it in place, so it is repacked into aligned,
+    zero-padded rows first when M and N reach 128); and the 64x64 staged
+    kernel, reached through row strips of 64 (below the repack size), the
+    reference's schedule.  Also with NaN and infinity in A's and B's stride
+    padding; C's padding untouched; rel-err <= 1e-5 against the tiled CPU
+    schedule."""
     m, n, k = dims
     lda, ldb, ldc = strides
     rng = np.random.default_rng(m + n + k)
@@ -177,17 +191,27 @@ def test_general_pipelined_tile_matches_staged_kernel(gpu, oracle, dims, strides
         b[r * ldb + n:(r + 1) * ldb] = 0xFF80
     c = rng.standard_normal(lc).astype(np.float32)
     kern = _kernels().tiled_gemm_general_v1_gpu.Kernel.load(gpu)
+    gb = gpu.to_device(b)
     gc = Guarded(gpu, c)
-    kern.prepare(gpu.to_device(a), gpu.to_device(b), gc.body, m, n, k, lda, ldb, ldc, alpha,
-                 beta).launch()
+    kern.prepare(gpu.to_device(a), gb, gc.body, m, n, k, lda, ldb, ldc, alpha, beta).launch()
     assert gc.guards_intact()
-    # the same A two bytes past a 16-byte boundary: the staged kernel
-    a_off = Guarded(gpu, np.concatenate([np.zeros(1, np.uint16), a]))
-    gs = Guarded(gpu, c)
-    kern.prepare(a_off.full.view(65, la), gpu.to_device(b), gs.body, m, n, k, lda, ldb, ldc,
-                 alpha, beta).launch()
     got = gc.download()
-    assert_same(got, gs.download(), "pipelined tile vs staged kernel")
+    # the same A two bytes past a 16-byte boundary
+    a_off = Guarded(gpu, np.concatenate([np.zeros(1, np.uint16), a]))
+    gr = Guarded(gpu, c)
+    kern.prepare(a_off.full.view(65, la), gb, gr.body, m, n, k, lda, ldb, ldc, alpha,
+                 beta).launch()
+    assert gr.guards_intact() and a_off.unchanged()
+    assert_same(gr.download(), got, "A at a 2-byte offset vs in place")
+    # the staged kernel, 64 rows at a time (strips of C, A and C offset by rows)
+    ga_s = gpu.to_device(a)
+    gs = gpu.to_device(c)
+    for r0 in range(0, m, 64):
+        rows = min(64, m - r0)
+        kern.prepare(ga_s.view(r0 * lda, (rows - 1) * lda + k), gb,
+                     gs.view(r0 * ldc, (rows - 1) * ldc + n), rows, n, k, lda, ldb, ldc, alpha,
+                     beta).launch()
+    assert_same(gs.download(), got, "pipelined tile vs staged kernel")
     for r in range(m - 1):
         assert got[r * ldc + n:(r + 1) * ldc].tobytes() == c[r * ldc + n:(r + 1) * ldc].tobytes()
     rows = np.concatenate([got[r * ldc:r * ldc + n] for r in range(m)])
@@ -365,6 +389,39 @@ def test_gemm_bf16_nt_fast_path(gpu, oracle, m, n, k):
 def test_gemm_bf16_nt_edge_tiles(gpu, oracle, m, n, k):
     rows = None if m * n <= 1_100_000 else [0, 255, 256, 1999, 3839, 3840, 3999]
     _nt_case(gpu, oracle, m, n, k, seed=6, rows=rows)
+
+
+# K a multiple of 8 but not of 64: the pipelined tiles' partial last stage
+# (chunks past K load zeros) on every launch form: 128x128 small grids
+# (three- and two-stage), 256x256 tiles, tail quarters
+@pytest.mark.parametrize("m,n,k", [(256, 256, 8), (512, 768, 72), (1000, 264, 1000),
+                                   (4096, 2048, 136), (4096, 4096, 4000), (6144, 6144, 200)])
+def test_gemm_bf16_nt_k_tail(gpu, oracle, m, n, k):
+    rows = None if m * n <= 1_100_000 else [0, 255, 256, 1999, 2048, m - 1]
+    _nt_case(gpu, oracle, m, n, k, seed=8, rows=rows)
+
+
+def test_gemm_bf16_nt_k_tail_matches_zero_padded_k(gpu):
+    """K = 4000 against the same operands zero-padded to K = 4032 (whole
+    stages, the plain tile): the partial stage's zero chunks are exactly the
+    padding, so C is bit-identical."""
+    kern = _kernels()
+    m = n = 1024
+    k, kp = 4000, 4032
+    da, db = gpu.alloc(m * k, np.uint16), gpu.alloc(n * k, np.uint16)
+    kern.fill_normal_bf16(da, 9, 0xA, 1.0 / 64)
+    kern.fill_normal_bf16(db, 9, 0xB, 1.0 / 64)
+    a = da.download().reshape(m, k)
+    b = db.download().reshape(n, k)
+    ap = np.zeros((m, kp), np.uint16)
+    bp = np.zeros((n, kp), np.uint16)
+    ap[:, :k], bp[:, :k] = a, b
+    dc, dcp = gpu.alloc(m * n, np.uint16), gpu.alloc(m * n, np.uint16)
+    kern.gemm_bf16_nt_gpu.Kernel.load(gpu).prepare(da, db, dc, m, n, k).launch()
+    kern.gemm_bf16_nt_gpu.Kernel.load(gpu).prepare(gpu.to_device(ap.ravel()),
+                                                   gpu.to_device(bp.ravel()), dcp, m, n,
+                                                   kp).launch()
+    assert_same(dc.download(), dcp.download(), "K 4000 vs zero-padded K 4032")
 
 
 def test_gemm_bf16_nt_small_grid_matches_large_tiles(gpu):

@@ -472,13 +472,52 @@ def test_gemm_fp8_all_outputs(gpu, oracle, m, n, k):
     assert _fp8_case(gpu, oracle, m, n, k, (rr.ravel(), cc.ravel())) <= 1e-2
 
 
-# any M, N: edge tiles on the fast path (K a multiple of 128), the generic
-# bounds-checked kernel otherwise (E4M3 widened exactly to bf16)
+# any M, N: edge tiles on the fast path (K a multiple of 16, the last stage
+# partial when K is not a multiple of 128), the generic bounds-checked kernel
+# otherwise (E4M3 widened exactly to bf16)
 @pytest.mark.parametrize("m,n,k", [(300, 520, 256), (1, 257, 128), (257, 256, 384),
                                    (100, 70, 96), (33, 65, 200), (256, 256, 160), (5, 3, 1)])
 def test_gemm_fp8_any_shape(gpu, oracle, m, n, k):
     rr, cc = np.meshgrid(np.arange(m), np.arange(n), indexing="ij")
     assert _fp8_case(gpu, oracle, m, n, k, (rr.ravel(), cc.ravel())) <= 1e-2
+
+
+# K a multiple of 16 but not of 128: the pipelined tiles with a partial last
+# stage (its chunks past K load zeros) on the 128x128 form (three and two
+# stages), the 256x256 tile and its tail round
+@pytest.mark.parametrize("m,n,k", [(256, 256, 16), (512, 768, 208), (300, 520, 272),
+                                   (4096, 2048, 144), (6144, 6144, 48)])
+def test_gemm_fp8_k_tail(gpu, oracle, m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    if m * n <= 400_000:
+        rr, cc = np.meshgrid(np.arange(m), np.arange(n), indexing="ij")
+        points = (rr.ravel(), cc.ravel())
+    else:
+        rows = np.concatenate([np.arange(0, m, 128), rng.integers(0, m, 4000), [m - 1]])
+        points = (rows, rng.integers(0, n, rows.size))
+    assert _fp8_case(gpu, oracle, m, n, k, points) <= 1e-2
+
+
+@pytest.mark.parametrize("m,n,k,kp", [(1024, 1024, 4000, 4096), (300, 520, 208, 256),
+                                      (6144, 6144, 80, 128)])
+def test_gemm_fp8_k_tail_matches_zero_padded_k(gpu, m, n, k, kp):
+    """K not a multiple of 128 against the same operands zero-padded to whole
+    stages (the plain tiles): the partial stage's zero chunks are exactly the
+    padding and the scales are the same, so C is bit-identical."""
+    kern = _k()
+    rng = np.random.default_rng(k)
+    # E4M3 codes without the NaN pair (0x7F, 0xFF)
+    a = rng.integers(0, 0x7F, (m, k), dtype=np.uint8) | (rng.integers(0, 2, (m, k), dtype=np.uint8) << 7)
+    b = rng.integers(0, 0x7F, (n, k), dtype=np.uint8) | (rng.integers(0, 2, (n, k), dtype=np.uint8) << 7)
+    ap = np.zeros((m, kp), np.uint8)
+    bp = np.zeros((n, kp), np.uint8)
+    ap[:, :k], bp[:, :k] = a, b
+    sa = gpu.to_device(np.array([1.0 / 64], np.float32))
+    sb = gpu.to_device(np.array([1.0 / 32], np.float32))
+    c, cp = gpu.alloc(m * n, np.uint16), gpu.alloc(m * n, np.uint16)
+    kern.gemm_fp8_nt(gpu.to_device(a.ravel()), gpu.to_device(b.ravel()), sa, sb, c, m, n, k)
+    kern.gemm_fp8_nt(gpu.to_device(ap.ravel()), gpu.to_device(bp.ravel()), sa, sb, cp, m, n, kp)
+    assert_same(c.download(), cp.download(), f"K {k} vs zero-padded K {kp}")
 
 
 @pytest.mark.parametrize("m,n,k", [(4096, 2048, 128), (4000, 2000, 256)])

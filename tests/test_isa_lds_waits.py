@@ -4,7 +4,8 @@ relies on the compiler's own s_waitcnt lgkmcnt for the A read issued before
 them.  This CPU test compiles gemm_small.hip for gfx950 to assembly and
 replays the instruction streams of gemm_general_pipe_kernel (256x256
 tiles) and gemm_general_pipe128_kernel<2>, <3> (128x128, whole grids and
-tail rounds) with in-order LDS
+tail rounds), each with whole stages and with a partial last stage, in
+text order with in-order LDS
 completion: no instruction -- an LDS read's address included -- may read a
 VGPR that an LDS read has not yet delivered (no s_waitcnt lgkmcnt covering
 it).  The two reads of one inline-asm pair are the case the compiler cannot
@@ -90,4 +91,6 @@ def test_general_pipe_kernel_lds_reads_are_waited_for(tmp_path):
                     for l in body]
         stripped = [l for l in stripped if l.strip() != "s_waitcnt"]
         assert _violations(stripped) > 50, name
-    assert found == 5  # 256x256, and 128x128 on two and three stages, whole grid or tail
+    # 256x256, and 128x128 on two and three stages, whole grid or tail; each
+    # with whole 64-k stages and with a partial last stage (K tail)
+    assert found == 10
