@@ -376,25 +376,40 @@ FE2O3_DEVICE void gate_up_tile(const uint16_t* __restrict__ xc, const uint16_t* 
   // accumulator column j (16 B rows each) of wave column wn: j = 0,1 gate
   // f .. f+31, j = 2,3 up f .. f+31, j = 4,5 gate f+32 .., j = 6,7 up f+32 ..
   // (f = f0 + 64 wn); gate j pairs with up j + 2
+  // Lane row g = lane / 16 holds columns 4g .. 4g + 3 of each 16-column
+  // block; the blocks sub = 0 and 1 of a half are adjacent, and one
+  // v_permlane16_swap per packed word (gemm_pipe::store_bf16_pairs) leaves
+  // row g with columns 8 (g / 2) .. + 7 of block g % 2: one 16-byte store per
+  // lane, 64 contiguous bytes per output row.  Partner lanes share their
+  // output row, so both or neither store.
   const uint32_t r0 = gemm_pipe::acc16_row0<RPW>();
-  const uint32_t c0 = gemm_pipe::acc16_col0();                // 128 wn + 4 (lane / 16)
-  const uint32_t fl = f0 + ((c0 & 128u) >> 1) + (c0 & 127u);  // f0 + 64 wn + 4 (lane / 16)
+  const uint32_t g = gemm_pipe::lane_id() >> 4;
+  const uint32_t wn = gemm_pipe::wave_id() & 1u;
+  const uint32_t fl = f0 + 64u * wn + 16u * (g & 1u) + 8u * (g >> 1);
 #pragma unroll
   for (int i = 0; i < Mma::kRB; ++i) {
     const uint32_t r = r0 + 16u * i;
     if (r >= rows) continue;
     uint16_t* out_row = hc + (uint64_t)(row0 + r) * ffn;
 #pragma unroll
-    for (int half = 0; half < 2; ++half)
+    for (int half = 0; half < 2; ++half) {
+      uint32_t w[2][2];
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         const f32x4_t& gv = acc.v[i][4 * half + sub];
         const f32x4_t& uv = acc.v[i][4 * half + sub + 2];
-        u32x2_t packed;
-        packed[0] = pack_bf16x2(silu_mul(gv[0], uv[0]), silu_mul(gv[1], uv[1]));
-        packed[1] = pack_bf16x2(silu_mul(gv[2], uv[2]), silu_mul(gv[3], uv[3]));
-        *reinterpret_cast<u32x2_t*>(out_row + fl + half * 32u + sub * 16u) = packed;
+        w[sub][0] = pack_bf16x2(silu_mul(gv[0], uv[0]), silu_mul(gv[1], uv[1]));
+        w[sub][1] = pack_bf16x2(silu_mul(gv[2], uv[2]), silu_mul(gv[3], uv[3]));
       }
+      const auto s0 = __builtin_amdgcn_permlane16_swap(w[0][0], w[1][0], false, false);
+      const auto s1 = __builtin_amdgcn_permlane16_swap(w[0][1], w[1][1], false, false);
+      u32x4_t packed;
+      packed[0] = s0[0];
+      packed[1] = s1[0];
+      packed[2] = s0[1];
+      packed[3] = s1[1];
+      *reinterpret_cast<u32x4_t*>(out_row + fl + half * 32u) = packed;
+    }
   }
 }
 
