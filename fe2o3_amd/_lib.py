@@ -193,6 +193,51 @@ class Fe2o3Slice1ObservationV1(C.Structure):
                 ("resources", Fe2o3Slice1ResourcesV1), ("dispatch_identity", u8 * 16),
                 ("last_error", Fe2o3Slice1ErrorV1)]
 
+# ---- protected profile lifecycles (fe2o3_protected_*) ----------------------------------
+
+PROTECTED_MAX_REGIONS = 8
+
+
+class Fe2o3ProtectedRegionV1(C.Structure):
+    _fields_ = [("address", vp), ("elements", u64)]
+
+
+class Fe2o3ProtectedProfileV1(C.Structure):
+    _fields_ = [("profile", u32), ("code_object_version", u32), ("name", C.c_char * 32),
+                ("target", C.c_char * 32), ("symbol", C.c_char * 64), ("grid", u32 * 3),
+                ("workgroup", u32 * 3), ("dynamic_lds_bytes", u32), ("static_lds_bytes", u32),
+                ("private_segment_bytes", u32), ("explicit_kernarg_bytes", u32),
+                ("complete_kernarg_bytes", u32), ("kernarg_alignment", u32),
+                ("hsa_kernarg_alignment", u32), ("regions", u32),
+                ("region_elements", u64 * PROTECTED_MAX_REGIONS),
+                ("region_element_bytes", u32 * PROTECTED_MAX_REGIONS),
+                ("region_writes", u32 * PROTECTED_MAX_REGIONS), ("shape", u32 * 4),
+                ("receipt_fields", u32), ("host_fields", u32),
+                ("receipt_field", (C.c_char * 40) * 16), ("host_field", (C.c_char * 40) * 16)]
+
+
+class Fe2o3ProtectedArtifactV1(C.Structure):
+    _fields_ = [("identity", u8 * 32), ("profile_identity", u8 * 32),
+                ("artifact_identity", u8 * 32), ("build_digest", u8 * 32),
+                ("source_digest", u8 * 32), ("compiler_identity", u8 * 32),
+                ("inspection", Fe2o3Slice1InspectionV1), ("profile", Fe2o3ProtectedProfileV1)]
+
+
+class Fe2o3ProtectedJoinFactsV1(C.Structure):
+    _fields_ = [("profile", u32), ("receipt", u8 * 16), ("host_target", C.c_char * 32),
+                ("host_shape", u32 * 4), ("host_argument_elements", u64),
+                ("host_grid", u32 * 3), ("host_workgroup", u32 * 3),
+                ("host_code_object_version", u32), ("host_explicit_kernarg", u32),
+                ("host_complete_kernarg", u32), ("host_kernarg_alignment", u32),
+                ("host_policy", u32)]
+
+
+class Fe2o3ProtectedReceiptV1(C.Structure):
+    _fields_ = [("identity", u8 * 32), ("artifact_identity", u8 * 32),
+                ("executable_object", u8 * 16), ("kernel_object", u8 * 16),
+                ("dispatch_identity", u8 * 16), ("unload_identity", u8 * 32)]
+
+
 # name -> (restype, argtypes).  Order and meaning follow the header.
 SIGNATURES = {
     "fe2o3_status_string": (C.c_char_p, [i32]),
@@ -291,6 +336,20 @@ SIGNATURES = {
     "fe2o3_lds_gemm_slice1_unload_v1": (i32, [vp, C.POINTER(Fe2o3Slice1ReceiptV1)]),
     "fe2o3_lds_gemm_slice1_release_v1": (None, [vp]),
     "fe2o3_lds_gemm_slice1_observe_v1": (i32, [vp, C.POINTER(Fe2o3Slice1ObservationV1)]),
+    "fe2o3_protected_profile_v1": (i32, [u32, C.POINTER(Fe2o3ProtectedProfileV1)]),
+    "fe2o3_protected_artifact_v1": (i32, [u32, C.POINTER(Fe2o3ProtectedArtifactV1)]),
+    "fe2o3_protected_join_facts_v1": (i32, [u32, C.POINTER(Fe2o3ProtectedJoinFactsV1)]),
+    "fe2o3_protected_validate_join_v1": (
+        i32, [C.POINTER(Fe2o3ProtectedJoinFactsV1), C.POINTER(Fe2o3Slice1ErrorV1)]),
+    "fe2o3_protected_join_v1": (
+        i32, [u32, C.POINTER(Fe2o3ProtectedRegionV1), u32, i32, SLICE1_RELEASE_FN, vp, pvp,
+              C.POINTER(Fe2o3Slice1ErrorV1)]),
+    "fe2o3_protected_load_v1": (
+        i32, [vp, C.POINTER(Fe2o3Slice1AdapterV1), C.POINTER(Fe2o3Slice1ErrorV1)]),
+    "fe2o3_protected_dispatch_and_wait_v1": (i32, [vp, C.POINTER(Fe2o3Slice1ErrorV1)]),
+    "fe2o3_protected_unload_v1": (i32, [vp, C.POINTER(Fe2o3ProtectedReceiptV1)]),
+    "fe2o3_protected_release_v1": (None, [vp]),
+    "fe2o3_protected_observe_v1": (i32, [vp, C.POINTER(Fe2o3Slice1ObservationV1)]),
 }
 
 

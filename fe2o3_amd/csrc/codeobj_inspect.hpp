@@ -164,22 +164,17 @@ struct Section {
   bool in_file;  // occupies bytes [offset, offset + size) inside the buffer
 };
 
-// Returns "" on success, else the first fact that could not be read.
-// `kernel` and `descriptor` name the kernel and its descriptor symbol.
-inline const char* inspect_code_object(const uint8_t* b, size_t n, const char* kernel,
-                                       const char* descriptor, Fe2o3Slice1InspectionV1* out) {
-  memset(out, 0, sizeof(*out));
-  out->byte_len = n;
+// The ELF header and section table; "" on success, else the fact that
+// could not be read.
+inline const char* read_sections(const uint8_t* b, size_t n, std::vector<Section>* out) {
   if (b == nullptr || n < 64 || memcmp(b, "\x7f" "ELF", 4) != 0 || b[4] != 2 || b[5] != 1)
     return "ELF header";
   if (get_le(b + 18, 2) != kEmAmdgpu || b[7] != kOsAbiAmdgpuHsa) return "ELF machine";
-  // EI_ABIVERSION: 2, 3, 4 = code object v4, v5, v6.
-  out->code_object_version = b[8] + 2u;
-  out->e_flags = (uint32_t)get_le(b + 48, 4);
   const uint64_t shoff = get_le(b + 40, 8);
   const uint64_t shentsize = get_le(b + 58, 2), shnum = get_le(b + 60, 2);
   if (shentsize != 64 || shoff > n || shnum > (n - shoff) / 64) return "section table";
-  std::vector<Section> sec(shnum);
+  std::vector<Section>& sec = *out;
+  sec.assign(shnum, Section{});
   for (uint64_t i = 0; i < shnum; ++i) {
     const uint8_t* s = b + shoff + 64 * i;
     Section& x = sec[i];
@@ -190,6 +185,44 @@ inline const char* inspect_code_object(const uint8_t* b, size_t n, const char* k
     // section has none and can serve as no table or descriptor below
     if (x.type != kShtNobits && !x.in_file) return "section bounds";
   }
+  return "";
+}
+
+// The NT_AMDGPU_METADATA note's map; "" on success.
+inline const char* read_metadata(const uint8_t* b, const std::vector<Section>& sec, MsgValue* md) {
+  for (const auto& st : sec) {
+    if (st.type != kShtNote) continue;
+    if (!st.in_file) return "metadata note";
+    uint64_t off = 0;
+    while (st.size - off >= 12) {
+      const uint8_t* note = b + st.offset + off;
+      const uint64_t namesz = get_le(note, 4), descsz = get_le(note + 4, 4), type = get_le(note + 8, 4);
+      const uint64_t name_pad = (namesz + 3) & ~3ull, desc_pad = (descsz + 3) & ~3ull;
+      if (name_pad + desc_pad > st.size - off - 12) return "metadata note";
+      if (type == kNtAmdgpuMetadata && namesz == 7 && memcmp(note + 12, "AMDGPU", 7) == 0) {
+        MsgReader r(note + 12 + name_pad, (size_t)descsz);
+        if (!r.read(md) || md->kind != MsgValue::kMap) return "metadata";
+        return "";
+      }
+      off += 12 + name_pad + desc_pad;
+    }
+  }
+  return "metadata note";
+}
+
+// Returns "" on success, else the first fact that could not be read.
+// `kernel` and `descriptor` name the kernel and its descriptor symbol.
+inline const char* inspect_code_object(const uint8_t* b, size_t n, const char* kernel,
+                                       const char* descriptor, Fe2o3Slice1InspectionV1* out) {
+  memset(out, 0, sizeof(*out));
+  out->byte_len = n;
+  std::vector<Section> sec;
+  const char* bad = read_sections(b, n, &sec);
+  if (bad[0]) return bad;
+  // EI_ABIVERSION: 2, 3, 4 = code object v4, v5, v6.
+  out->code_object_version = b[8] + 2u;
+  out->e_flags = (uint32_t)get_le(b + 48, 4);
+  const uint64_t shnum = sec.size();
   // kernel descriptor through the symbol table
   const uint8_t* kd = nullptr;
   for (const auto& st : sec) {
@@ -223,25 +256,8 @@ inline const char* inspect_code_object(const uint8_t* b, size_t n, const char* k
   out->kd_wavefront_size = (get_le(kd + 56, 2) >> 10 & 1u) ? 32u : 64u;
   // metadata note
   MsgValue md;
-  bool have_md = false;
-  for (const auto& st : sec) {
-    if (st.type != kShtNote) continue;
-    if (!st.in_file) return "metadata note";
-    uint64_t off = 0;
-    while (st.size - off >= 12 && !have_md) {
-      const uint8_t* note = b + st.offset + off;
-      const uint64_t namesz = get_le(note, 4), descsz = get_le(note + 4, 4), type = get_le(note + 8, 4);
-      const uint64_t name_pad = (namesz + 3) & ~3ull, desc_pad = (descsz + 3) & ~3ull;
-      if (name_pad + desc_pad > st.size - off - 12) return "metadata note";
-      if (type == kNtAmdgpuMetadata && namesz == 7 && memcmp(note + 12, "AMDGPU", 7) == 0) {
-        MsgReader r(note + 12 + name_pad, (size_t)descsz);
-        if (!r.read(&md) || md.kind != MsgValue::kMap) return "metadata";
-        have_md = true;
-      }
-      off += 12 + name_pad + desc_pad;
-    }
-  }
-  if (!have_md) return "metadata note";
+  bad = read_metadata(b, sec, &md);
+  if (bad[0]) return bad;
   const MsgValue* target = md.get("amdhsa.target");
   if (!target || target->kind != MsgValue::kStr) return "metadata target";
   const std::string triple = "amdgcn-amd-amdhsa--";
@@ -301,6 +317,34 @@ inline const char* inspect_code_object(const uint8_t* b, size_t n, const char* k
   out->implicit_bytes =
       out->md_kernarg_bytes - (uint32_t)std::min<uint64_t>(implicit_off, out->md_kernarg_bytes);
   return "";
+}
+
+// inspect_code_object for a code object that holds exactly one kernel,
+// whose name and descriptor symbol are read from the metadata first (into
+// `kernel` and `descriptor`, NUL-terminated, each of `room` bytes).
+inline const char* inspect_single_kernel(const uint8_t* b, size_t n, char* kernel,
+                                         char* descriptor, size_t room,
+                                         Fe2o3Slice1InspectionV1* out) {
+  memset(out, 0, sizeof(*out));
+  out->byte_len = n;
+  if (room == 0) return "metadata kernel";
+  kernel[0] = descriptor[0] = '\0';
+  std::vector<Section> sec;
+  const char* bad = read_sections(b, n, &sec);
+  if (bad[0]) return bad;
+  MsgValue md;
+  bad = read_metadata(b, sec, &md);
+  if (bad[0]) return bad;
+  const MsgValue* kernels = md.get("amdhsa.kernels");
+  if (!kernels || kernels->kind != MsgValue::kArr) return "metadata kernels";
+  if (kernels->items.size() != 1) return "metadata kernel";
+  const MsgValue* name = kernels->items[0].get(".name");
+  const MsgValue* sym = kernels->items[0].get(".symbol");
+  if (!name || name->kind != MsgValue::kStr || name->s.size() >= room) return "metadata kernel";
+  if (!sym || sym->kind != MsgValue::kStr || sym->s.size() >= room) return "metadata symbol";
+  memcpy(kernel, name->s.c_str(), name->s.size() + 1);
+  memcpy(descriptor, sym->s.c_str(), sym->s.size() + 1);
+  return inspect_code_object(b, n, kernel, descriptor, out);
 }
 
 }  // namespace fe2o3_inspect

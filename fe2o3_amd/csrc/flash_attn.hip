@@ -39,65 +39,24 @@
 //      diagonal tile.
 #include "common.hpp"
 #include "internal.hpp"
+#include "profiles.hpp"
 
 namespace {
 
 using namespace fe2o3;
 
 // ---- exact profile ---------------------------------------------------------------------
-constexpr int P_N = 8, P_D = 16;
+constexpr int P_N = fe2o3_profiles::kFlashN, P_D = fe2o3_profiles::kFlashD;
 
-// A NaN or an infinity anywhere in Q, K or V rejects the whole launch, as
-// the reference's kernel traps (kernel.rs:143-146): every output is written
-// as quiet NaN and the device's contract-status word is marked.  Lane l
-// probes elements 2l and 2l+1 of each input; a ballot combines the lanes.
+// The profile's arithmetic and its rejection of non-finite inputs are
+// fe2o3_profiles::flash_profile (profiles.hpp), shared with the code object
+// the protected lifecycle loads.
 __global__ void __launch_bounds__(64) flash_profile_kernel(const float* __restrict__ q,
                                                            const float* __restrict__ k,
                                                            const float* __restrict__ v,
                                                            float* __restrict__ out,
                                                            uint32_t* __restrict__ status) {
-#pragma clang fp contract(off)
-  const int lane = threadIdx.x;
-  const int first = lane * 2;
-  const int row = first / P_D, col = first % P_D;
-  float probe = 0.0f;
-  for (int i = first; i < first + 2; ++i)
-    probe = finite_probe(finite_probe(finite_probe(probe, q[i]), k[i]), v[i]);
-  if (__ballot(probe != probe) != 0ull) {
-    if (lane == 0) mark_nonfinite(status);
-    out[first] = quiet_nan();
-    out[first + 1] = quiet_nan();
-    return;
-  }
-  float m = 0.0f, l = 0.0f, n0 = 0.0f, n1 = 0.0f;
-  for (int kr = 0; kr <= row; ++kr) {
-    float dot = 0.0f;
-    for (int f = 0; f < P_D; ++f) {
-      const float p = q[row * P_D + f] * k[kr * P_D + f];
-      dot = dot + p;
-    }
-    const float s = dot * 0.25f;
-    const float v0 = v[kr * P_D + col], v1 = v[kr * P_D + col + 1];
-    if (kr == 0) {
-      m = s;
-      l = 1.0f;
-      n0 = v0;
-      n1 = v1;
-    } else {
-      const float nm = s > m ? s : m;
-      const float wp = expf(m - nm);
-      const float wc = expf(s - nm);
-      const float t0 = l * wp;
-      l = t0 + wc;
-      const float a0 = n0 * wp, b0 = v0 * wc;
-      n0 = a0 + b0;
-      const float a1 = n1 * wp, b1 = v1 * wc;
-      n1 = a1 + b1;
-      m = nm;
-    }
-  }
-  out[first] = n0 / l;
-  out[first + 1] = n1 / l;
+  fe2o3_profiles::flash_profile(q, k, v, out, status);
 }
 
 // ---- BASELINE-shape kernel -------------------------------------------------------------------

@@ -51,6 +51,9 @@
 #include "internal.hpp"
 
 #include "slice1_artifact.inc"
+#include "flash_attention_v1_artifact.inc"
+#include "row_softmax_v1_artifact.inc"
+#include "moe_top2_v1_artifact.inc"
 
 namespace {
 
@@ -177,7 +180,6 @@ constexpr uint32_t kWorkgroup[3] = {64, 1, 1};
 constexpr uint32_t kWavefront = 64;
 constexpr uint32_t kExplicitKernarg = FE2O3_SLICE1_EXPLICIT_KERNARG_BYTES;
 constexpr uint32_t kCompleteKernarg = FE2O3_SLICE1_COMPLETE_KERNARG_BYTES;
-constexpr uint32_t kImplicitKernarg = FE2O3_SLICE1_IMPLICIT_KERNARG_BYTES;
 constexpr uint32_t kContractKernargAlign = FE2O3_SLICE1_CONTRACT_KERNARG_ALIGNMENT;
 constexpr uint64_t kHsaKernargAlign = FE2O3_SLICE1_HSA_KERNARG_ALIGNMENT;
 constexpr uint32_t kStaticLds = FE2O3_SLICE1_STATIC_LDS_BYTES;
@@ -196,6 +198,29 @@ constexpr char kRuntimeDomain[] = "FE2O3/MI355X-HIP-RUNTIME-INSTANCE/V1";
 
 enum Role : uint32_t { kRoleA = 1, kRoleB = 2, kRoleC = 3 };
 enum Element : uint32_t { kBf16 = 1, kF32 = 2 };
+
+// What load, dispatch and unload check for one embedded code object: the
+// exact LDS GEMM, or one of the protected profiles below.  Every profile
+// launches grid [1,1,1] x workgroup [64,1,1] with no dynamic LDS, and its
+// kernarg is explicit bytes followed by the 256-byte implicit suffix.
+struct Spec {
+  uint32_t profile;  // FE2O3_PROFILE_*; 0 for the LDS GEMM
+  const char* symbol;
+  const uint8_t* code;
+  size_t code_len;
+  uint32_t explicit_bytes, complete_bytes, static_lds;
+  const char* unload_domain;
+  uint32_t implicit_bytes() const { return complete_bytes - explicit_bytes; }
+};
+
+const Spec kSlice1Spec = {0,
+                          kKernelSymbol,
+                          kSlice1CodeObject,
+                          sizeof(kSlice1CodeObject),
+                          kExplicitKernarg,
+                          kCompleteKernarg,
+                          kStaticLds,
+                          kUnloadDomain};
 
 // Domain strings are hashed with their terminating NUL, as the reference's
 // b"...\0" literals are.
@@ -521,10 +546,10 @@ void context_identity_for(int32_t device, uint8_t out[16]) {
   std::memcpy(out, full, 16);
 }
 
-void unload_identity(const Fe2o3Slice1UnloadV1& u, const uint8_t runtime[16], uint64_t agent,
-                     uint8_t out[32]) {
+void unload_identity(const char* domain, const Fe2o3Slice1UnloadV1& u, const uint8_t runtime[16],
+                     uint64_t agent, uint8_t out[32]) {
   Sha256 d;
-  hash_domain(d, kUnloadDomain);
+  hash_domain(d, domain);
   hash_field(d, u.executable_object, 16);
   hash_field(d, runtime, 16);
   hash_le<uint64_t>(d, agent);
@@ -579,12 +604,14 @@ Fe2o3Slice1GeometryV1 exact_geometry() {
 // ---- the lifecycle handle -------------------------------------------------------------
 
 struct Fe2o3Slice1Lifecycle {
+  const Spec* spec = &kSlice1Spec;
   int32_t state = FE2O3_SLICE1_JOINED;
   int32_t device = 0;
   bool leases = true;
   void (*release_leases)(void*) = nullptr;
   void* user = nullptr;
-  alignas(16) uint8_t kernarg[FE2O3_SLICE1_COMPLETE_KERNARG_BYTES] = {};
+  // the complete kernarg of the profile (spec->complete_bytes of it used)
+  alignas(16) uint8_t kernarg[FE2O3_PROTECTED_MAX_COMPLETE_KERNARG_BYTES] = {};
   bool has_adapter = false;
   Fe2o3Slice1AdapterV1 adapter{};
   bool has_executable = false, has_kernel = false;
@@ -690,27 +717,28 @@ int32_t do_load(Fe2o3Slice1Lifecycle* lc, Fe2o3Slice1ErrorV1* err) {
   for (const auto& ch : env_checks)
     if (!ch.ok) return load_error(lc, err, FE2O3_SLICE1_E_ENVIRONMENT, ch.field);
 
+  const Spec& spec = *lc->spec;
   uint8_t digest[32];
-  sha256(kSlice1CodeObject, sizeof(kSlice1CodeObject), digest);
-  rc = ad.load_executable ? ad.load_executable(self, kSlice1CodeObject, sizeof(kSlice1CodeObject),
-                                               digest, &lc->executable, &lc->load)
+  sha256(spec.code, spec.code_len, digest);
+  rc = ad.load_executable ? ad.load_executable(self, spec.code, spec.code_len, digest,
+                                               &lc->executable, &lc->load)
                           : -1;
   if (rc != 0) return load_error(lc, err, FE2O3_SLICE1_E_LOAD_ADAPTER, "", rc);
   lc->has_executable = true;
-  if (std::memcmp(lc->load.digest, digest, 32) != 0 || lc->load.byte_len != sizeof(kSlice1CodeObject) ||
+  if (std::memcmp(lc->load.digest, digest, 32) != 0 || lc->load.byte_len != spec.code_len ||
       !eq16(lc->load.runtime_instance, env.runtime_instance) ||
       lc->load.agent_handle != env.agent_handle)
     return load_error(lc, err, FE2O3_SLICE1_E_LOAD_OBSERVATION, "identity or content observation");
 
-  rc = ad.resolve_kernel ? ad.resolve_kernel(self, lc->executable, kKernelSymbol, &lc->kernel,
+  rc = ad.resolve_kernel ? ad.resolve_kernel(self, lc->executable, spec.symbol, &lc->kernel,
                                              &lc->resolution)
                          : -1;
   if (rc != 0) return load_error(lc, err, FE2O3_SLICE1_E_KERNEL_ADAPTER, "", rc);
   lc->has_kernel = true;
   const Fe2o3Slice1ResolutionV1& res = lc->resolution;
   if (!eq16(res.executable_object, lc->load.executable_object) ||
-      strncmp(res.symbol, kKernelSymbol, sizeof(res.symbol)) != 0 ||
-      res.kernarg_segment_bytes != kCompleteKernarg || res.kernarg_alignment != kHsaKernargAlign)
+      strncmp(res.symbol, spec.symbol, sizeof(res.symbol)) != 0 ||
+      res.kernarg_segment_bytes != spec.complete_bytes || res.kernarg_alignment != kHsaKernargAlign)
     return load_error(lc, err, FE2O3_SLICE1_E_KERNEL_OBSERVATION,
                       "object, symbol, size, or HSA alignment");
 
@@ -720,7 +748,7 @@ int32_t do_load(Fe2o3Slice1Lifecycle* lc, Fe2o3Slice1ErrorV1* err) {
   if (rc != 0) return load_error(lc, err, FE2O3_SLICE1_E_RESOURCE_ADAPTER, "", rc);
   const Fe2o3Slice1ResourcesV1& r = lc->resources;
   if (!eq16(r.executable_object, lc->load.executable_object) ||
-      !eq16(r.kernel_object, res.kernel_object) || r.group_segment_bytes != kStaticLds ||
+      !eq16(r.kernel_object, res.kernel_object) || r.group_segment_bytes != spec.static_lds ||
       r.private_segment_bytes != kPrivateSegment)
     return load_error(lc, err, FE2O3_SLICE1_E_RESOURCE_OBSERVATION,
                       "object, static LDS, or private segment");
@@ -734,28 +762,29 @@ int32_t do_load(Fe2o3Slice1Lifecycle* lc, Fe2o3Slice1ErrorV1* err) {
 // LoadedExactStateV1::dispatch_and_wait (:639-696).
 int32_t do_dispatch(Fe2o3Slice1Lifecycle* lc, Fe2o3Slice1ErrorV1* err) {
   Fe2o3Slice1AdapterV1& ad = lc->adapter;
+  const Spec& spec = *lc->spec;
   const Fe2o3Slice1GeometryV1 geometry = exact_geometry();
-  uint8_t explicit_bytes[kExplicitKernarg];
-  std::memcpy(explicit_bytes, lc->kernarg, kExplicitKernarg);
+  uint8_t explicit_bytes[FE2O3_PROTECTED_MAX_COMPLETE_KERNARG_BYTES];
+  std::memcpy(explicit_bytes, lc->kernarg, spec.explicit_bytes);
   Fe2o3Slice1ImplicitV1 imp{};
   int32_t rc = ad.initialize_implicit_kernarg
                    ? ad.initialize_implicit_kernarg(ad.self, lc->executable, lc->kernel, &geometry,
-                                                    kExplicitKernarg, kExplicitKernarg,
-                                                    kImplicitKernarg, lc->kernarg,
-                                                    sizeof(lc->kernarg), &imp)
+                                                    spec.explicit_bytes, spec.explicit_bytes,
+                                                    spec.implicit_bytes(), lc->kernarg,
+                                                    spec.complete_bytes, &imp)
                    : -1;
   if (rc != 0) return dispatch_error(lc, err, FE2O3_SLICE1_E_IMPLICIT_ADAPTER, "", rc);
-  if (std::memcmp(explicit_bytes, lc->kernarg, kExplicitKernarg) != 0)
+  if (std::memcmp(explicit_bytes, lc->kernarg, spec.explicit_bytes) != 0)
     return dispatch_error(lc, err, FE2O3_SLICE1_E_EXPLICIT_KERNARG_MUTATION);
   if (!eq16(imp.executable_object, lc->load.executable_object) ||
       !eq16(imp.kernel_object, lc->resolution.kernel_object) || !geometry_eq(imp.geometry, geometry) ||
-      imp.explicit_bytes != kExplicitKernarg || imp.implicit_offset != kExplicitKernarg ||
-      imp.implicit_bytes != kImplicitKernarg || !imp.completed)
+      imp.explicit_bytes != spec.explicit_bytes || imp.implicit_offset != spec.explicit_bytes ||
+      imp.implicit_bytes != spec.implicit_bytes() || !imp.completed)
     return dispatch_error(lc, err, FE2O3_SLICE1_E_IMPLICIT_OBSERVATION,
                           "object, geometry, span, or completion");
   Fe2o3Slice1DispatchV1 dsp{};
   rc = ad.launch_and_wait ? ad.launch_and_wait(ad.self, lc->executable, lc->kernel, &geometry,
-                                               lc->kernarg, sizeof(lc->kernarg), &dsp)
+                                               lc->kernarg, spec.complete_bytes, &dsp)
                           : -1;
   if (rc != 0) return dispatch_error(lc, err, FE2O3_SLICE1_E_DISPATCH_ADAPTER, "", rc);
   if (!eq16(dsp.executable_object, lc->load.executable_object) ||
@@ -769,6 +798,285 @@ int32_t do_dispatch(Fe2o3Slice1Lifecycle* lc, Fe2o3Slice1ErrorV1* err) {
   drop_kernel(lc);
   release_leases(lc);
   lc->state = FE2O3_SLICE1_COMPLETED;
+  set_error(err, FE2O3_SLICE1_E_NONE);
+  return FE2O3_OK;
+}
+
+int32_t lifecycle_load(Fe2o3Slice1Lifecycle* lc, const Fe2o3Slice1AdapterV1* adapter,
+                       Fe2o3Slice1ErrorV1* error);
+
+// ---- protected profiles ---------------------------------------------------------------
+//
+// crates/fe2o3-host/src/flash_attention_v1_lifecycle.rs,
+// protected_row_softmax_v1_lifecycle.rs and moe_top2_v1_lifecycle.rs: the
+// profile constants (:20-32 of each), validate_join's receipt and host
+// checks in their order, and the unload identity domains.
+
+constexpr char kReceiptDomain[] = "FE2O3/MI355X-PROTECTED-RECEIPT/V1";
+constexpr char kProtectedProfileDomain[] = "FE2O3/MI355X-PROTECTED-PROFILE/V1";
+constexpr char kCompilerDomain[] = "FE2O3/MI355X-PROTECTED-COMPILER/V1";
+constexpr uint32_t kMaxRegions = FE2O3_PROTECTED_MAX_REGIONS;
+
+struct ProtectedDef {
+  Spec spec;
+  const char* name;
+  const uint8_t* build_digest;
+  const uint8_t* source_digest;
+  const char* compiler;
+  const char* flags;
+  uint32_t regions;
+  uint64_t elements[kMaxRegions];
+  uint32_t element_bytes[kMaxRegions];
+  uint32_t writes[kMaxRegions];
+  uint32_t shape[4];
+  const char* receipt_fields[16];
+  const char* host_fields[16];
+};
+
+const ProtectedDef kProtected[] = {
+    {{FE2O3_PROFILE_FLASH_ATTENTION_V1, "flash_attention_causal_f32_b1_h1_n8_d16_v1",
+      kFlashV1CodeObject, sizeof(kFlashV1CodeObject), 64, 320, 0,
+      "FE2O3/FLASH-ATTENTION/UNLOAD/V1"},
+     "flash_attention_v1", kFlashV1BuildDigest, kFlashV1SourceDigest, kFlashV1Compiler,
+     kFlashV1Flags, 4, {128, 128, 128, 128}, {4, 4, 4, 4}, {0, 0, 0, 1}, {1, 1, 8, 16},
+     // flash_attention_v1_lifecycle.rs:720-799
+     {"identity", "artifact identity", "finalized output", "raw worker output", "target",
+      "code-object version", "frontend authority commitment", "OCML provider commitment",
+      "finalization", "compiler handoff", "machine identity", "OCML provider closure"},
+     {"target", "shape", "argument extent", "grid", "workgroup", "code-object version",
+      "explicit ABI", "complete ABI", "ABI alignment", "mask policy"}},
+    {{FE2O3_PROFILE_ROW_SOFTMAX_V1, "row_softmax_v1", kSoftmaxV1CodeObject,
+      sizeof(kSoftmaxV1CodeObject), 32, 288, 0, "FE2O3/ROW-SOFTMAX/UNLOAD/V1"},
+     "row_softmax_v1", kSoftmaxV1BuildDigest, kSoftmaxV1SourceDigest, kSoftmaxV1Compiler,
+     kSoftmaxV1Flags, 2, {64, 64}, {4, 4}, {0, 1}, {64, 0, 0, 0},
+     // protected_row_softmax_v1_lifecycle.rs:723-777
+     {"identity", "admission identity", "artifact identity", "finalized output", "target",
+      "row width", "grid", "workgroup", "explicit ABI", "complete ABI"},
+     {"target", "row width", "grid", "workgroup", "explicit ABI", "complete ABI",
+      "ABI alignment", "activity policy"}},
+    {{FE2O3_PROFILE_MOE_TOP2_V1, "moe_top2_route_f32_t8_e4_k2_c4_v1", kMoeTop2V1CodeObject,
+      sizeof(kMoeTop2V1CodeObject), 128, 384, 0, "FE2O3/MOE-TOP2/UNLOAD/V1"},
+     "moe_top2_v1", kMoeTop2V1BuildDigest, kMoeTop2V1SourceDigest, kMoeTop2V1Compiler,
+     kMoeTop2V1Flags, 8, {32, 16, 4, 4, 5, 16, 16, 16}, {4, 4, 4, 4, 4, 4, 4, 4},
+     {0, 1, 1, 1, 1, 1, 1, 1}, {8, 4, 2, 4},
+     // moe_top2_v1_lifecycle.rs:824-890
+     {"identity", "artifact identity", "finalized output", "raw worker output", "target",
+      "code-object version", "canonical digest", "source/KIR/compiler profile",
+      "upstream LLVM/LLD exchange"},
+     {"target", "T/E/K/C profile", "grid", "workgroup", "code-object version", "explicit ABI",
+      "complete ABI", "ABI alignment", "routing-only policy"}},
+};
+
+const ProtectedDef* protected_def(uint32_t profile) {
+  for (const auto& d : kProtected)
+    if (d.spec.profile == profile) return &d;
+  return nullptr;
+}
+
+uint32_t count_fields(const char* const* f) {
+  uint32_t n = 0;
+  while (n < 16 && f[n] != nullptr) ++n;
+  return n;
+}
+
+Fe2o3ProtectedProfileV1 profile_view(const ProtectedDef& d) {
+  Fe2o3ProtectedProfileV1 v{};
+  v.profile = d.spec.profile;
+  v.code_object_version = kCodeObjectVersion;
+  std::strncpy(v.name, d.name, sizeof(v.name) - 1);
+  std::strncpy(v.target, kTarget, sizeof(v.target) - 1);
+  std::strncpy(v.symbol, d.spec.symbol, sizeof(v.symbol) - 1);
+  for (int i = 0; i < 3; ++i) {
+    v.grid[i] = kGrid[i];
+    v.workgroup[i] = kWorkgroup[i];
+  }
+  v.dynamic_lds_bytes = kDynamicLds;
+  v.static_lds_bytes = d.spec.static_lds;
+  v.private_segment_bytes = kPrivateSegment;
+  v.explicit_kernarg_bytes = d.spec.explicit_bytes;
+  v.complete_kernarg_bytes = d.spec.complete_bytes;
+  v.kernarg_alignment = kContractKernargAlign;
+  v.hsa_kernarg_alignment = (uint32_t)kHsaKernargAlign;
+  v.regions = d.regions;
+  for (uint32_t i = 0; i < d.regions; ++i) {
+    v.region_elements[i] = d.elements[i];
+    v.region_element_bytes[i] = d.element_bytes[i];
+    v.region_writes[i] = d.writes[i];
+  }
+  std::memcpy(v.shape, d.shape, sizeof(v.shape));
+  v.receipt_fields = count_fields(d.receipt_fields);
+  v.host_fields = count_fields(d.host_fields);
+  for (uint32_t i = 0; i < v.receipt_fields; ++i)
+    std::strncpy(v.receipt_field[i], d.receipt_fields[i], sizeof(v.receipt_field[i]) - 1);
+  for (uint32_t i = 0; i < v.host_fields; ++i)
+    std::strncpy(v.host_field[i], d.host_fields[i], sizeof(v.host_field[i]) - 1);
+  return v;
+}
+
+bool nonzero32(const uint8_t* p) {
+  for (int i = 0; i < 32; ++i)
+    if (p[i]) return true;
+  return false;
+}
+
+struct ProtectedArtifact {
+  Fe2o3ProtectedArtifactV1 view{};
+  const char* inspect_error = "";
+  bool facts_agree = false;  // the code object's own facts against the profile
+};
+
+const ProtectedArtifact& protected_artifact(const ProtectedDef& d) {
+  static ProtectedArtifact cache[sizeof(kProtected) / sizeof(kProtected[0])];
+  static std::once_flag once[sizeof(kProtected) / sizeof(kProtected[0])];
+  const size_t slot = (size_t)(&d - kProtected);
+  std::call_once(once[slot], [&] {
+    ProtectedArtifact& x = cache[slot];
+    Fe2o3ProtectedArtifactV1& v = x.view;
+    v.profile = profile_view(d);
+    sha256(d.spec.code, d.spec.code_len, v.artifact_identity);
+    std::memcpy(v.build_digest, d.build_digest, 32);
+    std::memcpy(v.source_digest, d.source_digest, 32);
+    {
+      Sha256 h;
+      hash_domain(h, kCompilerDomain);
+      hash_str(h, d.compiler);
+      hash_str(h, d.flags);
+      h.finish(v.compiler_identity);
+    }
+    {
+      Sha256 h;
+      hash_domain(h, kProtectedProfileDomain);
+      hash_le<uint32_t>(h, d.spec.profile);
+      hash_str(h, d.name);
+      hash_str(h, kTarget);
+      hash_str(h, d.spec.symbol);
+      for (int i = 0; i < 3; ++i) hash_le<uint32_t>(h, kGrid[i]);
+      for (int i = 0; i < 3; ++i) hash_le<uint32_t>(h, kWorkgroup[i]);
+      hash_le<uint32_t>(h, d.spec.explicit_bytes);
+      hash_le<uint32_t>(h, d.spec.complete_bytes);
+      for (uint32_t i = 0; i < d.regions; ++i) {
+        hash_le<uint64_t>(h, d.elements[i]);
+        hash_le<uint32_t>(h, d.element_bytes[i]);
+        hash_le<uint32_t>(h, d.writes[i]);
+      }
+      for (int i = 0; i < 4; ++i) hash_le<uint32_t>(h, d.shape[i]);
+      h.finish(v.profile_identity);
+    }
+    {
+      Sha256 h;
+      hash_domain(h, kReceiptDomain);
+      hash_field(h, v.profile_identity, 32);
+      hash_field(h, v.artifact_identity, 32);
+      hash_field(h, v.source_digest, 32);
+      hash_field(h, v.compiler_identity, 32);
+      h.finish(v.identity);
+    }
+    char kernel[64], descriptor[64];
+    x.inspect_error = fe2o3_inspect::inspect_single_kernel(d.spec.code, d.spec.code_len, kernel,
+                                                           descriptor, sizeof(kernel),
+                                                           &v.inspection);
+    const Fe2o3Slice1InspectionV1& i = v.inspection;
+    x.facts_agree = x.inspect_error[0] == '\0' && std::strcmp(kernel, d.spec.symbol) == 0 &&
+                    i.kd_kernarg_bytes == d.spec.complete_bytes &&
+                    i.md_kernarg_bytes == d.spec.complete_bytes &&
+                    i.explicit_bytes == d.spec.explicit_bytes &&
+                    i.explicit_args == d.regions &&
+                    i.implicit_offset == d.spec.explicit_bytes &&
+                    i.kd_group_segment_bytes == d.spec.static_lds &&
+                    i.md_group_segment_bytes == d.spec.static_lds &&
+                    i.kd_private_segment_bytes == kPrivateSegment &&
+                    i.md_private_segment_bytes == kPrivateSegment &&
+                    i.kd_wavefront_size == kWavefront && i.md_wavefront_size == kWavefront &&
+                    i.md_max_flat_workgroup_size == kWorkgroup[0];
+  });
+  return cache[slot];
+}
+
+// One receipt check, by the reference's field name, as this library's
+// artifact answers it.
+bool receipt_check(const ProtectedDef& d, const ProtectedArtifact& a, const char* field) {
+  const Fe2o3ProtectedArtifactV1& v = a.view;
+  const Fe2o3Slice1InspectionV1& i = v.inspection;
+  const bool bytes_recorded = std::memcmp(v.artifact_identity, v.build_digest, 32) == 0;
+  const bool closure = a.facts_agree && i.sgpr_spills == 0 && i.vgpr_spills == 0 &&
+                       i.uses_dynamic_stack == 0;
+  auto is = [&](const char* f) { return std::strcmp(field, f) == 0; };
+  if (is("identity")) return nonzero32(v.identity);
+  if (is("admission identity")) return nonzero32(v.profile_identity);
+  if (is("artifact identity")) return nonzero32(v.artifact_identity);
+  if (is("finalized output")) return d.spec.code_len != 0;
+  if (is("raw worker output")) return nonzero32(v.build_digest);
+  if (is("target")) return std::strcmp(i.target, kTarget) == 0;
+  if (is("code-object version")) return i.code_object_version == kCodeObjectVersion;
+  if (is("frontend authority commitment") || is("canonical digest"))
+    return nonzero32(v.source_digest);
+  if (is("OCML provider commitment")) return nonzero32(v.compiler_identity);
+  if (is("finalization") || is("source/KIR/compiler profile")) return a.facts_agree;
+  if (is("compiler handoff") || is("upstream LLVM/LLD exchange")) return bytes_recorded;
+  if (is("machine identity")) return (i.e_flags & fe2o3_inspect::kMachMask) == fe2o3_inspect::kMachGfx950;
+  if (is("OCML provider closure")) return closure;
+  if (is("row width")) return d.shape[0] == 64;
+  if (is("grid")) return a.facts_agree;  // one workgroup: the profile's launch
+  if (is("workgroup")) return i.md_max_flat_workgroup_size == kWorkgroup[0];
+  if (is("explicit ABI")) return i.explicit_bytes == d.spec.explicit_bytes;
+  if (is("complete ABI")) return i.md_kernarg_bytes == d.spec.complete_bytes;
+  return false;
+}
+
+void protected_canonical_facts(const ProtectedDef& d, Fe2o3ProtectedJoinFactsV1* f) {
+  const ProtectedArtifact& a = protected_artifact(d);
+  std::memset(f, 0, sizeof(*f));
+  f->profile = d.spec.profile;
+  for (uint32_t r = 0; r < count_fields(d.receipt_fields); ++r)
+    f->receipt[r] = receipt_check(d, a, d.receipt_fields[r]) ? 1 : 0;
+  std::strncpy(f->host_target, kTarget, sizeof(f->host_target) - 1);
+  std::memcpy(f->host_shape, d.shape, sizeof(f->host_shape));
+  f->host_argument_elements = d.elements[0];
+  for (int i = 0; i < 3; ++i) {
+    f->host_grid[i] = kGrid[i];
+    f->host_workgroup[i] = kWorkgroup[i];
+  }
+  f->host_code_object_version = kCodeObjectVersion;
+  f->host_explicit_kernarg = d.spec.explicit_bytes;
+  f->host_complete_kernarg = d.spec.complete_bytes;
+  f->host_kernarg_alignment = kContractKernargAlign;
+  f->host_policy = 1;
+}
+
+// validate_join: the receipt fields, then the host fields, in the
+// reference's order; the first that does not hold.
+int32_t protected_validate_join(const ProtectedDef& d, const Fe2o3ProtectedJoinFactsV1& f,
+                                Fe2o3Slice1ErrorV1* err) {
+  for (uint32_t r = 0; r < count_fields(d.receipt_fields); ++r)
+    if (!f.receipt[r])
+      return set_error(err, FE2O3_SLICE1_E_RECEIPT_FIELD, d.receipt_fields[r]), FE2O3_ERR_JOIN;
+  for (uint32_t h = 0; h < count_fields(d.host_fields); ++h) {
+    const char* field = d.host_fields[h];
+    auto is = [&](const char* x) { return std::strcmp(field, x) == 0; };
+    bool ok = false;
+    if (is("target"))
+      ok = std::strncmp(f.host_target, kTarget, sizeof(f.host_target)) == 0;
+    else if (is("shape") || is("row width") || is("T/E/K/C profile"))
+      ok = std::memcmp(f.host_shape, d.shape, sizeof(f.host_shape)) == 0;
+    else if (is("argument extent"))
+      ok = f.host_argument_elements == d.elements[0];
+    else if (is("grid"))
+      ok = f.host_grid[0] == kGrid[0] && f.host_grid[1] == kGrid[1] && f.host_grid[2] == kGrid[2];
+    else if (is("workgroup"))
+      ok = f.host_workgroup[0] == kWorkgroup[0] && f.host_workgroup[1] == kWorkgroup[1] &&
+           f.host_workgroup[2] == kWorkgroup[2];
+    else if (is("code-object version"))
+      ok = f.host_code_object_version == kCodeObjectVersion;
+    else if (is("explicit ABI"))
+      ok = f.host_explicit_kernarg == d.spec.explicit_bytes;
+    else if (is("complete ABI"))
+      ok = f.host_complete_kernarg == d.spec.complete_bytes;
+    else if (is("ABI alignment"))
+      ok = f.host_kernarg_alignment == kContractKernargAlign;
+    else
+      ok = f.host_policy == 1;  // the profile's policy field
+    if (!ok) return set_error(err, FE2O3_SLICE1_E_HOST_FIELD, field), FE2O3_ERR_JOIN;
+  }
   set_error(err, FE2O3_SLICE1_E_NONE);
   return FE2O3_OK;
 }
@@ -789,6 +1097,8 @@ struct HipExecutable {
   hipModule_t module;
   hipStream_t stream;
   uint8_t identity[16];
+  // the code object's one kernel, as its own metadata names it
+  char kernel[64], descriptor[64];
   Fe2o3Slice1InspectionV1 inspection;
 };
 struct HipKernel {
@@ -868,8 +1178,10 @@ int32_t hip_load_executable(void* self, const uint8_t* bytes, uint64_t byte_len,
   if (!a->observed) return FE2O3_ERR_DEVICE;
   std::unique_ptr<HipExecutable> e(new HipExecutable{});
   e->magic = kHipExeMagic;
-  const char* bad = fe2o3_inspect::inspect_code_object(bytes, byte_len, kKernelSymbol,
-                                                       kDescriptorSymbol, &e->inspection);
+  // the object is read (bounds-checked) before the runtime sees it: one
+  // kernel, its descriptor and metadata readable
+  const char* bad = fe2o3_inspect::inspect_single_kernel(
+      bytes, byte_len, e->kernel, e->descriptor, sizeof(e->kernel), &e->inspection);
   if (bad[0]) return FE2O3_ERR_SHAPE;
   DeviceScope scope(a->device);
   if (!scope.ok()) return FE2O3_ERR_DEVICE;
@@ -898,6 +1210,7 @@ int32_t hip_resolve_kernel(void* self, uint64_t executable, const char* symbol, 
   if (!e) return FE2O3_ERR_NULL;
   DeviceScope scope(a->device);
   if (!scope.ok()) return FE2O3_ERR_DEVICE;
+  if (symbol == nullptr || std::strcmp(symbol, e->kernel) != 0) return (int32_t)hipErrorNotFound;
   std::unique_ptr<HipKernel> k(new HipKernel{});
   k->magic = kHipKernelMagic;
   k->exe = e;
@@ -1143,6 +1456,18 @@ int32_t fe2o3_lds_gemm_slice1_load_v1(Fe2o3Slice1Lifecycle* lc,
                                       Fe2o3Slice1ErrorV1* error) {
   FE2O3_ENTRY("fe2o3_lds_gemm_slice1_load_v1");
   if (!lc || !adapter) return FE2O3_ERR_NULL;
+  if (lc->spec != &kSlice1Spec) return state_error(error, lc->state);
+  return lifecycle_load(lc, adapter, error);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The JOINED -> LOADED transition of any handle (load_after_context_match
+// after the context check).
+int32_t lifecycle_load(Fe2o3Slice1Lifecycle* lc, const Fe2o3Slice1AdapterV1* adapter,
+                       Fe2o3Slice1ErrorV1* error) {
   if (lc->state != FE2O3_SLICE1_JOINED) return state_error(error, lc->state);
   lc->adapter = *adapter;
   lc->has_adapter = true;
@@ -1154,35 +1479,7 @@ int32_t fe2o3_lds_gemm_slice1_load_v1(Fe2o3Slice1Lifecycle* lc,
   return do_load(lc, error);
 }
 
-int32_t fe2o3_lds_gemm_slice1_dispatch_and_wait_v1(Fe2o3Slice1Lifecycle* lc,
-                                                   Fe2o3Slice1ErrorV1* error) {
-  FE2O3_ENTRY("fe2o3_lds_gemm_slice1_dispatch_and_wait_v1");
-  if (!lc) return FE2O3_ERR_NULL;
-  if (lc->state != FE2O3_SLICE1_LOADED) return state_error(error, lc->state);
-  return do_dispatch(lc, error);
-}
-
-int32_t fe2o3_lds_gemm_slice1_unload_v1(Fe2o3Slice1Lifecycle* lc, Fe2o3Slice1ReceiptV1* receipt) {
-  if (!lc || !receipt) return FE2O3_ERR_NULL;
-  if (lc->state != FE2O3_SLICE1_COMPLETED) return FE2O3_ERR_STATE;
-  const Fe2o3Slice1UnloadV1 u = terminal_unload(lc);
-  const Artifact& a = artifact();
-  std::memset(receipt, 0, sizeof(*receipt));
-  std::memcpy(receipt->finalizer_identity, a.view.finalizer_identity, 32);
-  std::memcpy(receipt->import_identity, a.view.import_identity, 32);
-  std::memcpy(receipt->profile_identity, a.view.profile_identity, 32);
-  std::memcpy(receipt->executable_object, lc->load.executable_object, 16);
-  std::memcpy(receipt->kernel_object, lc->resolution.kernel_object, 16);
-  std::memcpy(receipt->dispatch_identity, lc->dispatch_identity, 16);
-  unload_identity(u, lc->environment.runtime_instance, lc->environment.agent_handle,
-                  receipt->unload_identity);
-  drop_adapter(lc);
-  delete lc;
-  return FE2O3_OK;
-}
-
-void fe2o3_lds_gemm_slice1_release_v1(Fe2o3Slice1Lifecycle* lc) {
-  if (!lc) return;
+void lifecycle_release(Fe2o3Slice1Lifecycle* lc) {
   drop_kernel(lc);
   if (lc->has_executable) terminal_unload(lc);
   release_leases(lc);
@@ -1190,9 +1487,7 @@ void fe2o3_lds_gemm_slice1_release_v1(Fe2o3Slice1Lifecycle* lc) {
   delete lc;
 }
 
-int32_t fe2o3_lds_gemm_slice1_observe_v1(const Fe2o3Slice1Lifecycle* lc,
-                                         Fe2o3Slice1ObservationV1* out) {
-  if (!lc || !out) return FE2O3_ERR_NULL;
+void lifecycle_observe(const Fe2o3Slice1Lifecycle* lc, Fe2o3Slice1ObservationV1* out) {
   std::memset(out, 0, sizeof(*out));
   out->state = lc->state;
   out->leases_retained = lc->leases;
@@ -1204,6 +1499,193 @@ int32_t fe2o3_lds_gemm_slice1_observe_v1(const Fe2o3Slice1Lifecycle* lc,
   out->resources = lc->resources;
   std::memcpy(out->dispatch_identity, lc->dispatch_identity, 16);
   out->last_error = lc->last_error;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fe2o3_lds_gemm_slice1_dispatch_and_wait_v1(Fe2o3Slice1Lifecycle* lc,
+                                                   Fe2o3Slice1ErrorV1* error) {
+  FE2O3_ENTRY("fe2o3_lds_gemm_slice1_dispatch_and_wait_v1");
+  if (!lc) return FE2O3_ERR_NULL;
+  if (lc->spec != &kSlice1Spec || lc->state != FE2O3_SLICE1_LOADED)
+    return state_error(error, lc->state);
+  return do_dispatch(lc, error);
+}
+
+int32_t fe2o3_lds_gemm_slice1_unload_v1(Fe2o3Slice1Lifecycle* lc, Fe2o3Slice1ReceiptV1* receipt) {
+  if (!lc || !receipt) return FE2O3_ERR_NULL;
+  if (lc->spec != &kSlice1Spec || lc->state != FE2O3_SLICE1_COMPLETED) return FE2O3_ERR_STATE;
+  const Fe2o3Slice1UnloadV1 u = terminal_unload(lc);
+  const Artifact& a = artifact();
+  std::memset(receipt, 0, sizeof(*receipt));
+  std::memcpy(receipt->finalizer_identity, a.view.finalizer_identity, 32);
+  std::memcpy(receipt->import_identity, a.view.import_identity, 32);
+  std::memcpy(receipt->profile_identity, a.view.profile_identity, 32);
+  std::memcpy(receipt->executable_object, lc->load.executable_object, 16);
+  std::memcpy(receipt->kernel_object, lc->resolution.kernel_object, 16);
+  std::memcpy(receipt->dispatch_identity, lc->dispatch_identity, 16);
+  unload_identity(lc->spec->unload_domain, u, lc->environment.runtime_instance,
+                  lc->environment.agent_handle, receipt->unload_identity);
+  drop_adapter(lc);
+  delete lc;
+  return FE2O3_OK;
+}
+
+void fe2o3_lds_gemm_slice1_release_v1(Fe2o3Slice1Lifecycle* lc) {
+  if (!lc) return;
+  lifecycle_release(lc);
+}
+
+int32_t fe2o3_lds_gemm_slice1_observe_v1(const Fe2o3Slice1Lifecycle* lc,
+                                         Fe2o3Slice1ObservationV1* out) {
+  if (!lc || !out) return FE2O3_ERR_NULL;
+  lifecycle_observe(lc, out);
+  return FE2O3_OK;
+}
+
+// ---- protected profiles -----------------------------------------------------------------
+
+int32_t fe2o3_protected_profile_v1(uint32_t profile, Fe2o3ProtectedProfileV1* out) {
+  if (!out) return FE2O3_ERR_NULL;
+  const ProtectedDef* d = protected_def(profile);
+  if (!d) return FE2O3_ERR_SHAPE;
+  *out = profile_view(*d);
+  return FE2O3_OK;
+}
+
+int32_t fe2o3_protected_artifact_v1(uint32_t profile, Fe2o3ProtectedArtifactV1* out) {
+  if (!out) return FE2O3_ERR_NULL;
+  const ProtectedDef* d = protected_def(profile);
+  if (!d) return FE2O3_ERR_SHAPE;
+  *out = protected_artifact(*d).view;
+  return FE2O3_OK;
+}
+
+int32_t fe2o3_protected_join_facts_v1(uint32_t profile, Fe2o3ProtectedJoinFactsV1* out) {
+  if (!out) return FE2O3_ERR_NULL;
+  const ProtectedDef* d = protected_def(profile);
+  if (!d) return FE2O3_ERR_SHAPE;
+  protected_canonical_facts(*d, out);
+  return FE2O3_OK;
+}
+
+int32_t fe2o3_protected_validate_join_v1(const Fe2o3ProtectedJoinFactsV1* facts,
+                                         Fe2o3Slice1ErrorV1* error) {
+  if (!facts) return FE2O3_ERR_NULL;
+  const ProtectedDef* d = protected_def(facts->profile);
+  if (!d) return FE2O3_ERR_SHAPE;
+  return protected_validate_join(*d, *facts, error);
+}
+
+int32_t fe2o3_protected_join_v1(uint32_t profile, const Fe2o3ProtectedRegionV1* regions,
+                                uint32_t count, int32_t device, void (*release)(void*),
+                                void* user, Fe2o3ProtectedLifecycleV1** out,
+                                Fe2o3Slice1ErrorV1* error) {
+  FE2O3_ENTRY("fe2o3_protected_join_v1");
+  if (!out) return FE2O3_ERR_NULL;
+  *out = nullptr;
+  auto refuse = [&](int32_t status) {
+    if (release) release(user);
+    return status;
+  };
+  const ProtectedDef* d = protected_def(profile);
+  if (!d) return set_error(error, FE2O3_SLICE1_E_HOST_FIELD, "profile"), refuse(FE2O3_ERR_JOIN);
+  if (!regions || count != d->regions)
+    return set_error(error, FE2O3_SLICE1_E_HOST_LENGTH, "regions", -1, 0, d->regions, count),
+           refuse(FE2O3_ERR_JOIN);
+  // prepare_regions: each region in role order, then the pairs
+  uint64_t start[kMaxRegions], end[kMaxRegions];
+  for (uint32_t i = 0; i < count; ++i) {
+    const uint64_t eb = d->element_bytes[i];
+    if (regions[i].elements != d->elements[i])
+      return set_error(error, FE2O3_SLICE1_E_HOST_LENGTH, "", (int32_t)i, 0, d->elements[i],
+                       regions[i].elements),
+             refuse(FE2O3_ERR_JOIN);
+    if (!regions[i].address)
+      return set_error(error, FE2O3_SLICE1_E_HOST_NULL, "", (int32_t)i), refuse(FE2O3_ERR_JOIN);
+    const uint64_t addr = (uint64_t)(uintptr_t)regions[i].address;
+    if (addr % eb != 0)
+      return set_error(error, FE2O3_SLICE1_E_HOST_ALIGNMENT, "", (int32_t)i, 0, eb, addr % eb),
+             refuse(FE2O3_ERR_JOIN);
+    const uint64_t bytes = d->elements[i] * eb;
+    if (addr > UINT64_MAX - bytes)
+      return set_error(error, FE2O3_SLICE1_E_HOST_ADDRESS_OVERFLOW, "", (int32_t)i),
+             refuse(FE2O3_ERR_JOIN);
+    start[i] = addr;
+    end[i] = addr + bytes;
+  }
+  // a written region overlaps no other; read-only inputs may alias
+  for (uint32_t l = 0; l < count; ++l)
+    for (uint32_t r = l + 1; r < count; ++r)
+      if ((d->writes[l] || d->writes[r]) && start[l] < end[r] && start[r] < end[l])
+        return set_error(error, FE2O3_SLICE1_E_HOST_OUTPUT_OVERLAP, "", (int32_t)l, 0, 0, r),
+               refuse(FE2O3_ERR_JOIN);
+  Fe2o3ProtectedJoinFactsV1 facts;
+  protected_canonical_facts(*d, &facts);
+  const int32_t rc = protected_validate_join(*d, facts, error);
+  if (rc != FE2O3_OK) return refuse(rc);
+  auto* lc = new (std::nothrow) Fe2o3Slice1Lifecycle();
+  if (!lc) return refuse((int32_t)hipErrorOutOfMemory);
+  lc->spec = &d->spec;
+  lc->device = device;
+  lc->release_leases = release;
+  lc->user = user;
+  for (uint32_t i = 0; i < count; ++i) {
+    put_le64(lc->kernarg + 16 * i, start[i]);
+    put_le64(lc->kernarg + 16 * i + 8, d->elements[i]);
+  }
+  *out = lc;
+  set_error(error, FE2O3_SLICE1_E_NONE);
+  return FE2O3_OK;
+}
+
+int32_t fe2o3_protected_load_v1(Fe2o3ProtectedLifecycleV1* lc,
+                                const Fe2o3Slice1AdapterV1* adapter, Fe2o3Slice1ErrorV1* error) {
+  FE2O3_ENTRY("fe2o3_protected_load_v1");
+  if (!lc || !adapter) return FE2O3_ERR_NULL;
+  if (lc->spec == &kSlice1Spec) return state_error(error, lc->state);
+  return lifecycle_load(lc, adapter, error);
+}
+
+int32_t fe2o3_protected_dispatch_and_wait_v1(Fe2o3ProtectedLifecycleV1* lc,
+                                             Fe2o3Slice1ErrorV1* error) {
+  FE2O3_ENTRY("fe2o3_protected_dispatch_and_wait_v1");
+  if (!lc) return FE2O3_ERR_NULL;
+  if (lc->spec == &kSlice1Spec || lc->state != FE2O3_SLICE1_LOADED)
+    return state_error(error, lc->state);
+  return do_dispatch(lc, error);
+}
+
+int32_t fe2o3_protected_unload_v1(Fe2o3ProtectedLifecycleV1* lc, Fe2o3ProtectedReceiptV1* receipt) {
+  if (!lc || !receipt) return FE2O3_ERR_NULL;
+  if (lc->spec == &kSlice1Spec || lc->state != FE2O3_SLICE1_COMPLETED) return FE2O3_ERR_STATE;
+  const Fe2o3Slice1UnloadV1 u = terminal_unload(lc);
+  const ProtectedDef* d = protected_def(lc->spec->profile);
+  const ProtectedArtifact& a = protected_artifact(*d);
+  std::memset(receipt, 0, sizeof(*receipt));
+  std::memcpy(receipt->identity, a.view.identity, 32);
+  std::memcpy(receipt->artifact_identity, a.view.artifact_identity, 32);
+  std::memcpy(receipt->executable_object, lc->load.executable_object, 16);
+  std::memcpy(receipt->kernel_object, lc->resolution.kernel_object, 16);
+  std::memcpy(receipt->dispatch_identity, lc->dispatch_identity, 16);
+  unload_identity(lc->spec->unload_domain, u, lc->environment.runtime_instance,
+                  lc->environment.agent_handle, receipt->unload_identity);
+  drop_adapter(lc);
+  delete lc;
+  return FE2O3_OK;
+}
+
+void fe2o3_protected_release_v1(Fe2o3ProtectedLifecycleV1* lc) {
+  if (!lc) return;
+  lifecycle_release(lc);
+}
+
+int32_t fe2o3_protected_observe_v1(const Fe2o3ProtectedLifecycleV1* lc,
+                                   Fe2o3Slice1ObservationV1* out) {
+  if (!lc || !out) return FE2O3_ERR_NULL;
+  lifecycle_observe(lc, out);
   return FE2O3_OK;
 }
 

@@ -22,6 +22,7 @@
 // Reductions are wave-wide butterflies.
 #include "common.hpp"
 #include "internal.hpp"
+#include "profiles.hpp"
 
 namespace {
 
@@ -98,28 +99,8 @@ __global__ void __launch_bounds__(256) softmax_strided_kernel(const float* __res
                                                               uint32_t* __restrict__ status) {
   const uint64_t row = (uint64_t)blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const uint32_t lane = threadIdx.x & 63u;
-  const float* x = in + row * cols;
-  const uint8_t* m = mask ? mask + row * cols : nullptr;
-  float* y = out + row * cols;
-  float mx = -INFINITY, probe = 0.0f;
-  for (uint64_t c = lane; c < cols; c += 64) {
-    probe = finite_probe(probe, x[c]);
-    if (!m || m[c]) mx = fmaxf(mx, x[c]);
-  }
-  if (__ballot(probe != probe) != 0ull) {
-    if (lane == 0) mark_nonfinite(status);
-    for (uint64_t c = lane; c < cols; c += 64) y[c] = quiet_nan();
-    return;
-  }
-  mx = wave_max(mx);
-  float sum = 0.0f;
-  for (uint64_t c = lane; c < cols; c += 64)
-    if (!m || m[c]) sum += expf(x[c] - mx);
-  sum = wave_sum(sum);
-  const bool any = mx != -INFINITY;
-  for (uint64_t c = lane; c < cols; c += 64)
-    y[c] = (any && (!m || m[c])) ? expf(x[c] - mx) / sum : 0.0f;
+  fe2o3_profiles::softmax_row(in + row * cols, out + row * cols,
+                              mask ? mask + row * cols : nullptr, cols, status);
 }
 
 template <int NV>

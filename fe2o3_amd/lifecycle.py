@@ -36,7 +36,7 @@ KINDS = {
     24: "LoadObservation", 25: "KernelAdapter", 26: "KernelObservation",
     27: "ResourceAdapter", 28: "ResourceObservation",
     40: "ImplicitAdapter", 41: "ImplicitObservation", 42: "ExplicitKernargMutation",
-    43: "DispatchAdapter", 44: "DispatchObservation",
+    43: "DispatchAdapter", 44: "DispatchObservation", 14: "ReceiptField",
 }
 
 
@@ -195,23 +195,29 @@ class RuntimeAdapter:
 
 class _Handle:
     """Owner of one C lifecycle handle and of everything its callbacks need
-    kept alive (the lease-release thunk, a Python adapter)."""
+    kept alive (the lease-release thunk, a Python adapter).  `prefix` names
+    the entry-point family that drives it."""
 
-    def __init__(self, ptr: int, release_thunk, device: int):
+    def __init__(self, ptr: int, release_thunk, device: int,
+                 prefix: str = "fe2o3_lds_gemm_slice1"):
         self.ptr = ptr
         self.release_thunk = release_thunk
         self.device = device
         self.adapter = None
+        self.prefix = prefix
+
+    def fn(self, name: str):
+        return getattr(_lib.lib(), f"{self.prefix}_{name}")
 
     def observe(self) -> _lib.Fe2o3Slice1ObservationV1:
         out = _lib.Fe2o3Slice1ObservationV1()
-        _check(_lib.lib().fe2o3_lds_gemm_slice1_observe_v1(self.ptr, C.byref(out)), "observe")
+        _check(self.fn("observe_v1")(self.ptr, C.byref(out)), "observe")
         return out
 
     def release(self) -> None:
         if self.ptr:
             ptr, self.ptr = self.ptr, None
-            _lib.lib().fe2o3_lds_gemm_slice1_release_v1(ptr)
+            self.fn("release_v1")(ptr)
 
 
 class _Linear:
@@ -333,3 +339,159 @@ def join_exact_lds_gemm_slice1_v1(a, b, c, device: int = 0,
     if rc:
         _raise(rc, err, "join")
     return JoinedExactLdsGemmSlice1V1(_Handle(out.value, thunk, device))
+
+
+# ---- protected profile lifecycles -------------------------------------------------------
+#
+# crates/fe2o3-host/src/flash_attention_v1_lifecycle.rs,
+# protected_row_softmax_v1_lifecycle.rs and moe_top2_v1_lifecycle.rs over
+# the fe2o3_protected_* entry points: the same linear join -> load ->
+# dispatch_and_wait -> unload, each profile over its own embedded code
+# object.
+
+FLASH_ATTENTION_V1, ROW_SOFTMAX_V1, MOE_TOP2_V1 = 1, 2, 3
+
+
+def protected_profile(profile: int) -> _lib.Fe2o3ProtectedProfileV1:
+    out = _lib.Fe2o3ProtectedProfileV1()
+    _check(_lib.lib().fe2o3_protected_profile_v1(profile, C.byref(out)), "protected profile")
+    return out
+
+
+def protected_artifact(profile: int) -> _lib.Fe2o3ProtectedArtifactV1:
+    out = _lib.Fe2o3ProtectedArtifactV1()
+    _check(_lib.lib().fe2o3_protected_artifact_v1(profile, C.byref(out)), "protected artifact")
+    return out
+
+
+def protected_join_facts(profile: int) -> _lib.Fe2o3ProtectedJoinFactsV1:
+    out = _lib.Fe2o3ProtectedJoinFactsV1()
+    _check(_lib.lib().fe2o3_protected_join_facts_v1(profile, C.byref(out)), "join facts")
+    return out
+
+
+def protected_validate_join(facts: _lib.Fe2o3ProtectedJoinFactsV1) -> None:
+    err = _lib.Fe2o3Slice1ErrorV1()
+    rc = _lib.lib().fe2o3_protected_validate_join_v1(C.byref(facts), C.byref(err))
+    if rc:
+        _raise(rc, err, "validate_join")
+
+
+class JoinedProtectedV1(_Linear):
+    def __init__(self, handle: _Handle, profile: int):
+        super().__init__(handle)
+        self.profile = profile
+        a = protected_artifact(profile)
+        self.identity = bytes(a.identity)
+        self.artifact_identity = bytes(a.artifact_identity)
+
+    def load(self, adapter: RuntimeAdapter | None = None) -> "LoadedProtectedV1":
+        h = self._take()
+        if adapter is None:
+            table = _lib.Fe2o3Slice1AdapterV1()
+            rc = _lib.lib().fe2o3_lds_gemm_slice1_hip_adapter_v1(h.device, C.byref(table))
+            if rc:
+                h.release()
+                raise Fe2o3Error(rc, "HIP adapter")
+        else:
+            table = adapter.table()
+            h.adapter = adapter
+        err = _lib.Fe2o3Slice1ErrorV1()
+        rc = _lib.lib().fe2o3_protected_load_v1(h.ptr, C.byref(table), C.byref(err))
+        if rc:
+            h.release()
+            _raise(rc, err, "load")
+        return LoadedProtectedV1(h, self.profile)
+
+
+class LoadedProtectedV1(_Linear):
+    def __init__(self, handle: _Handle, profile: int):
+        super().__init__(handle)
+        self.profile = profile
+
+    def dispatch_and_wait(self) -> "CompletedProtectedV1":
+        h = self._take()
+        err = _lib.Fe2o3Slice1ErrorV1()
+        rc = _lib.lib().fe2o3_protected_dispatch_and_wait_v1(h.ptr, C.byref(err))
+        if rc:
+            h.release()
+            _raise(rc, err, "dispatch_and_wait")
+        return CompletedProtectedV1(h, self.profile)
+
+
+class CompletedProtectedV1(_Linear):
+    def __init__(self, handle: _Handle, profile: int):
+        super().__init__(handle)
+        self.profile = profile
+        o = handle.observe()
+        self.executable_object = bytes(o.load.executable_object)
+        self.kernel_object = bytes(o.resolution.kernel_object)
+        self.dispatch_identity = bytes(o.dispatch_identity)
+
+    def unload(self) -> "UnloadedProtectedV1":
+        h = self._take()
+        receipt = _lib.Fe2o3ProtectedReceiptV1()
+        rc = _lib.lib().fe2o3_protected_unload_v1(h.ptr, C.byref(receipt))
+        if rc:
+            h.release()
+            _raise(rc, None, "unload")
+        h.ptr = None  # freed by the unload
+        return UnloadedProtectedV1(self.profile, bytes(receipt.identity),
+                                   bytes(receipt.artifact_identity),
+                                   bytes(receipt.executable_object), bytes(receipt.kernel_object),
+                                   bytes(receipt.dispatch_identity),
+                                   bytes(receipt.unload_identity))
+
+
+@dataclass(frozen=True)
+class UnloadedProtectedV1:
+    """Terminal, inert receipt (e.g. UnloadedFlashAttentionV1,
+    flash_attention_v1_lifecycle.rs:503-556)."""
+
+    profile: int
+    identity: bytes
+    artifact_identity: bytes
+    executable_object: bytes
+    kernel_object: bytes
+    dispatch_identity: bytes
+    unload_identity: bytes
+
+
+def join_protected_v1(profile: int, regions, device: int = 0,
+                      on_release=None) -> JoinedProtectedV1:
+    """Prepares the host request -- `regions` in the profile's role order,
+    each a DeviceBuffer, a numpy array or an (address, elements) pair -- and
+    joins it to the profile's code object.  `on_release()` runs exactly
+    once, when the lifecycle stops referring to the regions."""
+    arr = (_lib.Fe2o3ProtectedRegionV1 * max(1, len(regions)))()
+    for i, r in enumerate(regions):
+        addr, n = _region(r, 4)
+        arr[i] = _lib.Fe2o3ProtectedRegionV1(addr or None, n)
+    thunk = _lib.SLICE1_RELEASE_FN(lambda user: on_release() if on_release else None)
+    out = C.c_void_p()
+    err = _lib.Fe2o3Slice1ErrorV1()
+    rc = _lib.lib().fe2o3_protected_join_v1(profile, arr, len(regions), device, thunk, None,
+                                            C.byref(out), C.byref(err))
+    if rc:
+        _raise(rc, err, "join")
+    return JoinedProtectedV1(_Handle(out.value, thunk, device, "fe2o3_protected"), profile)
+
+
+def join_flash_attention_v1(q, k, v, output, device: int = 0, on_release=None):
+    """flash_attention_v1_lifecycle.rs:228 join_flash_attention_v1: Q, K, V,
+    output (128 f32 each)."""
+    return join_protected_v1(FLASH_ATTENTION_V1, [q, k, v, output], device, on_release)
+
+
+def join_row_softmax_v1(input, output, device: int = 0, on_release=None):
+    """protected_row_softmax_v1_lifecycle.rs: input, output (64 f32 each)."""
+    return join_protected_v1(ROW_SOFTMAX_V1, [input, output], device, on_release)
+
+
+def join_moe_top2_v1(logits, top2_experts, requested_counts, admitted_counts, expert_offsets,
+                     route_slots, permutation, inverse, device: int = 0, on_release=None):
+    """moe_top2_v1_lifecycle.rs: logits (32 f32) and the seven u32 routing
+    outputs (16, 4, 4, 5, 16, 16, 16)."""
+    return join_protected_v1(MOE_TOP2_V1, [logits, top2_experts, requested_counts,
+                                           admitted_counts, expert_offsets, route_slots,
+                                           permutation, inverse], device, on_release)

@@ -618,6 +618,7 @@ enum {
   FE2O3_SLICE1_E_HOST_ALIGNMENT = 11,   /* expected: required bytes               */
   FE2O3_SLICE1_E_HOST_OUTPUT_OVERLAP = 12, /* index: the input C overlaps         */
   FE2O3_SLICE1_E_HOST_ADDRESS_OVERFLOW = 13,
+  FE2O3_SLICE1_E_RECEIPT_FIELD = 14,    /* protected profiles: field names it  */
   FE2O3_SLICE1_E_CONTEXT_IDENTITY = 20,
   FE2O3_SLICE1_E_ENVIRONMENT_ADAPTER = 21,
   FE2O3_SLICE1_E_ENVIRONMENT = 22,
@@ -855,6 +856,139 @@ int32_t fe2o3_lds_gemm_slice1_observe_v1(const Fe2o3Slice1Lifecycle *lifecycle,
                                          Fe2o3Slice1ObservationV1 *out);
 /* SHA-256 (FIPS 180-4), the digest every identity above is built from. */
 int32_t fe2o3_sha256_v1(const void *data, uint64_t len, uint8_t digest[32]);
+
+/* ---- protected profile lifecycles ------------------------------------------------------
+ *
+ * The same one-shot lifecycle for three more exact profiles, each over its
+ * own gfx950 code object (code object v6, xnack-) built from
+ * fe2o3_amd/csrc/codeobj/<name>.hip and embedded in the library:
+ *   FE2O3_PROFILE_FLASH_ATTENTION_V1 (crates/fe2o3-host/src/
+ *     flash_attention_v1_lifecycle.rs): flash_attention_causal_f32_b1_h1_n8_d16_v1,
+ *     regions Q, K, V (read) and output (written), 128 f32 each; 64 explicit
+ *     kernarg bytes, 320 in all.
+ *   FE2O3_PROFILE_ROW_SOFTMAX_V1 (protected_row_softmax_v1_lifecycle.rs):
+ *     row_softmax_v1, regions input (read) and output (written), 64 f32
+ *     each; 32 / 288 bytes.
+ *   FE2O3_PROFILE_MOE_TOP2_V1 (moe_top2_v1_lifecycle.rs):
+ *     moe_top2_route_f32_t8_e4_k2_c4_v1, regions logits (read, 32 f32), then
+ *     top2 (16), requested (4), admitted (4), offsets (5), slots (16),
+ *     permutation (16) and inverse (16) u32 (written); 128 / 384 bytes.
+ * Every profile launches grid [1,1,1] x workgroup [64,1,1] with no LDS and
+ * no private segment, its explicit kernarg one {u64 address, u64 elements}
+ * per region in role order.
+ *
+ * The handle, its states and transitions, the runtime adapter table and its
+ * observations, the error record and the abort on an ambiguous unload are
+ * the LDS GEMM lifecycle's above (an Fe2o3ProtectedLifecycleV1 is that
+ * handle bound to another code object): join -> load -> dispatch_and_wait
+ * -> unload, each failure doing the cleanup its state owes.
+ *
+ * Join runs the reference's order: the host request's regions (each region
+ * in role order: its length, a non-null address, element alignment, no
+ * address overflow; then every pair of regions that includes a written one
+ * must not overlap -- read-only inputs may alias), then validate_join: the
+ * profile's receipt fields (FE2O3_SLICE1_E_RECEIPT_FIELD, field = the
+ * reference's name) and its host fields (FE2O3_SLICE1_E_HOST_FIELD), each
+ * list in the reference's order.  The receipt fields are facts of the
+ * embedded artifact as this library checks them: the identities are
+ * nonzero, the code object's own ELF/descriptor/metadata facts (target, code
+ * object version, kernarg sizes, segment sizes, spill counts) agree with the
+ * profile, and the bytes are the ones the build recorded. */
+#define FE2O3_PROTECTED_MAX_COMPLETE_KERNARG_BYTES 384u
+#define FE2O3_PROTECTED_MAX_REGIONS 8u
+
+enum {
+  FE2O3_PROFILE_FLASH_ATTENTION_V1 = 1,
+  FE2O3_PROFILE_ROW_SOFTMAX_V1 = 2,
+  FE2O3_PROFILE_MOE_TOP2_V1 = 3
+};
+
+typedef struct Fe2o3ProtectedRegionV1 {
+  const void *address;
+  uint64_t elements;
+} Fe2o3ProtectedRegionV1;
+
+/* The profile's fixed facts. */
+typedef struct Fe2o3ProtectedProfileV1 {
+  uint32_t profile;
+  uint32_t code_object_version;
+  char name[32];
+  char target[32];
+  char symbol[64];
+  uint32_t grid[3], workgroup[3];
+  uint32_t dynamic_lds_bytes, static_lds_bytes, private_segment_bytes;
+  uint32_t explicit_kernarg_bytes, complete_kernarg_bytes, kernarg_alignment;
+  uint32_t hsa_kernarg_alignment;
+  uint32_t regions;
+  uint64_t region_elements[FE2O3_PROTECTED_MAX_REGIONS];
+  uint32_t region_element_bytes[FE2O3_PROTECTED_MAX_REGIONS];
+  uint32_t region_writes[FE2O3_PROTECTED_MAX_REGIONS];
+  uint32_t shape[4]; /* flash B, H, N, D; softmax row elements; MoE T, E, K, C */
+  uint32_t receipt_fields, host_fields;
+  char receipt_field[16][40]; /* validate_join's receipt checks, in order */
+  char host_field[16][40];    /* and its host checks */
+} Fe2o3ProtectedProfileV1;
+
+/* The embedded artifact.  artifact_identity: SHA-256 of the code-object
+ * bytes now; build_digest: recorded when the library was built;
+ * source_digest: of the kernel source; compiler_identity: over the compiler
+ * version and flags; profile_identity: over the profile's facts; identity:
+ * the receipt identity over all of these. */
+typedef struct Fe2o3ProtectedArtifactV1 {
+  uint8_t identity[32];
+  uint8_t profile_identity[32];
+  uint8_t artifact_identity[32];
+  uint8_t build_digest[32];
+  uint8_t source_digest[32];
+  uint8_t compiler_identity[32];
+  Fe2o3Slice1InspectionV1 inspection;
+  Fe2o3ProtectedProfileV1 profile;
+} Fe2o3ProtectedArtifactV1;
+
+/* Everything validate_join reconciles: the receipt checks as booleans (in
+ * the profile's receipt_field order) and the host request's fields. */
+typedef struct Fe2o3ProtectedJoinFactsV1 {
+  uint32_t profile;
+  uint8_t receipt[16];
+  char host_target[32];
+  uint32_t host_shape[4];
+  uint64_t host_argument_elements; /* flash: elements per region */
+  uint32_t host_grid[3], host_workgroup[3];
+  uint32_t host_code_object_version;
+  uint32_t host_explicit_kernarg, host_complete_kernarg, host_kernarg_alignment;
+  uint32_t host_policy; /* 1: causal / unmasked all-64 / routing-only, as the profile names */
+} Fe2o3ProtectedJoinFactsV1;
+
+typedef struct Fe2o3ProtectedReceiptV1 {
+  uint8_t identity[32], artifact_identity[32];
+  uint8_t executable_object[16], kernel_object[16], dispatch_identity[16];
+  uint8_t unload_identity[32];
+} Fe2o3ProtectedReceiptV1;
+
+typedef struct Fe2o3Slice1Lifecycle Fe2o3ProtectedLifecycleV1;
+
+int32_t fe2o3_protected_profile_v1(uint32_t profile, Fe2o3ProtectedProfileV1 *out);
+int32_t fe2o3_protected_artifact_v1(uint32_t profile, Fe2o3ProtectedArtifactV1 *out);
+int32_t fe2o3_protected_join_facts_v1(uint32_t profile, Fe2o3ProtectedJoinFactsV1 *out);
+int32_t fe2o3_protected_validate_join_v1(const Fe2o3ProtectedJoinFactsV1 *facts,
+                                         Fe2o3Slice1ErrorV1 *error);
+/* Prepares the host request (`count` regions in role order) and joins it to
+ * the profile's artifact.  `release_leases` and `device`: as for the LDS
+ * GEMM join. */
+int32_t fe2o3_protected_join_v1(uint32_t profile, const Fe2o3ProtectedRegionV1 *regions,
+                                uint32_t count, int32_t device,
+                                void (*release_leases)(void *user), void *user,
+                                Fe2o3ProtectedLifecycleV1 **out, Fe2o3Slice1ErrorV1 *error);
+int32_t fe2o3_protected_load_v1(Fe2o3ProtectedLifecycleV1 *lifecycle,
+                                const Fe2o3Slice1AdapterV1 *adapter, Fe2o3Slice1ErrorV1 *error);
+int32_t fe2o3_protected_dispatch_and_wait_v1(Fe2o3ProtectedLifecycleV1 *lifecycle,
+                                             Fe2o3Slice1ErrorV1 *error);
+/* COMPLETED only: terminal unload, receipt, handle freed. */
+int32_t fe2o3_protected_unload_v1(Fe2o3ProtectedLifecycleV1 *lifecycle,
+                                  Fe2o3ProtectedReceiptV1 *receipt);
+void fe2o3_protected_release_v1(Fe2o3ProtectedLifecycleV1 *lifecycle);
+int32_t fe2o3_protected_observe_v1(const Fe2o3ProtectedLifecycleV1 *lifecycle,
+                                   Fe2o3Slice1ObservationV1 *out);
 
 /* ---- collectives and workgroup synchronization ----------------------------------------- */
 

@@ -35,7 +35,7 @@ static uint64_t rnd() {
 
 static const char* kKernel = "tiled_gemm_lds_v1";
 static const char* kDescriptor = "tiled_gemm_lds_v1.kd";
-static long runs = 0, accepted = 0;
+static long runs = 0, accepted = 0, single_mismatches = 0;
 
 static const char* inspect(const std::vector<uint8_t>& v) {
   // exact-size heap copy: a read at v.size() is a heap overflow
@@ -43,9 +43,22 @@ static const char* inspect(const std::vector<uint8_t>& v) {
   if (!v.empty()) memcpy(p, v.data(), v.size());
   Fe2o3Slice1InspectionV1 out;
   const char* r = fe2o3_inspect::inspect_code_object(p, v.size(), kKernel, kDescriptor, &out);
+  // the single-kernel form (names read from the metadata first) on the same
+  // bytes: where the names it reads are the original ones it accepts exactly
+  // what the named form accepts, with the same facts (a mutation that renames
+  // the kernel is only required not to read out of bounds)
+  char kernel[64], descriptor[64];
+  Fe2o3Slice1InspectionV1 single;
+  const char* rs =
+      fe2o3_inspect::inspect_single_kernel(p, v.size(), kernel, descriptor, 64, &single);
   free(p);
   ++runs;
   if (r[0] == 0) ++accepted;
+  const bool same_names = rs[0] == 0 && strcmp(kernel, kKernel) == 0 &&
+                          strcmp(descriptor, kDescriptor) == 0;
+  if ((r[0] == 0) != same_names ||
+      (same_names && memcmp(&out, &single, sizeof(out)) != 0))
+    ++single_mismatches;
   return r;
 }
 
@@ -185,6 +198,10 @@ int main(int argc, char** argv) {
     const int k = 1 + (int)(rnd() % 8);
     for (int j = 0; j < k; ++j) v[rnd() % v.size()] = (uint8_t)rnd();
     inspect(v);
+  }
+  if (single_mismatches != 0) {
+    printf("FAIL single-kernel form disagrees on %ld objects\n", single_mismatches);
+    ++failures;
   }
   printf("runs %ld accepted %ld failures %d\n", runs, accepted, failures);
   return failures == 0 ? 0 : 1;

@@ -104,10 +104,11 @@ def test_kernel_resource_record_and_registry_without_gpu():
         assert L.fe2o3_kernel_resources(entry.encode(), 10**6, None, ctypes.byref(count)) == -2
         assert count.value == n, entry
     # every declared kernel entry point (not the runtime seam, and not the
-    # code-object lifecycle, whose kernel lives in its own loaded module)
+    # code-object lifecycles, whose kernels live in their own loaded modules)
     # registers a kernel
     kernel_entries = [n for n in _declared()
-                      if not n.startswith(("fe2o3_rt_", "fe2o3Hip", "fe2o3_lds_gemm_slice1_"))
+                      if not n.startswith(("fe2o3_rt_", "fe2o3Hip", "fe2o3_lds_gemm_slice1_",
+                                           "fe2o3_protected_"))
                       and n not in ("fe2o3_status_string", "fe2o3_kernel_resources",
                                     "fe2o3_moe_ffn_workspace_bytes", "fe2o3_sha256_v1")]
     for entry in kernel_entries:
