@@ -10,7 +10,7 @@
 //
 // The GEMM reuses the 256x256 tile machinery of the bf16 GEMM: one LDS stage
 // is 128 bytes of k per row, i.e. 128 fp8 values, and each substep of 64 k
-// issues v_mfma_scale_f32_32x32x64_f8f6f4 (5.0 PFLOP/s dense peak).  Any M
+// issues v_mfma_f32_32x32x64_f8f6f4 (5.0 PFLOP/s dense peak).  Any M
 // and N run on it (edge tiles store only their valid rows and columns);
 // K not a multiple of 128, or unaligned operands, take a bounds-checked
 // 64x64-tile kernel that widens E4M3 to bf16 exactly while staging and
