@@ -9,8 +9,8 @@
 // saturation to +-448.
 //
 // The GEMM reuses the 256x256 tile machinery of the bf16 GEMM: one LDS stage
-// is 128 bytes of k per row, i.e. 128 fp8 values, and each substep of 64 k
-// issues v_mfma_f32_32x32x64_f8f6f4 (5.0 PFLOP/s dense peak).  Any M
+// is 128 bytes of k per row, i.e. 128 fp8 values, each taken by one
+// v_mfma_f32_16x16x128_f8f6f4 (5.0 PFLOP/s dense peak).  Any M
 // and N run on it (edge tiles store only their valid rows and columns);
 // K not a multiple of 128, or unaligned operands, take a bounds-checked
 // 64x64-tile kernel that widens E4M3 to bf16 exactly while staging and
@@ -139,16 +139,16 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
   const auto br = gemm_pipe::dense_rows<kFp8RowBytes, 256, KT>(b16, k16, rows_b, k16);
   // the wave index, read before the K loop: the epilogue needs no thread id
   const uint32_t wave = gemm_pipe::wave_id();
-  gemm_pipe::Acc32 acc;
-  gemm_pipe::mainloop<gemm_pipe::Fp8Mma<kFp8RowBytes>, kFp8RowBytes, kFp8Stages, KT>(
+  gemm_pipe::Acc16 acc;
+  gemm_pipe::mainloop<gemm_pipe::Fp8Mma16<kFp8RowBytes>, kFp8RowBytes, kFp8Stages, KT>(
       ar, br, k16, smem, acc);
   const float sab = scale_a[0] * scale_b[0];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc.v[i][j][e] *= sab;
+      for (int e = 0; e < 4; ++e) acc.v[i][j][e] *= sab;
   uint16_t* c_tile = c + (uint64_t)tm * 256 * n + (uint64_t)tn * 256;
   if constexpr (EDGE)
     gemm_pipe::store_bf16_edge(acc, c_tile, n, rows_a, rows_b, wave);
@@ -158,9 +158,10 @@ __global__ void __launch_bounds__(256, 1) gemm_fp8_kernel(const uint8_t* __restr
     gemm_pipe::store_bf16(acc, c_tile, n, wave);
 }
 
-// The small-grid form: 128 x 128 tiles (Fp8Mma64) for GEMMs whose 256 x 256
-// tiles would leave most CUs idle; three 128-k stages (96 KiB) while the
-// tiles fit one per CU, else two (64 KiB, two workgroups per CU).  Every
+// The small-grid form: 128 x 128 tiles (Fp8Mma16 with 4 x 4 MFMA tiles per
+// wave) for GEMMs whose 256 x 256 tiles would leave most CUs idle; three
+// 128-k stages (96 KiB) while the tiles fit one per CU, else two (64 KiB,
+// two workgroups per CU).  Every
 // output gets the MFMAs of the 256 x 256 tile in the same k order, and the
 // same scaling, so C is bit-identical to it.  WHOLE: M and N multiples of
 // 128 and C 16-byte aligned; otherwise rows past M (N) repeat the last valid
@@ -190,18 +191,18 @@ __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_fp8_128_kernel(
   const uint16_t* b16 = reinterpret_cast<const uint16_t*>(b + (uint64_t)tn * 128 * k);
   const auto ar = gemm_pipe::dense_rows<kFp8RowBytes, 128, KT>(a16, k16, rows_a, k16);
   const auto br = gemm_pipe::dense_rows<kFp8RowBytes, 128, KT>(b16, k16, rows_b, k16);
-  typename gemm_pipe::Fp8Mma64<kFp8RowBytes>::Acc acc;
-  gemm_pipe::mainloop<gemm_pipe::Fp8Mma64<kFp8RowBytes>, kFp8RowBytes, STAGES, KT>(ar, br, k16,
-                                                                                   smem, acc);
+  using Mma = gemm_pipe::Fp8Mma16<kFp8RowBytes, 4, 4>;
+  typename Mma::Acc acc;
+  gemm_pipe::mainloop<Mma, kFp8RowBytes, STAGES, KT>(ar, br, k16, smem, acc);
   const float sab = scale_a[0] * scale_b[0];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc.v[i][j][e] *= sab;
-  gemm_pipe::store_bf16_fp8_128<WHOLE>(acc, c + (uint64_t)tm * 128 * n + (uint64_t)tn * 128, n,
-                                       rows_a, rows_b);
+      for (int e = 0; e < 4; ++e) acc.v[i][j][e] *= sab;
+  gemm_pipe::store_bf16_128<WHOLE>(acc, c + (uint64_t)tm * 128 * n + (uint64_t)tn * 128, n,
+                                   rows_a, rows_b);
 }
 
 // ---- any shape ---------------------------------------------------------------------------

@@ -4,7 +4,7 @@
 // Workgroup: 256 threads = 4 waves in 2x2, each wave a 128x128 block of the
 // output, accumulators in AGPRs.  The instruction is a policy:
 //   Bf16Mma  8x8 tiles of v_mfma_f32_16x16x32_bf16 (inline asm, Acc16)
-//   Fp8Mma   4x4 tiles of v_mfma_f32_32x32x64_f8f6f4 (builtin, Acc32)
+//   Fp8Mma16 8x8 tiles of v_mfma_f32_16x16x128_f8f6f4 (builtin, Acc16)
 // Parameters:
 //   ROW_BYTES  bytes of k per tile row per stage (128: 64 bf16 / 128 fp8)
 //   STAGES     LDS stages in flight (STAGES * 2 * 256 * ROW_BYTES bytes)
@@ -22,8 +22,7 @@
 //   ROW_BYTES  64: swz(r) = ((r >> 1) ^ (r >> 3)) & 3
 // The 128-byte form keeps both operand read patterns free of bank conflicts
 // (measured, SQ_LDS_BANK_CONFLICT = 0): 16 rows x chunks 4s + l/16 (bf16
-// 16x16x32) and 32 rows x chunks 4s + 2(l/32) + h (fp8 32x32x64).  The
-// earlier (r ^ (r >> 3)) & 7 is conflict-free for the second only.
+// 16x16x32) and 16 rows x chunks 2(l/16) + h (fp8 16x16x128).
 //
 // Fragment reads.  The K loop is unrolled over the STAGES buffers, so the
 // stage, tile and row-block offsets of every ds_read are compile-time
@@ -266,11 +265,6 @@ struct Acc16T {  // RB row blocks of 16 x CB column blocks of 16
   f32x4_t v[RB][CB];
 };
 using Acc16 = Acc16T<8>;
-template <int RB, int CB>
-struct Acc32T {  // RB row blocks of 32 x CB column blocks of 32
-  f32x16_t v[RB][CB];
-};
-using Acc32 = Acc32T<4, 4>;
 
 // bf16: v_mfma_f32_16x16x32_bf16, 32 k per substep.  Each wave owns RPW
 // output rows (RPW/16 row blocks) by 128 columns; the A tile holds 2 RPW
@@ -603,138 +597,142 @@ struct Bf16MmaKN64 {
   }
 };
 
-// OCP fp8 e4m3: v_mfma_f32_32x32x64_f8f6f4 with both formats e4m3
-// (cbsz = blgp = 0), 64 k per substep.  It is the scaled builtin with both
-// scale operands 0, for which the compiler selects the unscaled instruction:
-// no v_mfma_ld_scale prefix and no scale register per MFMA (+0.5% at 8192^3,
-// +1.6% at 4096^3 over unit E8M0 scales, 127 = 2^0, with the products
-// bit-identical; tests/test_isa_fp8_mfma.py checks the selection).  Lane l
-// holds k 32(l/32) .. +31 (chunks 4s + 2(l/32) and the next) of row
-// 32i + l%32; one read unit is a fragment's two ds_read_b128.  The builtin
-// keeps the compiler's hazard handling; its accumulators stay in place
-// without help.
-template <int ROW_BYTES>
-struct Fp8Mma {
-  using G = Geo<ROW_BYTES>;
-  using Acc = Acc32;
-  static constexpr int kSubsteps = ROW_BYTES / 64, kMfma = 16, kTn = 4, kReads = 8;
-  static constexpr int kARows = 256;
-  static constexpr bool kBKN = false;
-  static constexpr int kBTileBytes = G::kTileBytes;
-  // late copies over the first 3/4 of substep 0: they land earlier before
-  // the barrier's wait (8192^3: 318 -> 310 us; the bf16 tile is 1% slower
-  // with it, so it keeps the whole substep)
-  static constexpr int kLateSlots = 3 * kMfma / 4;
-  struct Frags {
-    i32x8_t a[4], b[4];
-  };
-  struct Lanes {
-    uint32_t a[kSubsteps][2][2], b[kSubsteps][2][2];  // [substep][row parity][chunk]
-  };
-  static FE2O3_DEVICE Lanes lanes(uint32_t b_region) {
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t wm = wave >> 1, wn = wave & 1u;
-    const uint32_t lr = lane & 31u, g = lane >> 5;
-    Lanes l;
-#pragma unroll
-    for (int s = 0; s < kSubsteps; ++s)
-#pragma unroll
-      for (int p = 0; p < 2; ++p)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint32_t c = 4u * s + 2u * g + h;
-          const uint32_t ra = wm * 128u + p * 32u + lr, rb = wn * 128u + p * 32u + lr;
-          l.a[s][p][h] = (wm * 128u + lr) * ROW_BYTES + ((c ^ G::swz(ra)) << 4);
-          l.b[s][p][h] = b_region + (wn * 128u + lr) * ROW_BYTES + ((c ^ G::swz(rb)) << 4);
-        }
-    return l;
-  }
-  static FE2O3_DEVICE i32x8_t frag(const uint8_t* smem, const uint32_t (&lo_hi)[2],
-                                   uint32_t imm) {
-    const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(smem + lo_hi[0] + imm);
-    const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(smem + lo_hi[1] + imm);
-    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-  }
-  // read unit R of substep S: a0, b0 .. b3, a1 .. a3
-  template <uint32_t A_TILE, uint32_t B_TILE, int S, int R>
-  static FE2O3_DEVICE void read(const uint8_t* smem, const Lanes& l, Frags& f) {
-    static_assert(R >= 0 && R < kReads, "read unit");
-    constexpr uint32_t kRow = 32u * ROW_BYTES;
-    if constexpr (R == 0) {
-      f.a[0] = frag(smem, l.a[S][0], A_TILE);
-    } else if constexpr (R <= 4) {
-      constexpr int j = R - 1;
-      f.b[j] = frag(smem, l.b[S][j & 1], B_TILE + j * kRow);
-    } else {
-      constexpr int i = R - 4;
-      f.a[i] = frag(smem, l.a[S][i & 1], A_TILE + i * kRow);
-    }
-  }
-  template <bool FIRST, int I>
-  static FE2O3_DEVICE void mfma(Acc& acc, const Frags& f) {
-    constexpr int i = I / kTn, j = I % kTn;
-    const f32x16_t c = FIRST ? f32x16_t{} : acc.v[i][j];
-    acc.v[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[j], f.a[i], c, 0, 0, 0,
-                                                                  0, 0, 0);
-  }
-  static FE2O3_DEVICE void finish(Acc&) {}
-};
+// A fragment of an fp8 operand: 32 bytes of one row, two ds_read_b128 at
+// the lane's two chunk offsets plus an immediate.
+FE2O3_DEVICE i32x8_t fp8_frag(const uint8_t* smem, const uint32_t (&lo_hi)[2], uint32_t imm) {
+  const i32x4_t lo = *reinterpret_cast<const i32x4_t*>(smem + lo_hi[0] + imm);
+  const i32x4_t hi = *reinterpret_cast<const i32x4_t*>(smem + lo_hi[1] + imm);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
 
-// OCP fp8 e4m3, 128 x 128 tiles: the small-grid form of Fp8Mma.  Each wave
-// owns 64 rows by 64 columns (2 x 2 MFMA tiles); A and B tiles of 128 rows.
-template <int ROW_BYTES>
-struct Fp8Mma64 {
+// OCP fp8 e4m3: v_mfma_f32_16x16x128_f8f6f4 with both formats e4m3 (cbsz =
+// blgp = 0).  It is the scaled builtin with both scale operands 0, which the
+// compiler lowers to the unscaled instruction (no v_mfma_ld_scale prefix, no
+// scale register; tests/test_isa_fp8_mfma.py checks the selection).  Each
+// wave owns RB x CB tiles of 16 x 16 in the bf16 tile's layout (Acc16T): 8 x
+// 8 for 256 x 256 workgroup tiles, 4 x 4 for the 128 x 128 form.  Lane l
+// holds k 32(l/16) .. +31 (chunks 2(l/16) and the next) of row 16i + l%16.
+//
+// One MFMA consumes a whole 128-k stage, so the two substeps of a stage
+// split the rows instead of k: substep s runs row blocks [s H, (s+1) H),
+// H = RB/2, with the column block outer (MFMA I: j = I / H).  Fragments live
+// in two buffers: X (f[FC] of substep 0) holds a0 .. a(H-1) and every b_j for
+// the whole stage, Y holds a(H) .. a(RB-1).  Each read overwrites a register
+// after the last MFMA that needs its old value:
+//   substep 0: b(CB-1) of this stage into X at slot 0 (first needed at slot
+//     (CB-1) H); a(H) .. a(RB-1) into Y over [M/8, 7M/8);
+//   substep 1, from the barrier (slot M/2, or 0 for 4 x 4): the next
+//     stage's b0 and a0 .. a(H-1) into X, then b1 .. b(CB-2), each at or
+//     after slot (j+1) H, past this substep's last MFMA of column block j.
+// Against 4 x 4 tiles of v_mfma_f32_32x32x64_f8f6f4 (the same MFMA rate and
+// copy plan): +3-4% at 8192^3 and 12288 x 4608 x 8192, +2-7% at 4096^3.
+template <int ROW_BYTES, int RB = 8, int CB = 8>
+struct Fp8Mma16 {
+  static_assert(ROW_BYTES == 128, "one 16x16x128 MFMA per 128-byte row");
+  static_assert(RB % 2 == 0 && CB >= 2, "two row halves, two column blocks");
   using G = Geo<ROW_BYTES>;
-  using Acc = Acc32T<2, 2>;
-  static constexpr int kSubsteps = ROW_BYTES / 64, kMfma = 4, kTn = 2, kReads = 4;
-  static constexpr int kARows = 128;
+  using Acc = Acc16T<RB, CB>;
+  static constexpr bool kRowSplit = true;
+  static constexpr int kH = RB / 2;
+  static constexpr int kSubsteps = 2, kMfma = kH * CB, kTn = CB;
+  static constexpr int kARows = 32 * RB;
   static constexpr bool kBKN = false;
-  static constexpr int kBTileBytes = 128 * ROW_BYTES;
-  static constexpr int kLateSlots = kMfma;
+  static constexpr int kBTileBytes = 32 * CB * ROW_BYTES;
+  // late copies over the first 3/4 of substep 0 for 256 x 256 tiles (as
+  // measured for their 32x32x64 predecessor), the whole substep for 128 x 128
+  static constexpr int kLateSlots = RB == 8 ? 3 * kMfma / 4 : kMfma;
+  // the barrier: halfway through substep 1 for 256 x 256 tiles; at its start
+  // for 128 x 128 tiles, whose eight-MFMA substeps leave half a substep too
+  // short for the next stage's reads (2048^3: 0.94 -> 0.99 of the 32x32x64
+  // form, 2048^2 x 8192: 1.00 -> 1.04)
+  static constexpr int kBarrier = RB == 8 ? kMfma / 2 : 0;
   struct Frags {
-    i32x8_t a[2], b[2];
+    i32x8_t a[RB], b[CB];
   };
   struct Lanes {
-    uint32_t a[kSubsteps][2][2], b[kSubsteps][2][2];  // [substep][row parity][chunk]
+    uint32_t a[2][2], b[2][2];  // [row block parity][chunk]
   };
   static FE2O3_DEVICE Lanes lanes(uint32_t b_region) {
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t wm = wave >> 1, wn = wave & 1u;
-    const uint32_t lr = lane & 31u, g = lane >> 5;
+    const uint32_t lr = lane & 15u, g = lane >> 4;
     Lanes l;
 #pragma unroll
-    for (int s = 0; s < kSubsteps; ++s)
+    for (int p = 0; p < 2; ++p)
 #pragma unroll
-      for (int p = 0; p < 2; ++p)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint32_t c = 4u * s + 2u * g + h;
-          const uint32_t ra = wm * 64u + p * 32u + lr, rb = wn * 64u + p * 32u + lr;
-          l.a[s][p][h] = (wm * 64u + lr) * ROW_BYTES + ((c ^ G::swz(ra)) << 4);
-          l.b[s][p][h] = b_region + (wn * 64u + lr) * ROW_BYTES + ((c ^ G::swz(rb)) << 4);
-        }
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t c = 2u * g + h;
+        const uint32_t ra = wm * 16u * RB + p * 16u + lr, rb = wn * 16u * CB + p * 16u + lr;
+        l.a[p][h] = (wm * 16u * RB + lr) * ROW_BYTES + ((c ^ G::swz(ra)) << 4);
+        l.b[p][h] = b_region + (wn * 16u * CB + lr) * ROW_BYTES + ((c ^ G::swz(rb)) << 4);
+      }
     return l;
   }
-  // read unit R of substep S: a0, b0, b1, a1
-  template <uint32_t A_TILE, uint32_t B_TILE, int S, int R>
-  static FE2O3_DEVICE void read(const uint8_t* smem, const Lanes& l, Frags& f) {
-    static_assert(R >= 0 && R < kReads, "read unit");
-    constexpr uint32_t kRow = 32u * ROW_BYTES;
-    if constexpr (R == 0) {
-      f.a[0] = Fp8Mma<ROW_BYTES>::frag(smem, l.a[S][0], A_TILE);
-    } else if constexpr (R <= 2) {
-      constexpr int j = R - 1;
-      f.b[j] = Fp8Mma<ROW_BYTES>::frag(smem, l.b[S][j], B_TILE + j * kRow);
-    } else {
-      f.a[1] = Fp8Mma<ROW_BYTES>::frag(smem, l.a[S][1], A_TILE + kRow);
+  static constexpr uint32_t kRow = 16u * ROW_BYTES;  // one row block
+  template <uint32_t A_TILE, int I>
+  static FE2O3_DEVICE void read_a(const uint8_t* smem, const Lanes& l, Frags& f) {
+    f.a[I] = fp8_frag(smem, l.a[I & 1], A_TILE + I * kRow);
+  }
+  template <uint32_t B_TILE, int J>
+  static FE2O3_DEVICE void read_b(const uint8_t* smem, const Lanes& l, Frags& f) {
+    f.b[J] = fp8_frag(smem, l.b[J & 1], B_TILE + J * kRow);
+  }
+  // substep 0's reads of a(H + u) and their slots
+  static constexpr int own_slot(int u) { return kMfma / 8 + u * (kMfma - kMfma / 4) / kH; }
+  // substep 1's reads of the next stage: unit 0 is b0, units 1 .. H are
+  // a0 .. a(H-1), unit H + j is b_j (j = 1 .. CB-2), spread from the barrier
+  // on, none before its register's last use
+  static constexpr int kNext = 1 + kH + (CB - 2);
+  static constexpr int next_slot(int u) {
+    const int base = kBarrier + u * (kMfma - kBarrier) / kNext;
+    const int least = u == 0 ? kH : u <= kH ? 0 : (u - kH + 1) * kH;
+    return base > least ? base : least;
+  }
+  static_assert(next_slot(kNext - 1) < kMfma, "every read of the next stage in substep 1");
+  template <uint32_t A_TILE, uint32_t B_TILE, int U>
+  static FE2O3_DEVICE void next_unit(const uint8_t* smem, const Lanes& l, Frags& f) {
+    if constexpr (U == 0) read_b<B_TILE, 0>(smem, l, f);
+    else if constexpr (U <= kH) read_a<A_TILE, U - 1>(smem, l, f);
+    else read_b<B_TILE, U - kH>(smem, l, f);
+  }
+  template <uint32_t A_TILE, uint32_t B_TILE, int I, int U = 0>
+  static FE2O3_DEVICE void next_reads(const uint8_t* smem, const Lanes& l, Frags& f) {
+    if constexpr (U < kNext) {
+      if constexpr (I < 0 || next_slot(U) == I) next_unit<A_TILE, B_TILE, U>(smem, l, f);
+      next_reads<A_TILE, B_TILE, I, U + 1>(smem, l, f);
     }
   }
-  template <bool FIRST, int I>
-  static FE2O3_DEVICE void mfma(Acc& acc, const Frags& f) {
-    constexpr int i = I / kTn, j = I % kTn;
-    const f32x16_t c = FIRST ? f32x16_t{} : acc.v[i][j];
-    acc.v[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[j], f.a[i], c, 0, 0, 0,
-                                                                  0, 0, 0);
+  template <uint32_t A_TILE, int I, int U = 0>
+  static FE2O3_DEVICE void own_reads(const uint8_t* smem, const Lanes& l, Frags& f) {
+    if constexpr (U < kH) {
+      if constexpr (own_slot(U) == I) read_a<A_TILE, kH + U>(smem, l, f);
+      own_reads<A_TILE, I, U + 1>(smem, l, f);
+    }
+  }
+  // what substep 1 of a step -1 would read, from stage 0 into X
+  template <uint32_t A_TILE, uint32_t B_TILE>
+  static FE2O3_DEVICE void prologue_reads(const uint8_t* smem, const Lanes& l, Frags& x) {
+    next_reads<A_TILE, B_TILE, -1>(smem, l, x);
+  }
+  // the reads at slot I of substep S (fc: this substep's buffer, fn: the other)
+  template <uint32_t A_CUR, uint32_t B_CUR, uint32_t A_NXT, uint32_t B_NXT, int S, int I>
+  static FE2O3_DEVICE void reads_at(const uint8_t* smem, const Lanes& l, Frags& fc, Frags& fn) {
+    if constexpr (S == 0) {
+      if constexpr (I == 0) read_b<B_CUR, CB - 1>(smem, l, fc);
+      own_reads<A_CUR, I>(smem, l, fn);
+    } else {
+      next_reads<A_NXT, B_NXT, I>(smem, l, fn);
+    }
+  }
+  // MFMA I of substep S: substep 0 takes A and B from X (fc); substep 1 its
+  // A from Y (fc) and B from X (fn)
+  template <bool FIRST, int S, int I>
+  static FE2O3_DEVICE void mfma2(Acc& acc, const Frags& fc, const Frags& fn) {
+    constexpr int j = I / kH, i = S * kH + I % kH;
+    const f32x4_t c = FIRST ? f32x4_t{} : acc.v[i][j];
+    const i32x8_t& bj = S == 0 ? fc.b[j] : fn.b[j];
+    acc.v[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bj, fc.a[i], c, 0, 0, 0,
+                                                                   0, 0, 0);
   }
   static FE2O3_DEVICE void finish(Acc&) {}
 };
@@ -759,7 +757,9 @@ struct Fp8Mma64 {
 // rather than in the next substep 0 gives them up to two substeps to land,
 // which is what operands streamed from HBM need.  The barrier sits halfway
 // through the last substep, whose fragments are already in registers, so the
-// waves meet with half a substep of MFMAs still to issue.
+// waves meet with half a substep of MFMAs still to issue.  A policy may move
+// it (kBarrier) and place its own fragment reads (Fp8Mma16, whose substeps
+// split rows rather than k).
 
 // item n of N over slots [S0, S1): call fn(n) for the items at slot I
 template <int N, int S0, int S1, int n = 0>
@@ -810,6 +810,22 @@ FE2O3_DEVICE void copy_one(const RA& ar, const RB& br, uint32_t kbytes, uint8_t*
              br.off(j, kbytes), br.soff(kbytes));
 }
 
+// Policies whose substeps split the tile's rows instead of k (Fp8Mma16)
+// place their own fragment reads and see both fragment buffers.
+template <class M, class = void>
+struct RowSplit : std::false_type {};
+// the barrier's slot in the last substep: the policy's kBarrier, else M/2
+template <class M, class = void>
+struct BarrierAt {
+  static constexpr int value = M::kMfma / 2;
+};
+template <class M>
+struct BarrierAt<M, std::void_t<decltype(M::kBarrier)>> {
+  static constexpr int value = M::kBarrier;
+};
+template <class M>
+struct RowSplit<M, std::void_t<decltype(M::kRowSplit)>> : std::bool_constant<M::kRowSplit> {};
+
 // Substep S_ of a K step held in stage buffer P.  FIRST: the K loop's first
 // substep (accumulators written, not added to).  k_next / k_next2: k byte
 // offsets of the stages one and two ahead (clamped to the last stage).
@@ -827,7 +843,7 @@ struct Substep {
   static constexpr int PN = (P + 1) % STAGES;     // buffer of the next step
   static constexpr int PL = (P + STAGES - 1) % STAGES;  // buffer of the late copies' stage
   static constexpr bool LAST = S_ + 1 == S;
-  static constexpr int kBarrierAt = MF / 2;
+  static constexpr int kBarrierAt = BarrierAt<M>::value;
   // late copies: all of substep 0, or its first half when it is also the
   // last substep (every late copy precedes the barrier, every early one
   // follows it, which keeps the wait counts exact)
@@ -852,7 +868,10 @@ struct Substep {
         __builtin_amdgcn_s_waitcnt(waitcnt_imm((STAGES - 2) * NC, 0));
         __builtin_amdgcn_s_barrier();
       }
-      M::template mfma<FIRST && S_ == 0, I>(acc, f[FC]);
+      if constexpr (RowSplit<M>::value)
+        M::template mfma2<FIRST, S_, I>(acc, f[FC], f[FN]);
+      else
+        M::template mfma<FIRST && S_ == 0, I>(acc, f[FC]);
       if constexpr (LAST)  // early copies: stage t+STAGES into buffer P
         Spread<kEarly, kBarrierAt, MF>::template at<I>([&](auto n) {
           copy_one<ROW_BYTES, STAGES, M::kARows, decltype(n)::value>(ar, br, k_next2, smem, wave,
@@ -863,9 +882,12 @@ struct Substep {
           copy_one<ROW_BYTES, STAGES, M::kARows, kEarly + decltype(n)::value>(ar, br, k_next,
                                                                               smem, wave, PL);
         });
-      Spread<M::kReads, kReadFrom, kReadTo>::template at<I>([&](auto n) {
-        M::template read<RA, RB, RS, decltype(n)::value>(smem, ln, f[FN]);
-      });
+      if constexpr (RowSplit<M>::value)
+        M::template reads_at<L::a(P), L::b(P), L::a(PN), L::b(PN), S_, I>(smem, ln, f[FC], f[FN]);
+      else
+        Spread<M::kReads, kReadFrom, kReadTo>::template at<I>([&](auto n) {
+          M::template read<RA, RB, RS, decltype(n)::value>(smem, ln, f[FN]);
+        });
       __builtin_amdgcn_sched_barrier(0);
       slot<I + 1>(ar, br, k_next, k_next2, smem, wave, ln, f, acc);
     }
@@ -950,9 +972,12 @@ FE2O3_DEVICE void mainloop(
   __builtin_amdgcn_s_waitcnt(waitcnt_imm((STAGES - 2) * Sub::NC + Sub::kEarly, 0));
   __builtin_amdgcn_s_barrier();
   typename M::Frags f[2];
-  Spread<M::kReads, 0, 1>::template at<0>([&](auto n) {
-    M::template read<L::a(0), L::b(0), 0, decltype(n)::value>(smem, ln, f[0]);
-  });
+  if constexpr (RowSplit<M>::value)
+    M::template prologue_reads<L::a(0), L::b(0)>(smem, ln, f[0]);
+  else
+    Spread<M::kReads, 0, 1>::template at<0>([&](auto n) {
+      M::template read<L::a(0), L::b(0), 0, decltype(n)::value>(smem, ln, f[0]);
+    });
   // every first fragment landed.  The wait is inline asm between scheduling
   // barriers: a policy's inline-asm reads are invisible to the compiler's
   // wait tracking, which may otherwise move reads past a builtin wait or
@@ -991,19 +1016,16 @@ FE2O3_DEVICE uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadId
 
 // Acc16T (i, j, e): tile row wm*RPW + 16i + lane%16, tile column
 // wn*CPW + 16j + 4(lane/16) + e (CPW = 128, or 64 for Bf16MmaKN64).
-template <int RPW = 128>
-FE2O3_DEVICE uint32_t acc16_row0() { return (wave_id() >> 1) * RPW + (lane_id() & 15u); }
-template <int CPW = 128>  // columns per wave
-FE2O3_DEVICE uint32_t acc16_col0() { return (wave_id() & 1u) * CPW + 4u * (lane_id() >> 4); }
-
-// Acc32T (i, j, e): tile row wm*RPW + 32i + lane%32, tile column
-// wn*RPW + 32j + 8(e/4) + 4(lane/32) + e%4 (RPW = 128, or 64 for Fp8Mma64).
 // (`w`: the wave index, when the caller read it before the K loop, so that
 // the thread id need not stay live across the loop)
 template <int RPW = 128>
-FE2O3_DEVICE uint32_t acc32_row0(uint32_t w) { return (w >> 1) * RPW + (lane_id() & 31u); }
-template <int RPW = 128>
-FE2O3_DEVICE uint32_t acc32_row0() { return acc32_row0<RPW>(wave_id()); }
+FE2O3_DEVICE uint32_t acc16_row0(uint32_t w = wave_id()) {
+  return (w >> 1) * RPW + (lane_id() & 15u);
+}
+template <int CPW = 128>  // columns per wave
+FE2O3_DEVICE uint32_t acc16_col0(uint32_t w = wave_id()) {
+  return (w & 1u) * CPW + 4u * (lane_id() >> 4);
+}
 
 // Acc16 (i, j, e) holds column 16j + 4g + e of the wave's block, g = lane /
 // 16 (the lane's 16-lane row of the wave).  For a pair of column blocks
@@ -1038,10 +1060,11 @@ FE2O3_DEVICE void store_bf16_pairs(const Acc16T<RB, CB>& acc, uint16_t* c_tile, 
     }
 }
 
-FE2O3_DEVICE void store_bf16(const Acc16& acc, uint16_t* c_tile, uint64_t ldc) {
+FE2O3_DEVICE void store_bf16(const Acc16& acc, uint16_t* c_tile, uint64_t ldc,
+                            uint32_t w = wave_id()) {
   const uint32_t g = lane_id() >> 4;
-  const uint32_t col0 = (wave_id() & 1u) * 128u + 16u * (g & 1u) + 8u * (g >> 1);
-  store_bf16_pairs(acc, c_tile, ldc, acc16_row0(), col0);
+  const uint32_t col0 = (w & 1u) * 128u + 16u * (g & 1u) + 8u * (g >> 1);
+  store_bf16_pairs(acc, c_tile, ldc, acc16_row0(w), col0);
 }
 
 // Edge tiles (the last tile row or column of a C whose M or N is not a
@@ -1049,8 +1072,9 @@ FE2O3_DEVICE void store_bf16(const Acc16& acc, uint16_t* c_tile, uint64_t ldc) {
 // written, one 2-byte store per element, so C rows need no alignment.  The
 // values are those store_bf16 writes.
 FE2O3_DEVICE void store_bf16_edge(const Acc16& acc, uint16_t* c_tile, uint64_t ldc,
-                                  uint32_t rows_valid, uint32_t cols_valid) {
-  const uint32_t row0 = acc16_row0(), col0 = acc16_col0();
+                                  uint32_t rows_valid, uint32_t cols_valid,
+                                  uint32_t w = wave_id()) {
+  const uint32_t row0 = acc16_row0(w), col0 = acc16_col0(w);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t r = row0 + 16u * i;
@@ -1095,28 +1119,8 @@ FE2O3_DEVICE void store_bf16_128(const Acc16T<4, 4>& acc, uint16_t* c_tile, uint
   }
 }
 
-FE2O3_DEVICE void store_bf16_edge(const Acc32& acc, uint16_t* c_tile, uint64_t ldc,
-                                  uint32_t rows_valid, uint32_t cols_valid,
-                                  uint32_t w = wave_id()) {
-  const uint32_t row0 = acc32_row0(w);
-  const uint32_t col0 = (w & 1u) * 128u + 4u * (lane_id() >> 5);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t r = row0 + 32u * i;
-    if (r >= rows_valid) continue;
-    uint16_t* out = c_tile + (uint64_t)r * ldc;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const uint32_t c = col0 + 32u * j + 8u * (e / 4) + (e % 4);
-        if (c < cols_valid) out[c] = bf16_bits_from_f32(acc.v[i][j][e]);
-      }
-  }
-}
-
 // Staged stores. Straight from the accumulators, one store instruction writes
-// 32 bytes into each of 16 (Acc16) or 32 (Acc32) rows, parts of cache
+// 32 bytes into each of 16 rows, parts of cache
 // lines. Here each wave first writes its 128x128 block as bf16 into its own
 // 32 KiB of the idle stage buffers (row-major, 256 bytes a row, the 16-byte
 // chunks of row r XOR-permuted by r & 15 so that the 16-byte reads are
@@ -1139,26 +1143,8 @@ FE2O3_DEVICE void stage_bf16(const Acc16& acc, uint8_t* region) {
     }
 }
 
-FE2O3_DEVICE void stage_bf16(const Acc32& acc, uint8_t* region) {
-  const uint32_t l = lane_id(), s = l & 15u;
-  const uint32_t wr = (l & 31u) * 256u + (l >> 5) * 8u;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        u32x2_t packed;
-        packed[0] = pack_bf16x2(acc.v[i][j][4 * q + 0], acc.v[i][j][4 * q + 1]);
-        packed[1] = pack_bf16x2(acc.v[i][j][4 * q + 2], acc.v[i][j][4 * q + 3]);
-        const uint32_t chunk = (4u * j + q) ^ s;
-        *reinterpret_cast<u32x2_t*>(region + 8192u * i + wr + chunk * 16u) = packed;
-      }
-}
-
 // `smem` needs 128 KiB, and the caller's copies must all have landed.
-template <class Acc>
-FE2O3_DEVICE void store_bf16_staged(const Acc& acc, uint8_t* smem, uint16_t* c_tile,
+FE2O3_DEVICE void store_bf16_staged(const Acc16& acc, uint8_t* smem, uint16_t* c_tile,
                                     uint64_t ldc, uint32_t w = wave_id()) {
   const uint32_t l = lane_id();
   uint8_t* region = smem + w * 32768u;
@@ -1173,89 +1159,6 @@ FE2O3_DEVICE void store_bf16_staged(const Acc& acc, uint8_t* smem, uint16_t* c_t
     const u32x4_t v =
         *reinterpret_cast<const u32x4_t*>(region + r * 256u + ((cc ^ (r & 15u)) << 4));
     __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(out + (uint64_t)(4u * p) * ldc));
-  }
-}
-
-// Acc32 (i, j, e) holds columns 32j + 8(e/4) + 4h + e%4 (h = lane/32), so
-// the two lane halves own alternating 4-column pieces.  One v_permlane32_swap
-// of the even-e/4 and odd-e/4 registers gives lanes 0-31 columns 32j + 16p +
-// 0..7 and lanes 32-63 columns 32j + 16p + 8..15: 16 bytes per lane and 32
-// bytes per row per store, twice the run and half the stores of storing the
-// 8-byte pieces in place.
-FE2O3_DEVICE void store_bf16(const Acc32& acc, uint16_t* c_tile, uint64_t ldc,
-                            uint32_t w = wave_id()) {
-  const uint32_t row0 = acc32_row0(w);
-  const uint32_t col0 = (w & 1u) * 128u + 8u * (lane_id() >> 5);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        const int qe = 2 * p, qo = 2 * p + 1;
-        const uint32_t y0 = pack_bf16x2(acc.v[i][j][4 * qe + 0], acc.v[i][j][4 * qe + 1]);
-        const uint32_t y1 = pack_bf16x2(acc.v[i][j][4 * qe + 2], acc.v[i][j][4 * qe + 3]);
-        const uint32_t x0 = pack_bf16x2(acc.v[i][j][4 * qo + 0], acc.v[i][j][4 * qo + 1]);
-        const uint32_t x1 = pack_bf16x2(acc.v[i][j][4 * qo + 2], acc.v[i][j][4 * qo + 3]);
-        const auto s0 = __builtin_amdgcn_permlane32_swap(y0, x0, false, false);
-        const auto s1 = __builtin_amdgcn_permlane32_swap(y1, x1, false, false);
-        u32x4_t packed;
-        packed[0] = s0[0];
-        packed[1] = s1[0];
-        packed[2] = s0[1];
-        packed[3] = s1[1];
-        *reinterpret_cast<u32x4_t*>(c_tile + (uint64_t)(row0 + 32u * i) * ldc + col0 + 32u * j +
-                                    16u * p) = packed;
-      }
-}
-
-
-// A 128 x 128 tile of Acc32T<2, 2> (waves of 64 x 64): whole tiles of a
-// 16-byte aligned C (WHOLE) with store_bf16(Acc32)'s lane-half exchange,
-// 16 bytes per lane; otherwise only rows < rows_valid and columns <
-// cols_valid, one 2-byte store per element.
-template <bool WHOLE>
-FE2O3_DEVICE void store_bf16_fp8_128(const Acc32T<2, 2>& acc, uint16_t* c_tile, uint64_t ldc,
-                                     uint32_t rows_valid, uint32_t cols_valid) {
-  const uint32_t row0 = acc32_row0<64>();
-  if constexpr (WHOLE) {
-    const uint32_t col0 = (wave_id() & 1u) * 64u + 8u * (lane_id() >> 5);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const int qe = 2 * p, qo = 2 * p + 1;
-          const uint32_t y0 = pack_bf16x2(acc.v[i][j][4 * qe + 0], acc.v[i][j][4 * qe + 1]);
-          const uint32_t y1 = pack_bf16x2(acc.v[i][j][4 * qe + 2], acc.v[i][j][4 * qe + 3]);
-          const uint32_t x0 = pack_bf16x2(acc.v[i][j][4 * qo + 0], acc.v[i][j][4 * qo + 1]);
-          const uint32_t x1 = pack_bf16x2(acc.v[i][j][4 * qo + 2], acc.v[i][j][4 * qo + 3]);
-          const auto s0 = __builtin_amdgcn_permlane32_swap(y0, x0, false, false);
-          const auto s1 = __builtin_amdgcn_permlane32_swap(y1, x1, false, false);
-          u32x4_t packed;
-          packed[0] = s0[0];
-          packed[1] = s1[0];
-          packed[2] = s0[1];
-          packed[3] = s1[1];
-          *reinterpret_cast<u32x4_t*>(c_tile + (uint64_t)(row0 + 32u * i) * ldc + col0 +
-                                      32u * j + 16u * p) = packed;
-        }
-  } else {
-    const uint32_t col0 = (wave_id() & 1u) * 64u + 4u * (lane_id() >> 5);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t r = row0 + 32u * i;
-      if (r >= rows_valid) continue;
-      uint16_t* out = c_tile + (uint64_t)r * ldc;
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const uint32_t c = col0 + 32u * j + 8u * (e / 4) + (e % 4);
-          if (c < cols_valid) out[c] = bf16_bits_from_f32(acc.v[i][j][e]);
-        }
-    }
   }
 }
 

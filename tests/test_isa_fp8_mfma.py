@@ -1,9 +1,9 @@
-"""The fp8 GEMM tiles (gemm_pipe::Fp8Mma, Fp8Mma64) call the scaled
-f8f6f4 MFMA builtin with both scale operands 0, for which the compiler
-selects the unscaled v_mfma_f32_32x32x64_f8f6f4: one instruction per MFMA,
-with no v_mfma_ld_scale prefix and no scale register.  This CPU test compiles
-fp8.hip for gfx950 to assembly and checks that every fp8 GEMM kernel issues
-only that instruction.  The products' values are checked on the GPU
+"""The fp8 GEMM tiles (gemm_pipe::Fp8Mma16, both tile forms) call the
+scaled f8f6f4 MFMA builtin with both scale operands 0, for which the
+compiler selects the unscaled v_mfma_f32_16x16x128_f8f6f4: one instruction
+per MFMA, with no v_mfma_ld_scale prefix and no scale register.  This CPU
+test compiles fp8.hip for gfx950 to assembly and checks that every fp8 GEMM
+tile kernel issues only that instruction.  The products' values are checked on the GPU
 (tests/test_gpu_moe_fp8.py) against the oracle."""
 from __future__ import annotations
 
@@ -37,4 +37,4 @@ def test_fp8_gemm_kernels_use_the_unscaled_mfma(tmp_path):
     for name, body in bodies:
         ops = re.findall(r"^\s*(v_mfma\S*)", body, re.M)
         assert ops, name
-        assert set(ops) == {"v_mfma_f32_32x32x64_f8f6f4"}, (name, sorted(set(ops)))
+        assert set(ops) == {"v_mfma_f32_16x16x128_f8f6f4"}, (name, sorted(set(ops)))
