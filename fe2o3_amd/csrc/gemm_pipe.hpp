@@ -621,11 +621,12 @@ FE2O3_DEVICE i32x8_t fp8_frag(const uint8_t* smem, const uint32_t (&lo_hi)[2], u
 // after the last MFMA that needs its old value:
 //   substep 0: b(CB-1) of this stage into X at slot 0 (first needed at slot
 //     (CB-1) H); a(H) .. a(RB-1) into Y over [M/8, 7M/8);
-//   substep 1, from the barrier (slot M/2, or 0 for 4 x 4): the next
+//   substep 1, from the barrier (slot M/4, or 0 for 4 x 4): the next
 //     stage's b0 and a0 .. a(H-1) into X, then b1 .. b(CB-2), each at or
 //     after slot (j+1) H, past this substep's last MFMA of column block j.
-// Against 4 x 4 tiles of v_mfma_f32_32x32x64_f8f6f4 (the same MFMA rate and
-// copy plan): +3-4% at 8192^3 and 12288 x 4608 x 8192, +2-7% at 4096^3.
+// Against 4 x 4 tiles of v_mfma_f32_32x32x64_f8f6f4 with the same copy
+// plan: +2.2% at 8192^3, +1.1% at 12288 x 4608 x 8192; with the barrier
+// and late copies below, +5-6% at 8192^3.
 template <int ROW_BYTES, int RB = 8, int CB = 8>
 struct Fp8Mma16 {
   static_assert(ROW_BYTES == 128, "one 16x16x128 MFMA per 128-byte row");
@@ -638,14 +639,15 @@ struct Fp8Mma16 {
   static constexpr int kARows = 32 * RB;
   static constexpr bool kBKN = false;
   static constexpr int kBTileBytes = 32 * CB * ROW_BYTES;
-  // late copies over the first 3/4 of substep 0 for 256 x 256 tiles (as
-  // measured for their 32x32x64 predecessor), the whole substep for 128 x 128
-  static constexpr int kLateSlots = RB == 8 ? 3 * kMfma / 4 : kMfma;
-  // the barrier: halfway through substep 1 for 256 x 256 tiles; at its start
-  // for 128 x 128 tiles, whose eight-MFMA substeps leave half a substep too
-  // short for the next stage's reads (2048^3: 0.94 -> 0.99 of the 32x32x64
-  // form, 2048^2 x 8192: 1.00 -> 1.04)
-  static constexpr int kBarrier = RB == 8 ? kMfma / 2 : 0;
+  // 256 x 256 tiles: the barrier a quarter of the way through substep 1 and
+  // the late copies over the first half of substep 0 (8192^3: +2.7-3.3% over
+  // halfway and 3/4; an eighth: -1.8%; 3/8: +-0).  128 x 128 tiles: the
+  // barrier at the start of substep 1 and the late copies over all of
+  // substep 0, since their eight-MFMA substeps leave half a substep too short
+  // for the next stage's reads (2048^3: 0.94 -> 0.99 of the 32x32x64 form,
+  // 2048^2 x 8192: 1.00 -> 1.04)
+  static constexpr int kLateSlots = RB == 8 ? kMfma / 2 : kMfma;
+  static constexpr int kBarrier = RB == 8 ? kMfma / 4 : 0;
   struct Frags {
     i32x8_t a[RB], b[CB];
   };
