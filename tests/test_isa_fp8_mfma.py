@@ -3,8 +3,8 @@ scaled f8f6f4 MFMA builtin with both scale operands 0, for which the
 compiler selects the unscaled v_mfma_f32_16x16x128_f8f6f4: one instruction
 per MFMA, with no v_mfma_ld_scale prefix and no scale register.  This CPU
 test compiles fp8.hip for gfx950 to assembly and checks that every fp8 GEMM
-tile kernel issues only that instruction.  The products' values are checked on the GPU
-(tests/test_gpu_moe_fp8.py) against the oracle."""
+tile kernel issues only that instruction.  The products' values are checked
+on the GPU (tests/test_gpu_moe_fp8.py) against the oracle."""
 from __future__ import annotations
 
 import os
