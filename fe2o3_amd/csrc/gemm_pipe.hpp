@@ -18,11 +18,19 @@
 // LDS layout.  The A tiles of all stages come first, then the B tiles (A of
 // stage p at p * T, B at (STAGES + p) * T, T = 256 * ROW_BYTES).  16-byte
 // chunk c of row r is stored at position c ^ swz(r):
-//   ROW_BYTES 128: swz(r) = (r ^ (r >> 2)) & 7
+//   ROW_BYTES 128: swz(r) = (r & 6) | parity(r & 7)
 //   ROW_BYTES  64: swz(r) = ((r >> 1) ^ (r >> 3)) & 3
-// The 128-byte form keeps both operand read patterns free of bank conflicts
-// (measured, SQ_LDS_BANK_CONFLICT = 0): 16 rows x chunks 4s + l/16 (bf16
-// 16x16x32) and 16 rows x chunks 2(l/16) + h (fp8 16x16x128).
+// A ds_read_b128 is served in four passes of 16 lanes, {8k .. 8k+7} and
+// {8k+16 .. 8k+23}, over 64 banks of 4 bytes: a pass is conflict-free when
+// its lanes' 16-byte pieces fall on distinct (row parity, chunk position)
+// pairs.  Both read patterns pair each row with chunks c and c ^ 1 (bf16
+// 16x16x32: 16 rows x chunks 4s + l/16) or c and c ^ 2 (fp8 16x16x128: 16
+// rows x chunks 2(l/16) + h), so among the even (odd) rows of each 8 the
+// swizzle values must differ in bits {1, 2} and in bits {0, 2}: the values
+// of even parity {0, 3, 5, 6} on even rows and {1, 2, 4, 7} on odd rows do.
+// Measured SQ_LDS_BANK_CONFLICT = 0 for both; the earlier (r ^ (r >> 2)) & 7
+// gave the fp8 pattern 2-way conflicts (3.4e7 cycles per 8192^3 GEMM, LDS
+// busy twice as long, at the same throughput).
 //
 // Fragment reads.  The K loop is unrolled over the STAGES buffers, so the
 // stage, tile and row-block offsets of every ds_read are compile-time
@@ -50,7 +58,7 @@ struct Geo {
   static constexpr int insts(int rows) { return rows * ROW_BYTES / 4096; }
 
   static FE2O3_DEVICE uint32_t swz(uint32_t r) {
-    if (ROW_BYTES == 128) return (r ^ (r >> 2)) & 7u;
+    if (ROW_BYTES == 128) return (r & 6u) | ((r ^ (r >> 1) ^ (r >> 2)) & 1u);
     return ((r >> 1) ^ (r >> 3)) & 3u;
   }
   // tile row moved by this thread in load j; the instruction covers rows
