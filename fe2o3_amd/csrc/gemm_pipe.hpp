@@ -823,7 +823,10 @@ FE2O3_DEVICE void copy_one(const RA& ar, const RB& br, uint32_t kbytes, uint8_t*
 // place their own fragment reads and see both fragment buffers.
 template <class M, class = void>
 struct RowSplit : std::false_type {};
-// the barrier's slot in the last substep: the policy's kBarrier, else M/2
+template <class M>
+struct RowSplit<M, std::void_t<decltype(M::kRowSplit)>> : std::bool_constant<M::kRowSplit> {};
+
+// The barrier's slot in the last substep: the policy's kBarrier, else M/2.
 template <class M, class = void>
 struct BarrierAt {
   static constexpr int value = M::kMfma / 2;
@@ -832,8 +835,6 @@ template <class M>
 struct BarrierAt<M, std::void_t<decltype(M::kBarrier)>> {
   static constexpr int value = M::kBarrier;
 };
-template <class M>
-struct RowSplit<M, std::void_t<decltype(M::kRowSplit)>> : std::bool_constant<M::kRowSplit> {};
 
 // Substep S_ of a K step held in stage buffer P.  FIRST: the K loop's first
 // substep (accumulators written, not added to).  k_next / k_next2: k byte
