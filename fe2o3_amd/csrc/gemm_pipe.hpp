@@ -138,6 +138,7 @@ template <int ROW_BYTES, int ROWS = 256, bool MASK = false>
 FE2O3_DEVICE Rows<ROW_BYTES, Geo<ROW_BYTES>::insts(ROWS), false, MASK> dense_rows(
     const uint16_t* base, uint32_t ld, uint32_t valid_rows, uint32_t k16) {
   using G = Geo<ROW_BYTES>;
+  static_assert(ROWS * ROW_BYTES % 4096 == 0, "whole 1-KiB loads per wave for the tile's rows");
   Rows<ROW_BYTES, G::insts(ROWS), false, MASK> t;
   t.bytes = ((valid_rows - 1u) * ld + k16) * 2u;
   if constexpr (MASK) t.k_end = k16 * 2u;
