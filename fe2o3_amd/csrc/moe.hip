@@ -340,18 +340,59 @@ FE2O3_DEVICE void by_tile_rows(uint32_t rows, Fn&& fn) {
   else fn(integral_constant<int, 0>{});
 }
 
+// A tile of a gate/up tile read straight from the token matrix x (tokens x
+// hidden, x_bytes bytes, below 2^31): tile row r is slot row0 + r of the
+// admitted routes, and the slot's permutation entry names its route (token =
+// route / 2).  A slot whose entry is not a route (>= routes) loads from an
+// offset past x's extent, which the buffer's range check turns into zeros:
+// the zero row gather_kernel writes for it.  Rows at or past valid_rows
+// repeat the last valid row, as dense_rows does; the bytes in LDS are those
+// of the gathered rows, so the products are the same.
+template <int ROW_BYTES, int ROWS>
+FE2O3_DEVICE gemm_pipe::Rows<ROW_BYTES, gemm_pipe::Geo<ROW_BYTES>::insts(ROWS)> token_rows(
+    const uint16_t* x, uint32_t x_bytes, const uint32_t* __restrict__ permutation,
+    uint32_t row0, uint32_t valid_rows, uint32_t routes, uint32_t hidden) {
+  using G = gemm_pipe::Geo<ROW_BYTES>;
+  static_assert(ROWS * ROW_BYTES % 4096 == 0, "whole 1-KiB loads per wave for the tile's rows");
+  gemm_pipe::Rows<ROW_BYTES, G::insts(ROWS)> t;
+  t.bytes = x_bytes;
+  uint32_t route[G::insts(ROWS)];
+#pragma unroll
+  for (int j = 0; j < G::insts(ROWS); ++j) {
+    const uint32_t row = G::inst_row(j);
+    route[j] = permutation[row0 + (row < valid_rows ? row : valid_rows - 1u)];
+  }
+#pragma unroll
+  for (int j = 0; j < G::insts(ROWS); ++j) {
+    const uint32_t chunk = G::inst_chunk(G::inst_row(j));
+    t.base[j] = x;
+    t.voff[j] = route[j] < routes ? ((route[j] >> 1) * hidden + chunk * 8u) * 2u
+                                  : gemm_pipe::kOutOfRange;
+  }
+  return t;
+}
+
 // One gate/up tile on the pipeline geometry G (ROW_BYTES of k per row and
 // stage, STAGES stages, RPW output rows per wave; the A tile holds 2 RPW
-// rows; the form by_tile_rows picks).
-template <int ROW_BYTES, int STAGES, int RPW>
-FE2O3_DEVICE void gate_up_tile(const uint16_t* __restrict__ xc, const uint16_t* __restrict__ wg,
-                               const uint16_t* __restrict__ wu, uint32_t e, uint32_t row0,
-                               uint32_t rows, uint32_t nb, uint32_t hidden, uint32_t ffn,
-                               uint16_t* __restrict__ hc, uint8_t* smem) {
+// rows; the form by_tile_rows picks).  TOKENS: the A rows come from the token
+// matrix through the permutation (token_rows; xa = x); otherwise from the
+// gathered rows (xa = xc, row row0 onward).
+template <bool TOKENS, int ROW_BYTES, int STAGES, int RPW>
+FE2O3_DEVICE void gate_up_tile(const uint16_t* __restrict__ xa, uint32_t x_bytes,
+                               const uint32_t* __restrict__ permutation, uint32_t routes,
+                               const uint16_t* __restrict__ wg, const uint16_t* __restrict__ wu,
+                               uint32_t e, uint32_t row0, uint32_t rows, uint32_t nb,
+                               uint32_t hidden, uint32_t ffn, uint16_t* __restrict__ hc,
+                               uint8_t* smem) {
   using G = gemm_pipe::Geo<ROW_BYTES>;
   const uint32_t f0 = nb * 128u;
-  const auto ar = gemm_pipe::dense_rows<ROW_BYTES, 2 * RPW>(xc + (uint64_t)row0 * hidden, hidden,
-                                                            rows, hidden);
+  const auto ar = [&] {
+    if constexpr (TOKENS)
+      return token_rows<ROW_BYTES, 2 * RPW>(xa, x_bytes, permutation, row0, rows, routes, hidden);
+    else
+      return gemm_pipe::dense_rows<ROW_BYTES, 2 * RPW>(xa + (uint64_t)row0 * hidden, hidden, rows,
+                                                       hidden);
+  }();
   // B tile row r: 32-row block jb = r/32 belongs to wave column wn = jb/4;
   // within a wave column the blocks are gate f, up f, gate f+32, up f+32 for
   // f = f0 + 64*wn, so each lane's gate and up accumulators of one (row, f)
@@ -413,11 +454,14 @@ FE2O3_DEVICE void gate_up_tile(const uint16_t* __restrict__ xc, const uint16_t* 
   }
 }
 
+// TOKENS: xa is the token matrix (x_bytes bytes) read through the
+// permutation; otherwise the gathered rows xc.
+template <bool TOKENS>
 __global__ void __launch_bounds__(256, 1) gate_up_kernel(
-    const uint16_t* __restrict__ xc, const uint16_t* __restrict__ wg,
-    const uint16_t* __restrict__ wu, const uint32_t* __restrict__ offsets, uint32_t e_begin,
-    uint32_t e_end, uint32_t hidden, uint32_t ffn, uint32_t routes, uint16_t* __restrict__ hc,
-    uint32_t xcds) {
+    const uint16_t* __restrict__ xa, uint32_t x_bytes, const uint32_t* __restrict__ permutation,
+    const uint16_t* __restrict__ wg, const uint16_t* __restrict__ wu,
+    const uint32_t* __restrict__ offsets, uint32_t e_begin, uint32_t e_end, uint32_t hidden,
+    uint32_t ffn, uint32_t routes, uint16_t* __restrict__ hc, uint32_t xcds) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   uint32_t e, row0, rows, nb;
   if (!expert_tile(offsets, e_begin, e_end, routes, ffn / 128u, xcds, &e, &row0, &rows, &nb))
@@ -425,9 +469,11 @@ __global__ void __launch_bounds__(256, 1) gate_up_kernel(
   by_tile_rows(rows, [&](auto rpw) {
     constexpr int R = decltype(rpw)::value;
     if constexpr (R == 0)
-      gate_up_tile<64, 4, 32>(xc, wg, wu, e, row0, rows, nb, hidden, ffn, hc, smem);
+      gate_up_tile<TOKENS, 64, 4, 32>(xa, x_bytes, permutation, routes, wg, wu, e, row0, rows, nb,
+                                      hidden, ffn, hc, smem);
     else
-      gate_up_tile<128, 2, R>(xc, wg, wu, e, row0, rows, nb, hidden, ffn, hc, smem);
+      gate_up_tile<TOKENS, 128, 2, R>(xa, x_bytes, permutation, routes, wg, wu, e, row0, rows, nb,
+                                      hidden, ffn, hc, smem);
   });
 }
 
@@ -748,11 +794,13 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_assign_kernel", (const void*)route_assign_kernel, RA_THREADS, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_expert_combine_f32_t8_k2_o16_v1", "combine_profile_kernel", (const void*)combine_profile_kernel, 128, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "gather_kernel", (const void*)gather_kernel, 256, 0}),
-    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "gate_up_kernel", (const void*)gate_up_kernel, 256, kSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "gate_up_kernel", (const void*)gate_up_kernel<true>, 256, kSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "gate_up_kernel<gathered>", (const void*)gate_up_kernel<false>, 256, kSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "down_kernel", (const void*)down_kernel, 256, kSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "combine_kernel", (const void*)combine_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2_noalloc", "gather_kernel", (const void*)gather_kernel, 256, 0}),
-    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2_noalloc", "gate_up_kernel", (const void*)gate_up_kernel, 256, kSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2_noalloc", "gate_up_kernel", (const void*)gate_up_kernel<true>, 256, kSmem}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2_noalloc", "gate_up_kernel<gathered>", (const void*)gate_up_kernel<false>, 256, kSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2_noalloc", "down_kernel", (const void*)down_kernel, 256, kSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2_noalloc", "combine_kernel", (const void*)combine_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_routing_check", "routing_check_kernel", (const void*)routing_check_kernel, ASSIGN_THREADS, CHECK_MAX_ROUTES * 4})};
@@ -763,7 +811,7 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
 struct SideStream {
   std::mutex mu;
   hipStream_t stream = nullptr;
-  hipEvent_t gathered = nullptr, done = nullptr;
+  hipEvent_t ready = nullptr, done = nullptr;
   bool ok = false;
 };
 
@@ -777,7 +825,7 @@ SideStream* side_stream() {
   std::lock_guard<std::mutex> lock(create_mu);
   if (!sd.ok) {
     if (hipStreamCreateWithFlags(&sd.stream, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&sd.gathered, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&sd.ready, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&sd.done, hipEventDisableTiming) != hipSuccess)
       return nullptr;
     sd.ok = true;
@@ -900,7 +948,9 @@ int32_t ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate, uint
         (uintptr_t)out | (uintptr_t)workspace) & 15u) != 0)
     return FE2O3_ERR_ALIGNMENT;
   static const int32_t lds_rc = fe2o3_host::set_dynamic_lds(
-      {(const void*)gate_up_kernel, (const void*)down_kernel}, kSmem);
+      {(const void*)gate_up_kernel<true>, (const void*)gate_up_kernel<false>,
+       (const void*)down_kernel},
+      kSmem);
   if (lds_rc != FE2O3_OK) return lds_rc;
   hipStream_t s = (hipStream_t)stream;
   // the most m-tiles any routing yields for experts [b, e): routes/288
@@ -915,18 +965,30 @@ int32_t ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate, uint
     *dn = expert_grid(routes, n_experts, kparts * (hidden / 256u), xcds);
     return *gu <= 0x7fffffffu && *dn <= 0x7fffffffu;
   };
+  // The gate/up tiles read the token rows in place, through the permutation,
+  // when x fits the 32-bit range of a buffer resource; otherwise from rows
+  // gathered into the workspace first.
+  const uint64_t x_bytes = (uint64_t)tokens * hidden * 2u;
+  const bool tokens_direct = x_bytes < (1ull << 31);
   auto experts_ffn = [&](uint32_t b, uint32_t e, hipStream_t st) {
     uint64_t gu, dn;
     grids(e - b, &gu, &dn);
-    gate_up_kernel<<<(unsigned)gu, 256, kSmem, st>>>(ws.xc, w_gate, w_up, expert_offsets, b, e,
-                                                     hidden, ffn, (uint32_t)routes, ws.hc, xcds);
+    if (tokens_direct)
+      gate_up_kernel<true><<<(unsigned)gu, 256, kSmem, st>>>(
+          x, (uint32_t)x_bytes, permutation, w_gate, w_up, expert_offsets, b, e, hidden, ffn,
+          (uint32_t)routes, ws.hc, xcds);
+    else
+      gate_up_kernel<false><<<(unsigned)gu, 256, kSmem, st>>>(
+          ws.xc, 0u, permutation, w_gate, w_up, expert_offsets, b, e, hidden, ffn,
+          (uint32_t)routes, ws.hc, xcds);
     down_kernel<<<(unsigned)dn, 256, kSmem, st>>>(ws.hc, w_down, expert_offsets, b, e, hidden,
                                                   ffn, routes, kparts, ws.yc, xcds);
   };
   uint64_t gu_all, dn_all;
   if (!grids(experts, &gu_all, &dn_all)) return FE2O3_ERR_SHAPE;
-  gather_kernel<<<(unsigned)routes, 256, 0, s>>>(x, permutation, expert_offsets, experts, hidden,
-                                                (uint32_t)routes, ws.xc);
+  if (!tokens_direct)
+    gather_kernel<<<(unsigned)routes, 256, 0, s>>>(x, permutation, expert_offsets, experts, hidden,
+                                                  (uint32_t)routes, ws.xc);
   // Two halves of the experts, each gate/up then down, on the caller's
   // stream and on a side stream: each grouped GEMM ends in a partly filled
   // round of tiles, which the other half's tiles fill.
@@ -934,8 +996,8 @@ int32_t ffn_top2(const uint16_t* x, uint64_t x_len, const uint16_t* w_gate, uint
   if (side != nullptr) {
     std::lock_guard<std::mutex> lock(side->mu);  // keeps one call's event waits its own
     const uint32_t half = experts / 2u;
-    hipError_t e = hipEventRecord(side->gathered, s);
-    if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->gathered, 0);
+    hipError_t e = hipEventRecord(side->ready, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->ready, 0);
     if (e != hipSuccess) return (int32_t)e;
     experts_ffn(0u, half, s);
     experts_ffn(half, experts, side->stream);

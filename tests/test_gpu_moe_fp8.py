@@ -385,6 +385,17 @@ def test_moe_ffn_config5_sampled_tokens(gpu, oracle):
     assert worst <= 1e-2, worst
 
 
+def test_moe_ffn_token_matrix_past_2gib(gpu, oracle):
+    """A token matrix of 2^31 bytes or more does not fit one 32-bit buffer
+    resource, so the gate/up tiles read rows gathered into the workspace
+    (gather_kernel, gate_up_kernel<false>) instead of the token rows in place
+    through the permutation: 2^22 tokens of hidden 256, FFN 128, 2 experts
+    (x is 2 GiB, the workspace 22 GiB); the tokens of the first and last 64
+    slots of each expert end to end."""
+    worst, _ = _ffn_case(gpu, oracle, 1 << 22, 256, 128, 2, 0xFFFFFFFF, _per_expert_tokens(64))
+    assert worst <= 1e-2, worst
+
+
 # ---- fp8 ------------------------------------------------------------------------------------
 
 def _edge_values():

@@ -42,6 +42,7 @@ def test_every_kernel_is_spill_free_and_fits(gpu):
     ("fe2o3_flash_attention_fwd", "flash_fwd_kernel<false>", 64 * 1024, 256),
     ("fe2o3_flash_attention_fwd", "flash_fwd_kernel<true>", 64 * 1024, 256),
     ("fe2o3_moe_ffn_top2", "gate_up_kernel", 136 * 1024, 256),
+    ("fe2o3_moe_ffn_top2", "gate_up_kernel<gathered>", 136 * 1024, 256),
     ("fe2o3_moe_ffn_top2", "down_kernel", 136 * 1024, 256),
     ("fe2o3_moe_routing_check", "routing_check_kernel", 96 * 1024, 128)])
 def test_hot_kernels_match_design(gpu, entry, kernel, dynamic_lds, threads):

@@ -99,7 +99,7 @@ def test_moe_kernels_accumulators_untouched_until_waited(tmp_path):
                     "--cuda-device-only", "-S", "-I" + os.path.join(CSRC, "_build"),
                     os.path.join(CSRC, "moe.hip"), "-o", str(out)],
                    check=True, capture_output=True)
-    bodies = _bodies(out.read_text(), ["gate_up_kernel", "down_kernel"])
+    bodies = _bodies(out.read_text(), ["gate_up_kernelILb1", "gate_up_kernelILb0", "down_kernel"])
     for name, body in bodies.items():
         n_vacc, span_bad, fewest = _check(body)
         # the 288-row form: 8 MFMAs per substep into VGPRs, in every unrolled step
