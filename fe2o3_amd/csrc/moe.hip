@@ -129,25 +129,39 @@ FE2O3_DEVICE void for_each_expert(uint32_t e, Fn&& fn) {
   }
 }
 
+// PREFIXED: the per-expert counts before this workgroup and the totals come
+// from route_scan_kernel (prefix: (experts + 1) words per workgroup, the
+// last unused here; totals: experts words, then the number of workgroups
+// that saw a rejected entry) instead of from counting all of top2 here.
+template <bool PREFIXED>
 __global__ void __launch_bounds__(RA_THREADS) route_assign_kernel(
     uint32_t* __restrict__ top2, uint32_t routes, uint32_t experts, uint32_t capacity,
     uint32_t* __restrict__ requested, uint32_t* __restrict__ admitted,
     uint32_t* __restrict__ offsets, uint32_t* __restrict__ slots,
     uint32_t* __restrict__ permutation, uint32_t* __restrict__ inverse,
-    float* __restrict__ weights) {
+    float* __restrict__ weights, const uint32_t* __restrict__ prefix,
+    const uint32_t* __restrict__ totals) {
   __shared__ uint32_t total[MAX_EXPERTS], before[MAX_EXPERTS], off_s[MAX_EXPERTS + 1];
   __shared__ uint32_t wave_cnt[RA_WAVES][MAX_EXPERTS];
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
   const uint32_t start = blockIdx.x * (uint32_t)RA_ROUTES;
   const uint64_t lt = (1ull << lane) - 1ull;
-  if (t < experts) total[t] = before[t] = 0;
+  if constexpr (PREFIXED) {
+    if (t < experts) {
+      total[t] = totals[t];
+      before[t] = prefix[(uint64_t)blockIdx.x * (experts + 1u) + t];
+    }
+  } else {
+    if (t < experts) total[t] = before[t] = 0;
+  }
   for (uint32_t i = t; i < RA_WAVES * MAX_EXPERTS; i += RA_THREADS) (&wave_cnt[0][0])[i] = 0;
   __syncthreads();
   // counts over all of top2, 64 routes per wave and chunk; the loads of
   // eight chunks are issued together, then counted
   constexpr int kBatch = 8;
-  int rejected = 0;
-  for (uint32_t base0 = wave * 64u; base0 < routes; base0 += kBatch * RA_THREADS) {
+  int rejected = PREFIXED && totals[experts] != 0u;
+  for (uint32_t base0 = wave * 64u; !PREFIXED && base0 < routes;
+       base0 += kBatch * RA_THREADS) {
     uint32_t ev[kBatch];
 #pragma unroll
     for (int q = 0; q < kBatch; ++q) {
@@ -222,6 +236,76 @@ __global__ void __launch_bounds__(RA_THREADS) route_assign_kernel(
   // slots below the accepted total are each written by their route; the rest
   // of the permutation holds the sentinel
   if (r >= off_s[experts]) permutation[r] = DROP;
+}
+
+// Slot assignment for many routes, in three kernels whose work is linear in
+// the routes (route_assign_kernel<false> has every workgroup count all of
+// top2, which grows as routes^2 / 512: 0.33 ms at 2^16 tokens, 8.6 ms at
+// 2^19).  route_count_kernel: workgroup b writes its own routes' count per
+// expert to counts[b][0 .. experts) and whether any of them holds an entry
+// that is not an expert to counts[b][experts].  route_scan_kernel (one
+// workgroup): each column's exclusive prefix over the workgroups in place,
+// and the column totals.  route_assign_kernel<true> then takes `before` and
+// `total` from there: the same numbers the single kernel counts, so the same
+// outputs.
+__global__ void __launch_bounds__(RA_THREADS) route_count_kernel(
+    const uint32_t* __restrict__ top2, uint32_t routes, uint32_t experts,
+    uint32_t* __restrict__ counts) {
+  __shared__ uint32_t cnt[MAX_EXPERTS];
+  const uint32_t t = threadIdx.x, lane = t & 63u;
+  if (t < experts) cnt[t] = 0;
+  __syncthreads();
+  const uint32_t r = blockIdx.x * (uint32_t)RA_ROUTES + t;
+  uint32_t e = r < routes ? top2[r] : DROP;
+  const int rejected = r < routes && e >= experts;
+  if (e >= experts) e = DROP;  // not an expert: counted nowhere
+  for_each_expert(e, [&](uint32_t x, uint64_t mask) {
+    if (lane == 0) atomicAdd(&cnt[x], (uint32_t)__builtin_popcountll(mask));
+  });
+  const int any = __syncthreads_or(rejected);
+  uint32_t* row = counts + (uint64_t)blockIdx.x * (experts + 1u);
+  if (t < experts) row[t] = cnt[t];
+  if (t == 0) row[experts] = any ? 1u : 0u;
+}
+
+constexpr int RS_THREADS = 1024;
+// Routes above which route() takes the three kernels (the single kernel's
+// quadratic counting costs more than the two extra launches from here on).
+constexpr uint64_t kRouteScanAbove = 8192;
+
+// One workgroup: thread i takes the rows [i * chunk, (i + 1) * chunk) of
+// every column in turn: its rows' sum, an exclusive scan of the sums over
+// the threads (wave scans, then the waves' sums), then the rows rewritten
+// with their exclusive prefixes.  Sums are below 2^32 (at most `routes`).
+__global__ void __launch_bounds__(RS_THREADS) route_scan_kernel(uint32_t* __restrict__ counts,
+                                                                uint32_t blocks, uint32_t experts,
+                                                                uint32_t* __restrict__ totals) {
+  __shared__ uint32_t wave_sum[RS_THREADS / 64];
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+  const uint32_t cols = experts + 1u;
+  const uint32_t chunk = (blocks + RS_THREADS - 1u) / RS_THREADS;
+  const uint32_t b0 = min(t * chunk, blocks), b1 = min(b0 + chunk, blocks);
+  for (uint32_t c = 0; c < cols; ++c) {
+    uint32_t sum = 0;
+    for (uint32_t b = b0; b < b1; ++b) sum += counts[(uint64_t)b * cols + c];
+    uint32_t incl = sum;  // inclusive scan within the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t v = (uint32_t)__shfl_up((int)incl, o, 64);
+      if (lane >= (uint32_t)o) incl += v;
+    }
+    if (lane == 63) wave_sum[wave] = incl;
+    __syncthreads();
+    uint32_t run = incl - sum;
+    for (uint32_t w = 0; w < wave; ++w) run += wave_sum[w];
+    for (uint32_t b = b0; b < b1; ++b) {
+      const uint32_t v = counts[(uint64_t)b * cols + c];
+      counts[(uint64_t)b * cols + c] = run;
+      run += v;
+    }
+    if (t == RS_THREADS - 1u) totals[c] = run;
+    __syncthreads();  // wave_sum is rewritten for the next column
+  }
 }
 
 // examples/moe_expert_v1/src/kernel.rs:104-157: T=8, K=2, O=16.
@@ -615,9 +699,30 @@ int32_t route(const void* logits, uint64_t logits_len, uint32_t dtype, uint32_t*
                                                            experts, top2, weights, status);
   }
   const unsigned assign_blocks = routes ? (unsigned)((routes + RA_ROUTES - 1) / RA_ROUTES) : 1u;
-  route_assign_kernel<<<assign_blocks, RA_THREADS, 0, s>>>(top2, (uint32_t)routes, experts, capacity,
-                                                   requested, admitted, offsets, slots,
-                                                   permutation, inverse, weights);
+  // Many routes: the count / scan / assign kernels, on stream-ordered
+  // scratch of (experts + 1) words per workgroup and the totals.  Without
+  // scratch on this device, the single kernel.
+  if (routes > kRouteScanAbove) {
+    void* scratch = nullptr;
+    const uint64_t rows = (uint64_t)assign_blocks * (experts + 1u);
+    if (fe2o3_host::scratch_alloc(&scratch, (rows + experts + 1u) * 4u, s) == FE2O3_OK) {
+      uint32_t* counts = static_cast<uint32_t*>(scratch);
+      uint32_t* totals = counts + rows;
+      route_count_kernel<<<assign_blocks, RA_THREADS, 0, s>>>(top2, (uint32_t)routes, experts,
+                                                               counts);
+      route_scan_kernel<<<1, RS_THREADS, 0, s>>>(counts, assign_blocks, experts, totals);
+      route_assign_kernel<true><<<assign_blocks, RA_THREADS, 0, s>>>(
+          top2, (uint32_t)routes, experts, capacity, requested, admitted, offsets, slots,
+          permutation, inverse, weights, counts, totals);
+      const int32_t rc = fe2o3_host::after_launch();
+      const int32_t free_rc = fe2o3_host::scratch_free(scratch, s);
+      return rc != FE2O3_OK ? rc : free_rc;
+    }
+    (void)hipGetLastError();
+  }
+  route_assign_kernel<false><<<assign_blocks, RA_THREADS, 0, s>>>(
+      top2, (uint32_t)routes, experts, capacity, requested, admitted, offsets, slots, permutation,
+      inverse, weights, nullptr, nullptr);
   return fe2o3_host::after_launch();
 }
 
@@ -788,10 +893,13 @@ __global__ void __launch_bounds__(ASSIGN_THREADS) routing_check_kernel(
 // kernels behind each entry point (fe2o3_kernel_resources)
 const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1", "route_select_kernel<float>", (const void*)route_select_kernel<float>, 256, 0}),
-    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1", "route_assign_kernel", (const void*)route_assign_kernel, RA_THREADS, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1", "route_assign_kernel", (const void*)route_assign_kernel<false>, RA_THREADS, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_select_kernel<float>", (const void*)route_select_kernel<float>, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_select_kernel<uint16_t>", (const void*)route_select_kernel<uint16_t>, 256, 0}),
-    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_assign_kernel", (const void*)route_assign_kernel, RA_THREADS, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_assign_kernel", (const void*)route_assign_kernel<false>, RA_THREADS, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_count_kernel", (const void*)route_count_kernel, RA_THREADS, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_scan_kernel", (const void*)route_scan_kernel, RS_THREADS, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route", "route_assign_kernel<prefixed>", (const void*)route_assign_kernel<true>, RA_THREADS, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_expert_combine_f32_t8_k2_o16_v1", "combine_profile_kernel", (const void*)combine_profile_kernel, 128, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "gather_kernel", (const void*)gather_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2", "gate_up_kernel", (const void*)gate_up_kernel<true>, 256, kSmem}),

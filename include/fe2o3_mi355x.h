@@ -334,7 +334,10 @@ int32_t fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1(
  * route_weights (may be NULL): w0 = 1/(1+exp(l1-l0)), w1 = 1 - w0, so every
  * pair sums to exactly 1 (examples/moe_expert_v1/src/pipeline.rs:137-148).
  * Lengths: top2/slots/permutation/inverse/route_weights 2*tokens,
- * requested/admitted experts, offsets experts+1. */
+ * requested/admitted experts, offsets experts+1.  Above 8192 routes the
+ * slot assignment takes 4 * (experts + 1) * (ceil(routes / 512) + 1) bytes
+ * of stream-ordered scratch from the library's pool (the general GEMM's);
+ * where the device has none, one kernel whose work grows as routes^2. */
 int32_t fe2o3_moe_top2_route(const void *logits, uint64_t logits_len,
                              uint32_t logits_dtype, uint32_t *top2_experts,
                              uint64_t top2_len, uint32_t *requested_counts,

@@ -128,6 +128,24 @@ def test_route_workgroup_boundaries(gpu, oracle, tokens, experts, capacity):
         assert_same(out[mine].download(), ref[theirs], mine)
 
 
+@pytest.mark.parametrize("tokens", [4097, 20000, 70001])
+@pytest.mark.parametrize("experts,capacity", [(8, 0xFFFFFFFF), (5, 3000), (64, 700)])
+def test_route_many_routes_bit_exact(gpu, oracle, tokens, experts, capacity):
+    """More than 8192 routes take the count / scan / assign kernels (the
+    single kernel's counting grows as routes^2): every output array bit-equal
+    to the oracle, with and without capacity drops, ragged last workgroups
+    (logits rounded to multiples of 1/4, so ties are frequent)."""
+    rng = np.random.default_rng(tokens + experts)
+    logits = (np.round(rng.standard_normal(tokens * experts) * 4) / 4).astype(np.float32)
+    out = _route(gpu, gpu.to_device(logits), tokens, experts, capacity)
+    rc, ref = oracle.moe_top2_route(logits, tokens, experts, capacity)
+    assert rc == 0
+    names = dict(zip(["top2", "requested", "admitted", "offsets", "slots", "permutation",
+                      "inverse"], ROUTE_KEYS))
+    for mine, theirs in names.items():
+        assert_same(out[mine].download(), ref[theirs], mine)
+
+
 def test_route_f32_logits_many_experts(gpu, oracle):
     tokens, experts = 1000, 64
     rng = np.random.default_rng(3)

@@ -139,16 +139,19 @@ def test_route_profile_rejects(gpu, oracle, bad):
         assert got[key] == [DROP] * 16, key
 
 
+@pytest.mark.parametrize("tokens", [4096, 20000])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("bad", list(BAD))
-def test_route_rejects_whole_launch(gpu, oracle, dtype, bad):
-    """One non-finite logit among 4096 tokens x 8 experts rejects the launch:
-    every output is its sentinel, weights +0, and a following FFN over that
-    routing writes an all-zero output (no expert receives a route)."""
-    tokens, experts = 4096, 8
+def test_route_rejects_whole_launch(gpu, oracle, dtype, bad, tokens):
+    """One non-finite logit among `tokens` tokens x 8 experts rejects the
+    launch: every output is its sentinel, weights +0, and a following FFN
+    over that routing writes an all-zero output (no expert receives a
+    route).  20000 tokens take the count / scan / assign kernels, with the
+    bad token in the last workgroup."""
+    experts = 8
     rng = np.random.default_rng(9)
     logits = rng.standard_normal((tokens, experts)).astype(np.float32)
-    logits[3001, 5] = BAD[bad]
+    logits[3001 if tokens == 4096 else tokens - 7, 5] = BAD[bad]
     assert oracle.moe_top2_route(logits, tokens, experts)[0] == -5
     if dtype == "bf16":
         dev = gpu.to_device(oracle.bf16_from_f32(logits.ravel()))
