@@ -760,7 +760,9 @@ def sec_fp8_fnuz(ctx, stream, args):
 
 def sec_routing_check(ctx, stream, args):
     """Routing-output consistency check of config 5's router output (4096
-    tokens, 8 experts, unbounded capacity): one workgroup, latency-bound."""
+    tokens, 8 experts, unbounded capacity): six small launches over
+    workgroups of 256 tokens (fill, count, claim, scan, verify, reduce),
+    latency-bound."""
     from fe2o3_amd import kernels
     t, e = 4096, 8
     lg = ctx.alloc(t * e, np.uint16)
@@ -775,9 +777,9 @@ def sec_routing_check(ctx, stream, args):
         r, t, e, DROP, rec, stream=stream, sync=False), args)
     kind = int(rec.download()[0])
     return {"workload": "MoE routing-output consistency check, 4096 tokens x 8 experts",
-            "kernel": "routing_check_kernel", "ms": ms, "value": round(ms * 1e3, 2),
-            "unit": "us", "record_kind": kind,
-            "roofline": {"bound": "latency (one workgroup)", "peak": None, "frac": None},
+            "kernel": "check_verify_kernel and five smaller launches", "ms": ms,
+            "value": round(ms * 1e3, 2), "unit": "us", "record_kind": kind,
+            "roofline": {"bound": "latency (six dependent launches)", "peak": None, "frac": None},
             "parity": {"record_kind": kind, "expected": 0,
                        "coverage": "the router's own output is consistent"}}
 

@@ -27,6 +27,7 @@
 // Expert row ranges come from the device-resident offsets, so the whole
 // layer runs without a host round trip: the grouped GEMM grids are sized
 // for the worst case and workgroups beyond the last expert tile exit.
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -890,6 +891,167 @@ __global__ void __launch_bounds__(ASSIGN_THREADS) routing_check_kernel(
   }
 }
 
+// The same check for more routes than the single workgroup's LDS table
+// holds, over workgroups of RA_ROUTES routes (RA_ROUTES / 2 tokens) on
+// stream-ordered scratch: the claimed-slot table (one word per slot, first
+// filled with DROP), the per-workgroup expert counts and their prefixes
+// (route_count_kernel, route_scan_kernel: the stable ranks), and one site
+// per workgroup (the key's two words, then the record).  Every site is
+// tested as in routing_check_kernel; that kernel stops a thread's route
+// range at its first failure or first out-of-range expert, which skips only
+// sites of larger keys (an out-of-range expert is itself a phase-1 failure),
+// so the smallest failing key, and the record written, are the same.
+constexpr uint32_t kSiteWords = 6;
+// routes above which fe2o3_moe_routing_check runs these kernels
+constexpr uint64_t kCheckWideAbove = 2048;
+
+FE2O3_DEVICE void block_min_site(const Site& site, uint32_t* __restrict__ out) {
+  __shared__ unsigned long long best;
+  if (threadIdx.x == 0) best = ~0ull;
+  __syncthreads();
+  if (site.key != ~0ull) atomicMin(&best, (unsigned long long)site.key);
+  __syncthreads();
+  const uint64_t k = best;
+  if (k == ~0ull ? threadIdx.x == 0 : site.key == k) {
+    out[0] = (uint32_t)k;
+    out[1] = (uint32_t)(k >> 32);
+    for (int i = 0; i < 4; ++i) out[2 + i] = k == ~0ull ? 0u : site.rec[i];
+  }
+}
+
+__global__ void __launch_bounds__(256) check_fill_kernel(uint32_t* __restrict__ claimant,
+                                                         uint32_t routes) {
+  for (uint32_t s = blockIdx.x * 256u + threadIdx.x; s < routes; s += gridDim.x * 256u)
+    claimant[s] = DROP;
+}
+
+// phase 1 for the workgroup's tokens, and its routes' slot claims
+__global__ void __launch_bounds__(RA_THREADS) check_claim_kernel(
+    const uint32_t* __restrict__ top2, const uint32_t* __restrict__ offsets,
+    const uint32_t* __restrict__ slots, uint32_t tokens, uint32_t experts,
+    uint32_t* __restrict__ claimant, uint32_t* __restrict__ sites) {
+  const uint32_t t = threadIdx.x, routes = 2u * tokens;
+  Site site;
+  const uint32_t tk = blockIdx.x * (uint32_t)(RA_ROUTES / 2) + t;
+  if (t < (uint32_t)(RA_ROUTES / 2) && tk < tokens) {
+    const uint32_t a = top2[2 * tk], b = top2[2 * tk + 1];
+    if (a >= experts) site.fail(site_key(1, tk, 0), RC_EXPERT_OUT_OF_RANGE, 2 * tk, 0, a);
+    else if (b >= experts) site.fail(site_key(1, tk, 1), RC_EXPERT_OUT_OF_RANGE, 2 * tk + 1, 0, b);
+    else if (a == b) site.fail(site_key(1, tk, 2), RC_DUPLICATE_TOKEN_EXPERT, tk, 0, a);
+  }
+  const uint32_t accepted = offsets[experts];
+  const uint32_t r = blockIdx.x * (uint32_t)RA_ROUTES + t;
+  if (r < routes) {
+    const uint32_t slot = slots[r];
+    if (slot != DROP && slot < accepted && slot < routes) atomicMin(&claimant[slot], r);
+  }
+  block_min_site(site, sites + (uint64_t)blockIdx.x * kSiteWords);
+}
+
+// phases 2-6 (workgroup 0), 7 for the workgroup's routes and 8-9 for its
+// slots; the workgroup's site becomes the smaller of this and the claim
+// kernel's
+__global__ void __launch_bounds__(RA_THREADS) check_verify_kernel(
+    const uint32_t* __restrict__ top2, const uint32_t* __restrict__ requested,
+    const uint32_t* __restrict__ admitted, const uint32_t* __restrict__ offsets,
+    const uint32_t* __restrict__ slots, const uint32_t* __restrict__ permutation,
+    const uint32_t* __restrict__ inverse, uint32_t tokens, uint32_t experts, uint32_t capacity,
+    const uint32_t* __restrict__ claimant, const uint32_t* __restrict__ prefix,
+    const uint32_t* __restrict__ totals, uint32_t* __restrict__ sites) {
+  __shared__ uint32_t wave_cnt[RA_WAVES][MAX_EXPERTS];
+  const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6, routes = 2u * tokens;
+  for (uint32_t i = t; i < RA_WAVES * MAX_EXPERTS; i += RA_THREADS) (&wave_cnt[0][0])[i] = 0;
+  Site site;
+  if (blockIdx.x == 0 && t == 0) {
+    for (uint32_t e = 0; e < experts && site.key == ~0ull; ++e)
+      if (requested[e] != totals[e]) site.fail(site_key(2, e, 0), RC_REQUESTED_COUNT, e, totals[e], requested[e]);
+    for (uint32_t e = 0; e < experts && site.key == ~0ull; ++e) {
+      const uint32_t want = requested[e] < capacity ? requested[e] : capacity;
+      if (admitted[e] > capacity) site.fail(site_key(3, e, 0), RC_CAPACITY, e, 0, admitted[e]);
+      else if (admitted[e] != want) site.fail(site_key(3, e, 1), RC_ADMITTED_COUNT, e, want, admitted[e]);
+    }
+    if (site.key == ~0ull && offsets[0] != 0) site.fail(site_key(4, 0, 0), RC_FIRST_OFFSET, 0, 0, offsets[0]);
+    uint32_t cum = 0;
+    for (uint32_t e = 0; e < experts && site.key == ~0ull; ++e) {
+      const uint32_t start = offsets[e], end = offsets[e + 1];
+      cum += admitted[e];
+      if (start > end) site.fail(site_key(5, e, 0), RC_NONMONOTONE_OFFSETS, e, start, end);
+      else if (end != cum) site.fail(site_key(5, e, 1), RC_OFFSET_MISMATCH, e + 1, cum, end);
+    }
+    for (uint32_t e = 0; e < experts && site.key == ~0ull; ++e) {
+      const uint32_t start = offsets[e], end = offsets[e + 1];
+      if (start > end || end > routes) site.fail(site_key(6, e, 0), RC_PLAN_OFFSET_ORDER, e, 0, end);
+      else if (end - start > capacity) site.fail(site_key(6, e, 1), RC_PLAN_CAPACITY, e, 0, end - start);
+    }
+  }
+  __syncthreads();
+  // phase 7: stable rank = this expert's routes in earlier workgroups, in
+  // earlier waves, in earlier lanes
+  const uint32_t r = blockIdx.x * (uint32_t)RA_ROUTES + t;
+  uint32_t e = r < routes ? top2[r] : DROP;
+  if (e >= experts) e = DROP;  // phase 1 reports it
+  uint32_t rank = 0;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  for_each_expert(e, [&](uint32_t x, uint64_t mask) {
+    if (e == x) rank = (uint32_t)__builtin_popcountll(mask & lt);
+    if (lane == 0) wave_cnt[wave][x] = (uint32_t)__builtin_popcountll(mask);
+  });
+  __syncthreads();
+  const uint32_t accepted = offsets[experts];
+  if (e != DROP) {
+    rank += prefix[(uint64_t)blockIdx.x * (experts + 1u) + e];
+    for (uint32_t w = 0; w < wave; ++w) rank += wave_cnt[w][e];
+    const uint32_t want = rank < capacity ? offsets[e] + rank : DROP;
+    const uint32_t slot = slots[r];
+    if (slot != DROP && slot >= accepted)
+      site.fail(site_key(7, r, 0), RC_SLOT_OUT_OF_RANGE, r, accepted, slot);
+    else if (slot != DROP && slot < routes && claimant[slot] < r)
+      site.fail(site_key(7, r, 1), RC_DUPLICATE_SLOT, r, 0, slot);
+    else if (slot != want)
+      site.fail(site_key(7, r, 2), RC_STABLE_SLOT, r, want, slot);
+    else if (inverse[r] != want)
+      site.fail(site_key(7, r, 3), RC_INVERSE, r, want, inverse[r]);
+    else if (want != DROP && want < routes && permutation[want] != r)
+      site.fail(site_key(7, r, 4), RC_PERMUTATION, want, r, permutation[want]);
+  }
+  // phases 8 and 9 for slot s = r
+  const uint32_t acc = accepted < routes ? accepted : routes;
+  if (r < acc) {
+    if (claimant[r] == DROP) {
+      site.fail(site_key(8, r, 0), RC_PREFIX_HOLE, r, 0, 0);
+    } else {
+      const uint32_t q = permutation[r];
+      if (q >= routes) site.fail(site_key(8, r, 1), RC_PERMUTATION_ROUTE, r, 0, q);
+      else if (slots[q] != r || inverse[q] != r) site.fail(site_key(8, r, 2), RC_PERMUTATION, r, q, q);
+    }
+  } else if (r < routes && r >= accepted && permutation[r] != DROP) {
+    site.fail(site_key(9, r, 0), RC_PERMUTATION_TAIL, r, 0, permutation[r]);
+  }
+  // the claim kernel's site of this workgroup competes too
+  uint32_t* mine = sites + (uint64_t)blockIdx.x * kSiteWords;
+  if (t == 0) {
+    const uint64_t k0 = (uint64_t)mine[0] | ((uint64_t)mine[1] << 32);
+    if (k0 != ~0ull) site.fail(k0, mine[2], mine[3], mine[4], mine[5]);
+  }
+  __syncthreads();  // every thread has read `mine` before it is rewritten
+  block_min_site(site, mine);
+}
+
+// the smallest site over the workgroups, as the record (zeros when none)
+__global__ void __launch_bounds__(RS_THREADS) check_reduce_kernel(
+    const uint32_t* __restrict__ sites, uint32_t blocks, uint32_t* __restrict__ record) {
+  Site site;
+  for (uint32_t b = threadIdx.x; b < blocks; b += RS_THREADS) {
+    const uint32_t* w = sites + (uint64_t)b * kSiteWords;
+    const uint64_t k = (uint64_t)w[0] | ((uint64_t)w[1] << 32);
+    if (k != ~0ull) site.fail(k, w[2], w[3], w[4], w[5]);
+  }
+  __shared__ uint32_t out[kSiteWords];
+  block_min_site(site, out);
+  __syncthreads();
+  if (threadIdx.x < 4) record[threadIdx.x] = out[2 + threadIdx.x];
+}
+
 // kernels behind each entry point (fe2o3_kernel_resources)
 const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_moe_top2_route_f32_t8_e4_k2_c4_v1", "route_select_kernel<float>", (const void*)route_select_kernel<float>, 256, 0}),
@@ -911,7 +1073,13 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2_noalloc", "gate_up_kernel<gathered>", (const void*)gate_up_kernel<false>, 256, kSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2_noalloc", "down_kernel", (const void*)down_kernel, 256, kSmem}),
     fe2o3_host::KernelRegistrar({"fe2o3_moe_ffn_top2_noalloc", "combine_kernel", (const void*)combine_kernel, 256, 0}),
-    fe2o3_host::KernelRegistrar({"fe2o3_moe_routing_check", "routing_check_kernel", (const void*)routing_check_kernel, ASSIGN_THREADS, CHECK_MAX_ROUTES * 4})};
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_routing_check", "routing_check_kernel", (const void*)routing_check_kernel, ASSIGN_THREADS, CHECK_MAX_ROUTES * 4}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_routing_check", "check_fill_kernel", (const void*)check_fill_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_routing_check", "route_count_kernel", (const void*)route_count_kernel, RA_THREADS, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_routing_check", "check_claim_kernel", (const void*)check_claim_kernel, RA_THREADS, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_routing_check", "route_scan_kernel", (const void*)route_scan_kernel, RS_THREADS, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_routing_check", "check_verify_kernel", (const void*)check_verify_kernel, RA_THREADS, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_moe_routing_check", "check_reduce_kernel", (const void*)check_reduce_kernel, RS_THREADS, 0})};
 
 // The expert FFN's second stream, one per device, created on first use and
 // kept for the life of the process (default priority, non-blocking so that it
@@ -1202,7 +1370,7 @@ int32_t fe2o3_moe_routing_check(const uint32_t* top2_experts, uint64_t top2_len,
   FE2O3_ENTRY("fe2o3_moe_routing_check");
   if (experts < 1 || experts > MAX_EXPERTS) return FE2O3_ERR_SHAPE;
   const uint64_t routes = 2ull * tokens;
-  if (routes > CHECK_MAX_ROUTES) return FE2O3_ERR_SHAPE;
+  if (routes > 0xFFFFFFFEull) return FE2O3_ERR_SHAPE;
   if (top2_len != routes || slots_len != routes || permutation_len != routes ||
       inverse_len != routes || requested_len != experts || admitted_len != experts ||
       offsets_len != experts + 1ull || record_len != 4)
@@ -1210,11 +1378,47 @@ int32_t fe2o3_moe_routing_check(const uint32_t* top2_experts, uint64_t top2_len,
   if (!requested_counts || !admitted_counts || !expert_offsets || !record ||
       (routes && (!top2_experts || !route_slots || !permutation || !inverse)))
     return FE2O3_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  // Above kCheckWideAbove routes the workgroups of 256 tokens (35-50 us at
+  // config 5, against 119 for one workgroup); without scratch on this
+  // device, one workgroup as long as its claimed-slot table fits LDS.
+  void* scratch = nullptr;
+  const uint32_t blocks = (uint32_t)((routes + RA_ROUTES - 1) / RA_ROUTES);
+  const uint64_t count_words = (uint64_t)blocks * (experts + 1u);
+  int32_t alloc_rc = FE2O3_OK;
+  if (routes > kCheckWideAbove) {
+    alloc_rc = fe2o3_host::scratch_alloc(
+        &scratch, (routes + count_words + experts + 1u + (uint64_t)blocks * kSiteWords) * 4u, s);
+    if (alloc_rc != FE2O3_OK) {
+      (void)hipGetLastError();
+      if (routes > CHECK_MAX_ROUTES) return alloc_rc;
+    }
+  }
+  if (alloc_rc == FE2O3_OK && scratch != nullptr) {
+    uint32_t* claimant = static_cast<uint32_t*>(scratch);
+    uint32_t* counts = claimant + routes;
+    uint32_t* totals = counts + count_words;
+    uint32_t* sites = totals + experts + 1u;
+    const uint32_t fill_blocks = (uint32_t)std::min<uint64_t>((routes + 255u) / 256u, 8192u);
+    check_fill_kernel<<<fill_blocks, 256, 0, s>>>(claimant, (uint32_t)routes);
+    route_count_kernel<<<blocks, RA_THREADS, 0, s>>>(top2_experts, (uint32_t)routes, experts,
+                                                     counts);
+    check_claim_kernel<<<blocks, RA_THREADS, 0, s>>>(top2_experts, expert_offsets, route_slots,
+                                                     tokens, experts, claimant, sites);
+    route_scan_kernel<<<1, RS_THREADS, 0, s>>>(counts, blocks, experts, totals);
+    check_verify_kernel<<<blocks, RA_THREADS, 0, s>>>(
+        top2_experts, requested_counts, admitted_counts, expert_offsets, route_slots, permutation,
+        inverse, tokens, experts, capacity, claimant, counts, totals, sites);
+    check_reduce_kernel<<<1, RS_THREADS, 0, s>>>(sites, blocks, record);
+    const int32_t rc = fe2o3_host::after_launch();
+    const int32_t free_rc = fe2o3_host::scratch_free(scratch, s);
+    return rc != FE2O3_OK ? rc : free_rc;
+  }
   const size_t lds = (size_t)(routes ? routes : 1) * sizeof(uint32_t);
   static const int32_t lds_rc = fe2o3_host::set_dynamic_lds(
       {(const void*)routing_check_kernel}, (int)(CHECK_MAX_ROUTES * sizeof(uint32_t)));
   if (lds_rc != FE2O3_OK) return lds_rc;
-  routing_check_kernel<<<1, ASSIGN_THREADS, lds, (hipStream_t)stream>>>(
+  routing_check_kernel<<<1, ASSIGN_THREADS, lds, s>>>(
       top2_experts, requested_counts, admitted_counts, expert_offsets, route_slots, permutation,
       inverse, tokens, experts, capacity, record);
   return fe2o3_host::after_launch();

@@ -486,9 +486,13 @@ int32_t fe2o3_gemm_fp8_nt(const uint8_t *a, uint64_t a_len, const uint8_t *b,
 /* crates/fe2o3-host/src/moe_routing_expert_bridge_v1.rs:220-389
  * (check_host_observed_moe_routing_output_v1) with the compact pack plan of
  * crates/fe2o3-host/src/generated_moe_expert_v1.rs:159-190, on the device
- * and for any tokens (at most 12288), experts (1..64) and capacity
- * (0xFFFFFFFF = unbounded).  Checks a complete routing output (the seven
- * arrays of fe2o3_moe_top2_route) and writes the reference's FIRST failing
+ * and for any tokens (2 * tokens below 2^32), experts (1..64) and capacity
+ * (0xFFFFFFFF = unbounded).  Above 1024 tokens the check runs over
+ * workgroups of 256 tokens on stream-ordered scratch from the library's
+ * pool (about 4 * (2 * tokens + (2 * tokens / 512 + 1) * (experts + 7))
+ * bytes); where the device has no pool, one workgroup up to 12288 tokens,
+ * and above that the allocation's HIP error.  Checks a complete routing
+ * output (the seven arrays of fe2o3_moe_top2_route) and writes the reference's FIRST failing
  * relation to record[0..3] = {kind, index, expected, actual}, kind
  * FE2O3_RC_OK (0) when every relation holds.  Lengths as
  * fe2o3_moe_top2_route; record 4. */

@@ -196,11 +196,14 @@ def _mutations(outs, rng, routes, experts, n):
 
 @pytest.mark.parametrize("tokens,experts,capacity", [(8, 4, 4), (4096, 8, 0xFFFFFFFF),
                                                      (4096, 8, 1000), (777, 64, 30),
-                                                     (12288, 16, 0xFFFFFFFF)])
+                                                     (12288, 16, 0xFFFFFFFF),
+                                                     (20000, 8, 0xFFFFFFFF), (15000, 64, 300)])
 def test_routing_check_matches_oracle_on_mutations(gpu, oracle, tokens, experts, capacity):
     """The router's own outputs are consistent; random one- and two-element
     corruptions of them (sentinels, in- and out-of-range values, swaps,
-    off-by-one) report exactly the oracle's first failing relation."""
+    off-by-one) report exactly the oracle's first failing relation.  Up to
+    1024 tokens one workgroup checks; above, the check runs over workgroups
+    of 256 tokens on stream-ordered scratch."""
     rng = np.random.default_rng(tokens + experts)
     rc, outs = oracle.moe_top2_route(rng.standard_normal((tokens, experts)).astype(np.float32),
                                      tokens, experts, capacity)
@@ -233,12 +236,14 @@ def test_routing_check_reference_mutations(gpu, oracle):
         assert _device_check(gpu, m, 8, 4, 4) == want, (key, i)
 
 
-def test_routing_check_every_permutation_tail_slot(gpu, oracle):
-    """A capacity-limited routing (4096 tokens, 8 experts, capacity 700, so
-    the permutation has a long sentinel tail): a non-sentinel value planted
-    in each tail slot in turn is reported as PermutationTail at that slot,
-    as the oracle reports it."""
-    tokens, experts, capacity = 4096, 8, 700
+@pytest.mark.parametrize("tokens,capacity,ends,random", [(4096, 700, 130, 40),
+                                                         (20000, 3000, 30, 20)])
+def test_routing_check_every_permutation_tail_slot(gpu, oracle, tokens, capacity, ends, random):
+    """A capacity-limited routing (8 experts, so the permutation has a long
+    sentinel tail): a non-sentinel value planted in each tail slot in turn
+    is reported as PermutationTail at that slot, as the oracle reports it
+    (both sizes run the many-workgroup check: 16 and 79 workgroups)."""
+    experts = 8
     rng = np.random.default_rng(11)
     rc, base = oracle.moe_top2_route(rng.standard_normal((tokens, experts)).astype(np.float32),
                                      tokens, experts, capacity)
@@ -246,7 +251,7 @@ def test_routing_check_every_permutation_tail_slot(gpu, oracle):
     accepted = int(base["expert_offsets"][-1])
     assert accepted < 2 * tokens - 200
     tail = list(range(accepted, 2 * tokens))
-    picks = tail[:130] + tail[-130:] + [int(x) for x in rng.choice(tail, 40, replace=False)]
+    picks = tail[:ends] + tail[-ends:] + [int(x) for x in rng.choice(tail, random, replace=False)]
     for s in picks:
         m = {k: np.array(v, np.uint32) for k, v in base.items()}
         m["permutation"][s] = 3
@@ -255,12 +260,14 @@ def test_routing_check_every_permutation_tail_slot(gpu, oracle):
         assert _device_check(gpu, m, tokens, experts, capacity) == want, s
 
 
-def test_routing_check_garbage_payloads_are_safe(gpu, oracle):
+@pytest.mark.parametrize("tokens,rounds", [(64, 20), (13000, 4)])
+def test_routing_check_garbage_payloads_are_safe(gpu, oracle, tokens, rounds):
     """Arbitrary arrays (ids, offsets and slots far out of range) read only
-    in bounds and still report the oracle's first error."""
+    in bounds and still report the oracle's first error (13000 tokens: the
+    many-workgroup check)."""
     rng = np.random.default_rng(5)
-    tokens, experts = 64, 8
-    for _ in range(20):
+    experts = 8
+    for _ in range(rounds):
         outs = {"top2_experts": rng.integers(0, experts + 2, 2 * tokens, dtype=np.uint32),
                 "requested_counts": rng.integers(0, 40, experts, dtype=np.uint32),
                 "admitted_counts": rng.integers(0, 40, experts, dtype=np.uint32),
@@ -272,7 +279,7 @@ def test_routing_check_garbage_payloads_are_safe(gpu, oracle):
             _oracle_check(oracle, outs, tokens, experts, 16)
     # valid ids, counts and offsets from the router; random slot arrays, so
     # the slot, permutation and tail phases see arbitrary values
-    for _ in range(20):
+    for _ in range(rounds):
         _, outs = oracle.moe_top2_route(rng.standard_normal((tokens, experts)).astype(np.float32),
                                         tokens, experts, 12)
         for key in ("route_slots", "permutation", "inverse"):
