@@ -37,6 +37,8 @@
 //      turn, so every workgroup does nq+1 key tiles; a wave skips the
 //      MFMAs of key tiles that lie entirely above its rows and masks the
 //      diagonal tile.
+#include <type_traits>
+
 #include "common.hpp"
 #include "internal.hpp"
 #include "profiles.hpp"
@@ -228,9 +230,12 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
   wait_vmcnt0();
   lds_barrier();
 
-  for (uint32_t j = 0; j < n_kv; ++j) {
-    const uint8_t* cur = smem + (j & 1u) * STAGE_BYTES;
-    uint8_t* nxt = smem + ((j + 1u) & 1u) * STAGE_BYTES;
+  // One key tile in stage buffer P: the loop runs the tiles in pairs, so P
+  // is a constant and every LDS address a per-lane base plus an immediate.
+  auto key_tile = [&](uint32_t j, auto parity) {
+    constexpr uint32_t P = decltype(parity)::value;
+    const uint8_t* cur = smem + P * STAGE_BYTES;
+    uint8_t* nxt = smem + (P ^ 1u) * STAGE_BYTES;
     // next tile's k offset; the last tile copies itself again (into a buffer
     // nobody reads) so that every tile issues the same copies
     const uint32_t nt =
@@ -362,7 +367,13 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
     }
     wait_vmcnt0();
     lds_barrier();
+  };
+  uint32_t j = 0;
+  for (; j + 2u <= n_kv; j += 2u) {
+    key_tile(j, std::integral_constant<uint32_t, 0>{});
+    key_tile(j + 1u, std::integral_constant<uint32_t, 1>{});
   }
+  if (j < n_kv) key_tile(j, std::integral_constant<uint32_t, 0>{});
 
   // finalize: full row sum across the lane pair, normalize, store
   const float l_tot = l_run + swap_half(l_run);
