@@ -17,10 +17,13 @@
 //      each key block; the other 16 sit in lane l^32.  Row max and row sum are
 //      in-lane reductions plus one v_permlane32_swap.
 //    * Softmax in the exp2 domain: p = exp2(s*c - m) with c = scale*log2(e)
-//      folded into one FMA before v_exp_f32.  The reference m is raised (and
-//      O, l rescaled by exp2(m_old - m_new)) only when some row's tile max
-//      exceeds it by 2^8, so most tiles skip the 64 rescale multiplies per
-//      lane; p stays <= 256, exact enough in bf16 and fp32.
+//      folded into one FMA before v_exp_f32.  The tile's p are computed
+//      against the running reference m first; only when some lane's sum of
+//      them is not <= 2^8 (every p is at most that sum; the first tile,
+//      against m = -inf, gives +inf or NaN) does the tile take its row max,
+//      raise m, rescale O and l by exp2(m_old - m_new) and compute its p
+//      again.  Most tiles thus skip both the max and the 64 rescale
+//      multiplies per lane; p stays <= 256, exact enough in bf16 and fp32.
 //    * O^T += V^T P^T: P (bf16) is the second operand straight from the S
 //      registers; the V^T operand is read from the row-major V tile with
 //      ds_read_b64_tr_b16 (the gfx950 transposing LDS read), two reads per
@@ -37,8 +40,6 @@
 //      turn, so every workgroup does nq+1 key tiles; a wave skips the
 //      MFMAs of key tiles that lie entirely above its rows and masks the
 //      diagonal tile.
-#include <type_traits>
-
 #include "common.hpp"
 #include "internal.hpp"
 #include "profiles.hpp"
@@ -72,6 +73,7 @@ constexpr int TILE_BYTES = BKV * D * 2;     // 16 KiB: 64 rows of 256 B
 constexpr int STAGE_BYTES = 2 * TILE_BYTES; // K tile then V tile
 constexpr int SMEM_BYTES = 2 * STAGE_BYTES; // 64 KiB: two stages
 constexpr float RESCALE_SLACK = 8.0f;       // log2 units: p may reach 2^8 before a rescale
+constexpr float kLazyBound = 256.0f;          // 2^RESCALE_SLACK
 
 // Both tiles are [64 keys][128 d] bf16 rows of 256 B holding 16 chunks of
 // 16 B.  K chunk c of row r sits at c ^ (r & 15): the S^T operand reads (32
@@ -230,12 +232,9 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
   wait_vmcnt0();
   lds_barrier();
 
-  // One key tile in stage buffer P: the loop runs the tiles in pairs, so P
-  // is a constant and every LDS address a per-lane base plus an immediate.
-  auto key_tile = [&](uint32_t j, auto parity) {
-    constexpr uint32_t P = decltype(parity)::value;
-    const uint8_t* cur = smem + P * STAGE_BYTES;
-    uint8_t* nxt = smem + (P ^ 1u) * STAGE_BYTES;
+  for (uint32_t j = 0; j < n_kv; ++j) {
+    const uint8_t* cur = smem + (j & 1u) * STAGE_BYTES;
+    uint8_t* nxt = smem + ((j + 1u) & 1u) * STAGE_BYTES;
     // next tile's k offset; the last tile copies itself again (into a buffer
     // nobody reads) so that every tile issues the same copies
     const uint32_t nt =
@@ -304,14 +303,37 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
             if (key > my_q) s[kb][e] = -INFINITY;
           }
       }
-      float mloc = -INFINITY;
+      bf16x8_t pf[2][2];
+      float psum;
+      auto probabilities = [&] {
+        psum = 0.0f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[kb][e]);
-      mloc = fmaxf(mloc, swap_half(mloc)) * scale_log2;
-      // rescale only when some row's tile max exceeds its reference by the slack
-      if (__any(mloc > m_ref + RESCALE_SLACK)) {
+          for (int h = 0; h < 2; ++h) {
+            float pv[8];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+              pv[jj] =
+                  __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][h * 8 + jj], scale_log2, -m_ref));
+              psum += pv[jj];
+            }
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) pf[kb][h][jj] = (__bf16)pv[jj];
+          }
+      };
+      probabilities();
+      // The reference is raised only when some lane's sum of this tile is not
+      // <= 2^slack: every p is at most that sum, and the first tile (reference
+      // -inf) gives +inf or NaN.  Then the row's tile max, the rescale, and
+      // this tile's probabilities again.
+      if (__any(!(psum <= kLazyBound))) {
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[kb][e]);
+        mloc = fmaxf(mloc, swap_half(mloc)) * scale_log2;
         const float m_new = fmaxf(m_ref, mloc);
         const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
         m_ref = m_new;
@@ -320,22 +342,8 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
         for (int db = 0; db < 4; ++db)
 #pragma unroll
           for (int e = 0; e < 16; ++e) acc[db][e] *= alpha;
+        probabilities();
       }
-      bf16x8_t pf[2][2];
-      float psum = 0.0f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          float pv[8];
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) {
-            pv[jj] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][h * 8 + jj], scale_log2, -m_ref));
-            psum += pv[jj];
-          }
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) pf[kb][h][jj] = (__bf16)pv[jj];
-        }
       l_run += psum;
       // O^T += V^T P^T.  Each SIMD runs one wave of each of two workgroups; a
       // wave raises its issue priority while it issues these MFMAs, so the
@@ -367,13 +375,7 @@ __global__ void __launch_bounds__(THREADS, 8 / WAVES) flash_fwd_kernel(
     }
     wait_vmcnt0();
     lds_barrier();
-  };
-  uint32_t j = 0;
-  for (; j + 2u <= n_kv; j += 2u) {
-    key_tile(j, std::integral_constant<uint32_t, 0>{});
-    key_tile(j + 1u, std::integral_constant<uint32_t, 1>{});
   }
-  if (j < n_kv) key_tile(j, std::integral_constant<uint32_t, 0>{});
 
   // finalize: full row sum across the lane pair, normalize, store
   const float l_tot = l_run + swap_half(l_run);

@@ -206,6 +206,38 @@ def test_flash_small_all_rows(gpu, oracle, b, h, s, causal):
 
 
 @pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("pattern", ["ramp", "spikes", "jump"])
+def test_flash_rescales_all_rows(gpu, oracle, pattern, causal):
+    """Scores that force the running reference up again and again: every key
+    tile raises every row's max by ~16 (log2 units; ramp), random keys far
+    above the rest (spikes), or a jump of ~228 halfway, where the
+    exponentials against the old reference overflow to +inf (jump).  Every
+    row and its LSE against the f64 oracle."""
+    b, h, s = 1, 2, 512
+    rng = np.random.default_rng({"ramp": 1, "spikes": 2, "jump": 3}[pattern])
+    t = np.zeros(b * h * s, np.float32)
+    j = np.tile(np.arange(s), b * h)
+    if pattern == "ramp":
+        t = (j / 64.0).astype(np.float32)
+    elif pattern == "spikes":
+        t = np.where(rng.random(b * h * s) < 0.04, 6.0, 0.0).astype(np.float32)
+    else:
+        t = np.where(j >= s // 2, 14.0, 0.0).astype(np.float32)
+    q = np.ones((b * h * s, 128), np.float32) + 0.05 * rng.standard_normal((b * h * s, 128))
+    k = t[:, None] + 0.1 * rng.standard_normal((b * h * s, 128))
+    v = rng.standard_normal((b * h * s, 128))
+    qkv = [oracle.bf16_from_f32(np.ascontiguousarray(x, np.float32).ravel()) for x in (q, k, v)]
+    (qh, kh, vh), out, lse, scale = _flash(gpu, b, h, s, causal, seed=0, qkv=qkv)
+    bh = np.repeat(np.arange(b * h, dtype=np.uint32), s)
+    rows = np.tile(np.arange(s, dtype=np.uint32), b * h)
+    rc, ref, ref_lse = oracle.flash_attention_rows_bf16(qh, kh, vh, s, 128, causal, scale, bh, rows)
+    assert rc == 0
+    assert np.all(np.isfinite(out)) and np.all(np.isfinite(lse))
+    assert rel_err(out.reshape(-1, 128), ref) <= 1e-2
+    assert rel_err(lse, ref_lse) <= 1e-5  # fp32 output: the 1e-5 bar
+
+
+@pytest.mark.parametrize("causal", [False, True])
 def test_flash_config3_sampled_rows(gpu, oracle, causal):
     """B8 H32 S4096 D128, Q/K/V ~ N(0,1) bf16, scale
     1/sqrt(128), against the two-pass f64 oracle with the LSE: 64 query rows
