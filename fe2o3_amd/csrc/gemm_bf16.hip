@@ -271,6 +271,10 @@ int32_t launch_fast(const uint16_t* a, const uint16_t* b, uint16_t* c, uint32_t 
 
 }  // namespace
 
+namespace {
+constexpr uint32_t kRepackMin = 128;  // outputs at least this in M and N repack
+}  // namespace
+
 extern "C" int32_t fe2o3_gemm_bf16_nt(const uint16_t* a, uint64_t a_len, const uint16_t* b,
                                       uint64_t b_len, uint16_t* c, uint64_t c_len, uint32_t m,
                                       uint32_t n, uint32_t k, void* stream) {
@@ -303,8 +307,43 @@ extern "C" int32_t fe2o3_gemm_bf16_nt(const uint16_t* a, uint64_t a_len, const u
       return launch_fast<true>(a, b, c, m, n, k, plan, topo.xcds, (hipStream_t)stream);
     return launch_fast<false>(a, b, c, m, n, k, plan, topo.xcds, (hipStream_t)stream);
   }
+  // Rows the tile cannot read in place (K not a multiple of 8, or A or B two
+  // bytes past a 16-byte boundary) are first copied into aligned rows of kp
+  // = K rounded up to 8, zeros from K on, in stream-ordered scratch; the
+  // tile then runs on kp, whose zeros fall where its partial last stage
+  // puts zeros anyway, so an operand that is only misaligned gives the bits
+  // of the aligned one.  Outputs below 128 x 128, and devices without
+  // stream-ordered scratch, take the generic kernel.
+  const uint32_t kp = (k + 7u) & ~7u;
+  hipStream_t s = (hipStream_t)stream;
+  if (m >= kRepackMin && n >= kRepackMin && 512ull * kp < (1ull << 31)) {
+    const bool ra = k % 8 != 0 || !aligned16(a), rb = k % 8 != 0 || !aligned16(b);
+    const int32_t lds_rc = set_fast_lds();
+    if (lds_rc != FE2O3_OK) return lds_rc;
+    tile_plan::Topology topo;
+    const int32_t topo_rc = fe2o3_host::device_topology(&topo);
+    if (topo_rc != FE2O3_OK) return topo_rc;
+    const tile_plan::Plan plan = tile_plan::plan(m, n, topo);
+    if (plan.grid > 0x7fffffffu || plan.tail_grid > 0x7fffffffu) return FE2O3_ERR_SHAPE;
+    const uint64_t a_elems = ra ? (uint64_t)m * kp : 0, b_elems = rb ? (uint64_t)n * kp : 0;
+    void* scratch = nullptr;
+    if (fe2o3_host::scratch_alloc(&scratch, (a_elems + b_elems) * 2u, s) == FE2O3_OK) {
+      uint16_t* ap = static_cast<uint16_t*>(scratch);
+      uint16_t* bp = ap + a_elems;
+      int32_t rc = FE2O3_OK;
+      if (ra) rc = fe2o3_host::repack_bf16_rows(a, m, k, k, ap, kp, s);
+      if (rb && rc == FE2O3_OK) rc = fe2o3_host::repack_bf16_rows(b, n, k, k, bp, kp, s);
+      if (rc == FE2O3_OK)
+        rc = kp % gemm_pipe::Geo<kRowBytes>::kK16 != 0
+                 ? launch_fast<true>(ra ? ap : a, rb ? bp : b, c, m, n, kp, plan, topo.xcds, s)
+                 : launch_fast<false>(ra ? ap : a, rb ? bp : b, c, m, n, kp, plan, topo.xcds, s);
+      const int32_t free_rc = fe2o3_host::scratch_free(scratch, s);
+      return rc != FE2O3_OK ? rc : free_rc;
+    }
+    (void)hipGetLastError();  // no stream-ordered scratch: the generic kernel
+  }
   dim3 grid((n + N_BN - 1) / N_BN, (m + N_BM - 1) / N_BM);
   if (grid.y > 65535u) return FE2O3_ERR_SHAPE;
-  gemm_bf16_nt_generic_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(a, b, c, m, n, k);
+  gemm_bf16_nt_generic_kernel<<<grid, 256, 0, s>>>(a, b, c, m, n, k);
   return fe2o3_host::after_launch();
 }

@@ -515,7 +515,9 @@ __global__ void __launch_bounds__(256) repack_rows_kernel(const uint16_t* __rest
 
 const fe2o3_host::KernelRegistrar kRegisteredPipe[] = {
     FE2O3_GENERAL_PIPE_KERNELS("fe2o3_tiled_gemm_general_v1"),
-    FE2O3_GENERAL_PIPE_KERNELS("fe2o3_tiled_gemm_general_vector_a_v1")};
+    FE2O3_GENERAL_PIPE_KERNELS("fe2o3_tiled_gemm_general_vector_a_v1"),
+    // fe2o3_gemm_bf16_nt repacks misaligned operand rows with it (gemm_bf16.hip)
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_bf16_nt", "repack_rows_kernel", (const void*)repack_rows_kernel, 256, 0})};
 
 // Raises every pipelined kernel's dynamic-LDS limit once per process.
 int32_t set_general_lds() {
@@ -673,6 +675,18 @@ staged:
 }
 
 }  // namespace
+
+namespace fe2o3_host {
+
+int32_t repack_bf16_rows(const uint16_t* src, uint32_t rows, uint32_t cols, uint32_t ld,
+                         uint16_t* dst, uint32_t dst_cols, hipStream_t s) {
+  const uint64_t g = ((uint64_t)rows * (dst_cols / 8u) + 255u) / 256u;
+  repack_rows_kernel<<<(unsigned)(g < 16384u ? g : 16384u), 256, 0, s>>>(src, rows, cols, ld, dst,
+                                                                         dst_cols);
+  return after_launch();
+}
+
+}  // namespace fe2o3_host
 
 extern "C" {
 

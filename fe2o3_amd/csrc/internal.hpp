@@ -50,6 +50,12 @@ int32_t device_topology(tile_plan::Topology* out);
 int32_t scratch_alloc(void** p, size_t bytes, hipStream_t s);
 int32_t scratch_free(void* p, hipStream_t s);
 
+// `rows` rows of `cols` bf16 elements, `ld` apart from src (any 2-byte
+// alignment), copied on stream s into rows of dst_cols elements (a multiple
+// of 8; zeros from cols on) at dst (16-byte aligned).  0, or a hipError_t.
+int32_t repack_bf16_rows(const uint16_t* src, uint32_t rows, uint32_t cols, uint32_t ld,
+                         uint16_t* dst, uint32_t dst_cols, hipStream_t s);
+
 // Enqueue status: 0, or the hipError_t of the launch just made.
 inline int32_t after_launch() {
   hipError_t e = hipGetLastError();

@@ -254,10 +254,17 @@ int32_t fe2o3_scalar_gemm_v1(const float *a, uint64_t a_len, const float *b,
  * A[m,k] (bf16, row-major) * B^T where B is stored column-major, i.e. as
  * [n,k] with k contiguous; fp32 accumulation, RNE bf16 output.  Exact
  * lengths m*k, n*k, m*n.  Any m, n, k.  The pipelined 256x256 MFMA tile
- * runs whenever k is a multiple of 64 (k*512 < 2^31) and A and B are 16-byte
- * aligned: whole tiles when m and n are multiples of 256 and C is 16-byte
- * aligned, edge tiles (element-wise masked stores) otherwise.  Other shapes
- * take a bounds-checked 64x64-tile kernel; k = 0 writes +0. */
+ * (128x128 for small grids) runs whenever k is a multiple of 8 (k*512 <
+ * 2^31) and A and B are 16-byte aligned, with a partial last k stage when k
+ * is not a multiple of 64: whole tiles when m and n are multiples of 256
+ * and C is 16-byte aligned, edge tiles (element-wise masked stores)
+ * otherwise.  For other k or alignments, when m and n are at least 128, the
+ * rows that cannot be read in place are first copied into aligned rows of
+ * k rounded up to 8 (zeros past k) in stream-ordered scratch from the
+ * library's pool and the tile runs on them (an operand that is only
+ * misaligned gives the aligned operand's bits).  Smaller outputs, and
+ * devices without a pool, take a bounds-checked 64x64-tile kernel; k = 0
+ * writes +0. */
 int32_t fe2o3_gemm_bf16_nt(const uint16_t *a, uint64_t a_len,
                            const uint16_t *b, uint64_t b_len, uint16_t *c,
                            uint64_t c_len, uint32_t m, uint32_t n, uint32_t k,

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from golden import reference_vectors as rv
-from gpu_util import Guarded, assert_same, bf16_to_f32, rel_err
+from gpu_util import GUARD, Guarded, assert_same, bf16_to_f32, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -380,6 +380,41 @@ def test_gemm_bf16_nt_generic_shapes(gpu, oracle, m, n, k):
                                    (512, 256, 192), (4096, 2048, 128)])
 def test_gemm_bf16_nt_fast_path(gpu, oracle, m, n, k):
     _nt_case(gpu, oracle, m, n, k, seed=1)
+
+
+@pytest.mark.parametrize("m,n,k,which", [(512, 384, 1000, "a"), (512, 384, 1000, "b"),
+                                         (384, 640, 4096, "ab"), (4096, 4096, 4096, "a")])
+def test_gemm_bf16_nt_misaligned_operands_match_aligned(gpu, m, n, k, which):
+    """A and/or B two bytes past a 16-byte boundary: their rows are copied
+    into aligned scratch and the pipelined tile runs on the copies, so C is
+    bit-identical to the aligned operands' (inputs unchanged, C's guards
+    intact)."""
+    kern = _kernels()
+    da, db = gpu.alloc(m * k, np.uint16), gpu.alloc(n * k, np.uint16)
+    kern.fill_normal_bf16(da, 9, 0xA, 1.0 / np.sqrt(k))
+    kern.fill_normal_bf16(db, 9, 0xB, 1.0 / np.sqrt(k))
+    prep = kern.gemm_bf16_nt_gpu.Kernel.load(gpu)
+    want = gpu.alloc(m * n, np.uint16)
+    prep.prepare(da, db, want, m, n, k).launch()
+    ha, hb = da.download(), db.download()
+    offs = {}
+    for key, host in (("a", ha), ("b", hb)):
+        if key in which:
+            offs[key] = Guarded(gpu, np.concatenate([np.zeros(1, np.uint16), host]))
+    ga = offs["a"].full.view(GUARD + 1, m * k) if "a" in offs else da
+    gb = offs["b"].full.view(GUARD + 1, n * k) if "b" in offs else db
+    got = Guarded(gpu, np.full(m * n, 0x7FDE, np.uint16))
+    prep.prepare(ga, gb, got.body, m, n, k).launch()
+    assert got.guards_intact() and all(o.unchanged() for o in offs.values())
+    assert_same(got.download(), want.download(), f"{which} at a 2-byte offset vs aligned")
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 260, 1003), (256, 512, 4097), (1024, 1024, 77),
+                                   (128, 128, 9)])
+def test_gemm_bf16_nt_odd_k_repacked(gpu, oracle, m, n, k):
+    """K not a multiple of 8 (rows not 16-byte aligned): both operands are
+    repacked into rows of K rounded up to 8 and the tile runs on them."""
+    _nt_case(gpu, oracle, m, n, k, seed=4)
 
 
 # M or N not a multiple of 256 with whole 64-k stages: edge tiles of the
