@@ -205,6 +205,46 @@ __global__ void __launch_bounds__(256, STAGES == 2 ? 2 : 1) gemm_fp8_128_kernel(
                                    rows_a, rows_b);
 }
 
+// ---- operand rows the tile cannot read in place ------------------------------------------
+// Rows of `cols` E4M3 bytes, `ld` apart from src (any alignment: K not a
+// multiple of 16, or a base off a 16-byte boundary), copied into rows of
+// dst_cols bytes (a multiple of 16; zeros, E4M3 +0, from cols on) at an
+// aligned dst.  16 bytes per thread and step: one load where the piece lies
+// inside the row (gfx950 global loads take any alignment), byte by byte at
+// the row's end; one 16-byte store.
+__global__ void __launch_bounds__(256) repack_bytes_kernel(const uint8_t* __restrict__ src,
+                                                           uint32_t rows, uint32_t cols,
+                                                           uint32_t ld, uint8_t* __restrict__ dst,
+                                                           uint32_t dst_cols) {
+  const uint64_t per_row = dst_cols / 16u, groups = (uint64_t)rows * per_row;
+  for (uint64_t g = (uint64_t)blockIdx.x * 256u + threadIdx.x; g < groups;
+       g += (uint64_t)gridDim.x * 256u) {
+    const uint64_t r = g / per_row;
+    const uint32_t c0 = (uint32_t)(g % per_row) * 16u;
+    const uint8_t* row = src + r * ld;
+    u32x4_t p;
+    if (c0 + 16u <= cols) {
+      __builtin_memcpy(&p, row + c0, 16);
+    } else {
+      uint8_t v[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = c0 + e < cols ? row[c0 + e] : (uint8_t)0;
+      __builtin_memcpy(&p, v, 16);
+    }
+    *reinterpret_cast<u32x4_t*>(dst + r * dst_cols + c0) = p;
+  }
+}
+
+int32_t repack_bytes(const uint8_t* src, uint32_t rows, uint32_t cols, uint8_t* dst,
+                     uint32_t dst_cols, hipStream_t s) {
+  const uint64_t g = ((uint64_t)rows * (dst_cols / 16u) + 255u) / 256u;
+  repack_bytes_kernel<<<(unsigned)(g < 16384u ? g : 16384u), 256, 0, s>>>(src, rows, cols, cols,
+                                                                          dst, dst_cols);
+  return fe2o3_host::after_launch();
+}
+
+constexpr uint32_t kRepackMin = 128;  // outputs at least this in M and N repack
+
 // ---- any shape ---------------------------------------------------------------------------
 // 64x64 output tiles, 32 k per step; each operand element is widened to bf16
 // (exact) on its way to LDS, zero outside m x k / n x k, and four waves (2x2,
@@ -304,6 +344,7 @@ const fe2o3_host::KernelRegistrar kRegistered[] = {
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<2, edge, tail, k tail>", (const void*)gemm_fp8_128_kernel<2, false, true, true>, 256, kFp8SmallSmem<2>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_128_kernel<3, edge, tail, k tail>", (const void*)gemm_fp8_128_kernel<3, false, true, true>, 256, kFp8SmallSmem<3>}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "gemm_fp8_generic_kernel", (const void*)gemm_fp8_generic_kernel, 256, 0}),
+    fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "repack_bytes_kernel", (const void*)repack_bytes_kernel, 256, 0}),
     fe2o3_host::KernelRegistrar({"fe2o3_gemm_fp8_nt", "zero_fill_bf16_kernel", (const void*)zero_fill_bf16_kernel, 256, 0})};
 
 }  // namespace
@@ -437,24 +478,61 @@ int32_t fe2o3_gemm_fp8_nt(const uint8_t* a, uint64_t a_len, const uint8_t* b, ui
   // fast path: 16-byte operand rows (K a multiple of 16) and a 256-row fp8
   // panel (256 * k bytes) within its buffer resource's 32-bit range; K not a
   // multiple of 128 takes the edge tiles with a partial last stage
-  const bool fast = k % 16 == 0 && 256ull * k < (1ull << 31) &&
-                    (((uintptr_t)a | (uintptr_t)b) & 15u) == 0;
-  if (!fast) {
+  const bool aligned_a = ((uintptr_t)a & 15u) == 0, aligned_b = ((uintptr_t)b & 15u) == 0;
+  const bool fast = k % 16 == 0 && 256ull * k < (1ull << 31) && aligned_a && aligned_b;
+  // Rows the tile cannot read in place (K not a multiple of 16, or A or B
+  // off a 16-byte boundary) are first copied into aligned rows of kp = K
+  // rounded up to 16, zeros from K on, in stream-ordered scratch; the tile
+  // then runs on kp, whose zeros fall where its partial last stage puts
+  // zeros anyway, so an operand that is only misaligned gives the bits of
+  // the aligned one.  Outputs below 128 x 128, and devices without
+  // stream-ordered scratch, take the generic kernel.
+  const uint32_t kp = (k + 15u) & ~15u;
+  const bool repack = !fast && m >= kRepackMin && n >= kRepackMin && 256ull * kp < (1ull << 31);
+  void* scratch = nullptr;
+  if (repack) {
+    const bool ra = k % 16 != 0 || !aligned_a, rb = k % 16 != 0 || !aligned_b;
+    const uint64_t a_bytes = ra ? (uint64_t)m * kp : 0, b_bytes = rb ? (uint64_t)n * kp : 0;
+    if (fe2o3_host::scratch_alloc(&scratch, a_bytes + b_bytes, s) != FE2O3_OK) {
+      (void)hipGetLastError();  // no stream-ordered scratch: the generic kernel
+      scratch = nullptr;
+    }
+  }
+  if (!fast && scratch == nullptr) {
     const dim3 grid((n + G8_BN - 1) / G8_BN, (m + G8_BM - 1) / G8_BM);
     if (grid.y > 65535u) return FE2O3_ERR_SHAPE;
     gemm_fp8_generic_kernel<<<grid, 256, 0, s>>>(a, b, scale_a, scale_b, c, m, n, k);
     return fe2o3_host::after_launch();
   }
-  const int32_t lds_rc = set_fp8_lds();  // before any launch: a failure leaves C untouched
-  if (lds_rc != FE2O3_OK) return lds_rc;
+  // every kernel's LDS limit is raised before anything is launched, so a
+  // failure leaves C untouched
+  int32_t rc = set_fp8_lds();
   tile_plan::Topology topo;
-  const int32_t topo_rc = fe2o3_host::device_topology(&topo);
-  if (topo_rc != FE2O3_OK) return topo_rc;
-  const tile_plan::Plan plan = tile_plan::plan(m, n, topo);
-  if (plan.grid > 0x7fffffffu || plan.tail_grid > 0x7fffffffu) return FE2O3_ERR_SHAPE;
-  if (k % 128 != 0)
-    return launch_fp8<true>(a, b, scale_a, scale_b, c, m, n, k, plan, topo.xcds, s);
-  return launch_fp8<false>(a, b, scale_a, scale_b, c, m, n, k, plan, topo.xcds, s);
+  if (rc == FE2O3_OK) rc = fe2o3_host::device_topology(&topo);
+  const tile_plan::Plan plan = rc == FE2O3_OK ? tile_plan::plan(m, n, topo) : tile_plan::Plan{};
+  if (rc == FE2O3_OK && (plan.grid > 0x7fffffffu || plan.tail_grid > 0x7fffffffu))
+    rc = FE2O3_ERR_SHAPE;
+  const uint8_t* ta = a;
+  const uint8_t* tb = b;
+  uint32_t tk = k;
+  if (rc == FE2O3_OK && scratch != nullptr) {
+    const bool ra = k % 16 != 0 || !aligned_a, rb = k % 16 != 0 || !aligned_b;
+    uint8_t* ap = static_cast<uint8_t*>(scratch);
+    uint8_t* bp = ap + (ra ? (uint64_t)m * kp : 0);
+    if (ra) rc = repack_bytes(a, m, k, ap, kp, s);
+    if (rb && rc == FE2O3_OK) rc = repack_bytes(b, n, k, bp, kp, s);
+    ta = ra ? ap : a;
+    tb = rb ? bp : b;
+    tk = kp;
+  }
+  if (rc == FE2O3_OK)
+    rc = tk % 128 != 0 ? launch_fp8<true>(ta, tb, scale_a, scale_b, c, m, n, tk, plan, topo.xcds, s)
+                       : launch_fp8<false>(ta, tb, scale_a, scale_b, c, m, n, tk, plan, topo.xcds, s);
+  if (scratch != nullptr) {
+    const int32_t free_rc = fe2o3_host::scratch_free(scratch, s);
+    if (rc == FE2O3_OK) rc = free_rc;
+  }
+  return rc;
 }
 
 }  // extern "C"

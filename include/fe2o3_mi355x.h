@@ -480,11 +480,16 @@ int32_t fe2o3_quantize_e4m3(const float *x, uint64_t x_len, const float *scale,
                             uint8_t *q, uint64_t q_len, void *stream);
 /* C[m,n] bf16 = (scale_a[0]*scale_b[0]) * (A_q[m,k] . B_q[n,k]^T), fp32
  * accumulation; A row-major, B stored [n,k] (k contiguous).  Any m, n, k.
- * The pipelined fp8 MFMA tile runs whenever k is a multiple of 128
- * (k*256 < 2^31) and A and B are 16-byte aligned (edge tiles for m or n not
- * a multiple of 256 or an unaligned C); otherwise a bounds-checked kernel
- * widens E4M3 to bf16 exactly and multiplies on bf16 MFMAs.  k = 0 writes
- * +0.  The products of two E4M3 values are exact in fp32 on both paths. */
+ * The pipelined fp8 MFMA tile runs whenever k is a multiple of 16
+ * (k*256 < 2^31; a partial last stage when k is not a multiple of 128) and
+ * A and B are 16-byte aligned (edge tiles for m or n not a multiple of 256
+ * or an unaligned C).  For other k or alignments, when m and n are at least
+ * 128, the rows that cannot be read in place are first copied into aligned
+ * rows of k rounded up to 16 (E4M3 +0 past k) in stream-ordered scratch
+ * from the library's pool and the tile runs on them; smaller outputs, and
+ * devices without a pool, take a bounds-checked kernel that widens E4M3 to
+ * bf16 exactly and multiplies on bf16 MFMAs.  k = 0 writes +0.  The
+ * products of two E4M3 values are exact in fp32 on every path. */
 int32_t fe2o3_gemm_fp8_nt(const uint8_t *a, uint64_t a_len, const uint8_t *b,
                           uint64_t b_len, const float *scale_a,
                           const float *scale_b, uint16_t *c, uint64_t c_len,

@@ -95,7 +95,7 @@ def test_kernel_resource_record_and_registry_without_gpu():
         assert getattr(R, name).offset == off
     L = _lib.lib()
     expected = {"fe2o3_gemm_bf16_nt": 24, "fe2o3_flash_attention_fwd": 4, "fe2o3_moe_ffn_top2": 5,
-                "fe2o3_gemm_fp8_nt": 23, "fe2o3_row_softmax": 13, "fe2o3_moe_routing_check": 7,
+                "fe2o3_gemm_fp8_nt": 24, "fe2o3_row_softmax": 13, "fe2o3_moe_routing_check": 7,
                 "fe2o3_wave64_collectives_v1": 1, "fe2o3_fp8_fnuz_from_f32": 4,
                 "fe2o3_fp8_fnuz_to_f32": 4, "fe2o3_tiled_gemm_general_v1": 12,
                 "fe2o3_bf16_from_f32": 2, "no_such_entry": 0}

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from golden import reference_vectors as rv
-from gpu_util import Guarded, assert_same, bf16_to_f32, rel_err
+from gpu_util import GUARD, Guarded, assert_same, bf16_to_f32, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -528,11 +528,14 @@ def test_gemm_fp8_k_tail(gpu, oracle, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,kp", [(1024, 1024, 4000, 4096), (300, 520, 208, 256),
-                                      (6144, 6144, 80, 128)])
+                                      (6144, 6144, 80, 128), (512, 384, 1001, 1008),
+                                      (300, 520, 77, 80)])
 def test_gemm_fp8_k_tail_matches_zero_padded_k(gpu, m, n, k, kp):
     """K not a multiple of 128 against the same operands zero-padded to whole
     stages (the plain tiles): the partial stage's zero chunks are exactly the
-    padding and the scales are the same, so C is bit-identical."""
+    padding and the scales are the same, so C is bit-identical.  K not a
+    multiple of 16 (1001, 77): the rows are first repacked into scratch rows
+    of K rounded up to 16, which is the padded operand itself."""
     kern = _k()
     rng = np.random.default_rng(k)
     # E4M3 codes without the NaN pair (0x7F, 0xFF)
@@ -547,6 +550,30 @@ def test_gemm_fp8_k_tail_matches_zero_padded_k(gpu, m, n, k, kp):
     kern.gemm_fp8_nt(gpu.to_device(a.ravel()), gpu.to_device(b.ravel()), sa, sb, c, m, n, k)
     kern.gemm_fp8_nt(gpu.to_device(ap.ravel()), gpu.to_device(bp.ravel()), sa, sb, cp, m, n, kp)
     assert_same(c.download(), cp.download(), f"K {k} vs zero-padded K {kp}")
+
+
+@pytest.mark.parametrize("m,n,k,which", [(512, 384, 1024, "a"), (384, 640, 4096, "b"),
+                                         (256, 256, 208, "ab")])
+def test_gemm_fp8_misaligned_operands_match_aligned(gpu, m, n, k, which):
+    """A and/or B one byte past a 16-byte boundary: their rows are copied
+    into aligned scratch and the pipelined tile runs on the copies, so C is
+    bit-identical to the aligned operands' (inputs unchanged)."""
+    kern = _k()
+    rng = np.random.default_rng(m + k)
+    a = rng.integers(0, 0x7F, m * k, dtype=np.uint8) | (rng.integers(0, 2, m * k, dtype=np.uint8) << 7)
+    b = rng.integers(0, 0x7F, n * k, dtype=np.uint8) | (rng.integers(0, 2, n * k, dtype=np.uint8) << 7)
+    sa = gpu.to_device(np.array([1.0 / 64], np.float32))
+    sb = gpu.to_device(np.array([1.0 / 32], np.float32))
+    want = gpu.alloc(m * n, np.uint16)
+    kern.gemm_fp8_nt(gpu.to_device(a), gpu.to_device(b), sa, sb, want, m, n, k)
+    offs = {key: Guarded(gpu, np.concatenate([np.zeros(1, np.uint8), host]))
+            for key, host in (("a", a), ("b", b)) if key in which}
+    ga = offs["a"].full.view(GUARD + 1, m * k) if "a" in offs else gpu.to_device(a)
+    gb = offs["b"].full.view(GUARD + 1, n * k) if "b" in offs else gpu.to_device(b)
+    got = Guarded(gpu, np.full(m * n, 0x7FDE, np.uint16))
+    kern.gemm_fp8_nt(ga, gb, sa, sb, got.body, m, n, k)
+    assert got.guards_intact() and all(o.unchanged() for o in offs.values())
+    assert_same(got.download(), want.download(), f"{which} at a 1-byte offset vs aligned")
 
 
 @pytest.mark.parametrize("m,n,k", [(4096, 2048, 128), (4000, 2000, 256)])
