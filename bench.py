@@ -438,7 +438,7 @@ def sec_moe(ctx, stream, args):
     flop = 3.0 * 2.0 * hdim * f * 2 * t
     tf = flop / (ms * 1e-3) / 1e12
     res = {"workload": "MoE top-2 layer: 4096 tokens, hidden 4096, 8 experts, FFN 14336, "
-                       "router + gather + gate/up SiLU + down + combine (config 5)",
+                       "router + gate/up SiLU (token rows read through the permutation) + down + combine (config 5)",
            "kernel": "gate_up_kernel + down_kernel", "ms": ms, "value": round(tf, 2),
            "unit": "TFLOP/s",
            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK["bf16"],
