@@ -278,12 +278,42 @@ constexpr uint64_t kRouteScanAbove = 8192;
 // every column in turn: its rows' sum, an exclusive scan of the sums over
 // the threads (wave scans, then the waves' sums), then the rows rewritten
 // with their exclusive prefixes.  Sums are below 2^32 (at most `routes`).
+// A table of at most kScanLdsWords words is first loaded whole into LDS (one
+// coalesced pass, where the column-by-column passes over global memory wait
+// for it once per column) and scanned there, one wave per column.
+constexpr uint32_t kScanLdsWords = 8192;
+
 __global__ void __launch_bounds__(RS_THREADS) route_scan_kernel(uint32_t* __restrict__ counts,
                                                                 uint32_t blocks, uint32_t experts,
                                                                 uint32_t* __restrict__ totals) {
   __shared__ uint32_t wave_sum[RS_THREADS / 64];
+  __shared__ uint32_t table[kScanLdsWords];
   const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
   const uint32_t cols = experts + 1u;
+  const uint64_t words = (uint64_t)blocks * cols;
+  if (words <= kScanLdsWords) {
+    for (uint32_t i = t; i < words; i += RS_THREADS) table[i] = counts[i];
+    __syncthreads();
+    // wave w scans columns w, w + 16, ...: rows in runs of 64 lanes, a
+    // running carry between runs
+    for (uint32_t c = wave; c < cols; c += RS_THREADS / 64) {
+      uint32_t carry = 0;
+      for (uint32_t b0 = 0; b0 < blocks; b0 += 64u) {
+        const uint32_t b = b0 + lane;
+        const uint32_t v = b < blocks ? table[b * cols + c] : 0u;
+        uint32_t incl = v;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const uint32_t u = (uint32_t)__shfl_up((int)incl, o, 64);
+          if (lane >= (uint32_t)o) incl += u;
+        }
+        if (b < blocks) counts[(uint64_t)b * cols + c] = carry + incl - v;
+        carry += (uint32_t)__shfl((int)incl, 63, 64);
+      }
+      if (lane == 0) totals[c] = carry;
+    }
+    return;
+  }
   const uint32_t chunk = (blocks + RS_THREADS - 1u) / RS_THREADS;
   const uint32_t b0 = min(t * chunk, blocks), b1 = min(b0 + chunk, blocks);
   for (uint32_t c = 0; c < cols; ++c) {
