@@ -15,11 +15,13 @@
 //      bit-identical to the reference's sort-based oracle.
 //
 // Expert FFN at the BASELINE shape (gate/up SiLU, down, weighted combine):
-//   gather      Xc[slot] = X[permutation[slot] / 2]              (bf16 rows)
 //   gate/up     Hc = bf16(silu(Xc Wg_e^T) * (Xc Wu_e^T))  per expert e,
-//               one 256x256 MFMA tile whose B rows interleave 32 gate rows
-//               and the matching 32 up rows, so gate and up accumulators of
-//               the same (row, f) sit in the same lane for the fused epilogue
+//               Xc[slot] = X[permutation[slot] / 2] read in place by the
+//               A-tile copies (a gather pass into the workspace first only
+//               for an X of 2 GiB or more); one 256x256 MFMA tile whose B
+//               rows interleave 32 gate rows and the matching 32 up rows,
+//               so gate and up accumulators of the same (row, f) sit in the
+//               same lane for the fused epilogue
 //   down        Yc = Hc Wd_e^T (fp32)
 //   combine     out[t] = bf16((+0 + w0*Yc[inv[2t]]) + w1*Yc[inv[2t+1]]),
 //               dropped routes contribute nothing (moe_expert_v1 combine
